@@ -1,0 +1,134 @@
+/*
+ * saf_attn.h — C-ABI of libsafattn.so, the MI355X (gfx950) implementation of
+ * Selective Attention Freezing's mixed-head causal attention prefill.
+ *
+ * The entry points replace the GPU launches behind the reference's operator
+ * surface (reference files under waylonli/Selective-Attention-Freezing):
+ *
+ *   saf_mixed_attn_fwd       kernel/fused_attn.py:572-591 (_fwd + _fwd_kernel,
+ *                            all head states in one call) and the GQA twin
+ *                            qwen/kernel/fused_attn.py:581-603 (kvidx map)
+ *   saf_flash_fwd            kernel/fused_attn.py:182-226 (_acc_flash, state 0)
+ *   saf_frozen_dense_pv_fwd  kernel/fused_attn.py:125-143 (_acc_dense, state 1)
+ *   saf_frozen_decomp_fwd    kernel/fused_attn.py:145-180 (_acc_decomp, state 2)
+ *   saf_frozen_scan_fwd      state-2 heads whose pattern is the causal mean,
+ *                            an exponential decay or a sliding window
+ *                            (kernel/fused_attn.py:12-19 defines the pattern;
+ *                            the reference evaluates it with _acc_decomp)
+ *   saf_frozen_pv_fwd        kernel/frozen_attn.py:133-148 (_launch_fwd of
+ *                            frozen_pv, compact frozen-head V)
+ *
+ * Conventions
+ *   - Every tensor is described by saf_tensor_t: a device pointer, a dtype
+ *     code, and 4-D sizes/strides counted in elements.  The innermost stride
+ *     must be 1; q/k/v rows must start on 16-byte boundaries and out rows on
+ *     8-byte boundaries (status SAF_EALIGN otherwise: make the tensor
+ *     contiguous and call again).
+ *   - The caller allocates every buffer, including out, the optional lse and
+ *     the workspace.  The library allocates no device memory.
+ *   - Head-routing tables (frozen, hidx, pidx, kvidx, closed_kind,
+ *     closed_param) are HOST arrays of n_heads entries, read during the call.
+ *   - Kernels are enqueued on `stream` (a hipStream_t) without any host
+ *     synchronisation.  Calls are re-entrant; the only mutable global state is
+ *     the thread-local error string.
+ *   - Return value: SAF_OK (0) or a negative status; saf_last_error() then
+ *     holds a message for the calling thread.
+ */
+#ifndef SAF_ATTN_H
+#define SAF_ATTN_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum {
+  SAF_OK = 0,
+  SAF_EINVAL = -1,        /* inconsistent shapes, indices or arguments */
+  SAF_EUNSUPPORTED = -2,  /* dtype / head_dim / head count not implemented */
+  SAF_EALIGN = -3,        /* pointer or stride alignment not met */
+  SAF_ELAUNCH = -4,       /* a kernel launch failed */
+  SAF_EWORKSPACE = -5     /* workspace missing or too small */
+};
+
+enum { SAF_F32 = 0, SAF_F16 = 1, SAF_BF16 = 2, SAF_I32 = 3 };
+
+/* Head states (kernel/fused_attn.py:12-19, nanogpt/model.py:869-874). */
+enum { SAF_LIVE = 0, SAF_FROZEN_DENSE = 1, SAF_FROZEN_DECOMP = 2 };
+
+/* Closed forms of a decomposed pattern softmax(alpha[j] + rho[i-j]) with
+ * alpha = 0: mean (rho = 0), decay (rho[d] = -c*d, param c > 0) and window
+ * (rho[d] = 0 for d < w and -inf beyond, param w >= 1). */
+enum { SAF_CLOSED_NONE = 0, SAF_CLOSED_MEAN = 1, SAF_CLOSED_DECAY = 2, SAF_CLOSED_WINDOW = 3 };
+
+#define SAF_MAX_HEADS 128
+
+typedef struct saf_tensor {
+  void* data;         /* device pointer (NULL = absent) */
+  int32_t dtype;      /* SAF_F32 / SAF_F16 / SAF_BF16 / SAF_I32 */
+  int32_t ndim;       /* number of used sizes/strides (<= 4) */
+  int64_t size[4];
+  int64_t stride[4];  /* in elements */
+} saf_tensor_t;
+
+typedef struct saf_mixed_attn_args {
+  /* q, k: (B, U, T, HD) compact live-head slots (U = live heads), or with
+   * kvidx: k is (B, HKV, T, HD) raw key heads.  May be absent (data NULL)
+   * when no head is live. */
+  saf_tensor_t q, k;
+  /* v: (B, H, T, HD), or (B, HKV, T, HD) with kvidx. */
+  saf_tensor_t v;
+  /* out: (B, H, T, HD), any strides with stride[3] == 1. */
+  saf_tensor_t out;
+  /* lse: optional (B, H, T) fp32, base-2 log-sum-exp of live heads. */
+  saf_tensor_t lse;
+  /* patt: (P, S, S) dense patterns, S >= T (required iff a head is state 1). */
+  saf_tensor_t patt;
+  /* alpha, rho, z: (H, S) decomposed buffers (required iff a head is
+   * state 2 without a closed form), fp32 / bf16 / fp16. */
+  saf_tensor_t alpha, rho, z;
+  int32_t n_heads;              /* H (output heads) */
+  const int32_t* frozen;        /* [H] head state, host */
+  const int32_t* hidx;          /* [H] live head -> q/k slot, host; NULL = identity */
+  const int32_t* pidx;          /* [H] dense head -> patt row, host; NULL = identity */
+  const int32_t* kvidx;         /* [H] head -> k/v head (GQA), host; NULL = none */
+  const int32_t* closed_kind;   /* [H] SAF_CLOSED_*, host; NULL = none */
+  const float* closed_param;    /* [H] decay rate or window length, host */
+  float sm_scale;               /* softmax scale (1/sqrt(HD) by default) */
+  void* workspace;              /* device scratch, saf_workspace_bytes() bytes */
+  int64_t workspace_bytes;
+  int32_t flash_qtiles;         /* 0 = auto; 1 or 2 query tiles per wave */
+  int32_t scan_spin_limit;      /* 0 = default bound of each look-back wait */
+} saf_mixed_attn_args;
+
+/* All head kinds: live flash, dense P.V, decomposed rebuild, closed-form scan. */
+int saf_mixed_attn_fwd(const saf_mixed_attn_args* args, void* stream);
+
+/* Subsets of saf_mixed_attn_fwd: each computes only its heads' rows of out. */
+int saf_flash_fwd(const saf_mixed_attn_args* args, void* stream);
+int saf_frozen_dense_pv_fwd(const saf_mixed_attn_args* args, void* stream);
+int saf_frozen_decomp_fwd(const saf_mixed_attn_args* args, void* stream);
+int saf_frozen_scan_fwd(const saf_mixed_attn_args* args, void* stream);
+
+/* frozen_pv: out[b, f] = patt[fz_idx[f], :T, :T] @ v[b, f] for compact
+ * frozen-head values v (B, nf, T, HD); fz_idx is a host array of nf entries. */
+int saf_frozen_pv_fwd(const saf_tensor_t* patt, const saf_tensor_t* v, const int32_t* fz_idx,
+                      int32_t nf, int32_t T, const saf_tensor_t* out, void* stream);
+
+/* Workspace needed by saf_mixed_attn_fwd / saf_frozen_scan_fwd for n_scan_heads
+ * closed-form heads (0 bytes when there are none). */
+int64_t saf_workspace_bytes(int32_t B, int32_t T, int32_t head_dim, int32_t n_scan_heads);
+
+/* Reads the scan's look-back error word from a workspace after the stream
+ * has been synchronised: 1 if a wait hit its spin limit, else 0. */
+int saf_workspace_error(const void* workspace, void* stream, int32_t* error_out);
+
+const char* saf_last_error(void);
+const char* saf_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* SAF_ATTN_H */

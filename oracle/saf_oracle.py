@@ -1,0 +1,286 @@
+"""CPU oracle for SAF's mixed-head causal attention prefill (numpy, float64).
+
+TEST INFRASTRUCTURE ONLY.  This module is the checker that the HIP path is
+compared against; only tests/, __graft_entry__.smoke() and bench.py's
+cpu_baseline leg may import it, and never as the thing measured or shipped.
+
+Each function restates the reference's algorithm from its source
+(waylonli/Selective-Attention-Freezing, read-only at /root/reference):
+
+  eager_mixed_attention   kernel/test_fused_attn.py:53-63 (ref) and
+                          nanogpt/model.py:824-844 (_attend_dynamic), with the
+                          GQA map of qwen/kernel/fused_attn.py:254-259
+  decomp_logits           kernel/fused_attn.py:83-98
+  decomposed_logz         kernel/fused_attn.py:101-116
+  make_rho_band           kernel/fused_attn.py:65-80
+  decomp_pattern          nanogpt/model.py:796-803 (exp(L - z))
+  frozen_pv               kernel/frozen_attn.py:185-192 / test_frozen_attn.py:27-28
+  mean/decay/window       supplement/attention.py:10-25 (causal mean),
+                          nanogpt/model.py:338-353 (uniform, local_window),
+                          nanogpt/test_prior_flash.py:47-59 (exp(-dist/scale))
+  refresh_routing         nanogpt/model.py:846-898 (_refresh_freeze_cache)
+  rope                    nanogpt/model.py:57-99
+
+How each is pinned (tests/test_oracle.py): torch SDPA as the library special
+case of the all-live case; brute-force pure-Python loops on tiny inputs;
+closed forms (prefix sums, IIR recurrences, box filters) against the dense
+patterns; invariants (rows sum to 1, T = 1 gives y = v, frozen heads ignore
+Q/K, head-permutation equivariance); routing tables brute-forced over every
+mask for H <= 8; golden vectors written from the reference's own CPU code
+(tests/golden/).
+"""
+import math
+
+import numpy as np
+
+
+def _f64(x):
+    return np.asarray(x, dtype=np.float64)
+
+
+# ---------------------------------------------------------------------------
+# patterns
+# ---------------------------------------------------------------------------
+
+def decomp_logits(alpha, rho, rows=None):
+    """L[h, i, j] = alpha[h, j] + rho[h, i - j] (j <= i), -inf above."""
+    alpha, rho = _f64(alpha), _f64(rho)
+    H, S = alpha.shape
+    r0, r1 = (0, S) if rows is None else rows
+    i = np.arange(r0, r1)[:, None]
+    j = np.arange(S)[None, :]
+    dist = i - j
+    out = alpha[:, None, :] + rho[:, np.clip(dist, 0, None)]
+    out = np.where(dist[None] < 0, -np.inf, out)
+    return out
+
+
+def logsumexp(x, axis=-1):
+    m = np.max(x, axis=axis, keepdims=True)
+    m_safe = np.where(np.isfinite(m), m, 0.0)
+    with np.errstate(divide="ignore"):
+        s = np.log(np.sum(np.exp(x - m_safe), axis=axis, keepdims=True)) + m_safe
+    return np.squeeze(s, axis=axis)
+
+
+def decomposed_logz(alpha, rho):
+    """z[h, i] = logsumexp_{j <= i}(alpha[h, j] + rho[h, i - j])."""
+    H, S = np.shape(alpha)
+    z = np.empty((H, S))
+    step = max(1, (1 << 22) // max(H * S, 1))
+    for r0 in range(0, S, step):
+        r1 = min(S, r0 + step)
+        z[:, r0:r1] = logsumexp(decomp_logits(alpha, rho, rows=(r0, r1)), axis=-1)
+    return z
+
+
+def make_rho_band(rho, band_rows=64):
+    """band[h, r, u] = rho[h, r - u + S - band_rows], -inf outside [0, S)."""
+    rho = _f64(rho)
+    H, S = rho.shape
+    r = np.arange(band_rows)[:, None]
+    u = np.arange(S)[None, :]
+    src = r - u + (S - band_rows)
+    valid = (src >= 0) & (src < S)
+    band = rho[:, np.clip(src, 0, S - 1)]
+    return np.where(valid[None], band, -np.inf)
+
+
+def decomp_pattern(alpha, rho, z, T):
+    """(H, T, T) pattern exp(alpha[j] + rho[i-j] - z[i]) with exact zeros above
+    the diagonal (what the reference materialises for its eager oracle)."""
+    alpha, rho, z = _f64(alpha), _f64(rho), _f64(z)
+    lg = decomp_logits(alpha[:, :T], rho[:, :T])
+    with np.errstate(invalid="ignore"):
+        return np.exp(lg - z[:, :T, None])
+
+
+def mean_pattern(T):
+    i = np.arange(T)
+    return np.where(i[None, :] <= i[:, None], 1.0 / (i[:, None] + 1.0), 0.0)
+
+
+def decay_pattern(T, c):
+    i = np.arange(T)
+    dist = i[:, None] - i[None, :]
+    w = np.where(dist >= 0, np.exp(-c * np.clip(dist, 0, None)), 0.0)
+    return w / w.sum(-1, keepdims=True)
+
+
+def window_pattern(T, w):
+    i = np.arange(T)
+    dist = i[:, None] - i[None, :]
+    m = (dist >= 0) & (dist < w)
+    return m / np.minimum(i + 1, w)[:, None]
+
+
+def closed_form_params(kind, param, S):
+    """(alpha, rho) vectors of length S encoding a closed-form pattern as a
+    decomposed head: mean (rho = 0), decay (rho[d] = -c d), window (0 / -inf)."""
+    d = np.arange(S, dtype=np.float64)
+    alpha = np.zeros(S)
+    if kind == "mean":
+        rho = np.zeros(S)
+    elif kind == "decay":
+        rho = -float(param) * d
+    elif kind == "window":
+        rho = np.where(d < int(param), 0.0, -np.inf)
+    else:
+        raise ValueError(kind)
+    return alpha, rho
+
+
+# closed forms evaluated directly on V (independent of the dense patterns)
+
+def mean_apply(v):
+    """y_i = (1 / (i+1)) sum_{j<=i} v_j along axis -2."""
+    v = _f64(v)
+    T = v.shape[-2]
+    return np.cumsum(v, axis=-2) / (np.arange(T) + 1.0)[:, None]
+
+
+def decay_apply(v, c):
+    """IIR s_i = e^{-c} s_{i-1} + v_i, y_i = s_i / sum_{d<=i} e^{-c d}."""
+    v = _f64(v)
+    T = v.shape[-2]
+    r = math.exp(-c)
+    s = np.zeros(v.shape[:-2] + (v.shape[-1],))
+    out = np.empty_like(v)
+    zsum = 0.0
+    for i in range(T):
+        s = r * s + v[..., i, :]
+        zsum = r * zsum + 1.0
+        out[..., i, :] = s / zsum
+    return out
+
+
+def window_apply(v, w):
+    """Box filter: mean of v over rows max(0, i-w+1)..i."""
+    v = _f64(v)
+    T = v.shape[-2]
+    c = np.concatenate([np.zeros(v.shape[:-2] + (1, v.shape[-1])), np.cumsum(v, axis=-2)], axis=-2)
+    i = np.arange(T)
+    lo = np.maximum(i - w + 1, 0)
+    return (c[..., i + 1, :] - c[..., lo, :]) / (i - lo + 1.0)[:, None]
+
+
+# ---------------------------------------------------------------------------
+# attention
+# ---------------------------------------------------------------------------
+
+def causal_attention(q, k, v, scale):
+    """softmax(q k^T * scale) v with a causal mask, for one head (T, HD)."""
+    q, k, v = _f64(q), _f64(k), _f64(v)
+    T = q.shape[0]
+    s = (q @ k.T) * scale
+    s = np.where(np.tril(np.ones((T, T), dtype=bool)), s, -np.inf)
+    s = s - s.max(-1, keepdims=True)
+    p = np.exp(s)
+    p /= p.sum(-1, keepdims=True)
+    return p @ v
+
+
+def eager_mixed_attention(q, k, v, frozen, hidx=None, pidx=None, kvidx=None,
+                          patt=None, alpha=None, rho=None, z=None, sm_scale=None,
+                          heads=None):
+    """Reference eager semantics of fused_mixed_attn for every head.
+
+    q, k: (B, U, T, HD) compact live slots (or k raw (B, HKV, T, HD) with
+    kvidx); v: (B, H or HKV, T, HD); frozen: (H,) states 0/1/2.  Returns
+    (B, H, T, HD) float64.  `heads` restricts the computation to a subset
+    (other heads are left as NaN)."""
+    v = _f64(v)
+    frozen = np.asarray(frozen)
+    H = frozen.shape[0]
+    B, _, T, HD = v.shape
+    if sm_scale is None:
+        sm_scale = 1.0 / math.sqrt(HD)
+    out = np.full((B, H, T, HD), np.nan)
+    dec_cache = {}
+    for h in (range(H) if heads is None else heads):
+        vh = h if kvidx is None else int(kvidx[h])
+        st = int(frozen[h])
+        if st == 0:
+            qs = h if hidx is None else int(hidx[h])
+            ks = qs if kvidx is None else int(kvidx[h])
+            for b in range(B):
+                out[b, h] = causal_attention(q[b, qs], k[b, ks], v[b, vh], sm_scale)
+            continue
+        if st == 1:
+            row = h if pidx is None else int(pidx[h])
+            P = _f64(patt[row, :T, :T])
+        else:
+            if h not in dec_cache:
+                dec_cache[h] = decomp_pattern(np.asarray(alpha)[h:h + 1], np.asarray(rho)[h:h + 1],
+                                              np.asarray(z)[h:h + 1], T)[0]
+            P = dec_cache[h]
+        for b in range(B):
+            out[b, h] = P @ v[b, vh]
+    return out
+
+
+def frozen_pv(patt, v, fz_idx, T):
+    """y[b, f] = patt[fz_idx[f], :T, :T] @ v[b, f]."""
+    v = _f64(v)
+    B, nf = v.shape[:2]
+    out = np.empty((B, nf, T, v.shape[-1]))
+    for f in range(nf):
+        P = _f64(patt[int(fz_idx[f]), :T, :T])
+        for b in range(B):
+            out[b, f] = P @ v[b, f, :T]
+    return out
+
+
+# ---------------------------------------------------------------------------
+# routing tables (nanogpt/model.py:846-898)
+# ---------------------------------------------------------------------------
+
+def refresh_routing(frozen, decomp=None, head_dim=1):
+    """Host restatement of _refresh_freeze_cache for one attention module."""
+    frozen = np.asarray(frozen, dtype=bool)
+    H = frozen.shape[0]
+    fz_idx = np.nonzero(frozen)[0]
+    uf_idx = np.nonzero(~frozen)[0]
+    ar = np.arange(head_dim)
+    uf_cols = (uf_idx[:, None] * head_dim + ar).reshape(-1) if uf_idx.size else None
+    fz_cols = (fz_idx[:, None] * head_dim + ar).reshape(-1) if fz_idx.size else None
+    if fz_cols is None:
+        cperm = None
+    else:
+        cperm = fz_cols if uf_cols is None else np.concatenate([uf_cols, fz_cols])
+    if decomp is None:
+        mask = frozen.astype(np.int32)
+    else:
+        dec = np.asarray(decomp, dtype=bool) & frozen
+        mask = frozen.astype(np.int32) + dec.astype(np.int32)
+    hidx = np.zeros(H, dtype=np.int32)
+    hidx[uf_idx] = np.arange(uf_idx.size, dtype=np.int32)
+    return {"fz_idx": fz_idx, "uf_idx": uf_idx, "n_frozen": int(fz_idx.size),
+            "uf_cols": uf_cols, "fz_cols": fz_cols, "cperm_cols": cperm,
+            "mask_i32": mask, "hidx_i32": hidx,
+            "hidx_id_i32": np.arange(H, dtype=np.int32),
+            "fz_idx_i32": fz_idx.astype(np.int32)}
+
+
+def gqa_kvidx(n_head, n_kv_head):
+    """kvidx[h] = h // (H / HKV) (qwen/nanogpt/hybrid_prior_attention.py:526-528)."""
+    groups = n_head // n_kv_head
+    return (np.arange(n_head) // groups).astype(np.int32)
+
+
+# ---------------------------------------------------------------------------
+# RoPE (nanogpt/model.py:57-99)
+# ---------------------------------------------------------------------------
+
+def rope_cache(dim, T, base=10000.0):
+    inv = 1.0 / (base ** (np.arange(0, dim, 2, dtype=np.float64) / dim))
+    freqs = np.outer(np.arange(T, dtype=np.float64), inv)
+    emb = np.concatenate([freqs, freqs], axis=-1)
+    return np.cos(emb), np.sin(emb)
+
+
+def apply_rope(x, cos, sin):
+    x = _f64(x)
+    half = x.shape[-1] // 2
+    rot = np.concatenate([-x[..., half:], x[..., :half]], axis=-1)
+    return x * cos + rot * sin

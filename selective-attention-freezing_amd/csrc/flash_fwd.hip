@@ -1,0 +1,197 @@
+// Live-head causal flash attention forward (state 0 heads) for gfx950.
+//
+// Semantics follow the reference's live-head accumulator
+// (/root/reference/kernel/fused_attn.py:182-226, GQA variant
+// /root/reference/qwen/kernel/fused_attn.py:183-231): base-2 online softmax
+// with qk_scale = sm_scale * log2(e), fp32 running max / sum / accumulator,
+// P rounded to the input dtype before the P.V product, output divided by the
+// row sum, and LSE = m + log2(l) in base-2 units.
+//
+// Work decomposition: one workgroup = 4 waves = (4 * 32 * QT) query rows of
+// one (batch, live head); each wave owns 32*QT queries and walks 64-key
+// blocks up to its own causal limit.  K and V^T tiles are double-buffered in
+// LDS; the next tile's global loads are issued before the current tile's
+// MFMAs.  Workgroups are ordered heaviest query block first.
+#include "saf_kernels.h"
+
+namespace saf {
+
+template <typename T, int HD, int QT>
+__global__ __launch_bounds__(256) void flash_fwd_kernel(const FlashParams p) {
+  constexpr int NW = 4, NTHR = 256;
+  constexpr int BM = NW * 32 * QT;
+  constexpr int NDT = HD / 32;   // 32-wide d tiles of O^T
+  constexpr int NKT = HD / 16;   // 16-deep k steps of Q.K
+  __shared__ __align__(16) uint4 k_lds[2][KLayout<HD>::BYTES / 16];
+  __shared__ __align__(16) uint4 v_lds[2][VLayout<HD>::BYTES / 16];
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int n = lane & 31, g = lane >> 5;
+
+  // heaviest query block first; (batch, live slot) fastest
+  const int nbh = p.B * p.n_slots;
+  const int qb = p.n_qblk - 1 - (int)(blockIdx.x / nbh);
+  const int r = blockIdx.x % nbh;
+  const int b = r / p.n_slots, slot = r % p.n_slots;
+  const int h = p.out_head[slot];
+
+  const T* qbase = reinterpret_cast<const T*>(p.q) + b * p.q_sb + (int64_t)p.q_head[slot] * p.q_sh;
+  const T* kbase = reinterpret_cast<const T*>(p.k) + b * p.k_sb + (int64_t)p.k_head[slot] * p.k_sh;
+  const T* vbase = reinterpret_cast<const T*>(p.v) + b * p.v_sb + (int64_t)p.v_head[slot] * p.v_sh;
+  T* obase = reinterpret_cast<T*>(p.out) + b * p.o_sb + (int64_t)h * p.o_sh;
+
+  const int T_len = p.T;
+  const int q0 = qb * BM;
+  const int q0w = q0 + wave * 32 * QT;
+  const int kend_wg = min(q0 + BM, T_len);
+  const int nkb = (kend_wg + 63) / 64;
+  const int kend_w = min(q0w + 32 * QT, T_len);
+  const int nkb_w = kend_w > 0 ? (kend_w + 63) / 64 : 0;
+
+  // Q as the B operand: lane (n, g), step t -> Q[q][16t + 8g .. +7]
+  uint4 qf[QT][NKT];
+#pragma unroll
+  for (int qt = 0; qt < QT; ++qt) {
+    const int q = q0w + 32 * qt + n;
+#pragma unroll
+    for (int t = 0; t < NKT; ++t)
+      qf[qt][t] = q < T_len ? *reinterpret_cast<const uint4*>(qbase + (int64_t)q * p.q_st + 16 * t + 8 * g)
+                            : make_uint4(0, 0, 0, 0);
+  }
+
+  f32x16_t o[QT][NDT];
+  float m_run[QT], l_run[QT];
+#pragma unroll
+  for (int qt = 0; qt < QT; ++qt) {
+    m_run[qt] = -INFINITY;
+    l_run[qt] = 0.f;
+#pragma unroll
+    for (int dt = 0; dt < NDT; ++dt) o[qt][dt] = zero16();
+  }
+  const float c = p.scale_log2;
+
+  KStager<T, HD, NTHR> kst;
+  VStager<T, HD, NTHR> vst;
+  kst.load(kbase, p.k_st, 0, T_len, tid);
+  vst.load(vbase, p.v_st, 0, T_len, tid);
+  kst.store(k_lds[0], tid);
+  vst.store(reinterpret_cast<uint32_t*>(v_lds[0]), tid);
+  __syncthreads();
+
+  for (int j = 0; j < nkb; ++j) {
+    const int buf = j & 1;
+    const bool more = j + 1 < nkb;
+    if (more) {
+      kst.load(kbase, p.k_st, 64 * (j + 1), T_len, tid);
+      vst.load(vbase, p.v_st, 64 * (j + 1), T_len, tid);
+    }
+    if (j < nkb_w) {
+      const int j0 = 64 * j;
+      const uint4* kt = k_lds[buf];
+      f32x16_t s[2][QT];
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks) {
+#pragma unroll
+        for (int qt = 0; qt < QT; ++qt) s[ks][qt] = zero16();
+        const int key = 32 * ks + kperm(n);
+#pragma unroll
+        for (int t = 0; t < NKT; ++t) {
+          const uint4 a = kt[KLayout<HD>::chunk(key, 2 * t + g)];
+#pragma unroll
+          for (int qt = 0; qt < QT; ++qt) s[ks][qt] = Elem<T>::mfma(a, qf[qt][t], s[ks][qt]);
+        }
+      }
+
+      const bool diag = j0 + 63 > q0w;  // some key of this block exceeds some query
+      uint4 pb[2][2][QT];
+#pragma unroll
+      for (int qt = 0; qt < QT; ++qt) {
+        const int q = q0w + 32 * qt + n;
+        float mx = -INFINITY;
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+          for (int i = 0; i < 16; ++i) {
+            float x = s[ks][qt][i];
+            if (diag && j0 + 32 * ks + acc_key(i, g) > q) x = -INFINITY;
+            s[ks][qt][i] = x;
+            mx = fmaxf(mx, x);
+          }
+        mx = fmaxf(mx, __shfl_xor(mx, 32));
+        const float m_new = fmaxf(m_run[qt], mx * c);
+        const float m_use = m_new == -INFINITY ? 0.f : m_new;
+        const float alpha = fast_exp2(m_run[qt] - m_use);
+        m_run[qt] = m_new;
+        float psum = 0.f;
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+          for (int sh = 0; sh < 2; ++sh) {
+            float e[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+              e[u] = fast_exp2(fmaf(s[ks][qt][8 * sh + u], c, -m_use));
+              psum += e[u];
+            }
+            pb[ks][sh][qt] = make_uint4(Elem<T>::pack2(e[0], e[1]), Elem<T>::pack2(e[2], e[3]),
+                                        Elem<T>::pack2(e[4], e[5]), Elem<T>::pack2(e[6], e[7]));
+          }
+        l_run[qt] = l_run[qt] * alpha + psum;
+#pragma unroll
+        for (int dt = 0; dt < NDT; ++dt)
+#pragma unroll
+          for (int i = 0; i < 16; ++i) o[qt][dt][i] *= alpha;
+      }
+      pv_block<T, HD, QT>(o, pb, v_lds[buf], lane);
+    }
+    if (more) {
+      kst.store(k_lds[buf ^ 1], tid);
+      vst.store(reinterpret_cast<uint32_t*>(v_lds[buf ^ 1]), tid);
+    }
+    __syncthreads();
+  }
+
+#pragma unroll
+  for (int qt = 0; qt < QT; ++qt) {
+    const int q = q0w + 32 * qt + n;
+    const float l_tot = l_run[qt] + __shfl_xor(l_run[qt], 32);
+    const float l_safe = l_tot == 0.f ? 1.f : l_tot;
+    if (q < T_len) {
+      store_out_tile<T, HD>(obase + (int64_t)q * p.o_st, o[qt], 1.f / l_safe, g);
+      if (p.lse != nullptr && g == 0) {
+        const float m_store = m_run[qt] == -INFINITY ? 0.f : m_run[qt];
+        p.lse[b * p.l_sb + (int64_t)h * p.l_sh + (int64_t)q * p.l_st] = m_store + __log2f(l_safe);
+      }
+    }
+  }
+}
+
+template <typename T, int HD, int QT>
+static hipError_t launch_flash_t(const FlashParams& p, hipStream_t s) {
+  const dim3 grid((unsigned)((int64_t)p.n_qblk * p.B * p.n_slots));
+  hipLaunchKernelGGL((flash_fwd_kernel<T, HD, QT>), grid, dim3(256), 0, s, p);
+  return hipGetLastError();
+}
+
+template <typename T>
+static hipError_t launch_flash_hd(const FlashParams& p, int hd, int qt, hipStream_t s) {
+  switch (hd * 4 + qt) {
+    case 32 * 4 + 1: return launch_flash_t<T, 32, 1>(p, s);
+    case 32 * 4 + 2: return launch_flash_t<T, 32, 2>(p, s);
+    case 64 * 4 + 1: return launch_flash_t<T, 64, 1>(p, s);
+    case 64 * 4 + 2: return launch_flash_t<T, 64, 2>(p, s);
+    case 96 * 4 + 1: return launch_flash_t<T, 96, 1>(p, s);
+    case 96 * 4 + 2: return launch_flash_t<T, 96, 2>(p, s);
+    case 128 * 4 + 1: return launch_flash_t<T, 128, 1>(p, s);
+    case 128 * 4 + 2: return launch_flash_t<T, 128, 2>(p, s);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+hipError_t launch_flash(const FlashParams& p, int dtype, int hd, int qt, hipStream_t s) {
+  if (dtype == kBF16) return launch_flash_hd<__bf16>(p, hd, qt, s);
+  if (dtype == kF16) return launch_flash_hd<_Float16>(p, hd, qt, s);
+  return hipErrorInvalidValue;
+}
+
+}  // namespace saf

@@ -1,0 +1,428 @@
+// Host side of libsafattn.so: argument validation, head routing and kernel
+// launches behind the C-ABI declared in include/saf_attn.h.
+//
+// Routing follows the reference's per-head state machine
+// (/root/reference/nanogpt/model.py:846-898, kernel/fused_attn.py:650-734,
+// qwen/kernel/fused_attn.py:667-768): state 0 heads read Q/K slot hidx[h]
+// (and K/V head kvidx[h] under a GQA map), state 1 heads read pattern row
+// pidx[h] (identity when absent), state 2 heads read row h of alpha/rho/z.
+// Each head kind becomes its own kernel launch over a compact head list, and
+// every kernel writes its heads' rows of the natural-order output directly.
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <string>
+#include <vector>
+
+#include "saf_attn.h"
+#include "saf_kernels.h"
+
+using namespace saf;
+
+namespace {
+
+thread_local std::string g_last_error;
+
+int fail(int code, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof(buf), fmt, ap);
+  va_end(ap);
+  g_last_error = buf;
+  return code;
+}
+
+bool present(const saf_tensor_t& t) { return t.data != nullptr; }
+
+int elem_size(int dtype) { return dtype == SAF_F32 || dtype == SAF_I32 ? 4 : 2; }
+
+const char* dtype_name(int d) {
+  switch (d) {
+    case SAF_F32: return "float32";
+    case SAF_F16: return "float16";
+    case SAF_BF16: return "bfloat16";
+    case SAF_I32: return "int32";
+    default: return "unknown";
+  }
+}
+
+// Row-aligned 4-D activation: stride[3] == 1, base and row strides aligned to
+// `align` bytes.
+int check_act(const saf_tensor_t& t, const char* name, int align) {
+  if (t.ndim != 4) return fail(SAF_EINVAL, "%s must be 4-D (got %d-D)", name, t.ndim);
+  if (t.stride[3] != 1 && t.size[3] != 1)
+    return fail(SAF_EALIGN, "%s must have a contiguous last dimension (stride %lld)", name,
+                (long long)t.stride[3]);
+  const int es = elem_size(t.dtype);
+  if (reinterpret_cast<uintptr_t>(t.data) % align != 0)
+    return fail(SAF_EALIGN, "%s data pointer is not %d-byte aligned", name, align);
+  for (int i = 0; i < 3; ++i)
+    if (t.size[i] > 1 && (t.stride[i] * es) % align != 0)
+      return fail(SAF_EALIGN, "%s stride %d (%lld elements) is not a multiple of %d bytes", name, i,
+                  (long long)t.stride[i], align);
+  return SAF_OK;
+}
+
+bool supported_hd(int64_t hd) { return hd == 32 || hd == 64 || hd == 96 || hd == 128; }
+
+int n_scan_chunks(int T, int hd) { return (T + scan_chunk_rows(hd) - 1) / scan_chunk_rows(hd); }
+
+struct WsLayout {
+  int64_t flags_off, agg_off, incl_off, total;
+};
+
+WsLayout ws_layout(int64_t B, int64_t T, int hd, int64_t n_scan) {
+  WsLayout w{0, 0, 0, 0};
+  if (n_scan <= 0 || T <= 0 || B <= 0) return w;
+  const int64_t nseq = B * n_scan, nch = n_scan_chunks((int)T, hd);
+  w.flags_off = 8;
+  const int64_t words_end = 8 + 4 * nseq * nch;
+  w.agg_off = (words_end + 255) / 256 * 256;
+  w.incl_off = w.agg_off + 4 * nseq * nch * hd;
+  w.total = w.incl_off + 4 * nseq * nch * hd;
+  return w;
+}
+
+enum Which : unsigned { kDoFlash = 1, kDoDense = 2, kDoDecomp = 4, kDoScan = 8, kDoAll = 15 };
+
+struct Plan {
+  int B = 0, T = 0, H = 0, HD = 0, HV = 0, dtype = 0;
+  std::vector<int> live, dense, decomp, scan;
+};
+
+int plan_and_validate(const saf_mixed_attn_args* a, unsigned which, Plan& pl) {
+  if (a == nullptr) return fail(SAF_EINVAL, "args is NULL");
+  const saf_tensor_t& v = a->v;
+  if (!present(v)) return fail(SAF_EINVAL, "v is required");
+  if (v.ndim != 4) return fail(SAF_EINVAL, "q, k, v must be 4-D");
+  if (v.dtype == SAF_F32)
+    return fail(SAF_EUNSUPPORTED, "float32 attention inputs are not supported by the MFMA path (use bf16 or fp16)");
+  if (v.dtype != SAF_BF16 && v.dtype != SAF_F16)
+    return fail(SAF_EUNSUPPORTED, "unsupported v dtype %s", dtype_name(v.dtype));
+  pl.B = (int)v.size[0];
+  pl.HV = (int)v.size[1];
+  pl.T = (int)v.size[2];
+  pl.HD = (int)v.size[3];
+  pl.dtype = v.dtype;
+  pl.H = a->n_heads;
+  if (!supported_hd(pl.HD)) return fail(SAF_EUNSUPPORTED, "head_dim %d is not supported (32, 64, 96, 128)", pl.HD);
+  if (pl.H <= 0 || pl.H > SAF_MAX_HEADS)
+    return fail(SAF_EUNSUPPORTED, "n_heads %d outside 1..%d", pl.H, SAF_MAX_HEADS);
+  if (a->frozen == nullptr) return fail(SAF_EINVAL, "frozen (host head-state table) is required");
+  if (a->kvidx == nullptr && pl.HV != pl.H)
+    return fail(SAF_EINVAL, "v must hold one head per output head (or pass kvidx)");
+  if (int rc = check_act(v, "v", 16)) return rc;
+
+  const saf_tensor_t& o = a->out;
+  if (!present(o)) return fail(SAF_EINVAL, "out is required");
+  if (o.ndim != 4 || o.size[0] != pl.B || o.size[1] != pl.H || o.size[2] != pl.T || o.size[3] != pl.HD)
+    return fail(SAF_EINVAL, "out must have shape (B, H, T, HD) = (%d, %d, %d, %d)", pl.B, pl.H, pl.T, pl.HD);
+  if (o.dtype != v.dtype) return fail(SAF_EINVAL, "out dtype must match v");
+  if (int rc = check_act(o, "out", 8)) return rc;
+
+  for (int h = 0; h < pl.H; ++h) {
+    const int st = a->frozen[h];
+    if (st < 0 || st > 2) return fail(SAF_EINVAL, "frozen[%d] = %d is not a head state (0, 1, 2)", h, st);
+    if (a->kvidx && (a->kvidx[h] < 0 || a->kvidx[h] >= pl.HV))
+      return fail(SAF_EINVAL, "kvidx must index the HKV heads of k/v (kvidx[%d] = %d)", h, a->kvidx[h]);
+    if (st == 0) {
+      pl.live.push_back(h);
+    } else if (st == 1) {
+      pl.dense.push_back(h);
+    } else {
+      const int ck = a->closed_kind ? a->closed_kind[h] : SAF_CLOSED_NONE;
+      if (ck < SAF_CLOSED_NONE || ck > SAF_CLOSED_WINDOW)
+        return fail(SAF_EINVAL, "closed_kind[%d] = %d is not a closed form", h, ck);
+      if (ck != SAF_CLOSED_NONE) {
+        if (a->closed_param == nullptr) return fail(SAF_EINVAL, "closed_param is required with closed_kind");
+        const float prm = a->closed_param[h];
+        if (ck == SAF_CLOSED_DECAY && !(prm > 0.f && std::isfinite(prm)))
+          return fail(SAF_EINVAL, "decay rate of head %d must be finite and > 0 (got %g)", h, prm);
+        if (ck == SAF_CLOSED_WINDOW && !(prm >= 1.f && prm < 2.1e9f && prm == std::floor(prm)))
+          return fail(SAF_EINVAL, "window length of head %d must be an integer >= 1 (got %g)", h, prm);
+        pl.scan.push_back(h);
+      } else {
+        pl.decomp.push_back(h);
+      }
+    }
+  }
+
+  if ((which & kDoFlash) && !pl.live.empty()) {
+    const saf_tensor_t& q = a->q;
+    const saf_tensor_t& k = a->k;
+    if (!present(q) || !present(k)) return fail(SAF_EINVAL, "live heads require q and k");
+    if (q.ndim != 4 || k.ndim != 4) return fail(SAF_EINVAL, "q, k, v must be 4-D");
+    if (q.dtype != v.dtype || k.dtype != v.dtype) return fail(SAF_EINVAL, "q, k and v must share a dtype");
+    if (q.size[0] != pl.B || q.size[2] != pl.T || q.size[3] != pl.HD)
+      return fail(SAF_EINVAL, "q/k batch, sequence, and head dimensions must match v");
+    if (a->kvidx) {
+      for (int i = 0; i < 4; ++i)
+        if (k.size[i] != v.size[i]) return fail(SAF_EINVAL, "with kvidx, k and v are the raw (B, HKV, T, HD) heads");
+    } else {
+      for (int i = 0; i < 4; ++i)
+        if (k.size[i] != q.size[i]) return fail(SAF_EINVAL, "q and k must have the same compact shape");
+    }
+    if (int rc = check_act(q, "q", 16)) return rc;
+    if (int rc = check_act(k, "k", 16)) return rc;
+    const int U = (int)q.size[1];
+    for (int h : pl.live) {
+      const int slot = a->hidx ? a->hidx[h] : h;
+      if (slot < 0 || slot >= U)
+        return fail(SAF_EINVAL, "hidx[%d] = %d does not index the %d compact q/k heads", h, slot, U);
+    }
+  }
+  if ((which & kDoDense) && !pl.dense.empty()) {
+    const saf_tensor_t& p = a->patt;
+    if (!present(p)) return fail(SAF_EINVAL, "dense-frozen heads require patt");
+    if (p.ndim != 3 || p.size[1] < pl.T || p.size[2] < pl.T)
+      return fail(SAF_EINVAL, "patt must have shape (P, S, S) with S >= T");
+    if (p.dtype != SAF_F32 && p.dtype != SAF_BF16 && p.dtype != SAF_F16)
+      return fail(SAF_EUNSUPPORTED, "unsupported patt dtype %s", dtype_name(p.dtype));
+    for (int h : pl.dense) {
+      const int row = a->pidx ? a->pidx[h] : h;
+      if (row < 0 || row >= p.size[0])
+        return fail(a->pidx ? SAF_EINVAL : SAF_EINVAL,
+                    a->pidx ? "pidx for dense-frozen heads must index patt (pidx[%d] = %d)"
+                            : "identity pattern mapping requires at least H pattern rows (head %d)",
+                    h, row);
+    }
+  }
+  if ((which & kDoDecomp) && !pl.decomp.empty()) {
+    const saf_tensor_t* bufs[3] = {&a->alpha, &a->rho, &a->z};
+    const char* names[3] = {"alpha", "rho", "z"};
+    for (int i = 0; i < 3; ++i) {
+      const saf_tensor_t& t = *bufs[i];
+      if (!present(t)) return fail(SAF_EINVAL, "decomposed-frozen heads require alpha/rho/z");
+      if (t.ndim != 2 || t.size[0] != pl.H || t.size[1] < pl.T)
+        return fail(SAF_EINVAL, "decomposed buffers must have shape (H, S) with S >= T (%s)", names[i]);
+      if (t.dtype != SAF_F32 && t.dtype != SAF_BF16 && t.dtype != SAF_F16)
+        return fail(SAF_EUNSUPPORTED, "unsupported %s dtype %s", names[i], dtype_name(t.dtype));
+    }
+  }
+  if ((which & kDoScan) && !pl.scan.empty()) {
+    const WsLayout w = ws_layout(pl.B, pl.T, pl.HD, (int64_t)pl.scan.size());
+    if (a->workspace == nullptr || a->workspace_bytes < w.total)
+      return fail(SAF_EWORKSPACE, "closed-form heads need a %lld-byte workspace (got %lld)", (long long)w.total,
+                  (long long)a->workspace_bytes);
+    if (reinterpret_cast<uintptr_t>(a->workspace) % 256 != 0)
+      return fail(SAF_EALIGN, "workspace must be 256-byte aligned");
+  }
+  return SAF_OK;
+}
+
+int launched(hipError_t e, const char* what) {
+  if (e != hipSuccess) return fail(SAF_ELAUNCH, "%s launch failed: %s", what, hipGetErrorString(e));
+  return SAF_OK;
+}
+
+int run_flash(const saf_mixed_attn_args* a, const Plan& pl, hipStream_t s) {
+  if (pl.live.empty() || pl.T == 0 || pl.B == 0) return SAF_OK;
+  FlashParams p{};
+  p.q = a->q.data;
+  p.k = a->k.data;
+  p.v = a->v.data;
+  p.out = a->out.data;
+  p.lse = present(a->lse) ? reinterpret_cast<float*>(a->lse.data) : nullptr;
+  p.q_sb = a->q.stride[0]; p.q_sh = a->q.stride[1]; p.q_st = a->q.stride[2];
+  p.k_sb = a->k.stride[0]; p.k_sh = a->k.stride[1]; p.k_st = a->k.stride[2];
+  p.v_sb = a->v.stride[0]; p.v_sh = a->v.stride[1]; p.v_st = a->v.stride[2];
+  p.o_sb = a->out.stride[0]; p.o_sh = a->out.stride[1]; p.o_st = a->out.stride[2];
+  if (p.lse) {
+    const saf_tensor_t& l = a->lse;
+    if (l.ndim != 3 || l.size[0] != pl.B || l.size[1] != pl.H || l.size[2] != pl.T || l.dtype != SAF_F32)
+      return fail(SAF_EINVAL, "lse must be (B, H, T) float32");
+    p.l_sb = l.stride[0]; p.l_sh = l.stride[1]; p.l_st = l.stride[2];
+  }
+  int qt = a->flash_qtiles;
+  if (qt == 0) qt = pl.HD <= 64 ? 2 : 1;
+  if (qt != 1 && qt != 2) return fail(SAF_EINVAL, "flash_qtiles must be 0, 1 or 2");
+  p.B = pl.B;
+  p.T = pl.T;
+  p.n_slots = (int)pl.live.size();
+  p.n_qblk = (pl.T + block_rows(qt) - 1) / block_rows(qt);
+  p.scale_log2 = a->sm_scale * kLog2e;
+  for (int i = 0; i < p.n_slots; ++i) {
+    const int h = pl.live[i];
+    const int slot = a->hidx ? a->hidx[h] : h;
+    p.out_head[i] = (int16_t)h;
+    p.q_head[i] = (int16_t)slot;
+    p.k_head[i] = (int16_t)(a->kvidx ? a->kvidx[h] : slot);
+    p.v_head[i] = (int16_t)(a->kvidx ? a->kvidx[h] : h);
+  }
+  return launched(launch_flash(p, pl.dtype, pl.HD, qt, s), "flash");
+}
+
+void fill_frozen_common(FrozenParams& p, const saf_tensor_t& v, const saf_tensor_t& o, int B, int T) {
+  p.v = v.data;
+  p.out = o.data;
+  p.v_sb = v.stride[0]; p.v_sh = v.stride[1]; p.v_st = v.stride[2];
+  p.o_sb = o.stride[0]; p.o_sh = o.stride[1]; p.o_st = o.stride[2];
+  p.B = B;
+  p.T = T;
+}
+
+int frozen_qtiles(int hd) { return hd <= 64 ? 2 : 1; }
+
+int run_dense(const saf_tensor_t& patt, const saf_tensor_t& v, const saf_tensor_t& o, int B, int T, int HD,
+              int dtype, const std::vector<int>& out_head, const std::vector<int>& v_head,
+              const std::vector<int>& pat_head, hipStream_t s) {
+  if (out_head.empty() || T == 0 || B == 0) return SAF_OK;
+  FrozenParams p{};
+  fill_frozen_common(p, v, o, B, T);
+  p.patt = patt.data;
+  p.patt_dtype = patt.dtype;
+  p.p_sh = patt.stride[0]; p.p_si = patt.stride[1]; p.p_sj = patt.stride[2];
+  const int es = elem_size(patt.dtype);
+  p.patt_vec = patt.stride[2] == 1 && reinterpret_cast<uintptr_t>(patt.data) % 16 == 0 &&
+               (patt.stride[1] * es) % 16 == 0 && (patt.stride[0] * es) % 16 == 0;
+  p.n_slots = (int)out_head.size();
+  p.n_qblk = (T + block_rows(frozen_qtiles(HD)) - 1) / block_rows(frozen_qtiles(HD));
+  for (int i = 0; i < p.n_slots; ++i) {
+    p.out_head[i] = (int16_t)out_head[i];
+    p.v_head[i] = (int16_t)v_head[i];
+    p.pat_head[i] = (int16_t)pat_head[i];
+  }
+  return launched(launch_frozen_pv(p, dtype, HD, 0, s), "dense P.V");
+}
+
+int run_decomp(const saf_mixed_attn_args* a, const Plan& pl, hipStream_t s) {
+  if (pl.decomp.empty() || pl.T == 0 || pl.B == 0) return SAF_OK;
+  FrozenParams p{};
+  fill_frozen_common(p, a->v, a->out, pl.B, pl.T);
+  p.alpha = a->alpha.data; p.a_dtype = a->alpha.dtype; p.a_sh = a->alpha.stride[0]; p.a_ss = a->alpha.stride[1];
+  p.rho = a->rho.data; p.r_dtype = a->rho.dtype; p.r_sh = a->rho.stride[0]; p.r_ss = a->rho.stride[1];
+  p.z = a->z.data; p.z_dtype = a->z.dtype; p.z_sh = a->z.stride[0]; p.z_ss = a->z.stride[1];
+  p.n_slots = (int)pl.decomp.size();
+  p.n_qblk = (pl.T + block_rows(frozen_qtiles(pl.HD)) - 1) / block_rows(frozen_qtiles(pl.HD));
+  for (int i = 0; i < p.n_slots; ++i) {
+    const int h = pl.decomp[i];
+    p.out_head[i] = (int16_t)h;
+    p.v_head[i] = (int16_t)(a->kvidx ? a->kvidx[h] : h);
+    p.pat_head[i] = (int16_t)h;
+  }
+  return launched(launch_frozen_pv(p, pl.dtype, pl.HD, 1, s), "decomposed P.V");
+}
+
+int run_scan(const saf_mixed_attn_args* a, const Plan& pl, hipStream_t s) {
+  if (pl.scan.empty() || pl.T == 0 || pl.B == 0) return SAF_OK;
+  const WsLayout w = ws_layout(pl.B, pl.T, pl.HD, (int64_t)pl.scan.size());
+  char* ws = reinterpret_cast<char*>(a->workspace);
+  ScanParams p{};
+  p.v = a->v.data;
+  p.out = a->out.data;
+  p.v_sb = a->v.stride[0]; p.v_sh = a->v.stride[1]; p.v_st = a->v.stride[2];
+  p.o_sb = a->out.stride[0]; p.o_sh = a->out.stride[1]; p.o_st = a->out.stride[2];
+  p.B = pl.B;
+  p.T = pl.T;
+  p.n_slots = (int)pl.scan.size();
+  p.n_chunks = n_scan_chunks(pl.T, pl.HD);
+  p.counter = reinterpret_cast<uint32_t*>(ws);
+  p.error = reinterpret_cast<uint32_t*>(ws + 4);
+  p.flags = reinterpret_cast<uint32_t*>(ws + w.flags_off);
+  p.agg = reinterpret_cast<float*>(ws + w.agg_off);
+  p.incl = reinterpret_cast<float*>(ws + w.incl_off);
+  p.spin_limit = a->scan_spin_limit > 0 ? a->scan_spin_limit : (1 << 24);
+  for (int i = 0; i < p.n_slots; ++i) {
+    const int h = pl.scan[i];
+    p.out_head[i] = (int16_t)h;
+    p.v_head[i] = (int16_t)(a->kvidx ? a->kvidx[h] : h);
+    p.kind[i] = (int8_t)a->closed_kind[h];
+    p.param[i] = a->closed_param[h];
+  }
+  const int64_t words = 2 + (int64_t)pl.B * p.n_slots * p.n_chunks;
+  if (int rc = launched(launch_zero_u32(p.counter, words, s), "workspace clear")) return rc;
+  return launched(launch_scan(p, pl.dtype, pl.HD, s), "closed-form scan");
+}
+
+int run_dense_mixed(const saf_mixed_attn_args* a, const Plan& pl, hipStream_t s) {
+  std::vector<int> vh, ph;
+  for (int h : pl.dense) {
+    vh.push_back(a->kvidx ? a->kvidx[h] : h);
+    ph.push_back(a->pidx ? a->pidx[h] : h);
+  }
+  return run_dense(a->patt, a->v, a->out, pl.B, pl.T, pl.HD, pl.dtype, pl.dense, vh, ph, s);
+}
+
+int run(const saf_mixed_attn_args* a, unsigned which, void* stream) {
+  Plan pl;
+  if (int rc = plan_and_validate(a, which, pl)) return rc;
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  if (which & kDoFlash)
+    if (int rc = run_flash(a, pl, s)) return rc;
+  if (which & kDoScan)
+    if (int rc = run_scan(a, pl, s)) return rc;
+  if (which & kDoDense)
+    if (int rc = run_dense_mixed(a, pl, s)) return rc;
+  if (which & kDoDecomp)
+    if (int rc = run_decomp(a, pl, s)) return rc;
+  return SAF_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int saf_mixed_attn_fwd(const saf_mixed_attn_args* args, void* stream) { return run(args, kDoAll, stream); }
+int saf_flash_fwd(const saf_mixed_attn_args* args, void* stream) { return run(args, kDoFlash, stream); }
+int saf_frozen_dense_pv_fwd(const saf_mixed_attn_args* args, void* stream) { return run(args, kDoDense, stream); }
+int saf_frozen_decomp_fwd(const saf_mixed_attn_args* args, void* stream) { return run(args, kDoDecomp, stream); }
+int saf_frozen_scan_fwd(const saf_mixed_attn_args* args, void* stream) { return run(args, kDoScan, stream); }
+
+int saf_frozen_pv_fwd(const saf_tensor_t* patt, const saf_tensor_t* v, const int32_t* fz_idx, int32_t nf,
+                      int32_t T, const saf_tensor_t* out, void* stream) {
+  if (patt == nullptr || v == nullptr || out == nullptr) return fail(SAF_EINVAL, "patt, v and out are required");
+  if (!present(*v) || !present(*out)) return fail(SAF_EINVAL, "v and out must be device tensors");
+  if (v->ndim != 4 || out->ndim != 4) return fail(SAF_EINVAL, "v and out must be 4-D (B, nf, T, hd)");
+  if (v->dtype == SAF_F32)
+    return fail(SAF_EUNSUPPORTED, "float32 values are not supported by the MFMA path (use bf16 or fp16)");
+  if (v->dtype != SAF_BF16 && v->dtype != SAF_F16)
+    return fail(SAF_EUNSUPPORTED, "unsupported v dtype %s", dtype_name(v->dtype));
+  const int B = (int)v->size[0], HD = (int)v->size[3];
+  if (nf != v->size[1]) return fail(SAF_EINVAL, "fz_idx must have one entry per compact head (%d != %lld)", nf,
+                                    (long long)v->size[1]);
+  if (nf > SAF_MAX_HEADS) return fail(SAF_EUNSUPPORTED, "more than %d frozen heads", SAF_MAX_HEADS);
+  if (T < 0 || T > v->size[2]) return fail(SAF_EINVAL, "T must be within v's sequence length");
+  if (!supported_hd(HD)) return fail(SAF_EUNSUPPORTED, "head_dim %d is not supported (32, 64, 96, 128)", HD);
+  if (out->size[0] != B || out->size[1] != nf || out->size[2] != T || out->size[3] != HD || out->dtype != v->dtype)
+    return fail(SAF_EINVAL, "out must be (B, nf, T, hd) in v's dtype");
+  if (int rc = check_act(*v, "v", 16)) return rc;
+  if (int rc = check_act(*out, "out", 8)) return rc;
+  if (nf == 0 || T == 0 || B == 0) return SAF_OK;
+  if (!present(*patt) || patt->ndim != 3 || patt->size[1] < T || patt->size[2] < T)
+    return fail(SAF_EINVAL, "patt must have shape (P, S, S) with S >= T");
+  if (patt->dtype != SAF_F32 && patt->dtype != SAF_BF16 && patt->dtype != SAF_F16)
+    return fail(SAF_EUNSUPPORTED, "unsupported patt dtype %s", dtype_name(patt->dtype));
+  if (fz_idx == nullptr) return fail(SAF_EINVAL, "fz_idx (host) is required");
+  std::vector<int> oh, vh, ph;
+  for (int f = 0; f < nf; ++f) {
+    if (fz_idx[f] < 0 || fz_idx[f] >= patt->size[0])
+      return fail(SAF_EINVAL, "fz_idx[%d] = %d does not index patt", f, fz_idx[f]);
+    oh.push_back(f);
+    vh.push_back(f);
+    ph.push_back(fz_idx[f]);
+  }
+  return run_dense(*patt, *v, *out, B, T, HD, v->dtype, oh, vh, ph, reinterpret_cast<hipStream_t>(stream));
+}
+
+int64_t saf_workspace_bytes(int32_t B, int32_t T, int32_t head_dim, int32_t n_scan_heads) {
+  if (!supported_hd(head_dim)) return 0;
+  return ws_layout(B, T, head_dim, n_scan_heads).total;
+}
+
+int saf_workspace_error(const void* workspace, void* stream, int32_t* error_out) {
+  if (workspace == nullptr || error_out == nullptr) return fail(SAF_EINVAL, "workspace and error_out are required");
+  uint32_t e = 0;
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  hipError_t rc = hipMemcpyAsync(&e, reinterpret_cast<const char*>(workspace) + 4, 4, hipMemcpyDeviceToHost, s);
+  if (rc == hipSuccess) rc = hipStreamSynchronize(s);
+  if (rc != hipSuccess) return fail(SAF_ELAUNCH, "reading the workspace failed: %s", hipGetErrorString(rc));
+  *error_out = (int32_t)e;
+  return SAF_OK;
+}
+
+const char* saf_last_error(void) { return g_last_error.c_str(); }
+
+const char* saf_version(void) { return "saf-mi355x 0.1.0 (gfx950)"; }
+
+}  // extern "C"

@@ -1,0 +1,247 @@
+// Device-side building blocks shared by the SAF mixed-head attention kernels
+// (gfx950 / CDNA4 only).
+//
+// Every attention kernel in this library uses the same "transposed" MFMA
+// formulation on v_mfma_f32_32x32x16_{bf16,f16}:
+//
+//   S^T[key][query] = K[key][:] . Q^T[:][query]      (A = K tile from LDS,
+//                                                      B = Q held in VGPRs)
+//   O^T[d][query]  += V^T[d][key] . P^T[key][query]   (A = V^T tile from LDS,
+//                                                      B = P^T in VGPRs)
+//
+// With a 32x32 accumulator, lane l owns column (l % 32) = one query, and its
+// 16 accumulator registers hold 16 rows.  So every per-query quantity of the
+// online softmax (running max, running sum, rescale factor) lives in a single
+// lane (plus its partner lane l ^ 32), and no cross-lane row reduction is
+// needed apart from one swap between the two wave halves.
+//
+// Lane layout of v_mfma_f32_32x32x16 (A: 32xK16, B: K16x32, C: 32x32):
+//   A: lane l holds row (l % 32), k = 8*(l/32) + 0..7       (8 x 16-bit)
+//   B: lane l holds col (l % 32), k = 8*(l/32) + 0..7       (8 x 16-bit)
+//   C: lane l, reg i holds col (l % 32), row 8*(i/4) + 4*(l/32) + (i%4)
+// A k-permutation applied identically to A and B leaves the product
+// unchanged, and a row permutation of A permutes the rows of C.  The kernels
+// use the latter: A-lane row m of the S^T product is loaded with key
+// kperm(m), chosen so that C register i of lane-half g holds key
+// 16*(i/8) + 8*g + (i%8).  Registers 8s..8s+7 of a lane are then exactly the
+// B operand (keys 16s + 8g + 0..7) of the P.V product, with no shuffles.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace saf {
+
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
+typedef float f32x16_t __attribute__((ext_vector_type(16)));
+
+constexpr float kLog2e = 1.4426950408889634f;  // 1 / ln(2)
+
+// ---- element types: bf16 and fp16 storage, fp32 arithmetic -----------------
+
+template <typename T> struct Elem;
+
+template <> struct Elem<__bf16> {
+  __device__ static inline f32x16_t mfma(uint4 a, uint4 b, f32x16_t c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+        __builtin_bit_cast(bf16x8_t, a), __builtin_bit_cast(bf16x8_t, b), c, 0, 0, 0);
+  }
+  // two fp32 values -> one dword of two round-to-nearest-even bf16
+  __device__ static inline uint32_t pack2(float lo, float hi) {
+    bf16x2_t v;
+    v[0] = (__bf16)lo;
+    v[1] = (__bf16)hi;
+    return __builtin_bit_cast(uint32_t, v);
+  }
+  __device__ static inline float lo(uint32_t w) { return __uint_as_float(w << 16); }
+  __device__ static inline float hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
+};
+
+template <> struct Elem<_Float16> {
+  __device__ static inline f32x16_t mfma(uint4 a, uint4 b, f32x16_t c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(
+        __builtin_bit_cast(f16x8_t, a), __builtin_bit_cast(f16x8_t, b), c, 0, 0, 0);
+  }
+  __device__ static inline uint32_t pack2(float lo, float hi) {
+    f16x2_t v;
+    v[0] = (_Float16)lo;
+    v[1] = (_Float16)hi;
+    return __builtin_bit_cast(uint32_t, v);
+  }
+  __device__ static inline float lo(uint32_t w) {
+    return (float)__builtin_bit_cast(_Float16, (uint16_t)(w & 0xffffu));
+  }
+  __device__ static inline float hi(uint32_t w) {
+    return (float)__builtin_bit_cast(_Float16, (uint16_t)(w >> 16));
+  }
+};
+
+// Pattern / parameter buffers may be stored in fp32, bf16 or fp16; the
+// kernels always widen them to fp32 first.
+__device__ inline float load_as_f32(const void* p, int64_t idx, int dtype) {
+  if (dtype == 0) return reinterpret_cast<const float*>(p)[idx];
+  uint16_t bits = reinterpret_cast<const uint16_t*>(p)[idx];
+  if (dtype == 2) return __uint_as_float(((uint32_t)bits) << 16);
+  return (float)__builtin_bit_cast(_Float16, bits);
+}
+
+__device__ inline f32x16_t zero16() {
+  f32x16_t z;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) z[i] = 0.f;
+  return z;
+}
+
+__device__ inline float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// Row permutation of the S^T product (see header comment).  A-lane row
+// m = 8a + 4g + r  loads key 16*(a/2) + 8g + 4*(a%2) + r.
+__device__ inline int kperm(int m) {
+  const int a = m >> 3, g = (m >> 2) & 1, r = m & 3;
+  return 16 * (a >> 1) + 8 * g + 4 * (a & 1) + r;
+}
+
+// Key held by accumulator register i of lane-half g (0..31 within a 32-key
+// S^T subtile), given the kperm row order above.
+__device__ inline int acc_key(int i, int g) { return 16 * (i >> 3) + 8 * g + (i & 7); }
+
+// ---- LDS layouts -------------------------------------------------------------
+// K tile: 64 keys x HD, row pitch KCHP 16-byte chunks (KCHP = next pow2 of
+// HD/8).  Chunks are XOR-swizzled by a function of the key so that the 32
+// A-lanes of an MFMA (32 different keys, same chunk) hit distinct banks.
+template <int HD> struct KLayout {
+  static constexpr int KCH = HD / 8;
+  static constexpr int KCHP = KCH <= 4 ? 4 : (KCH <= 8 ? 8 : 16);
+  static constexpr int BYTES = 64 * KCHP * 16;
+  __device__ static inline int chunk(int key, int c) {
+    const int f = (key & 3) | ((key >> 1) & 4);
+    return key * KCHP + (c ^ (f & (KCHP - 1)));
+  }
+};
+
+// V^T tile: HD rows (d) x 64 keys = 8 chunks of 8 keys per row, swizzled so
+// that both the transposing 4-byte writes and the 16-byte A-operand reads are
+// spread over all banks.
+template <int HD> struct VLayout {
+  static constexpr int BYTES = HD * 128;
+  __device__ static inline int chunk(int d, int kc) {
+    return d * 8 + (kc ^ ((d ^ (d >> 3)) & 7));
+  }
+};
+
+// Stage a 64-key V tile (rows j0..j0+63 of one head) into registers:
+// item idx covers keys 2kp, 2kp+1 and columns 8c..8c+7.  Rows >= T are zero.
+template <typename T, int HD, int NTHR> struct VStager {
+  static constexpr int KCH = HD / 8;
+  static constexpr int ITEMS = 32 * KCH;
+  static constexpr int PER_THR = (ITEMS + NTHR - 1) / NTHR;
+  uint4 r0[PER_THR], r1[PER_THR];
+
+  __device__ inline void load(const T* vbase, int64_t v_st, int j0, int T_len, int tid) {
+#pragma unroll
+    for (int p = 0; p < PER_THR; ++p) {
+      const int idx = tid + p * NTHR;
+      r0[p] = make_uint4(0, 0, 0, 0);
+      r1[p] = make_uint4(0, 0, 0, 0);
+      if (ITEMS % NTHR == 0 || idx < ITEMS) {
+        const int kp = idx / KCH, c = idx % KCH;
+        const int row = j0 + 2 * kp;
+        if (row < T_len)
+          r0[p] = *reinterpret_cast<const uint4*>(vbase + (int64_t)row * v_st + 8 * c);
+        if (row + 1 < T_len)
+          r1[p] = *reinterpret_cast<const uint4*>(vbase + (int64_t)(row + 1) * v_st + 8 * c);
+      }
+    }
+  }
+
+  // Transposed store: dword (key 2kp, key 2kp+1) of column d = 8c + e.
+  __device__ inline void store(uint32_t* vt, int tid) const {
+#pragma unroll
+    for (int p = 0; p < PER_THR; ++p) {
+      const int idx = tid + p * NTHR;
+      if (ITEMS % NTHR == 0 || idx < ITEMS) {
+        const int kp = idx / KCH, c = idx % KCH;
+        const int kc = kp >> 2, sub = kp & 3;
+        const uint32_t a[4] = {r0[p].x, r0[p].y, r0[p].z, r0[p].w};
+        const uint32_t b[4] = {r1[p].x, r1[p].y, r1[p].z, r1[p].w};
+#pragma unroll
+        for (int m = 0; m < 4; ++m) {
+          const uint32_t even = (a[m] & 0xffffu) | (b[m] << 16);
+          const uint32_t odd = (a[m] >> 16) | (b[m] & 0xffff0000u);
+          const int d0 = 8 * c + 2 * m;
+          vt[VLayout<HD>::chunk(d0, kc) * 4 + sub] = even;
+          vt[VLayout<HD>::chunk(d0 + 1, kc) * 4 + sub] = odd;
+        }
+      }
+    }
+  }
+};
+
+// Stage a 64-key K tile (rows j0..j0+63) into registers / swizzled LDS.
+template <typename T, int HD, int NTHR> struct KStager {
+  static constexpr int KCH = HD / 8;
+  static constexpr int ITEMS = 64 * KCH;
+  static constexpr int PER_THR = (ITEMS + NTHR - 1) / NTHR;
+  uint4 r[PER_THR];
+
+  __device__ inline void load(const T* kbase, int64_t k_st, int j0, int T_len, int tid) {
+#pragma unroll
+    for (int p = 0; p < PER_THR; ++p) {
+      const int idx = tid + p * NTHR;
+      r[p] = make_uint4(0, 0, 0, 0);
+      if (ITEMS % NTHR == 0 || idx < ITEMS) {
+        const int key = idx / KCH, c = idx % KCH;
+        if (j0 + key < T_len)
+          r[p] = *reinterpret_cast<const uint4*>(kbase + (int64_t)(j0 + key) * k_st + 8 * c);
+      }
+    }
+  }
+
+  __device__ inline void store(uint4* ks, int tid) const {
+#pragma unroll
+    for (int p = 0; p < PER_THR; ++p) {
+      const int idx = tid + p * NTHR;
+      if (ITEMS % NTHR == 0 || idx < ITEMS) {
+        const int key = idx / KCH, c = idx % KCH;
+        ks[KLayout<HD>::chunk(key, c)] = r[p];
+      }
+    }
+  }
+};
+
+// O^T accumulation for one 64-key block: o[qt][dt] += V^T(dt) . P^T(qt).
+// pb[ks][s][qt] is the B operand for keys 32ks + 16s + (8g + 0..7).
+template <typename T, int HD, int QT>
+__device__ inline void pv_block(f32x16_t (&o)[QT][HD / 32], const uint4 (&pb)[2][2][QT],
+                                const uint4* vt, int lane) {
+  const int m = lane & 31, g = lane >> 5;
+#pragma unroll
+  for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+    for (int s = 0; s < 2; ++s)
+#pragma unroll
+      for (int dt = 0; dt < HD / 32; ++dt) {
+        const uint4 a = vt[VLayout<HD>::chunk(32 * dt + m, 4 * ks + 2 * s + g)];
+#pragma unroll
+        for (int qt = 0; qt < QT; ++qt) o[qt][dt] = Elem<T>::mfma(a, pb[ks][s][qt], o[qt][dt]);
+      }
+}
+
+// Store O^T (already normalised) for one 32-query tile: lane (n, g) writes
+// query `q`, columns 32dt + 8r + 4g + 0..3 as 8-byte packets.
+template <typename T, int HD>
+__device__ inline void store_out_tile(T* orow, const f32x16_t (&o)[HD / 32], float scale, int g) {
+#pragma unroll
+  for (int dt = 0; dt < HD / 32; ++dt)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      uint2 w;
+      w.x = Elem<T>::pack2(o[dt][4 * r + 0] * scale, o[dt][4 * r + 1] * scale);
+      w.y = Elem<T>::pack2(o[dt][4 * r + 2] * scale, o[dt][4 * r + 3] * scale);
+      *reinterpret_cast<uint2*>(orow + 32 * dt + 8 * r + 4 * g) = w;
+    }
+}
+
+}  // namespace saf

@@ -1,0 +1,95 @@
+// Kernel parameter blocks and host-side launchers of the SAF attention
+// library.  Everything here is internal to libsafattn.so; the public C-ABI
+// lives in include/saf_attn.h.
+#pragma once
+#include "saf_device.h"
+
+namespace saf {
+
+// Largest number of heads one launch can route (per-head tables are passed
+// by value in the kernel arguments).
+constexpr int kMaxHeads = 128;
+
+// dtype codes shared with the C-ABI (saf_attn.h)
+enum : int { kF32 = 0, kF16 = 1, kBF16 = 2, kI32 = 3 };
+
+// Live heads (state 0).
+struct FlashParams {
+  const void* q;
+  const void* k;
+  const void* v;
+  void* out;
+  float* lse;  // may be null
+  int64_t q_sb, q_sh, q_st;
+  int64_t k_sb, k_sh, k_st;
+  int64_t v_sb, v_sh, v_st;
+  int64_t o_sb, o_sh, o_st;
+  int64_t l_sb, l_sh, l_st;
+  int B, T, n_slots, n_qblk;
+  float scale_log2;  // sm_scale * log2(e)
+  int16_t out_head[kMaxHeads];
+  int16_t q_head[kMaxHeads];
+  int16_t k_head[kMaxHeads];
+  int16_t v_head[kMaxHeads];
+};
+
+// Frozen heads whose pattern is applied as an MFMA P.V product: dense
+// patterns (state 1) and decomposed patterns rebuilt in registers (state 2).
+struct FrozenParams {
+  const void* v;
+  void* out;
+  int64_t v_sb, v_sh, v_st;
+  int64_t o_sb, o_sh, o_st;
+  // dense pattern buffer (P, S, S) and its dtype code
+  const void* patt;
+  int patt_dtype;
+  int patt_vec;  // rows contiguous and aligned for 16/32-byte loads
+  int64_t p_sh, p_si, p_sj;
+  // decomposed buffers (H, S) indexed by the natural head
+  const void* alpha;
+  const void* rho;
+  const void* z;
+  int a_dtype, r_dtype, z_dtype;
+  int64_t a_sh, a_ss, r_sh, r_ss, z_sh, z_ss;
+  int B, T, n_slots, n_qblk;
+  int16_t out_head[kMaxHeads];
+  int16_t v_head[kMaxHeads];
+  int16_t pat_head[kMaxHeads];  // dense: pattern row; decomposed: buffer row
+};
+
+// Closed-form frozen heads (state 2 heads recognised as causal mean,
+// exponential decay or sliding window): a single-pass chunked scan along T
+// with decoupled look-back between chunks.
+enum : int { kScanMean = 1, kScanDecay = 2, kScanWindow = 3 };
+
+struct ScanParams {
+  const void* v;
+  void* out;
+  int64_t v_sb, v_sh, v_st;
+  int64_t o_sb, o_sh, o_st;
+  int B, T, n_slots, n_chunks;
+  uint32_t* counter;  // ticket counter (zeroed before launch)
+  uint32_t* error;    // set to 1 if a look-back wait hit the spin limit
+  uint32_t* flags;    // [n_seq * n_chunks]: 0 empty, 1 aggregate, 2 inclusive
+  float* agg;         // [n_seq * n_chunks * HD]
+  float* incl;        // [n_seq * n_chunks * HD]
+  int spin_limit;
+  int16_t out_head[kMaxHeads];
+  int16_t v_head[kMaxHeads];
+  int8_t kind[kMaxHeads];
+  float param[kMaxHeads];  // decay rate (> 0) or window length
+};
+
+// Rows of one scan chunk for a head dimension (must match the kernel).
+inline int scan_chunk_rows(int hd) { return hd <= 64 ? 32 * 16 : 16 * 16; }
+
+// Launchers: return hipSuccess or the launch error.  dtype is kBF16 / kF16.
+hipError_t launch_flash(const FlashParams& p, int dtype, int hd, int qt, hipStream_t s);
+hipError_t launch_frozen_pv(const FrozenParams& p, int dtype, int hd, int mode, hipStream_t s);
+hipError_t launch_scan(const ScanParams& p, int dtype, int hd, hipStream_t s);
+hipError_t launch_zero_u32(uint32_t* ptr, int64_t n, hipStream_t s);
+
+// Queries per flash / frozen workgroup for a query-tile count.
+inline int block_rows(int qt) { return 4 * 32 * qt; }
+
+}  // namespace saf

@@ -1,0 +1,359 @@
+"""Mixed-head causal attention: live and frozen heads behind one call.
+
+Drop-in for the reference operator ``fused_mixed_attn``
+(/root/reference/kernel/fused_attn.py:650-734, with the GQA ``kvidx`` map of
+/root/reference/qwen/kernel/fused_attn.py:667-768).  Head states:
+
+    0  live               y = softmax(Q K^T * sm_scale) V, causal
+    1  frozen, dense      y_i = sum_{j<=i} patt[pidx(h), i, j] v_j
+    2  frozen, decomposed y_i = sum_{j<=i} exp(alpha[j] + rho[i-j] - z[i]) v_j
+
+The work runs in libsafattn.so on the current HIP stream: a live-head flash
+kernel on bf16/fp16 MFMA, a dense P.V MFMA kernel, an in-register decomposed
+rebuild kernel, and, for decomposed heads whose pattern is the causal mean, an
+exponential decay or a sliding window (``closed_form=``), a single-pass scan
+that reads V once.  Output is in natural head order.
+
+Pattern helpers (``make_rho_band``, ``decomp_logits``, ``decomposed_logz``)
+follow the reference's definitions (/root/reference/kernel/fused_attn.py:50-116)
+and run as ordinary torch ops at freeze time.
+"""
+import math
+
+import numpy as np
+import torch
+
+from . import _ext
+
+RCP_LN2 = 1.4426950408889634   # 1 / ln 2
+
+# Rows of the reference's pre-expanded rho band (its BLOCK_M).  The HIP
+# decomposed kernel reads rho directly, so the band is accepted for API
+# compatibility and validated for shape, but never read.
+BAND_ROWS = 64
+
+# Closed-form codes (include/saf_attn.h SAF_CLOSED_*)
+CLOSED_NONE, CLOSED_MEAN, CLOSED_DECAY, CLOSED_WINDOW = 0, 1, 2, 3
+
+
+def fused_attn_usable(q):
+    """True for tensors on a HIP device (torch's "cuda" device on ROCm).
+
+    Deliberately independent of whether libsafattn.so was built: on a GPU the
+    operator must run the HIP path or fail loudly, never fall back."""
+    return bool(q.is_cuda)
+
+
+def make_rho_band(rho):
+    """(H, S) rho -> (H, BAND_ROWS, S) band with band[h, r, u] =
+    rho[h, r - u + S - BAND_ROWS], -inf where that index leaves [0, S)
+    (/root/reference/kernel/fused_attn.py:65-80)."""
+    H, S = rho.shape
+    assert S % BAND_ROWS == 0, \
+        f"decomposed prior buffer length {S} must be a multiple of {BAND_ROWS}"
+    src = (torch.arange(BAND_ROWS, device=rho.device)[:, None]
+           - torch.arange(S, device=rho.device)[None, :] + (S - BAND_ROWS))
+    valid = (src >= 0) & (src < S)
+    band = rho[:, src.clamp(0, S - 1)]
+    return band.masked_fill(~valid, float("-inf")).contiguous()
+
+
+def decomp_logits(alpha, rho, rows=None):
+    """L[h, i, j] = alpha[h, j] + rho[h, i - j] for j <= i, -inf above the
+    diagonal; rows=(r0, r1) selects a row range
+    (/root/reference/kernel/fused_attn.py:83-98)."""
+    H, S = alpha.shape
+    r0, r1 = (0, S) if rows is None else rows
+    i = torch.arange(r0, r1, device=alpha.device)[:, None]
+    j = torch.arange(S, device=alpha.device)[None, :]
+    dist = i - j
+    logits = alpha[:, None, :] + rho[:, dist.clamp(min=0)]
+    return logits.masked_fill(dist < 0, float("-inf"))
+
+
+@torch.no_grad()
+def decomposed_logz(alpha, rho, chunk=None):
+    """z[h, i] = logsumexp_{j <= i}(alpha[h, j] + rho[h, i - j]), row-chunked so
+    the (H, chunk, S) workspace stays near 2^27 elements
+    (/root/reference/kernel/fused_attn.py:101-116)."""
+    H, S = alpha.shape
+    if chunk is None:
+        chunk = max(1, (1 << 27) // max(H * S, 1))
+    z = torch.empty_like(alpha)
+    for r0 in range(0, S, chunk):
+        r1 = min(r0 + chunk, S)
+        z[:, r0:r1] = decomp_logits(alpha, rho, rows=(r0, r1)).logsumexp(-1)
+    return z
+
+
+# ---------------------------------------------------------------------------
+# Closed-form recognition of decomposed patterns
+# ---------------------------------------------------------------------------
+
+@torch.no_grad()
+def classify_closed_form(alpha, rho, z=None, heads=None, rtol=1e-5):
+    """Recognise decomposed heads whose pattern softmax(alpha[j] + rho[i-j]) is
+    the causal mean, an exponential decay or a sliding window.
+
+    Returns (kind int32[H], param float32[H]) as numpy arrays: kind is
+    CLOSED_MEAN (alpha = rho = 0), CLOSED_DECAY (alpha = 0, rho[d] = -c d with
+    c > 0; param = c) or CLOSED_WINDOW (alpha = 0, rho[d] = 0 for d < w and
+    -inf beyond; param = w), else CLOSED_NONE.  If z is given it must be the
+    pattern's own normaliser (checked against the closed form), otherwise the
+    head is left to the in-register rebuild, which uses z as given.  Runs once
+    per freeze change (one host sync)."""
+    H, S = alpha.shape
+    a = alpha.detach().float().cpu()
+    r = rho.detach().float().cpu()
+    zz = None if z is None else z.detach().float().cpu()
+    kind = np.zeros(H, dtype=np.int32)
+    param = np.zeros(H, dtype=np.float32)
+    d = torch.arange(S, dtype=torch.float64)
+    rows = heads if heads is not None else range(H)
+    for h in rows:
+        if not bool((a[h] == 0).all()):
+            continue
+        rh = r[h].double()
+        finite = torch.isfinite(rh)
+        k = CLOSED_NONE
+        if bool((rh == 0).all()):
+            k, p = CLOSED_MEAN, 0.0
+            logz = torch.log(d + 1.0)
+        elif bool(finite[0]) and rh[0] == 0 and not bool(finite.all()) and \
+                bool((rh[finite] == 0).all()):
+            w = int(finite.long().sum())
+            if bool(finite[:w].all()) and bool((rh[w:] == float("-inf")).all()):
+                k, p = CLOSED_WINDOW, float(w)
+                logz = torch.log(torch.clamp(d + 1.0, max=float(w)))
+        elif bool(finite.all()) and rh[0] == 0 and S > 1 and rh[1] < 0:
+            c = -float(r[h, 1])
+            if bool(((rh + c * d).abs() <= rtol * (1.0 + c * d)).all()):
+                k, p = CLOSED_DECAY, c
+                # log sum_{t<=i} e^{-c t} = log(-expm1(-c (i+1))) - log(-expm1(-c))
+                logz = torch.log(-torch.expm1(-c * (d + 1.0))) - math.log(-math.expm1(-c))
+        if k == CLOSED_NONE:
+            continue
+        if zz is not None:
+            zerr = (zz[h].double() - logz).abs()
+            if not bool((zerr <= 1e-4 * (1.0 + logz.abs())).all()):
+                continue
+        kind[h] = k
+        param[h] = p
+    return kind, param
+
+
+# ---------------------------------------------------------------------------
+# Host copies of the device routing tables
+# ---------------------------------------------------------------------------
+
+def _host_table(t, np_dtype=np.int32):
+    """Host copy of a small per-head table, cached on the tensor itself and
+    refreshed when its version counter moves (one sync per change, the same
+    moment the reference syncs: nanogpt/model.py:853, :875)."""
+    if t is None:
+        return None
+    if not isinstance(t, torch.Tensor):
+        return np.asarray(t, dtype=np_dtype)
+    cached = getattr(t, "_saf_host", None)
+    if cached is not None and cached[0] == t._version and cached[1] == t.data_ptr():
+        return cached[2]
+    arr = t.detach().cpu().numpy().astype(np_dtype, copy=False).reshape(-1)
+    arr = np.ascontiguousarray(arr)
+    try:
+        t._saf_host = (t._version, t.data_ptr(), arr)
+    except (AttributeError, RuntimeError):
+        pass
+    return arr
+
+
+def _row_aligned(t, align):
+    if t is None:
+        return True
+    if t.stride(-1) != 1 and t.size(-1) != 1:
+        return False
+    es = t.element_size()
+    if t.data_ptr() % align:
+        return False
+    return all(s <= 1 or (st * es) % align == 0
+               for s, st in zip(t.shape[:-1], t.stride()[:-1]))
+
+
+def _aligned_view(t, align=16):
+    return t if _row_aligned(t, align) else t.contiguous()
+
+
+class _MixedAttnFn(torch.autograd.Function):
+    """Forward-only autograd node: prefill runs under inference_mode; the
+    backward kernels (dQ/dK/dV with exactly-zero frozen Q/K grads) are not
+    part of this library yet."""
+
+    @staticmethod
+    def forward(ctx, q, k, v, run):
+        return run()
+
+    @staticmethod
+    def backward(ctx, dout):
+        raise NotImplementedError(
+            "fused_mixed_attn backward is not implemented in the MI355X build "
+            "(forward / prefill only)")
+
+
+def fused_mixed_attn(q, k, v, patt, frozen, hidx=None, pidx=None,
+                     sm_scale=None, alpha=None, rho=None, z=None,
+                     rho_band=None, validate=True, kvidx=None,
+                     closed_form=None, lse=None, flash_qtiles=0):
+    """Causal attention over all heads, frozen heads using a fixed prior.
+
+    Arguments follow /root/reference/kernel/fused_attn.py:650-680 (and
+    ``kvidx`` from the GQA twin):
+      v        (B, H, T, HD), or the raw (B, HKV, T, HD) heads with kvidx
+      q, k     (B, U, T, HD) compact live-head slots (hidx[h] = slot of h);
+               with kvidx, k is the raw (B, HKV, T, HD) key heads
+      patt     (P, S, S) dense patterns, S >= T (pidx[h] selects a row)
+      frozen   (H,) int32 head states 0 / 1 / 2
+      alpha, rho, z  (H, S) decomposed buffers; z defaults to
+               decomposed_logz(alpha, rho) computed per call
+      rho_band accepted for compatibility (shape-checked, not read)
+    Extensions of this build:
+      closed_form  (kind int32[H], param float32[H]) from
+               classify_closed_form(): state-2 heads with a non-zero kind run
+               the closed-form scan instead of the in-register rebuild
+      lse      optional (B, H, T) fp32 output for the live heads' base-2 LSE
+      flash_qtiles 0 (auto) / 1 / 2 query tiles per wave of the flash kernel
+    Returns (B, H, T, HD) in natural head order, strided like v (like the
+    reference's empty_like(v)).
+    """
+    H = frozen.numel()
+    if sm_scale is None:
+        sm_scale = 1.0 / (v.size(-1) ** 0.5)
+    kv_identity = kvidx is None
+    if alpha is not None and z is None:
+        z = decomposed_logz(alpha.float(), rho.float()).to(alpha.dtype)
+    if validate:
+        _validate(q, k, v, patt, frozen, hidx, pidx, alpha, rho, z, rho_band, kvidx)
+    if not v.is_cuda:
+        raise RuntimeError(
+            "fused_mixed_attn runs on HIP devices only (got a CPU tensor); "
+            "this build has no CPU kernel path")
+
+    frozen_h = _host_table(frozen)
+    hidx_h = None if hidx is None else _host_table(hidx)
+    pidx_h = None if pidx is None else _host_table(pidx)
+    kvidx_h = None if kvidx is None else _host_table(kvidx)
+    ck = cp = None
+    if closed_form is not None:
+        ck = _host_table(closed_form[0], np.int32)
+        cp = _host_table(closed_form[1], np.float32)
+
+    B, HV, T, HD = v.shape
+    n_live = int((frozen_h == 0).sum())
+    q_d = k_d = None
+    if n_live:
+        q_d = _aligned_view(q, 16)
+        k_d = _aligned_view(k, 16)
+    v_d = _aligned_view(v, 16)
+    if kv_identity:
+        out = torch.empty_like(v_d)
+        if not _row_aligned(out, 8):
+            out = torch.empty((B, H, T, HD), device=v.device, dtype=v.dtype)
+    else:
+        out = torch.empty((B, H, T, HD), device=v.device, dtype=v.dtype)
+
+    n_scan = 0
+    if ck is not None:
+        n_scan = int(((frozen_h == 2) & (ck != 0)).sum())
+    L = _ext.lib()
+    ws = None
+    ws_bytes = 0
+    if n_scan:
+        ws_bytes = int(L.saf_workspace_bytes(B, T, HD, n_scan))
+        ws = torch.empty(ws_bytes, dtype=torch.uint8, device=v.device)
+
+    need_dec = alpha is not None and bool(
+        ((frozen_h == 2) & ((ck == 0) if ck is not None else True)).any())
+
+    args = _ext.SafMixedAttnArgs()
+    args.q = _ext.tensor_desc(q_d)
+    args.k = _ext.tensor_desc(k_d)
+    args.v = _ext.tensor_desc(v_d)
+    args.out = _ext.tensor_desc(out)
+    args.lse = _ext.tensor_desc(lse)
+    args.patt = _ext.tensor_desc(patt)
+    if need_dec:
+        args.alpha = _ext.tensor_desc(alpha)
+        args.rho = _ext.tensor_desc(rho)
+        args.z = _ext.tensor_desc(z)
+    args.n_heads = H
+    keep = [_ext.host_i32(frozen_h), _ext.host_i32(hidx_h), _ext.host_i32(pidx_h),
+            _ext.host_i32(kvidx_h), _ext.host_i32(ck), _ext.host_f32(cp)]
+    args.frozen, args.hidx, args.pidx, args.kvidx, args.closed_kind = keep[:5]
+    args.closed_param = keep[5]
+    args.sm_scale = float(sm_scale)
+    args.workspace = None if ws is None else ws.data_ptr()
+    args.workspace_bytes = ws_bytes
+    args.flash_qtiles = int(flash_qtiles)
+
+    def run():
+        stream = _ext.current_stream_ptr(v.device)
+        _ext.check(L.saf_mixed_attn_fwd(args, stream))
+        return out
+
+    if torch.is_grad_enabled() and any(
+            t is not None and t.requires_grad for t in (q, k, v)):
+        return _MixedAttnFn.apply(q, k, v, run)
+    return run()
+
+
+def _validate(q, k, v, patt, frozen, hidx, pidx, alpha, rho, z, rho_band, kvidx):
+    """The reference's argument checks (kernel/fused_attn.py:695-732 and
+    qwen/kernel/fused_attn.py:720-731), same messages."""
+    assert q.ndim == k.ndim == v.ndim == 4, "q, k, v must be 4-D"
+    B, HV, T, HD = v.shape
+    H = frozen.numel()
+    if kvidx is None:
+        assert HV == H, "v must hold one head per output head (or pass kvidx)"
+        assert q.shape == k.shape, "q and k must have the same compact shape"
+    else:
+        assert k.shape == v.shape, "with kvidx, k and v are the raw (B, HKV, T, HD) heads"
+        assert kvidx.shape == (H,) and kvidx.dtype == torch.int32 \
+            and kvidx.device == v.device, "kvidx must be (H,) int32 on v.device"
+        assert int(kvidx.max()) < HV and int(kvidx.min()) >= 0, \
+            "kvidx must index the HKV heads of k/v"
+    assert q.shape[0] == B and q.shape[2:] == (T, HD), \
+        "q/k batch, sequence, and head dimensions must match v"
+    hidx_t = hidx if hidx is not None else frozen
+    pidx_t = pidx if pidx is not None else frozen
+    assert frozen.shape == hidx_t.shape == pidx_t.shape == (H,), \
+        "frozen, hidx, and pidx must have one entry per output head"
+    assert frozen.dtype == hidx_t.dtype == pidx_t.dtype == torch.int32, \
+        "frozen, hidx, and pidx must be int32"
+    assert frozen.device == hidx_t.device == pidx_t.device == v.device, \
+        "head-state and index tensors must be on v.device"
+    assert q.device == k.device == v.device, "q, k, v must share a device"
+    if patt is not None:
+        assert patt.ndim == 3 and patt.shape[1] >= T and patt.shape[2] >= T, \
+            "patt must have shape (P, S, S) with S >= T"
+        assert patt.device == v.device, "patt must be on v.device"
+        if pidx is None:
+            assert patt.shape[0] >= H, \
+                "identity pattern mapping requires at least H pattern rows"
+        elif bool((frozen == 1).any()):
+            dense_pidx = pidx[frozen == 1]
+            assert int(dense_pidx.min()) >= 0 and \
+                int(dense_pidx.max()) < patt.shape[0], \
+                "pidx for dense-frozen heads must index patt"
+    else:
+        assert not bool((frozen == 1).any()), "dense-frozen heads require patt"
+    if alpha is not None:
+        assert rho is not None and alpha.shape == rho.shape == z.shape, \
+            "alpha, rho, and z must have matching (H, S) shapes"
+        assert alpha.shape[0] == H and alpha.shape[1] >= T, \
+            "decomposed buffers must have shape (H, S) with S >= T"
+        assert alpha.device == rho.device == z.device == v.device, \
+            "decomposed buffers must be on v.device"
+        if rho_band is not None:
+            assert rho_band.shape == (H, BAND_ROWS, alpha.size(1)), \
+                "rho_band must be make_rho_band(rho) with matching block size"
+    else:
+        assert not bool((frozen == 2).any()), \
+            "decomposed-frozen heads require alpha/rho/z"

@@ -1,0 +1,278 @@
+"""GPU parity of fused_mixed_attn (libsafattn.so) against the CPU oracle.
+
+Mirrors the reference's kernel test grid (kernel/test_fused_attn.py:162-230):
+dense / decomposed / live mixes, nothing or everything frozen, non-contiguous
+freeze sets, unaligned T with S > T, tiny T, hd in {32, 64, 96, 128}, strided
+q/k views of one fused projection, bf16 decomposed buffers, extreme logits,
+compact pidx; plus the GQA kvidx map (qwen/kernel/fused_attn.py:667-768), the
+closed-form scan heads and the base-2 LSE.  Bound: max-abs <= 2e-2 and
+relative-L2 <= 1e-2 against float64 oracle outputs computed from the same
+(rounded) inputs.
+"""
+import numpy as np
+import pytest
+import torch
+
+from oracle import saf_oracle as orc
+from saf_cases import (closed_params, compare, f64, make_decomp, make_pattern,
+                       qkv, routing, scale_of)
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+def _kernel():
+    import kernel
+    return kernel
+
+
+def run_case(B, H, T, hd, S, dense, dec=(), dtype=torch.bfloat16, strided=False,
+             no_patt=False, buf_dtype=torch.float32, dec_scale=0.8, compact_patt=False,
+             closed=None, check_lse=False):
+    K = _kernel()
+    closed = closed or {}
+    states = {h: 1 for h in dense}
+    states.update({h: 2 for h in dec})
+    states.update({h: 2 for h in closed})
+    frozen, hidx, live = routing(H, states)
+    patt = make_pattern(H, S, seed=H * S + T)
+    alpha, rho, z = make_decomp(H, S, seed=H + S + T, scale=dec_scale)
+    if closed:
+        ca, cr, cz = closed_params(H, S, closed)
+        for h in closed:
+            alpha[h], rho[h], z[h] = ca[h], cr[h], cz[h]
+    alpha, rho, z = (t.to(buf_dtype) for t in (alpha, rho, z))
+    q, k, v = qkv(B, H, T, hd, seed=T * hd + B, dtype=dtype)
+
+    pidx = None
+    kern_patt = None if no_patt else patt
+    if compact_patt:
+        pidx = torch.zeros(H, dtype=torch.int32)
+        for slot, h in enumerate(dense):
+            pidx[h] = slot
+        kern_patt = None if no_patt else patt[list(dense)].contiguous()
+
+    qd = q[:, live].to(DEV)
+    kd = k[:, live].to(DEV)
+    if strided:
+        # q/k as interleaved views of one (B, T, 2, U, hd) projection output
+        qk = torch.stack([q[:, live], k[:, live]], dim=2).permute(0, 3, 2, 1, 4).contiguous().to(DEV)
+        qd, kd = qk[:, :, 0].transpose(1, 2), qk[:, :, 1].transpose(1, 2)
+    has_dec = bool(dec) or bool(closed)
+    cf = None
+    if closed:
+        cf = K.classify_closed_form(alpha, rho, z)
+        for h in closed:
+            assert cf[0][h] != 0, f"head {h} not recognised as closed form"
+    lse = torch.empty(B, H, T, device=DEV, dtype=torch.float32) if check_lse else None
+    y = K.fused_mixed_attn(
+        qd, kd, v.to(DEV), None if kern_patt is None else kern_patt.to(DEV),
+        frozen.to(DEV), hidx.to(DEV), None if pidx is None else pidx.to(DEV),
+        alpha=alpha.to(DEV) if has_dec else None, rho=rho.to(DEV) if has_dec else None,
+        z=z.to(DEV) if has_dec else None, closed_form=cf, lse=lse)
+    torch.cuda.synchronize()
+
+    ref = orc.eager_mixed_attention(
+        f64(q[:, live]), f64(k[:, live]), f64(v), frozen.numpy(), hidx.numpy(),
+        None if pidx is None else pidx.numpy(), None,
+        patt=patt.numpy() if not compact_patt else patt[list(dense)].numpy(),
+        alpha=f64(alpha), rho=f64(rho), z=f64(z), sm_scale=scale_of(hd))
+    compare(y, ref, what=f"B{B} H{H} T{T} hd{hd} dense={list(dense)} dec={list(dec)} "
+                         f"closed={closed} {dtype}")
+    if check_lse and live:
+        for h in live:
+            for b in range(B):
+                qh = f64(q[b, h]); kh = f64(k[b, h])
+                s = (qh @ kh.T) * scale_of(hd) * orc.math.log2(orc.math.e)
+                s = np.where(np.tril(np.ones((T, T), dtype=bool)), s, -np.inf)
+                m = s.max(-1)
+                ref_lse = m + np.log2(np.exp2(s - m[:, None]).sum(-1))
+                got = lse[b, h].cpu().numpy()
+                assert np.abs(got - ref_lse).max() < 2e-2, f"lse b{b} h{h}"
+    return y
+
+
+CASES = [
+    (2, 12, 1024, 64, 1024, [0, 1, 2]),
+    (2, 12, 1024, 64, 1024, []),
+    (2, 12, 1024, 64, 1024, list(range(12))),
+    (2, 12, 1024, 64, 1024, [3, 7, 11]),
+    (2, 12, 700, 64, 1024, [0, 5, 11]),
+    (2, 12, 37, 64, 1024, [0, 5]),
+    (1, 16, 2048, 96, 2048, [0, 7, 8, 15]),
+    (4, 12, 2048, 64, 2048, [0, 1, 2]),
+    (1, 8, 1000, 128, 1024, [1, 6]),
+    (2, 4, 333, 32, 512, [2]),
+    (1, 4, 1, 64, 64, [1]),
+]
+
+
+@pytest.mark.parametrize("case", CASES, ids=lambda c: f"B{c[0]}H{c[1]}T{c[2]}d{c[3]}nf{len(c[5])}")
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16], ids=["bf16", "fp16"])
+def test_dense_and_live(case, dtype):
+    run_case(*case, dtype=dtype)
+
+
+@pytest.mark.parametrize("case", CASES[:6], ids=lambda c: f"B{c[0]}H{c[1]}T{c[2]}nf{len(c[5])}")
+def test_strided_qk_views(case):
+    run_case(*case, dtype=torch.bfloat16, strided=True)
+
+
+DEC_CASES = [
+    (2, 12, 1024, 64, 1024, [0, 1], [2, 3], False),
+    (2, 12, 1024, 64, 1024, [], [0, 5, 11], True),
+    (2, 12, 1024, 64, 1024, [], list(range(12)), True),
+    (2, 12, 700, 64, 1024, [3], [0, 7], False),
+    (2, 12, 37, 64, 1024, [5], [0, 2], False),
+    (1, 16, 2048, 96, 2048, [0, 8], [7, 15], False),
+    (4, 12, 2048, 64, 2048, [1], [0, 2], False),
+    (1, 8, 1000, 128, 1024, [2], [3, 5], False),
+]
+
+
+@pytest.mark.parametrize("case", DEC_CASES, ids=lambda c: f"T{c[2]}d{c[3]}nf{len(c[5])}nd{len(c[6])}")
+def test_decomposed(case):
+    B, H, T, hd, S, fz, dec, np_ = case
+    run_case(B, H, T, hd, S, fz, dec, no_patt=np_)
+
+
+@pytest.mark.parametrize("case", DEC_CASES[:3], ids=lambda c: f"nd{len(c[6])}")
+def test_decomposed_bf16_buffers(case):
+    B, H, T, hd, S, fz, dec, np_ = case
+    run_case(B, H, T, hd, S, fz, dec, no_patt=np_, buf_dtype=torch.bfloat16)
+
+
+@pytest.mark.parametrize("case", [
+    (2, 12, 700, 64, 1024, [3], [0, 7], False),
+    (2, 12, 37, 64, 1024, [], [0, 2, 5], True),
+    (2, 12, 1000, 64, 1024, [], list(range(12)), True),
+], ids=["T700", "T37", "T1000all"])
+def test_decomposed_extreme_logits(case):
+    B, H, T, hd, S, fz, dec, np_ = case
+    run_case(B, H, T, hd, S, fz, dec, no_patt=np_, dec_scale=40.0)
+
+
+def test_compact_pidx_with_decomposed():
+    run_case(2, 12, 700, 64, 1024, [3, 9], [0, 7], strided=True, compact_patt=True)
+
+
+CLOSED = [
+    (2, 12, 1024, 64, 1024, {0: ("mean", 0), 5: ("decay", 0.01), 9: ("window", 64)}),
+    (1, 12, 3000, 64, 3072, {1: ("decay", 0.001), 2: ("decay", 0.1), 3: ("window", 1000),
+                             4: ("mean", 0), 11: ("window", 1)}),
+    (2, 8, 777, 128, 1024, {0: ("mean", 0), 7: ("decay", 0.05), 3: ("window", 300)}),
+    (1, 4, 600, 96, 640, {0: ("window", 700), 1: ("decay", 0.02)}),
+    (1, 4, 1, 64, 64, {2: ("mean", 0)}),
+    (2, 6, 513, 32, 576, {0: ("mean", 0), 1: ("window", 128)}),
+]
+
+
+@pytest.mark.parametrize("case", CLOSED, ids=lambda c: f"T{c[2]}d{c[3]}n{len(c[5])}")
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16], ids=["bf16", "fp16"])
+def test_closed_form_scan(case, dtype):
+    B, H, T, hd, S, kinds = case
+    run_case(B, H, T, hd, S, [], closed=kinds, dtype=dtype)
+
+
+def test_closed_form_with_all_kinds_and_lse():
+    run_case(2, 12, 1024, 64, 1024, [4], dec=[6],
+             closed={0: ("mean", 0), 1: ("decay", 0.03), 2: ("window", 256)}, check_lse=True)
+
+
+def test_gqa_kvidx():
+    """Qwen-style map: 14 query heads over 2 KV heads, frozen query heads read
+    the shared V of their group (qwen/kernel/fused_attn.py:254-259)."""
+    K = _kernel()
+    B, H, HKV, T, hd, S = 2, 14, 2, 700, 64, 768
+    kvidx = torch.from_numpy(orc.gqa_kvidx(H, HKV))
+    states = {0: 2, 3: 2, 8: 1, 13: 2}
+    frozen, hidx, live = routing(H, states)
+    g = torch.Generator().manual_seed(7)
+    q = torch.randn(B, len(live), T, hd, generator=g).bfloat16()
+    k = torch.randn(B, HKV, T, hd, generator=g).bfloat16()
+    v = torch.randn(B, HKV, T, hd, generator=g).bfloat16()
+    patt = make_pattern(1, S, seed=3)
+    pidx = torch.zeros(H, dtype=torch.int32)
+    alpha, rho, z = closed_params(H, S, {0: ("mean", 0), 3: ("decay", 0.02)})
+    a2, r2, z2 = make_decomp(H, S, seed=11)
+    alpha[13], rho[13], z[13] = a2[13], r2[13], z2[13]
+    cf = K.classify_closed_form(alpha, rho, z)
+    assert cf[0][0] == K.CLOSED_MEAN and cf[0][3] == K.CLOSED_DECAY and cf[0][13] == 0
+    y = K.fused_mixed_attn(q.to(DEV), k.to(DEV), v.to(DEV), patt.to(DEV), frozen.to(DEV),
+                           hidx.to(DEV), pidx.to(DEV), alpha=alpha.to(DEV), rho=rho.to(DEV),
+                           z=z.to(DEV), kvidx=kvidx.to(DEV), closed_form=cf)
+    torch.cuda.synchronize()
+    assert y.shape == (B, H, T, hd)
+    ref = orc.eager_mixed_attention(f64(q), f64(k), f64(v), frozen.numpy(), hidx.numpy(),
+                                    pidx.numpy(), kvidx.numpy(), patt=patt.numpy(),
+                                    alpha=f64(alpha), rho=f64(rho), z=f64(z),
+                                    sm_scale=scale_of(hd))
+    compare(y, ref, what="gqa")
+
+
+def test_frozen_heads_ignore_qk():
+    """With the identity hidx (full Q/K), frozen heads' Q/K slots are never
+    read: poisoning them with NaN leaves the output finite and unchanged."""
+    K = _kernel()
+    B, H, T, hd = 1, 6, 300, 64
+    frozen, _, live = routing(H, {1: 1, 4: 1})
+    hid = torch.arange(H, dtype=torch.int32)
+    q, k, v = qkv(B, H, T, hd, seed=5, dtype=torch.bfloat16)
+    patt = make_pattern(H, T, seed=9)
+    y0 = K.fused_mixed_attn(q.to(DEV), k.to(DEV), v.to(DEV), patt.to(DEV), frozen.to(DEV), hid.to(DEV))
+    q2, k2 = q.clone(), k.clone()
+    q2[:, [1, 4]] = float("nan")
+    k2[:, [1, 4]] = float("nan")
+    y1 = K.fused_mixed_attn(q2.to(DEV), k2.to(DEV), v.to(DEV), patt.to(DEV), frozen.to(DEV), hid.to(DEV))
+    torch.cuda.synchronize()
+    assert torch.isfinite(y1).all()
+    assert torch.equal(y0, y1)
+
+
+def test_routing_bit_exact_vs_permutation():
+    """Head-permutation equivariance: permuting heads (and their routing rows)
+    permutes the output heads exactly."""
+    K = _kernel()
+    B, H, T, hd, S = 1, 8, 256, 64, 256
+    frozen, hidx, live = routing(H, {0: 1, 3: 1, 6: 1})
+    q, k, v = qkv(B, H, T, hd, seed=21, dtype=torch.bfloat16)
+    patt = make_pattern(H, S, seed=4)
+    y = K.fused_mixed_attn(q[:, live].to(DEV), k[:, live].to(DEV), v.to(DEV), patt.to(DEV),
+                           frozen.to(DEV), hidx.to(DEV))
+    perm = torch.tensor([5, 2, 7, 0, 1, 6, 4, 3])
+    fz_p = frozen[perm]
+    frozen_p, hidx_p, live_p = routing(H, {i: int(fz_p[i]) for i in range(H) if int(fz_p[i])})
+    y_p = K.fused_mixed_attn(q[:, perm][:, live_p].to(DEV), k[:, perm][:, live_p].to(DEV),
+                             v[:, perm].to(DEV), patt[perm].to(DEV), frozen_p.to(DEV), hidx_p.to(DEV))
+    torch.cuda.synchronize()
+    assert torch.equal(y[:, perm], y_p)
+
+
+@pytest.mark.parametrize("T,S,hd,nf", [(1, 64, 64, 2), (37, 64, 64, 3), (700, 1024, 64, 3),
+                                       (700, 1024, 96, 2), (513, 576, 128, 2)])
+def test_frozen_pv_compact(T, S, hd, nf):
+    """frozen_pv on compact frozen-head values (kernel/test_frozen_attn.py:57-87)."""
+    K = _kernel()
+    B, H = 2, 6
+    patt = make_pattern(H, S, seed=T + S)
+    fz = torch.tensor([5, 0, 3][:nf], dtype=torch.int32)
+    g = torch.Generator().manual_seed(T * hd)
+    v = torch.randn(B, nf, T, hd, generator=g).bfloat16()
+    y = K.frozen_pv(patt.to(DEV), v.to(DEV), fz.to(DEV), T)
+    torch.cuda.synchronize()
+    compare(y, orc.frozen_pv(patt.numpy(), f64(v), fz.numpy(), T), what="frozen_pv")
+
+
+def test_invalid_args_raise():
+    K = _kernel()
+    q, k, v = qkv(1, 4, 64, 80, seed=1, dtype=torch.bfloat16)
+    frozen = torch.zeros(4, dtype=torch.int32, device=DEV)
+    with pytest.raises(NotImplementedError):
+        K.fused_mixed_attn(q.to(DEV), k.to(DEV), v.to(DEV), None, frozen)
+    q, k, v = qkv(1, 4, 64, 64, seed=1, dtype=torch.float32)
+    with pytest.raises(NotImplementedError):
+        K.fused_mixed_attn(q.to(DEV), k.to(DEV), v.to(DEV), None, frozen)
+    q, k, v = qkv(1, 4, 64, 64, seed=1, dtype=torch.bfloat16)
+    with pytest.raises(AssertionError, match="dense-frozen heads require patt"):
+        K.fused_mixed_attn(q.to(DEV), k.to(DEV), v.to(DEV), None,
+                           torch.tensor([1, 0, 0, 0], dtype=torch.int32, device=DEV))

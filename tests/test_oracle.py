@@ -1,0 +1,224 @@
+"""Pins the CPU oracle (oracle/saf_oracle.py) before it is trusted.
+
+Each check is chosen so that a plausible slip in the oracle (dropped term,
+wrong sign or index, transposed operand) fails one of them: library special
+cases (torch SDPA), brute-force loops on tiny inputs, closed forms against
+dense patterns, and invariants.
+"""
+import itertools
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import saf_oracle as orc
+
+
+def _rand(shape, seed):
+    return np.random.default_rng(seed).standard_normal(shape)
+
+
+def test_all_live_matches_torch_sdpa():
+    B, H, T, hd = 2, 3, 97, 16
+    q, k, v = (_rand((B, H, T, hd), s) for s in (1, 2, 3))
+    y = orc.eager_mixed_attention(q, k, v, np.zeros(H, dtype=np.int32))
+    ref = torch.nn.functional.scaled_dot_product_attention(
+        torch.from_numpy(q), torch.from_numpy(k), torch.from_numpy(v), is_causal=True).numpy()
+    np.testing.assert_allclose(y, ref, atol=1e-12, rtol=1e-10)
+
+
+def test_attention_brute_force_loops():
+    T, hd = 6, 3
+    q, k, v = (_rand((T, hd), s) for s in (4, 5, 6))
+    scale = 0.7
+    out = np.zeros((T, hd))
+    for i in range(T):
+        logits = [sum(q[i, d] * k[j, d] for d in range(hd)) * scale for j in range(i + 1)]
+        m = max(logits)
+        w = [math.exp(x - m) for x in logits]
+        s = sum(w)
+        for d in range(hd):
+            out[i, d] = sum(w[j] / s * v[j, d] for j in range(i + 1))
+    np.testing.assert_allclose(orc.causal_attention(q, k, v, scale), out, atol=1e-12)
+
+
+def test_decomp_logits_and_logz_brute_force():
+    H, S = 2, 7
+    a, r = _rand((H, S), 7), _rand((H, S), 8)
+    L = orc.decomp_logits(a, r)
+    z = orc.decomposed_logz(a, r)
+    for h in range(H):
+        for i in range(S):
+            for j in range(S):
+                want = a[h, j] + r[h, i - j] if j <= i else -np.inf
+                assert L[h, i, j] == want
+            zz = math.log(sum(math.exp(a[h, j] + r[h, i - j]) for j in range(i + 1)))
+            assert abs(z[h, i] - zz) < 1e-12
+
+
+def test_decomp_pattern_rows_sum_to_one():
+    H, S, T = 3, 64, 50
+    a, r = _rand((H, S), 9) * 3, _rand((H, S), 10) * 3
+    P = orc.decomp_pattern(a, r, orc.decomposed_logz(a, r), T)
+    np.testing.assert_allclose(P.sum(-1), 1.0, atol=1e-12)
+    assert (np.triu(P, 1) == 0).all()
+
+
+def test_zero_logits_are_causal_mean():
+    """alpha = rho = 0 is exactly the causal-uniform prior
+    (nanogpt/bench_inference_triton.py:92-97)."""
+    S, T = 32, 20
+    z = np.zeros((1, S))
+    P = orc.decomp_pattern(z, z, orc.decomposed_logz(z, z), T)[0]
+    np.testing.assert_allclose(P, orc.mean_pattern(T), atol=1e-14)
+
+
+@pytest.mark.parametrize("kind,prm", [("mean", 0), ("decay", 0.003), ("decay", 0.4),
+                                      ("window", 1), ("window", 5), ("window", 100)])
+def test_closed_forms_as_decomposed_heads(kind, prm):
+    S, T = 96, 80
+    a, r = orc.closed_form_params(kind, prm, S)
+    z = orc.decomposed_logz(a[None], r[None])
+    P = orc.decomp_pattern(a[None], r[None], z, T)[0]
+    dense = {"mean": lambda: orc.mean_pattern(T), "decay": lambda: orc.decay_pattern(T, prm),
+             "window": lambda: orc.window_pattern(T, prm)}[kind]()
+    np.testing.assert_allclose(P, dense, atol=1e-13)
+
+
+@pytest.mark.parametrize("kind,prm", [("mean", 0), ("decay", 0.02), ("window", 7)])
+def test_closed_form_recurrences_match_patterns(kind, prm):
+    T, hd = 200, 5
+    v = _rand((2, T, hd), 11)
+    if kind == "mean":
+        y, P = orc.mean_apply(v), orc.mean_pattern(T)
+    elif kind == "decay":
+        y, P = orc.decay_apply(v, prm), orc.decay_pattern(T, prm)
+    else:
+        y, P = orc.window_apply(v, prm), orc.window_pattern(T, prm)
+    np.testing.assert_allclose(y, P @ v, atol=1e-11)
+
+
+def test_window_matches_reference_loop_definition():
+    """local_window (nanogpt/model.py:347-353) restated as loops."""
+    T, W = 40, 6
+    ref = np.zeros((T, T))
+    for i in range(T):
+        start = max(0, i - W + 1)
+        ref[i, start:i + 1] = 1.0 / (i - start + 1)
+    np.testing.assert_allclose(orc.window_pattern(T, W), ref, atol=0)
+
+
+def test_decay_matches_normalised_exponential_prior():
+    """exp(-dist/scale) row-normalised (nanogpt/test_prior_flash.py:47-59)."""
+    T, scale = 50, 7.0
+    i = np.arange(T)
+    dist = i[:, None] - i[None, :]
+    p = np.where(dist >= 0, np.exp(-np.clip(dist, 0, None) / scale), 0.0)
+    p /= p.sum(-1, keepdims=True)
+    np.testing.assert_allclose(orc.decay_pattern(T, 1.0 / scale), p, atol=1e-14)
+
+
+def test_rho_band_addressing():
+    """band[r, u] = rho[r - u + S - 64]: every aligned (i0, j) tile access of the
+    reference kernel (kernel/fused_attn.py:157, :170) reads rho[i - j], and the
+    cells with j > i are -inf."""
+    H, S = 1, 192
+    rho = _rand((H, S), 12)
+    band = orc.make_rho_band(rho)
+    for i0 in range(0, S, 64):
+        for r in range(64):
+            i = i0 + r
+            for j in range(S):
+                got = band[0, r, (S - 64) - i0 + j] if 0 <= (S - 64) - i0 + j < S else None
+                if got is None:
+                    continue
+                if j <= i:
+                    assert got == rho[0, i - j]
+                else:
+                    assert got == -np.inf
+
+
+def test_t1_gives_v_for_every_head_kind():
+    B, H, hd, S = 2, 4, 8, 16
+    q, k, v = _rand((B, H, 1, hd), 13), _rand((B, H, 1, hd), 14), _rand((B, H, 1, hd), 15)
+    frozen = np.array([0, 1, 2, 2])
+    patt = np.tril(np.abs(_rand((H, S, S), 16)))
+    patt /= patt.sum(-1, keepdims=True)
+    a, r = _rand((H, S), 17), _rand((H, S), 18)
+    y = orc.eager_mixed_attention(q, k, v, frozen, patt=patt, alpha=a, rho=r,
+                                  z=orc.decomposed_logz(a, r))
+    np.testing.assert_allclose(y, v, atol=1e-12)
+
+
+def test_frozen_heads_ignore_qk_and_permutation_equivariance():
+    B, H, T, hd = 1, 5, 30, 4
+    q, k, v = (_rand((B, H, T, hd), s) for s in (19, 20, 21))
+    frozen = np.array([0, 1, 0, 1, 0])
+    patt = orc.decay_pattern(T, 0.1)[None].repeat(H, 0)
+    y = orc.eager_mixed_attention(q, k, v, frozen, patt=patt)
+    q2, k2 = q.copy(), k.copy()
+    q2[:, [1, 3]] = np.nan
+    k2[:, [1, 3]] = np.nan
+    np.testing.assert_array_equal(orc.eager_mixed_attention(q2, k2, v, frozen, patt=patt), y)
+    perm = np.array([3, 0, 4, 1, 2])
+    yp = orc.eager_mixed_attention(q[:, perm], k[:, perm], v[:, perm], frozen[perm], patt=patt[perm])
+    np.testing.assert_allclose(yp, y[:, perm], atol=0)
+
+
+def test_gqa_map_equals_repeated_kv():
+    B, H, HKV, T, hd = 1, 6, 2, 20, 4
+    q = _rand((B, H, T, hd), 22)
+    k, v = _rand((B, HKV, T, hd), 23), _rand((B, HKV, T, hd), 24)
+    kvidx = orc.gqa_kvidx(H, HKV)
+    assert list(kvidx) == [0, 0, 0, 1, 1, 1]
+    frozen = np.array([0, 1, 0, 0, 1, 0])
+    patt = orc.mean_pattern(T)[None].repeat(H, 0)
+    y = orc.eager_mixed_attention(q, k, v, frozen, kvidx=kvidx, patt=patt)
+    kr, vr = k[:, kvidx], v[:, kvidx]
+    y2 = orc.eager_mixed_attention(q, kr, vr, frozen, patt=patt)
+    np.testing.assert_allclose(y, y2, atol=0)
+
+
+@pytest.mark.parametrize("H", [1, 3, 8])
+def test_routing_tables_brute_force(H):
+    hd = 3
+    for bits in itertools.product([False, True], repeat=H):
+        fz = np.array(bits)
+        dec = np.array([b and (h % 2 == 0) for h, b in enumerate(bits)])
+        t = orc.refresh_routing(fz, dec, hd)
+        live = [h for h in range(H) if not fz[h]]
+        frz = [h for h in range(H) if fz[h]]
+        assert list(t["uf_idx"]) == live and list(t["fz_idx"]) == frz
+        for slot, h in enumerate(live):
+            assert t["hidx_i32"][h] == slot
+        for h in range(H):
+            want = 0 if not fz[h] else (2 if dec[h] else 1)
+            assert t["mask_i32"][h] == want
+        if frz:
+            cols = [h * hd + d for h in live + frz for d in range(hd)]
+            assert list(t["cperm_cols"]) == cols
+        else:
+            assert t["cperm_cols"] is None
+
+
+def test_rope_is_a_rotation():
+    T, dim = 9, 8
+    cos, sin = orc.rope_cache(dim, T)
+    x = _rand((T, dim), 25)
+    y = orc.apply_rope(x, cos, sin)
+    half = dim // 2
+    inv = 1.0 / (10000.0 ** (np.arange(0, dim, 2) / dim))
+    for t in range(T):
+        zc = (x[t, :half] + 1j * x[t, half:]) * np.exp(1j * t * inv)
+        np.testing.assert_allclose(y[t, :half], zc.real, atol=1e-12)
+        np.testing.assert_allclose(y[t, half:], zc.imag, atol=1e-12)
+
+
+def test_planted_oracle_mistake_is_caught():
+    """A transposed pattern (a plausible slip) breaks the causal-mean check."""
+    T = 12
+    wrong = orc.mean_pattern(T).T
+    v = _rand((T, 3), 26)
+    assert not np.allclose(wrong @ v, orc.mean_apply(v))
+    assert np.allclose(orc.mean_pattern(T) @ v, orc.mean_apply(v))
