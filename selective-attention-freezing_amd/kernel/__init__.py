@@ -16,11 +16,11 @@ from .indexed_linear import linear_rows, linear_rows2, linear_permuted_cols
 from .fused_attn import (fused_mixed_attn, fused_attn_usable, decomposed_logz,
                          decomp_logits, make_rho_band, BAND_ROWS,
                          classify_closed_form, CLOSED_NONE, CLOSED_MEAN,
-                         CLOSED_DECAY, CLOSED_WINDOW)
+                         CLOSED_DECAY, CLOSED_WINDOW, KernelTimer, set_kernel_timer)
 
 __all__ = ["frozen_pv", "frozen_pv_usable", "HAVE_TRITON",
            "linear_rows", "linear_rows2", "linear_permuted_cols",
            "fused_mixed_attn", "fused_attn_usable", "decomposed_logz",
            "decomp_logits", "make_rho_band", "BAND_ROWS",
            "classify_closed_form", "CLOSED_NONE", "CLOSED_MEAN",
-           "CLOSED_DECAY", "CLOSED_WINDOW"]
+           "CLOSED_DECAY", "CLOSED_WINDOW", "KernelTimer", "set_kernel_timer"]

@@ -182,6 +182,36 @@ def _aligned_view(t, align=16):
     return t if _row_aligned(t, align) else t.contiguous()
 
 
+class KernelTimer:
+    """Brackets each per-kind launch of fused_mixed_attn with HIP events on the
+    launch stream and records the algorithmic work of that launch:
+    flash: 4*hd*T(T+1)/2 flops per (batch, live head); scan: V read once and
+    Y written once, 2*T*hd*elem bytes per (batch, closed-form head)."""
+
+    KINDS = ("flash", "scan", "dense", "decomp")
+
+    def __init__(self):
+        self.records = {k: [] for k in self.KINDS}
+
+    def summary(self):
+        """{kind: (launches, total_ms, total_work)} after synchronisation."""
+        out = {}
+        for k, recs in self.records.items():
+            if recs:
+                ms = sum(a.elapsed_time(b) for a, b, _ in recs)
+                out[k] = (len(recs), ms, sum(w for _, _, w in recs))
+        return out
+
+
+_TIMER = None
+
+
+def set_kernel_timer(timer):
+    """Install (or remove with None) a KernelTimer for subsequent calls."""
+    global _TIMER
+    _TIMER = timer
+
+
 class _MixedAttnFn(torch.autograd.Function):
     """Forward-only autograd node: prefill runs under inference_mode; the
     backward kernels (dQ/dK/dV with exactly-zero frozen Q/K grads) are not
@@ -295,7 +325,27 @@ def fused_mixed_attn(q, k, v, patt, frozen, hidx=None, pidx=None,
 
     def run():
         stream = _ext.current_stream_ptr(v.device)
-        _ext.check(L.saf_mixed_attn_fwd(args, stream))
+        timer = _TIMER
+        if timer is None:
+            _ext.check(L.saf_mixed_attn_fwd(args, stream))
+            return out
+        n_dense = int((frozen_h == 1).sum())
+        n_dec = int((frozen_h == 2).sum()) - n_scan
+        work = {"flash": (L.saf_flash_fwd, n_live * B * 4 * HD * T * (T + 1) // 2),
+                "scan": (L.saf_frozen_scan_fwd, n_scan * B * 2 * T * HD * v.element_size()),
+                "dense": (L.saf_frozen_dense_pv_fwd, n_dense * B * 2 * HD * T * (T + 1) // 2),
+                "decomp": (L.saf_frozen_decomp_fwd, n_dec * B * 2 * HD * T * (T + 1) // 2)}
+        cur = torch.cuda.current_stream(v.device)
+        for kind in KernelTimer.KINDS:
+            fn, w = work[kind]
+            if w == 0:
+                continue
+            e0 = torch.cuda.Event(enable_timing=True)
+            e1 = torch.cuda.Event(enable_timing=True)
+            e0.record(cur)
+            _ext.check(fn(args, stream))
+            e1.record(cur)
+            timer.records[kind].append((e0, e1, w))
         return out
 
     if torch.is_grad_enabled() and any(

@@ -1,0 +1,141 @@
+"""Model-level checks of the nanoGPT caller (selective-attention-freezing_amd/nanogpt).
+
+GPU: final logits of the bf16 HIP model vs the fp32 CPU oracle restatement of
+the reference forward, cosine >= 0.9999 (flattened, float64), for a model
+with live, dense-frozen, generic decomposed and closed-form (mean / decay /
+window) heads; one fused dispatch per layer.
+CPU: routing tables bit-exact against the oracle's restatement of
+_refresh_freeze_cache, oracle eager and split paths agree, and the product
+model refuses to run on CPU tensors.
+"""
+import numpy as np
+import pytest
+import torch
+
+from oracle import model_oracle, saf_oracle as orc
+
+
+def _small_model(T=256, layers=4, device="cpu", dtype=torch.float32, seed=3):
+    from nanogpt.model import GPT, GPTConfig
+    torch.manual_seed(seed)
+    cfg = GPTConfig(block_size=T, vocab_size=50304, n_layer=layers, n_head=12, n_embd=768,
+                    bias=False, position_encoding="rope", rand_attn_prior_repr="decomposed")
+    m = GPT(cfg).to(device=device, dtype=dtype).eval()
+    d = torch.arange(T, dtype=torch.float32, device=device)
+    g = torch.Generator().manual_seed(seed)
+    for l, blk in enumerate(m.transformer.h):
+        a = blk.attn
+        # closed forms on heads 0, 1, 2; generic decomposed on 3; dense on 4, 5
+        alpha = torch.zeros(4, T, device=device)
+        rho = torch.stack([torch.zeros(T, device=device), -0.02 * (l + 1) * d,
+                           torch.where(d < 40 + 10 * l, 0.0, float("-inf")).to(device),
+                           (torch.randn(T, generator=g) * 0.5).to(device)])
+        alpha[3] = (torch.randn(T, generator=g) * 0.5).to(device)
+        a.freeze_heads_decomposed([0, 1, 2, 3 + l % 2], alpha, rho)
+        p = torch.rand(2, T, T, generator=g).to(device)
+        a.freeze_heads([6 + l % 3, 9], p)
+    x = torch.randint(0, 50257, (1, T), generator=g).to(device)
+    return m, x
+
+
+def _oracle_inputs(m):
+    cfg = m.config
+    sd = {k: v.detach().float().cpu() for k, v in m.state_dict().items()}
+    freeze = []
+    for blk in m.transformer.h:
+        a = blk.attn
+        rec = {"frozen": a.dyn_frozen.cpu().tolist(), "patterns": {}, "decomp": {}}
+        for h in range(cfg.n_head):
+            if not rec["frozen"][h]:
+                continue
+            if bool(a.dyn_decomp[h]):
+                rec["decomp"][h] = (a.dyn_alpha[h].cpu(), a.dyn_rho[h].cpu(), a.dyn_z[h].cpu())
+            else:
+                rec["patterns"][h] = a.dyn_pattern[int(a.dyn_pattern_slot[h])].float().cpu()
+        freeze.append(rec)
+    ocfg = {"n_layer": cfg.n_layer, "n_head": cfg.n_head, "n_embd": cfg.n_embd,
+            "position_encoding": cfg.position_encoding, "rope_base": cfg.rope_base}
+    return sd, ocfg, freeze
+
+
+def _cos(a, b):
+    a = a.double().flatten()
+    b = b.double().flatten()
+    return float((a @ b) / (a.norm() * b.norm()))
+
+
+@pytest.mark.gpu
+def test_gpu_model_logits_match_oracle():
+    from nanogpt import model as model_mod
+    m, x = _small_model(T=384, layers=4, device="cuda", dtype=torch.bfloat16)
+    with torch.inference_mode():
+        n0 = model_mod.fused_dispatch_count()
+        logits = m.forward_all_positions(x).float().cpu()
+        assert model_mod.fused_dispatch_count() - n0 == m.config.n_layer
+    closed = m.transformer.h[0].attn._closed[0]
+    assert list(closed[:3]) == [1, 2, 3] and closed[3] == 0
+    sd, ocfg, freeze = _oracle_inputs(m)
+    ref = model_oracle.gpt_forward(sd, ocfg, freeze, x.cpu(), path="eager", all_positions=True)
+    c = _cos(logits, ref)
+    assert c >= 0.9999, f"logits cosine {c:.6f}"
+    last = m(x).float().cpu()
+    assert _cos(last, ref[:, -1:]) >= 0.9999
+
+
+@pytest.mark.gpu
+def test_gpu_model_nothing_frozen_and_all_frozen():
+    from nanogpt.model import GPT, GPTConfig
+    torch.manual_seed(0)
+    T = 200
+    cfg = GPTConfig(block_size=256, vocab_size=1000, n_layer=2, n_head=4, n_embd=256, bias=False)
+    m = GPT(cfg).to("cuda", torch.bfloat16).eval()
+    x = torch.randint(0, 1000, (2, T)).cuda()
+    sd, ocfg, freeze = _oracle_inputs(m)
+    with torch.inference_mode():
+        got = m.forward_all_positions(x).float().cpu()
+    ref = model_oracle.gpt_forward(sd, ocfg, freeze, x.cpu(), path="eager", all_positions=True)
+    assert _cos(got, ref) >= 0.9999
+    for blk in m.transformer.h:
+        z = torch.zeros(4, 256, device="cuda")
+        blk.attn.freeze_heads_decomposed(range(4), z, z)
+    sd, ocfg, freeze = _oracle_inputs(m)
+    with torch.inference_mode():
+        got = m.forward_all_positions(x).float().cpu()
+    ref = model_oracle.gpt_forward(sd, ocfg, freeze, x.cpu(), path="eager", all_positions=True)
+    assert _cos(got, ref) >= 0.9999
+
+
+def test_routing_tables_match_oracle():
+    m, _ = _small_model(T=128, layers=3)
+    for blk in m.transformer.h:
+        a = blk.attn
+        a._refresh_freeze_cache()
+        ref = orc.refresh_routing(a.dyn_frozen.numpy(), a.dyn_decomp.numpy(), a.head_dim)
+        assert np.array_equal(a._fz_mask_i32.numpy(), ref["mask_i32"])
+        assert np.array_equal(a._hidx_i32.numpy(), ref["hidx_i32"])
+        assert np.array_equal(a._uf_cols.numpy(), ref["uf_cols"])
+        assert np.array_equal(a._fz_idx.numpy(), ref["fz_idx"])
+
+
+def test_oracle_eager_and_split_paths_agree():
+    m, x = _small_model(T=128, layers=2)
+    sd, ocfg, freeze = _oracle_inputs(m)
+    e = model_oracle.gpt_forward(sd, ocfg, freeze, x, path="eager", all_positions=True)
+    s = model_oracle.gpt_forward(sd, ocfg, freeze, x, path="split", all_positions=True)
+    torch.testing.assert_close(e, s, atol=2e-4, rtol=1e-4)
+
+
+def test_fp32_pattern_buffers_survive_bf16_cast():
+    m, _ = _small_model(T=64, layers=1)
+    a = m.transformer.h[0].attn
+    z32 = a.dyn_z.clone()
+    m.to(torch.bfloat16)
+    assert a.dyn_z.dtype == torch.float32 and torch.equal(a.dyn_z, z32)
+    assert m.rotary.cos_f32.dtype == torch.float32
+
+
+def test_product_model_has_no_cpu_path():
+    m, x = _small_model(T=64, layers=1)
+    with pytest.raises(RuntimeError, match="HIP devices only"):
+        with torch.inference_mode():
+            m(x)
