@@ -5,7 +5,11 @@
 // /root/reference/qwen/kernel/fused_attn.py:183-231): base-2 online softmax
 // with qk_scale = sm_scale * log2(e), fp32 running max / sum / accumulator,
 // P rounded to the input dtype before the P.V product, output divided by the
-// row sum, and LSE = m + log2(l) in base-2 units.
+// row sum, and LSE = m + log2(l) in base-2 units.  Two deliberate changes of
+// bookkeeping, both exact up to rounding: the running max is only moved when
+// a block exceeds it by more than kSlack (lazy rescale), and the row sum adds
+// the rounded P values (v_dot2 on packed pairs), i.e. exactly the weights
+// that multiply V.
 //
 // Work decomposition: one workgroup = 4 waves = (4 * 32 * QT) query rows of
 // one (batch, live head); each wave owns 32*QT queries and walks 64-key
@@ -16,8 +20,19 @@
 
 namespace saf {
 
+// Slack of the lazy rescale (base-2 units): P values stay below 2^8.
+constexpr float kSlack = 8.f;
+
+// Two waves per SIMD (one from each of two resident workgroups) lets one
+// wave's softmax VALU work overlap the other's MFMAs; the register budget
+// (256 per lane) fits every variant except hd >= 96 with two query tiles.
+template <int HD, int QT>
+constexpr int flash_waves_per_eu() { return (HD <= 64 || QT == 1) ? 2 : 1; }
+
 template <typename T, int HD, int QT>
-__global__ __launch_bounds__(256) void flash_fwd_kernel(const FlashParams p) {
+__global__ __launch_bounds__(256)
+__attribute__((amdgpu_waves_per_eu(flash_waves_per_eu<HD, QT>(), flash_waves_per_eu<HD, QT>())))
+void flash_fwd_kernel(const FlashParams p) {
   constexpr int NW = 4, NTHR = 256;
   constexpr int BM = NW * 32 * QT;
   constexpr int NDT = HD / 32;   // 32-wide d tiles of O^T
@@ -86,63 +101,80 @@ __global__ __launch_bounds__(256) void flash_fwd_kernel(const FlashParams p) {
       vst.load(vbase, p.v_st, 64 * (j + 1), T_len, tid);
     }
     if (j < nkb_w) {
-      const int j0 = 64 * j;
       const uint4* kt = k_lds[buf];
-      f32x16_t s[2][QT];
+      const uint4* vt = v_lds[buf];
+      // two 32-key sub-blocks: S^T, softmax and P.V per sub-block keeps the
+      // live S / P registers at 16 + 8 per query tile
 #pragma unroll
       for (int ks = 0; ks < 2; ++ks) {
+        const int j0 = 64 * j + 32 * ks;
+        f32x16_t sacc[QT];
 #pragma unroll
-        for (int qt = 0; qt < QT; ++qt) s[ks][qt] = zero16();
+        for (int qt = 0; qt < QT; ++qt) sacc[qt] = zero16();
         const int key = 32 * ks + kperm(n);
 #pragma unroll
         for (int t = 0; t < NKT; ++t) {
           const uint4 a = kt[KLayout<HD>::chunk(key, 2 * t + g)];
 #pragma unroll
-          for (int qt = 0; qt < QT; ++qt) s[ks][qt] = Elem<T>::mfma(a, qf[qt][t], s[ks][qt]);
+          for (int qt = 0; qt < QT; ++qt) sacc[qt] = Elem<T>::mfma(a, qf[qt][t], sacc[qt]);
         }
-      }
-
-      const bool diag = j0 + 63 > q0w;  // some key of this block exceeds some query
-      uint4 pb[2][2][QT];
+        if (j0 + 31 > q0w) {  // causal mask only where a key can exceed a query
 #pragma unroll
-      for (int qt = 0; qt < QT; ++qt) {
-        const int q = q0w + 32 * qt + n;
-        float mx = -INFINITY;
+          for (int qt = 0; qt < QT; ++qt) {
+            const int q = q0w + 32 * qt + n;
 #pragma unroll
-        for (int ks = 0; ks < 2; ++ks)
-#pragma unroll
-          for (int i = 0; i < 16; ++i) {
-            float x = s[ks][qt][i];
-            if (diag && j0 + 32 * ks + acc_key(i, g) > q) x = -INFINITY;
-            s[ks][qt][i] = x;
-            mx = fmaxf(mx, x);
+            for (int i = 0; i < 16; ++i)
+              if (j0 + acc_key(i, g) > q) sacc[qt][i] = -INFINITY;
           }
-        mx = fmaxf(mx, __shfl_xor(mx, 32));
-        const float m_new = fmaxf(m_run[qt], mx * c);
-        const float m_use = m_new == -INFINITY ? 0.f : m_new;
-        const float alpha = fast_exp2(m_run[qt] - m_use);
-        m_run[qt] = m_new;
-        float psum = 0.f;
+        }
+        uint4 pb[2][QT];
 #pragma unroll
-        for (int ks = 0; ks < 2; ++ks)
+        for (int qt = 0; qt < QT; ++qt) {
+          float mx = sacc[qt][0];
+#pragma unroll
+          for (int i = 1; i < 16; ++i) mx = fmaxf(mx, sacc[qt][i]);
+          mx = half_swap_max(mx);
+          // Lazy rescaling: a query's reference max only moves when the block
+          // max exceeds it by more than kSlack (base-2 units), so P stays
+          // <= 2^kSlack and most blocks skip the O rescale.  Exact: O and l
+          // always share the same reference max.
+          const float mb = mx * c;
+          const bool up = mb > m_run[qt] + kSlack;
+          if (__builtin_amdgcn_ballot_w64(up)) {
+            const float m_new = up ? mb : m_run[qt];
+            const float alpha = up ? fast_exp2(m_run[qt] - m_new) : 1.f;
+            m_run[qt] = m_new;
+            l_run[qt] *= alpha;
+#pragma unroll
+            for (int dt = 0; dt < NDT; ++dt)
+#pragma unroll
+              for (int i = 0; i < 16; ++i) o[qt][dt][i] *= alpha;
+          }
+          const float mneg = -m_run[qt];
+          float psum = l_run[qt];
 #pragma unroll
           for (int sh = 0; sh < 2; ++sh) {
-            float e[8];
+            uint32_t w[4];
 #pragma unroll
-            for (int u = 0; u < 8; ++u) {
-              e[u] = fast_exp2(fmaf(s[ks][qt][8 * sh + u], c, -m_use));
-              psum += e[u];
+            for (int u = 0; u < 4; ++u) {
+              const float e0 = fast_exp2(fmaf(sacc[qt][8 * sh + 2 * u], c, mneg));
+              const float e1 = fast_exp2(fmaf(sacc[qt][8 * sh + 2 * u + 1], c, mneg));
+              w[u] = Elem<T>::pack2(e0, e1);
+              psum = Elem<T>::sum2(w[u], psum);
             }
-            pb[ks][sh][qt] = make_uint4(Elem<T>::pack2(e[0], e[1]), Elem<T>::pack2(e[2], e[3]),
-                                        Elem<T>::pack2(e[4], e[5]), Elem<T>::pack2(e[6], e[7]));
+            pb[sh][qt] = make_uint4(w[0], w[1], w[2], w[3]);
           }
-        l_run[qt] = l_run[qt] * alpha + psum;
+          l_run[qt] = psum;
+        }
 #pragma unroll
-        for (int dt = 0; dt < NDT; ++dt)
+        for (int sh = 0; sh < 2; ++sh)
 #pragma unroll
-          for (int i = 0; i < 16; ++i) o[qt][dt][i] *= alpha;
+          for (int dt = 0; dt < NDT; ++dt) {
+            const uint4 a = vt[VLayout<HD>::chunk(32 * dt + n, 4 * ks + 2 * sh + g)];
+#pragma unroll
+            for (int qt = 0; qt < QT; ++qt) o[qt][dt] = Elem<T>::mfma(a, pb[sh][qt], o[qt][dt]);
+          }
       }
-      pv_block<T, HD, QT>(o, pb, v_lds[buf], lane);
     }
     if (more) {
       kst.store(k_lds[buf ^ 1], tid);
@@ -154,7 +186,7 @@ __global__ __launch_bounds__(256) void flash_fwd_kernel(const FlashParams p) {
 #pragma unroll
   for (int qt = 0; qt < QT; ++qt) {
     const int q = q0w + 32 * qt + n;
-    const float l_tot = l_run[qt] + __shfl_xor(l_run[qt], 32);
+    const float l_tot = half_swap_sum(l_run[qt]);
     const float l_safe = l_tot == 0.f ? 1.f : l_tot;
     if (q < T_len) {
       store_out_tile<T, HD>(obase + (int64_t)q * p.o_st, o[qt], 1.f / l_safe, g);

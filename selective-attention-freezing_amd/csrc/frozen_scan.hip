@@ -18,10 +18,16 @@
 // chunk's predecessors always hold smaller tickets and are already running),
 // scans its chunk in registers (threads = column groups x row lanes, R rows
 // per thread), publishes its chunk aggregate, and obtains the carry from its
-// predecessors by decoupled look-back.  Every wait is bounded by spin_limit.
+// predecessors by decoupled look-back over tagged 64-bit words.  Every wait is
+// bounded by spin_limit.
 #include "saf_kernels.h"
 
 namespace saf {
+
+__device__ inline uint64_t pack_word(uint32_t tag, float v) {
+  return ((uint64_t)tag << 32) | (uint64_t)__float_as_uint(v);
+}
+__device__ inline float word_value(uint64_t w) { return __uint_as_float((uint32_t)(w & 0xffffffffu)); }
 
 template <typename T, int HD, int R>
 __global__ __launch_bounds__(256) void scan_kernel(const ScanParams p) {
@@ -102,69 +108,54 @@ __global__ __launch_bounds__(256) void scan_kernel(const ScanParams p) {
     __syncthreads();
   }
 
-  // decoupled look-back (wave 0; lane owns columns lane, lane + 64)
+  // Decoupled look-back (wave 0; lane owns columns lane, lane + 64).  Each
+  // published value is one 64-bit word: tag in the high half (1 = chunk
+  // aggregate, 2 = inclusive prefix, 0 = not yet written), fp32 value in the
+  // low half, so a single relaxed device-scope atomic store publishes it and
+  // no fence (L2 write-back / invalidate) is needed on either side.  Columns
+  // are independent, so lanes may look back to different depths.
   if (tid < 64) {
     const int lane = tid;
     constexpr int NC = (HD + 63) / 64;
     const int64_t idx = (int64_t)seq * p.n_chunks + chunk;
     const float r_ch = rpow((float)CH);
-    float a_wg[NC], carry[NC];
 #pragma unroll
     for (int u = 0; u < NC; ++u) {
       const int col = lane + 64 * u;
-      a_wg[u] = col < HD ? sh_x[NRL - 1][col] : 0.f;
-      carry[u] = 0.f;
-    }
-    if (chunk > 0) {
-#pragma unroll
-      for (int u = 0; u < NC; ++u) {
-        const int col = lane + 64 * u;
-        if (col < HD) p.agg[idx * HD + col] = a_wg[u];
-      }
-      __threadfence();
-      if (lane == 0) __hip_atomic_store(p.flags + idx, 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
-      float factor = 1.f;
-      int k = chunk - 1;
-      while (k >= 0) {
-        const int64_t kidx = (int64_t)seq * p.n_chunks + k;
-        uint32_t f = 0;
-        if (lane == 0) {
-          int spins = 0;
-          for (;;) {
-            f = __hip_atomic_load(p.flags + kidx, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_AGENT);
-            if (f != 0) break;
-            if (++spins > p.spin_limit) {
-              atomicOr(p.error, 1u);
-              f = 3;  // give up: carry is incomplete, the kernel still drains
-              break;
-            }
-            __builtin_amdgcn_s_sleep(2);
+      if (col >= HD) continue;
+      const float a_wg = sh_x[NRL - 1][col];
+      float carry = 0.f;
+      if (chunk > 0) {
+        __hip_atomic_store(p.agg + idx * HD + col, pack_word(1u, a_wg), __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
+        float factor = 1.f;
+        int k = chunk - 1;
+        int spins = 0;
+        while (k >= 0) {
+          const int64_t kc = ((int64_t)seq * p.n_chunks + k) * HD + col;
+          const uint64_t wi = __hip_atomic_load(p.incl + kc, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          if (wi >> 32) {
+            carry = fmaf(factor, word_value(wi), carry);
+            break;
           }
+          const uint64_t wa = __hip_atomic_load(p.agg + kc, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          if (wa >> 32) {
+            carry = fmaf(factor, word_value(wa), carry);
+            factor *= r_ch;
+            --k;
+            continue;
+          }
+          if (++spins > p.spin_limit) {  // give up: carry incomplete, kernel still drains
+            atomicOr(p.error, 1u);
+            break;
+          }
+          __builtin_amdgcn_s_sleep(1);
         }
-        f = __shfl(f, 0);
-        __threadfence();
-        if (f == 3) break;
-        const float* src = (f == 2 ? p.incl : p.agg) + kidx * HD;
-#pragma unroll
-        for (int u = 0; u < NC; ++u) {
-          const int col = lane + 64 * u;
-          if (col < HD) carry[u] = fmaf(factor, src[col], carry[u]);
-        }
-        if (f == 2) break;
-        factor *= r_ch;
-        --k;
       }
+      __hip_atomic_store(p.incl + idx * HD + col, pack_word(2u, fmaf(carry, r_ch, a_wg)), __ATOMIC_RELAXED,
+                         __HIP_MEMORY_SCOPE_AGENT);
+      sh_carry[col] = carry;
     }
-#pragma unroll
-    for (int u = 0; u < NC; ++u) {
-      const int col = lane + 64 * u;
-      if (col < HD) {
-        p.incl[idx * HD + col] = fmaf(carry[u], r_ch, a_wg[u]);
-        sh_carry[col] = carry[u];
-      }
-    }
-    __threadfence();
-    if (lane == 0) __hip_atomic_store(p.flags + idx, 2u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
   }
   __syncthreads();
 

@@ -68,19 +68,19 @@ bool supported_hd(int64_t hd) { return hd == 32 || hd == 64 || hd == 96 || hd ==
 
 int n_scan_chunks(int T, int hd) { return (T + scan_chunk_rows(hd) - 1) / scan_chunk_rows(hd); }
 
+// Workspace: [counter u32, error u32, pad to 256] [agg u64 x n] [incl u64 x n]
+// with n = n_seq * n_chunks * hd; the whole block is cleared before a scan.
 struct WsLayout {
-  int64_t flags_off, agg_off, incl_off, total;
+  int64_t agg_off, incl_off, total;
 };
 
 WsLayout ws_layout(int64_t B, int64_t T, int hd, int64_t n_scan) {
-  WsLayout w{0, 0, 0, 0};
+  WsLayout w{0, 0, 0};
   if (n_scan <= 0 || T <= 0 || B <= 0) return w;
-  const int64_t nseq = B * n_scan, nch = n_scan_chunks((int)T, hd);
-  w.flags_off = 8;
-  const int64_t words_end = 8 + 4 * nseq * nch;
-  w.agg_off = (words_end + 255) / 256 * 256;
-  w.incl_off = w.agg_off + 4 * nseq * nch * hd;
-  w.total = w.incl_off + 4 * nseq * nch * hd;
+  const int64_t n = B * n_scan * n_scan_chunks((int)T, hd) * hd;
+  w.agg_off = 256;
+  w.incl_off = w.agg_off + 8 * n;
+  w.total = w.incl_off + 8 * n;
   return w;
 }
 
@@ -319,10 +319,9 @@ int run_scan(const saf_mixed_attn_args* a, const Plan& pl, hipStream_t s) {
   p.n_chunks = n_scan_chunks(pl.T, pl.HD);
   p.counter = reinterpret_cast<uint32_t*>(ws);
   p.error = reinterpret_cast<uint32_t*>(ws + 4);
-  p.flags = reinterpret_cast<uint32_t*>(ws + w.flags_off);
-  p.agg = reinterpret_cast<float*>(ws + w.agg_off);
-  p.incl = reinterpret_cast<float*>(ws + w.incl_off);
-  p.spin_limit = a->scan_spin_limit > 0 ? a->scan_spin_limit : (1 << 24);
+  p.agg = reinterpret_cast<uint64_t*>(ws + w.agg_off);
+  p.incl = reinterpret_cast<uint64_t*>(ws + w.incl_off);
+  p.spin_limit = a->scan_spin_limit > 0 ? a->scan_spin_limit : (1 << 20);
   for (int i = 0; i < p.n_slots; ++i) {
     const int h = pl.scan[i];
     p.out_head[i] = (int16_t)h;
@@ -330,8 +329,7 @@ int run_scan(const saf_mixed_attn_args* a, const Plan& pl, hipStream_t s) {
     p.kind[i] = (int8_t)a->closed_kind[h];
     p.param[i] = a->closed_param[h];
   }
-  const int64_t words = 2 + (int64_t)pl.B * p.n_slots * p.n_chunks;
-  if (int rc = launched(launch_zero_u32(p.counter, words, s), "workspace clear")) return rc;
+  if (int rc = launched(launch_zero_u32(p.counter, w.total / 4, s), "workspace clear")) return rc;
   return launched(launch_scan(p, pl.dtype, pl.HD, s), "closed-form scan");
 }
 

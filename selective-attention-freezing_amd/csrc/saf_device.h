@@ -57,6 +57,11 @@ template <> struct Elem<__bf16> {
   }
   __device__ static inline float lo(uint32_t w) { return __uint_as_float(w << 16); }
   __device__ static inline float hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
+  // acc + lo(w) + hi(w) with one v_dot2 (row sums of packed P)
+  __device__ static inline float sum2(uint32_t w, float acc) {
+    const bf16x2_t one = {(__bf16)1.f, (__bf16)1.f};
+    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, w), one, acc, false);
+  }
 };
 
 template <> struct Elem<_Float16> {
@@ -75,6 +80,10 @@ template <> struct Elem<_Float16> {
   }
   __device__ static inline float hi(uint32_t w) {
     return (float)__builtin_bit_cast(_Float16, (uint16_t)(w >> 16));
+  }
+  __device__ static inline float sum2(uint32_t w, float acc) {
+    const f16x2_t one = {(_Float16)1.f, (_Float16)1.f};
+    return __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2_t, w), one, acc, false);
   }
 };
 
@@ -95,6 +104,17 @@ __device__ inline f32x16_t zero16() {
 }
 
 __device__ inline float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// Combine a per-lane value with the partner lane l ^ 32 (v_permlane32_swap
+// hands each lane both its own and its partner's value, in some order).
+__device__ inline float half_swap_max(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ inline float half_swap_sum(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
 
 // Row permutation of the S^T product (see header comment).  A-lane row
 // m = 8a + 4g + r  loads key 16*(a/2) + 8g + 4*(a%2) + r.

@@ -70,9 +70,10 @@ struct ScanParams {
   int B, T, n_slots, n_chunks;
   uint32_t* counter;  // ticket counter (zeroed before launch)
   uint32_t* error;    // set to 1 if a look-back wait hit the spin limit
-  uint32_t* flags;    // [n_seq * n_chunks]: 0 empty, 1 aggregate, 2 inclusive
-  float* agg;         // [n_seq * n_chunks * HD]
-  float* incl;        // [n_seq * n_chunks * HD]
+  // [n_seq * n_chunks * HD] tagged words (tag << 32 | fp32 bits), zeroed
+  // before launch: chunk aggregates and inclusive prefixes
+  uint64_t* agg;
+  uint64_t* incl;
   int spin_limit;
   int16_t out_head[kMaxHeads];
   int16_t v_head[kMaxHeads];

@@ -244,8 +244,13 @@ class CausalSelfAttention(nn.Module):
         self._fz_dirty = True
 
     # -- routing cache (nanogpt/model.py:846-898) --------------------------
-    @torch.no_grad()
     def _refresh_freeze_cache(self):
+        # normal (non-inference) tensors, so a cache built under inference_mode
+        # can still feed a later grad-enabled forward
+        with torch.inference_mode(False), torch.no_grad():
+            self._refresh_freeze_cache_impl()
+
+    def _refresh_freeze_cache_impl(self):
         frozen = self.dyn_frozen
         dev = frozen.device
         hd = self.head_dim
