@@ -77,6 +77,23 @@ def build_c2_model(T, device, dtype, seed=1337, n_layer=12):
     return model, x, plan
 
 
+TRAFFIC_FILE = os.path.join(REPO, "profiles", "flash_fwd_c2_hbm_traffic.txt")
+
+
+def pmc_traffic(kernel_label):
+    """HBM bytes per dispatch of a kernel from the committed rocprofv3
+    FETCH_SIZE / WRITE_SIZE summary (copy-calibrated), or None."""
+    if not os.path.exists(TRAFFIC_FILE):
+        return None
+    for line in open(TRAFFIC_FILE):
+        if line.startswith(kernel_label + ":"):
+            for part in line.split(","):
+                k, _, v = part.partition("=")
+                if k.strip() == "traffic_bytes":
+                    return int(float(v))
+    return None
+
+
 def live_flops(plan, n_layer, n_head, B, T, hd):
     n_frozen = sum(len(v) for v in plan.values())
     n_live = n_layer * n_head - n_frozen
@@ -132,6 +149,9 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-layers", type=int, default=2)
     ap.add_argument("--no-timer", action="store_true", help="skip per-kernel HIP events")
+    ap.add_argument("--copy-calibration-mib", type=int, default=0,
+                    help="only run device-to-device copies of this many MiB (the known-size "
+                         "kernel that scales rocprofv3 FETCH_SIZE / WRITE_SIZE readings)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this build runs the mixed-head prefill on a single "
@@ -141,6 +161,16 @@ def main():
     import torch
     import kernel
     from nanogpt import model as model_mod
+
+    if args.copy_calibration_mib:
+        n = args.copy_calibration_mib << 20
+        src = torch.ones(n, dtype=torch.uint8, device="cuda")
+        dst = torch.empty_like(src)
+        for _ in range(5):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_calibration_bytes": n, "copies": 5}), flush=True)
+        return
 
     dev = "cuda"
     T = args.seq_len
@@ -189,9 +219,11 @@ def main():
             n, ms, work = summ["flash"]
             per_launch_ms = ms / n
             achieved = (work / n) / (per_launch_ms / 1000.0) / 1e12
+            label = "flash_fwd_kernel<bf16,64,2>"
             roof = {"bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_BF16_TFLOPS,
                     "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
-                    "traffic": None, "kernel": "flash_fwd_kernel<bf16,64,2>",
+                    "traffic": pmc_traffic(label) if T == 16384 else None,
+                    "traffic_source": "profiles/flash_fwd_c2_hbm_traffic.txt", "kernel": label,
                     "launches": n, "avg_launch_ms": round(per_launch_ms, 4),
                     "flop_per_launch": work // n}
         if "scan" in summ:
