@@ -116,9 +116,18 @@ int saf_frozen_scan_fwd(const saf_mixed_attn_args* args, void* stream);
 int saf_frozen_pv_fwd(const saf_tensor_t* patt, const saf_tensor_t* v, const int32_t* fz_idx,
                       int32_t nf, int32_t T, const saf_tensor_t* out, void* stream);
 
-/* Workspace needed by saf_mixed_attn_fwd / saf_frozen_scan_fwd for n_scan_heads
- * closed-form heads (0 bytes when there are none). */
+/* Workspace needed by saf_frozen_scan_fwd for n_scan_heads closed-form heads
+ * (0 bytes when there are none). */
 int64_t saf_workspace_bytes(int32_t B, int32_t T, int32_t head_dim, int32_t n_scan_heads);
+
+/* Workspace that lets one saf_mixed_attn_fwd / saf_flash_fwd call with these
+ * arguments (workspace fields ignored) use every optimisation: the closed-form
+ * scan's look-back words, then fp32 partials of the live-head kernel's causal
+ * load balancing (long query blocks split into key segments and merged by a
+ * combine kernel).  A smaller workspace still works if it covers the scan:
+ * the live-head kernel then runs unsplit.  Returns -1 on invalid arguments.
+ * No counterpart in the reference (its Triton launch needs no workspace). */
+int64_t saf_mixed_attn_workspace_bytes(const saf_mixed_attn_args* args);
 
 /* Reads the scan's look-back error word from a workspace after the stream
  * has been synchronised: 1 if a wait hit its spin limit, else 0. */

@@ -16,6 +16,8 @@
 // blocks up to its own causal limit.  K and V^T tiles are double-buffered in
 // LDS; the next tile's global loads are issued before the current tile's
 // MFMAs.  Workgroups are ordered heaviest query block first.
+#include <type_traits>
+
 #include "saf_kernels.h"
 
 namespace saf {
@@ -40,16 +42,24 @@ void flash_fwd_kernel(const FlashParams p) {
   __shared__ __align__(16) uint4 k_lds[2][KLayout<HD>::BYTES / 16];
   __shared__ __align__(16) uint4 v_lds[2][VLayout<HD>::BYTES / 16];
 
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (SGPR)
   const int n = lane & 31, g = lane >> 5;
 
-  // heaviest query block first; (batch, live slot) fastest
+  // work item: query block (and key segment) of one (batch, live slot);
+  // items are ordered heaviest first, (batch, live slot) fastest
   const int nbh = p.B * p.n_slots;
-  const int qb = p.n_qblk - 1 - (int)(blockIdx.x / nbh);
   const int r = blockIdx.x % nbh;
   const int b = r / p.n_slots, slot = r % p.n_slots;
   const int h = p.out_head[slot];
-
+  int qb, seg = 0;
+  if (p.n_items) {
+    const int it = p.items[blockIdx.x / nbh];
+    qb = it >> 8;
+    seg = it & 255;
+  } else {
+    qb = p.n_qblk - 1 - (int)(blockIdx.x / nbh);
+  }
   const T* qbase = reinterpret_cast<const T*>(p.q) + b * p.q_sb + (int64_t)p.q_head[slot] * p.q_sh;
   const T* kbase = reinterpret_cast<const T*>(p.k) + b * p.k_sb + (int64_t)p.k_head[slot] * p.k_sh;
   const T* vbase = reinterpret_cast<const T*>(p.v) + b * p.v_sb + (int64_t)p.v_head[slot] * p.v_sh;
@@ -58,8 +68,10 @@ void flash_fwd_kernel(const FlashParams p) {
   const int T_len = p.T;
   const int q0 = qb * BM;
   const int q0w = q0 + wave * 32 * QT;
-  const int kend_wg = min(q0 + BM, T_len);
-  const int nkb = (kend_wg + 63) / 64;
+  const int nkb_qb = (min(q0 + BM, T_len) + 63) / 64;  // key blocks of the query block
+  const int kb0 = p.n_items ? seg * p.seg_len : 0;     // this item's key-block range
+  const int nkb = p.n_items ? min(kb0 + p.seg_len, nkb_qb) : nkb_qb;
+  const bool split = p.n_items && p.part_base[qb] >= 0;
   const int kend_w = min(q0w + 32 * QT, T_len);
   const int nkb_w = kend_w > 0 ? (kend_w + 63) / 64 : 0;
 
@@ -87,14 +99,14 @@ void flash_fwd_kernel(const FlashParams p) {
 
   KStager<T, HD, NTHR> kst;
   VStager<T, HD, NTHR> vst;
-  kst.load(kbase, p.k_st, 0, T_len, tid);
-  vst.load(vbase, p.v_st, 0, T_len, tid);
+  kst.load(kbase, p.k_st, 64 * kb0, T_len, tid);
+  vst.load(vbase, p.v_st, 64 * kb0, T_len, tid);
   kst.store(k_lds[0], tid);
   vst.store(reinterpret_cast<uint32_t*>(v_lds[0]), tid);
   __syncthreads();
 
-  for (int j = 0; j < nkb; ++j) {
-    const int buf = j & 1;
+  auto block = [&](const int j, auto masked) {
+    const int buf = (j - kb0) & 1;
     const bool more = j + 1 < nkb;
     if (more) {
       kst.load(kbase, p.k_st, 64 * (j + 1), T_len, tid);
@@ -112,13 +124,27 @@ void flash_fwd_kernel(const FlashParams p) {
 #pragma unroll
         for (int qt = 0; qt < QT; ++qt) sacc[qt] = zero16();
         const int key = 32 * ks + kperm(n);
+        // all A operands of the sub-block are read from LDS up front, so only
+        // the first MFMA waits for LDS latency
+        uint4 ka[NKT];
 #pragma unroll
-        for (int t = 0; t < NKT; ++t) {
-          const uint4 a = kt[KLayout<HD>::chunk(key, 2 * t + g)];
+        for (int t = 0; t < NKT; ++t) ka[t] = kt[KLayout<HD>::chunk(key, 2 * t + g)];
+        // MFMA phases run at raised wave priority so that, of the two waves
+        // sharing a SIMD, the one with matrix work ready issues it first and
+        // the other fills the VALU with its softmax
+        __builtin_amdgcn_s_setprio(1);
 #pragma unroll
-          for (int qt = 0; qt < QT; ++qt) sacc[qt] = Elem<T>::mfma(a, qf[qt][t], sacc[qt]);
-        }
-        if (j0 + 31 > q0w) {  // causal mask only where a key can exceed a query
+        for (int t = 0; t < NKT; ++t)
+#pragma unroll
+          for (int qt = 0; qt < QT; ++qt) sacc[qt] = Elem<T>::mfma(ka[t], qf[qt][t], sacc[qt]);
+        __builtin_amdgcn_s_setprio(0);
+        // V^T operands of this sub-block arrive while the softmax runs
+        uint4 va[2][NDT];
+#pragma unroll
+        for (int sh = 0; sh < 2; ++sh)
+#pragma unroll
+          for (int dt = 0; dt < NDT; ++dt) va[sh][dt] = vt[VLayout<HD>::chunk(32 * dt + n, 4 * ks + 2 * sh + g)];
+        if (decltype(masked)::value && j0 + 31 > q0w) {  // keys past a query of this wave
 #pragma unroll
           for (int qt = 0; qt < QT; ++qt) {
             const int q = q0w + 32 * qt + n;
@@ -166,14 +192,14 @@ void flash_fwd_kernel(const FlashParams p) {
           }
           l_run[qt] = psum;
         }
+        __builtin_amdgcn_s_setprio(1);
 #pragma unroll
         for (int sh = 0; sh < 2; ++sh)
 #pragma unroll
-          for (int dt = 0; dt < NDT; ++dt) {
-            const uint4 a = vt[VLayout<HD>::chunk(32 * dt + n, 4 * ks + 2 * sh + g)];
+          for (int dt = 0; dt < NDT; ++dt)
 #pragma unroll
-            for (int qt = 0; qt < QT; ++qt) o[qt][dt] = Elem<T>::mfma(a, pb[sh][qt], o[qt][dt]);
-          }
+            for (int qt = 0; qt < QT; ++qt) o[qt][dt] = Elem<T>::mfma(va[sh][dt], pb[sh][qt], o[qt][dt]);
+        __builtin_amdgcn_s_setprio(0);
       }
     }
     if (more) {
@@ -181,12 +207,34 @@ void flash_fwd_kernel(const FlashParams p) {
       vst.store(reinterpret_cast<uint32_t*>(v_lds[buf ^ 1]), tid);
     }
     __syncthreads();
-  }
+  };
+  // blocks wholly below the workgroup's first query need no causal mask; the
+  // masked variant runs only for the last BM/64 blocks of a query block
+  const int jd = min(nkb, max(kb0, q0 / 64));
+  for (int j = kb0; j < jd; ++j) block(j, std::false_type());
+  for (int j = jd; j < nkb; ++j) block(j, std::true_type());
 
 #pragma unroll
   for (int qt = 0; qt < QT; ++qt) {
     const int q = q0w + 32 * qt + n;
     const float l_tot = half_swap_sum(l_run[qt]);
+    if (split) {
+      // unnormalised partial of this key segment, merged by flash_combine_kernel
+      const int64_t pidx = (int64_t)r * p.n_part_per_head + p.part_base[qb] + seg;
+      const int rl = q - q0;
+      float* po = p.part_o + (pidx * BM + rl) * HD;
+#pragma unroll
+      for (int dt = 0; dt < NDT; ++dt)
+#pragma unroll
+        for (int r4 = 0; r4 < 4; ++r4)
+          *reinterpret_cast<float4*>(po + 32 * dt + 8 * r4 + 4 * g) =
+              make_float4(o[qt][dt][4 * r4], o[qt][dt][4 * r4 + 1], o[qt][dt][4 * r4 + 2], o[qt][dt][4 * r4 + 3]);
+      if (g == 0) {
+        p.part_ml[(pidx * 2) * BM + rl] = m_run[qt];
+        p.part_ml[(pidx * 2 + 1) * BM + rl] = l_tot;
+      }
+      continue;
+    }
     const float l_safe = l_tot == 0.f ? 1.f : l_tot;
     if (q < T_len) {
       store_out_tile<T, HD>(obase + (int64_t)q * p.o_st, o[qt], 1.f / l_safe, g);
@@ -198,9 +246,57 @@ void flash_fwd_kernel(const FlashParams p) {
   }
 }
 
+// Merge the key-segment partials of split query blocks (one workgroup per
+// (batch, live slot, split query block); 16 threads x 4 columns per row).
+template <typename T, int HD>
+__global__ __launch_bounds__(256) void flash_combine_kernel(const CombineParams p) {
+  const int tid = threadIdx.x;
+  const int nbh = p.B * p.n_slots;
+  const int bh = blockIdx.x % nbh;
+  const int qb = p.split_qb[blockIdx.x / nbh];
+  const int b = bh / p.n_slots, slot = bh % p.n_slots;
+  const int h = p.out_head[slot];
+  const int BM = p.BM;
+  const int q0 = qb * BM;
+  const int nkb_qb = (min(q0 + BM, p.T) + 63) / 64;
+  const int nseg = (nkb_qb + p.seg_len - 1) / p.seg_len;
+  const int64_t pbase = (int64_t)bh * p.n_part_per_head + p.part_base[qb];
+  constexpr int CPR = HD / 4;          // float4 columns per row
+  constexpr int RPP = 256 / CPR;       // rows per pass
+  const int c4 = tid % CPR;
+  T* obase = reinterpret_cast<T*>(p.out) + b * p.o_sb + (int64_t)h * p.o_sh;
+  if (tid >= RPP * CPR) return;
+  for (int rl = tid / CPR; rl < BM; rl += RPP) {
+    const int q = q0 + rl;
+    if (q >= p.T) break;
+    float mmax = -INFINITY;
+    for (int s = 0; s < nseg; ++s) mmax = fmaxf(mmax, p.part_ml[((pbase + s) * 2) * BM + rl]);
+    const float mref = mmax == -INFINITY ? 0.f : mmax;
+    float l = 0.f;
+    float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+    for (int s = 0; s < nseg; ++s) {
+      const float w = fast_exp2(p.part_ml[((pbase + s) * 2) * BM + rl] - mref);
+      l = fmaf(w, p.part_ml[((pbase + s) * 2 + 1) * BM + rl], l);
+      const float4 v = *reinterpret_cast<const float4*>(p.part_o + ((pbase + s) * BM + rl) * HD + 4 * c4);
+      acc.x = fmaf(w, v.x, acc.x);
+      acc.y = fmaf(w, v.y, acc.y);
+      acc.z = fmaf(w, v.z, acc.z);
+      acc.w = fmaf(w, v.w, acc.w);
+    }
+    const float inv = 1.f / (l == 0.f ? 1.f : l);
+    uint2 wv;
+    wv.x = Elem<T>::pack2(acc.x * inv, acc.y * inv);
+    wv.y = Elem<T>::pack2(acc.z * inv, acc.w * inv);
+    *reinterpret_cast<uint2*>(obase + (int64_t)q * p.o_st + 4 * c4) = wv;
+    if (p.lse != nullptr && c4 == 0)
+      p.lse[b * p.l_sb + (int64_t)h * p.l_sh + (int64_t)q * p.l_st] = mref + __log2f(l == 0.f ? 1.f : l);
+  }
+}
+
 template <typename T, int HD, int QT>
 static hipError_t launch_flash_t(const FlashParams& p, hipStream_t s) {
-  const dim3 grid((unsigned)((int64_t)p.n_qblk * p.B * p.n_slots));
+  const int64_t items = p.n_items ? p.n_items : p.n_qblk;
+  const dim3 grid((unsigned)(items * p.B * p.n_slots));
   hipLaunchKernelGGL((flash_fwd_kernel<T, HD, QT>), grid, dim3(256), 0, s, p);
   return hipGetLastError();
 }
@@ -223,6 +319,25 @@ static hipError_t launch_flash_hd(const FlashParams& p, int hd, int qt, hipStrea
 hipError_t launch_flash(const FlashParams& p, int dtype, int hd, int qt, hipStream_t s) {
   if (dtype == kBF16) return launch_flash_hd<__bf16>(p, hd, qt, s);
   if (dtype == kF16) return launch_flash_hd<_Float16>(p, hd, qt, s);
+  return hipErrorInvalidValue;
+}
+
+template <typename T>
+static hipError_t launch_combine_t(const CombineParams& p, int hd, hipStream_t s) {
+  const dim3 grid((unsigned)((int64_t)p.n_split * p.B * p.n_slots));
+  switch (hd) {
+    case 32: hipLaunchKernelGGL((flash_combine_kernel<T, 32>), grid, dim3(256), 0, s, p); break;
+    case 64: hipLaunchKernelGGL((flash_combine_kernel<T, 64>), grid, dim3(256), 0, s, p); break;
+    case 96: hipLaunchKernelGGL((flash_combine_kernel<T, 96>), grid, dim3(256), 0, s, p); break;
+    case 128: hipLaunchKernelGGL((flash_combine_kernel<T, 128>), grid, dim3(256), 0, s, p); break;
+    default: return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
+hipError_t launch_flash_combine(const CombineParams& p, int dtype, int hd, hipStream_t s) {
+  if (dtype == kBF16) return launch_combine_t<__bf16>(p, hd, s);
+  if (dtype == kF16) return launch_combine_t<_Float16>(p, hd, s);
   return hipErrorInvalidValue;
 }
 

@@ -64,7 +64,8 @@ __global__ __launch_bounds__(256) void frozen_pv_kernel(const FrozenParams p) {
   __shared__ float a_lds[2][MODE == 1 ? 64 : 1];
   __shared__ float r_lds[2][MODE == 1 ? RW : 1];
 
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (SGPR)
   const int n = lane & 31, g = lane >> 5;
 
   const int nbh = p.B * p.n_slots;

@@ -8,6 +8,7 @@
 // pidx[h] (identity when absent), state 2 heads read row h of alpha/rho/z.
 // Each head kind becomes its own kernel launch over a compact head list, and
 // every kernel writes its heads' rows of the natural-order output directly.
+#include <algorithm>
 #include <cmath>
 #include <cstdarg>
 #include <cstdio>
@@ -84,6 +85,10 @@ WsLayout ws_layout(int64_t B, int64_t T, int hd, int64_t n_scan) {
   return w;
 }
 
+// Bytes of the workspace used by the closed-form scan (placed first).
+struct Plan;
+int64_t scan_ws_bytes(const Plan& pl);
+
 enum Which : unsigned { kDoFlash = 1, kDoDense = 2, kDoDecomp = 4, kDoScan = 8, kDoAll = 15 };
 
 struct Plan {
@@ -91,7 +96,7 @@ struct Plan {
   std::vector<int> live, dense, decomp, scan;
 };
 
-int plan_and_validate(const saf_mixed_attn_args* a, unsigned which, Plan& pl) {
+int plan_and_validate(const saf_mixed_attn_args* a, unsigned which, Plan& pl, bool need_workspace = true) {
   if (a == nullptr) return fail(SAF_EINVAL, "args is NULL");
   const saf_tensor_t& v = a->v;
   if (!present(v)) return fail(SAF_EINVAL, "v is required");
@@ -200,7 +205,7 @@ int plan_and_validate(const saf_mixed_attn_args* a, unsigned which, Plan& pl) {
         return fail(SAF_EUNSUPPORTED, "unsupported %s dtype %s", names[i], dtype_name(t.dtype));
     }
   }
-  if ((which & kDoScan) && !pl.scan.empty()) {
+  if (need_workspace && (which & kDoScan) && !pl.scan.empty()) {
     const WsLayout w = ws_layout(pl.B, pl.T, pl.HD, (int64_t)pl.scan.size());
     if (a->workspace == nullptr || a->workspace_bytes < w.total)
       return fail(SAF_EWORKSPACE, "closed-form heads need a %lld-byte workspace (got %lld)", (long long)w.total,
@@ -209,6 +214,90 @@ int plan_and_validate(const saf_mixed_attn_args* a, unsigned which, Plan& pl) {
       return fail(SAF_EALIGN, "workspace must be 256-byte aligned");
   }
   return SAF_OK;
+}
+
+// ---- causal load balancing of the live-head kernel ------------------------
+// Resident flash workgroups per device (2 per CU), cached per device per thread.
+int flash_slots() {
+  thread_local int cached_dev = -1, cached_slots = 0;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return 512;
+  if (dev != cached_dev) {
+    int cus = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
+      cus = 256;
+    cached_dev = dev;
+    cached_slots = 2 * cus;
+  }
+  return cached_slots;
+}
+
+struct FlashPlan {
+  int n_items = 0, seg_len = 0, n_part_per_head = 0, n_split = 0;
+  std::vector<int32_t> items;
+  std::vector<int16_t> part_base, split_qb;
+  int64_t part_bytes = 0;  // workspace for the partials
+};
+
+// Splits the key range of the heaviest query blocks into segments of about
+// the average per-slot work, so the causal tail (the last query block walks
+// every key) does not outlast the rest of the grid.
+FlashPlan plan_flash(int B, int n_slots, int T, int HD, int qt) {
+  FlashPlan fp;
+  const int BM = block_rows(qt), BMb = BM / 64;
+  const int nqb = (T + BM - 1) / BM;
+  if (nqb <= 1 || nqb > kMaxQblk) return fp;
+  std::vector<int> nkb(nqb);
+  int64_t per_head = 0;
+  for (int qb = 0; qb < nqb; ++qb) {
+    nkb[qb] = (std::min((qb + 1) * BM, T) + 63) / 64;
+    per_head += nkb[qb];
+  }
+  const int64_t nbh = (int64_t)B * n_slots;
+  const int64_t slots = flash_slots();
+  int64_t L = (nbh * per_head + slots - 1) / slots;
+  L = std::max<int64_t>(L, 4 * BMb);
+  L = (L + BMb - 1) / BMb * BMb;
+  for (;; L *= 2) {
+    if (L >= nkb[nqb - 1]) return fp;  // nothing to split
+    int64_t n = 0;
+    for (int qb = 0; qb < nqb; ++qb) n += (nkb[qb] + L - 1) / L;
+    if (n <= kMaxItems && L < 65536) break;
+  }
+  struct It { int len, qb, seg; };
+  std::vector<It> its;
+  fp.part_base.assign(kMaxQblk, (int16_t)-1);
+  int parts = 0;
+  for (int qb = 0; qb < nqb; ++qb) {
+    const int nseg = (int)((nkb[qb] + L - 1) / L);
+    if (nseg > 1) {
+      fp.part_base[qb] = (int16_t)parts;
+      fp.split_qb.push_back((int16_t)qb);
+      parts += nseg;
+    }
+    for (int sg = 0; sg < nseg; ++sg) its.push_back({(int)std::min<int64_t>(L, nkb[qb] - sg * L), qb, sg});
+  }
+  std::stable_sort(its.begin(), its.end(), [](const It& a, const It& b) {
+    return a.len != b.len ? a.len > b.len : a.qb > b.qb;
+  });
+  for (const It& it : its) fp.items.push_back((it.qb << 8) | it.seg);
+  fp.n_items = (int)fp.items.size();
+  fp.seg_len = (int)L;
+  fp.n_part_per_head = parts;
+  fp.n_split = (int)fp.split_qb.size();
+  fp.part_bytes = nbh * parts * (int64_t)BM * (HD + 2) * 4;
+  return fp;
+}
+
+int flash_qtiles_for(const saf_mixed_attn_args* a, int HD) {
+  int qt = a->flash_qtiles;
+  if (qt == 0) qt = HD <= 64 ? 2 : 1;
+  return qt;
+}
+
+int64_t scan_ws_bytes(const Plan& pl) {
+  const int64_t t = ws_layout(pl.B, pl.T, pl.HD, (int64_t)pl.scan.size()).total;
+  return (t + 255) / 256 * 256;
 }
 
 int launched(hipError_t e, const char* what) {
@@ -234,14 +323,29 @@ int run_flash(const saf_mixed_attn_args* a, const Plan& pl, hipStream_t s) {
       return fail(SAF_EINVAL, "lse must be (B, H, T) float32");
     p.l_sb = l.stride[0]; p.l_sh = l.stride[1]; p.l_st = l.stride[2];
   }
-  int qt = a->flash_qtiles;
-  if (qt == 0) qt = pl.HD <= 64 ? 2 : 1;
+  const int qt = flash_qtiles_for(a, pl.HD);
   if (qt != 1 && qt != 2) return fail(SAF_EINVAL, "flash_qtiles must be 0, 1 or 2");
   p.B = pl.B;
   p.T = pl.T;
   p.n_slots = (int)pl.live.size();
   p.n_qblk = (pl.T + block_rows(qt) - 1) / block_rows(qt);
   p.scale_log2 = a->sm_scale * kLog2e;
+  // split the causal tail when the caller's workspace holds the partials
+  FlashPlan fp = plan_flash(pl.B, p.n_slots, pl.T, pl.HD, qt);
+  const int64_t part_off = scan_ws_bytes(pl);
+  if (fp.n_items && a->workspace != nullptr && a->workspace_bytes >= part_off + fp.part_bytes) {
+    char* ws = reinterpret_cast<char*>(a->workspace) + part_off;
+    const int64_t nbh = (int64_t)pl.B * p.n_slots;
+    p.n_items = fp.n_items;
+    p.seg_len = fp.seg_len;
+    p.n_part_per_head = fp.n_part_per_head;
+    p.part_o = reinterpret_cast<float*>(ws);
+    p.part_ml = reinterpret_cast<float*>(ws + nbh * fp.n_part_per_head * (int64_t)block_rows(qt) * pl.HD * 4);
+    std::copy(fp.items.begin(), fp.items.end(), p.items);
+    std::copy(fp.part_base.begin(), fp.part_base.end(), p.part_base);
+  } else {
+    fp = FlashPlan();
+  }
   for (int i = 0; i < p.n_slots; ++i) {
     const int h = pl.live[i];
     const int slot = a->hidx ? a->hidx[h] : h;
@@ -250,7 +354,21 @@ int run_flash(const saf_mixed_attn_args* a, const Plan& pl, hipStream_t s) {
     p.k_head[i] = (int16_t)(a->kvidx ? a->kvidx[h] : slot);
     p.v_head[i] = (int16_t)(a->kvidx ? a->kvidx[h] : h);
   }
-  return launched(launch_flash(p, pl.dtype, pl.HD, qt, s), "flash");
+  if (int rc = launched(launch_flash(p, pl.dtype, pl.HD, qt, s), "flash")) return rc;
+  if (fp.n_split == 0) return SAF_OK;
+  CombineParams c{};
+  c.out = p.out;
+  c.lse = p.lse;
+  c.o_sb = p.o_sb; c.o_sh = p.o_sh; c.o_st = p.o_st;
+  c.l_sb = p.l_sb; c.l_sh = p.l_sh; c.l_st = p.l_st;
+  c.B = p.B; c.T = p.T; c.n_slots = p.n_slots; c.BM = block_rows(qt);
+  c.seg_len = fp.seg_len; c.n_part_per_head = fp.n_part_per_head; c.n_split = fp.n_split;
+  c.part_o = p.part_o;
+  c.part_ml = p.part_ml;
+  std::copy(p.out_head, p.out_head + kMaxHeads, c.out_head);
+  std::copy(fp.split_qb.begin(), fp.split_qb.end(), c.split_qb);
+  std::copy(fp.part_base.begin(), fp.part_base.end(), c.part_base);
+  return launched(launch_flash_combine(c, pl.dtype, pl.HD, s), "flash combine");
 }
 
 void fill_frozen_common(FrozenParams& p, const saf_tensor_t& v, const saf_tensor_t& o, int B, int T) {
@@ -401,6 +519,17 @@ int saf_frozen_pv_fwd(const saf_tensor_t* patt, const saf_tensor_t* v, const int
     ph.push_back(fz_idx[f]);
   }
   return run_dense(*patt, *v, *out, B, T, HD, v->dtype, oh, vh, ph, reinterpret_cast<hipStream_t>(stream));
+}
+
+int64_t saf_mixed_attn_workspace_bytes(const saf_mixed_attn_args* args) {
+  Plan pl;
+  if (plan_and_validate(args, kDoFlash | kDoScan, pl, false)) return -1;
+  int64_t total = scan_ws_bytes(pl);
+  if (!pl.live.empty()) {
+    const FlashPlan fp = plan_flash(pl.B, (int)pl.live.size(), pl.T, pl.HD, flash_qtiles_for(args, pl.HD));
+    total += fp.part_bytes;
+  }
+  return total;
 }
 
 int64_t saf_workspace_bytes(int32_t B, int32_t T, int32_t head_dim, int32_t n_scan_heads) {

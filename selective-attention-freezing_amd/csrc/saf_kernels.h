@@ -13,6 +13,14 @@ constexpr int kMaxHeads = 128;
 // dtype codes shared with the C-ABI (saf_attn.h)
 enum : int { kF32 = 0, kF16 = 1, kBF16 = 2, kI32 = 3 };
 
+// Causal load balancing of the live-head kernel: the per-head work list
+// holds (query block, key segment) items, heaviest first; query blocks whose
+// key range spans several segments write fp32 partials that a combine kernel
+// merges.  Limits keep the parameter block under the 4 KiB kernel-argument
+// budget.
+constexpr int kMaxItems = 384;
+constexpr int kMaxQblk = 256;
+
 // Live heads (state 0).
 struct FlashParams {
   const void* q;
@@ -31,6 +39,28 @@ struct FlashParams {
   int16_t q_head[kMaxHeads];
   int16_t k_head[kMaxHeads];
   int16_t v_head[kMaxHeads];
+  // work list (n_items == 0: one item per query block, heaviest first)
+  int n_items;
+  int seg_len;          // key blocks (of 64 keys) per segment
+  int n_part_per_head;  // partial slots per (batch, live head)
+  float* part_o;        // [bh][part][BM][HD] unnormalised O (fp32)
+  float* part_ml;       // [bh][part][2][BM]: running max (base 2), row sum
+  int32_t items[kMaxItems];      // (qb << 8) | segment
+  int16_t part_base[kMaxQblk];   // first partial slot of a split query block, -1 if not split
+};
+
+// Merge of split query blocks: out = sum_s 2^(m_s - M) O_s / sum_s 2^(m_s - M) l_s.
+struct CombineParams {
+  void* out;
+  float* lse;
+  int64_t o_sb, o_sh, o_st;
+  int64_t l_sb, l_sh, l_st;
+  int B, T, n_slots, BM, seg_len, n_part_per_head, n_split;
+  const float* part_o;
+  const float* part_ml;
+  int16_t out_head[kMaxHeads];
+  int16_t split_qb[kMaxQblk];    // split query blocks
+  int16_t part_base[kMaxQblk];   // indexed by query block
 };
 
 // Frozen heads whose pattern is applied as an MFMA P.V product: dense
@@ -86,6 +116,7 @@ inline int scan_chunk_rows(int hd) { return hd <= 64 ? 32 * 16 : 16 * 16; }
 
 // Launchers: return hipSuccess or the launch error.  dtype is kBF16 / kF16.
 hipError_t launch_flash(const FlashParams& p, int dtype, int hd, int qt, hipStream_t s);
+hipError_t launch_flash_combine(const CombineParams& p, int dtype, int hd, hipStream_t s);
 hipError_t launch_frozen_pv(const FrozenParams& p, int dtype, int hd, int mode, hipStream_t s);
 hipError_t launch_scan(const ScanParams& p, int dtype, int hd, hipStream_t s);
 hipError_t launch_zero_u32(uint32_t* ptr, int64_t n, hipStream_t s);

@@ -22,8 +22,8 @@ _DTYPE_CODE = {torch.float32: SAF_F32, torch.float16: SAF_F16,
 # Exported symbols, in header order (checked by the CPU test suite).
 EXPORTS = ("saf_mixed_attn_fwd", "saf_flash_fwd", "saf_frozen_dense_pv_fwd",
            "saf_frozen_decomp_fwd", "saf_frozen_scan_fwd", "saf_frozen_pv_fwd",
-           "saf_workspace_bytes", "saf_workspace_error", "saf_last_error",
-           "saf_version")
+           "saf_workspace_bytes", "saf_mixed_attn_workspace_bytes",
+           "saf_workspace_error", "saf_last_error", "saf_version")
 
 
 class SafTensor(ctypes.Structure):
@@ -80,6 +80,8 @@ def lib():
         L.saf_frozen_pv_fwd.restype = ctypes.c_int
         L.saf_workspace_bytes.argtypes = [ctypes.c_int32] * 4
         L.saf_workspace_bytes.restype = ctypes.c_int64
+        L.saf_mixed_attn_workspace_bytes.argtypes = [P(SafMixedAttnArgs)]
+        L.saf_mixed_attn_workspace_bytes.restype = ctypes.c_int64
         L.saf_workspace_error.argtypes = [ctypes.c_void_p, ctypes.c_void_p, P(ctypes.c_int32)]
         L.saf_workspace_error.restype = ctypes.c_int
         L.saf_last_error.argtypes = []

@@ -293,11 +293,6 @@ def fused_mixed_attn(q, k, v, patt, frozen, hidx=None, pidx=None,
     if ck is not None:
         n_scan = int(((frozen_h == 2) & (ck != 0)).sum())
     L = _ext.lib()
-    ws = None
-    ws_bytes = 0
-    if n_scan:
-        ws_bytes = int(L.saf_workspace_bytes(B, T, HD, n_scan))
-        ws = torch.empty(ws_bytes, dtype=torch.uint8, device=v.device)
 
     need_dec = alpha is not None and bool(
         ((frozen_h == 2) & ((ck == 0) if ck is not None else True)).any())
@@ -319,9 +314,14 @@ def fused_mixed_attn(q, k, v, patt, frozen, hidx=None, pidx=None,
     args.frozen, args.hidx, args.pidx, args.kvidx, args.closed_kind = keep[:5]
     args.closed_param = keep[5]
     args.sm_scale = float(sm_scale)
+    args.flash_qtiles = int(flash_qtiles)
+    # scan look-back words + partials of the causally balanced live-head kernel
+    ws_bytes = int(L.saf_mixed_attn_workspace_bytes(args))
+    if ws_bytes < 0:
+        _ext.check(L.saf_mixed_attn_fwd(args, None))  # raises with the validation message
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=v.device) if ws_bytes else None
     args.workspace = None if ws is None else ws.data_ptr()
     args.workspace_bytes = ws_bytes
-    args.flash_qtiles = int(flash_qtiles)
 
     def run():
         stream = _ext.current_stream_ptr(v.device)

@@ -179,6 +179,29 @@ def test_closed_form_with_all_kinds_and_lse():
              closed={0: ("mean", 0), 1: ("decay", 0.03), 2: ("window", 256)}, check_lse=True)
 
 
+@pytest.mark.parametrize("B,H,T,hd,qt", [(1, 2, 4096, 64, 2), (1, 3, 3000, 128, 1), (2, 2, 2500, 64, 1),
+                                         (1, 1, 8192, 32, 2)])
+def test_causal_split_of_long_query_blocks(B, H, T, hd, qt):
+    """Few heads at long T: the live-head kernel splits the heaviest query
+    blocks into key segments and merges the fp32 partials (values and LSE)."""
+    import kernel
+    q, k, v = qkv(B, H, T, hd, seed=T + H, dtype=torch.bfloat16)
+    frozen = torch.zeros(H, dtype=torch.int32)
+    lse = torch.empty(B, H, T, device=DEV, dtype=torch.float32)
+    y = kernel.fused_mixed_attn(q.to(DEV), k.to(DEV), v.to(DEV), None, frozen.to(DEV), lse=lse,
+                                flash_qtiles=qt)
+    torch.cuda.synchronize()
+    ref = orc.eager_mixed_attention(f64(q), f64(k), f64(v), frozen.numpy())
+    compare(y, ref, what=f"split B{B} H{H} T{T} hd{hd} qt{qt}")
+    for h in range(H):
+        qh, kh = f64(q[0, h]), f64(k[0, h])
+        s = (qh @ kh.T) * scale_of(hd) * np.log2(np.e)
+        s = np.where(np.tril(np.ones((T, T), dtype=bool)), s, -np.inf)
+        m = s.max(-1)
+        ref_lse = m + np.log2(np.exp2(s - m[:, None]).sum(-1))
+        assert np.abs(lse[0, h].cpu().numpy() - ref_lse).max() < 2e-2
+
+
 def test_gqa_kvidx():
     """Qwen-style map: 14 query heads over 2 KV heads, frozen query heads read
     the shared V of their group (qwen/kernel/fused_attn.py:254-259)."""
