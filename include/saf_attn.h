@@ -116,6 +116,15 @@ int saf_frozen_scan_fwd(const saf_mixed_attn_args* args, void* stream);
 int saf_frozen_pv_fwd(const saf_tensor_t* patt, const saf_tensor_t* v, const int32_t* fz_idx,
                       int32_t nf, int32_t T, const saf_tensor_t* out, void* stream);
 
+/* Rotary embedding of the live-head q (B, Uq, T, HD) and k (B, Uk, T, HD), in
+ * place (the two may be interleaved views of one projection output): Llama
+ * half rotation with the (T', HD) cos/sin caches (fp32, bf16 or fp16),
+ * positions 0..T-1, fp32 arithmetic, one rounding to the activation dtype.
+ * Replaces apply_rotary_pos_emb (nanogpt/model.py:63-68) on the fused
+ * path (:1007-1008). */
+int saf_rope_qk_inplace(const saf_tensor_t* q, const saf_tensor_t* k, const saf_tensor_t* cos,
+                        const saf_tensor_t* sin, void* stream);
+
 /* Workspace needed by saf_frozen_scan_fwd for n_scan_heads closed-form heads
  * (0 bytes when there are none). */
 int64_t saf_workspace_bytes(int32_t B, int32_t T, int32_t head_dim, int32_t n_scan_heads);

@@ -521,6 +521,44 @@ int saf_frozen_pv_fwd(const saf_tensor_t* patt, const saf_tensor_t* v, const int
   return run_dense(*patt, *v, *out, B, T, HD, v->dtype, oh, vh, ph, reinterpret_cast<hipStream_t>(stream));
 }
 
+int saf_rope_qk_inplace(const saf_tensor_t* q, const saf_tensor_t* k, const saf_tensor_t* cos,
+                        const saf_tensor_t* sin, void* stream) {
+  if (q == nullptr || k == nullptr || cos == nullptr || sin == nullptr)
+    return fail(SAF_EINVAL, "q, k, cos and sin are required");
+  if (!present(*q) || !present(*k) || !present(*cos) || !present(*sin))
+    return fail(SAF_EINVAL, "q, k, cos and sin must be device tensors");
+  if (q->ndim != 4 || k->ndim != 4) return fail(SAF_EINVAL, "q and k must be 4-D (B, U, T, HD)");
+  if (q->dtype != k->dtype) return fail(SAF_EINVAL, "q and k must share a dtype");
+  if (q->dtype != SAF_BF16 && q->dtype != SAF_F16)
+    return fail(SAF_EUNSUPPORTED, "rope: unsupported q/k dtype %s (bf16 or fp16)", dtype_name(q->dtype));
+  const int64_t B = q->size[0], T = q->size[2], hd = q->size[3];
+  if (k->size[0] != B || k->size[2] != T || k->size[3] != hd)
+    return fail(SAF_EINVAL, "q and k batch, sequence and head dimensions must match");
+  if (!supported_hd(hd)) return fail(SAF_EUNSUPPORTED, "head_dim %lld is not supported (32, 64, 96, 128)", (long long)hd);
+  const saf_tensor_t* cs[2] = {cos, sin};
+  for (int i = 0; i < 2; ++i) {
+    const saf_tensor_t& t = *cs[i];
+    if (t.ndim != 2 || t.size[0] < T || t.size[1] != hd)
+      return fail(SAF_EINVAL, "cos/sin must be (T', HD) caches with T' >= T");
+    if (t.dtype != SAF_F32 && t.dtype != SAF_BF16 && t.dtype != SAF_F16)
+      return fail(SAF_EUNSUPPORTED, "rope: unsupported cache dtype %s", dtype_name(t.dtype));
+    if (t.stride[1] != 1 || (t.stride[0] * elem_size(t.dtype)) % 16 || reinterpret_cast<uintptr_t>(t.data) % 16)
+      return fail(SAF_EALIGN, "cos/sin rows must be contiguous and 16-byte aligned");
+  }
+  if (cos->dtype != sin->dtype) return fail(SAF_EINVAL, "cos and sin must share a dtype");
+  if (int rc = check_act(*q, "q", 16)) return rc;
+  if (int rc = check_act(*k, "k", 16)) return rc;
+  RopeParams p{};
+  p.q = q->data; p.k = k->data;
+  p.q_sb = q->stride[0]; p.q_sh = q->stride[1]; p.q_st = q->stride[2];
+  p.k_sb = k->stride[0]; p.k_sh = k->stride[1]; p.k_st = k->stride[2];
+  p.cos = cos->data; p.sin = sin->data;
+  p.cs_st = cos->stride[0]; p.sn_st = sin->stride[0];
+  p.cs_dtype = cos->dtype;
+  p.B = (int)B; p.Uq = (int)q->size[1]; p.Uk = (int)k->size[1]; p.T = (int)T; p.hd = (int)hd;
+  return launched(launch_rope(p, q->dtype, reinterpret_cast<hipStream_t>(stream)), "rope");
+}
+
 int64_t saf_mixed_attn_workspace_bytes(const saf_mixed_attn_args* args) {
   Plan pl;
   if (plan_and_validate(args, kDoFlash | kDoScan, pl, false)) return -1;

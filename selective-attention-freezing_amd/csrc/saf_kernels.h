@@ -111,6 +111,19 @@ struct ScanParams {
   float param[kMaxHeads];  // decay rate (> 0) or window length
 };
 
+// In-place rotary embedding of the live-head q and k.
+struct RopeParams {
+  void* q;
+  void* k;
+  int64_t q_sb, q_sh, q_st;
+  int64_t k_sb, k_sh, k_st;
+  const void* cos;
+  const void* sin;
+  int64_t cs_st, sn_st;  // row strides of the (T', hd) caches
+  int cs_dtype;
+  int B, Uq, Uk, T, hd;
+};
+
 // Rows of one scan chunk for a head dimension (must match the kernel).
 inline int scan_chunk_rows(int hd) { return hd <= 64 ? 32 * 16 : 16 * 16; }
 
@@ -120,6 +133,7 @@ hipError_t launch_flash_combine(const CombineParams& p, int dtype, int hd, hipSt
 hipError_t launch_frozen_pv(const FrozenParams& p, int dtype, int hd, int mode, hipStream_t s);
 hipError_t launch_scan(const ScanParams& p, int dtype, int hd, hipStream_t s);
 hipError_t launch_zero_u32(uint32_t* ptr, int64_t n, hipStream_t s);
+hipError_t launch_rope(const RopeParams& p, int dtype, hipStream_t s);
 
 // Queries per flash / frozen workgroup for a query-tile count.
 inline int block_rows(int qt) { return 4 * 32 * qt; }

@@ -1,0 +1,26 @@
+"""Rotary position embedding of the live-head Q/K, fused into one HIP kernel.
+
+The reference applies ``apply_rotary_pos_emb`` (/root/reference/nanogpt/model.py:63-68)
+to the compact live-head q/k of the fused path (:1007-1008) as a chain of
+elementwise torch ops.  ``rope_qk_`` does the same rotation in place, in one
+pass over the projection output (libsafattn.so ``saf_rope_qk_inplace``):
+fp32 arithmetic with the model's cos/sin cache, one rounding to the activation
+dtype.  Forward only (the operators of this build have no backward).
+"""
+import torch
+
+from . import _ext
+
+
+def rope_qk_(q, k, cos, sin):
+    """Rotate q (B, Uq, T, hd) and k (B, Uk, T, hd) in place; cos/sin are the
+    (T', hd) caches (any leading singleton dims are squeezed).  Returns (q, k)."""
+    if not q.is_cuda:
+        raise RuntimeError("rope_qk_ runs on HIP devices only (got a CPU tensor)")
+    cos2 = cos.reshape(-1, cos.size(-1))
+    sin2 = sin.reshape(-1, sin.size(-1))
+    L = _ext.lib()
+    rc = L.saf_rope_qk_inplace(_ext.tensor_desc(q), _ext.tensor_desc(k), _ext.tensor_desc(cos2),
+                               _ext.tensor_desc(sin2), _ext.current_stream_ptr(q.device))
+    _ext.check(rc)
+    return q, k

@@ -281,20 +281,24 @@ class CausalSelfAttention(nn.Module):
         return super().train(mode)
 
     def _infer_weight_cache(self):
-        """[Wq[live]; Wk[live]] gathered once per weight version / freeze change
-        (nanogpt/model.py:920-944)."""
-        qw, kw = self.q_proj.weight, self.k_proj.weight
-        key = (qw._version, kw._version, qw.data_ptr(), kw.data_ptr())
+        """[Wq[live]; Wk[live]; Wv] gathered once per weight version / freeze
+        change, so inference runs ONE projection GEMM for Q/K of the live heads
+        and V of every head (nanogpt/model.py:920-944 keeps V in its own GEMM)."""
+        qw, kw, vw = self.q_proj.weight, self.k_proj.weight, self.v_proj.weight
+        key = tuple((w._version, w.data_ptr()) for w in (qw, kw, vw))
         if self._wc_key != key:
             uf = self._uf_cols
-            if uf is not None:
-                self._wc_qk = torch.cat([qw.index_select(0, uf), kw.index_select(0, uf)]).detach()
-                self._wc_qkb = None if self.q_proj.bias is None else torch.cat(
-                    [self.q_proj.bias.index_select(0, uf), self.k_proj.bias.index_select(0, uf)]).detach()
+            ws = [vw] if uf is None else [qw.index_select(0, uf), kw.index_select(0, uf), vw]
+            self._wc_qkv = torch.cat(ws).detach()
+            if self.q_proj.bias is None:
+                self._wc_qkvb = None
             else:
-                self._wc_qk = self._wc_qkb = None
+                bs = [self.v_proj.bias] if uf is None else [
+                    self.q_proj.bias.index_select(0, uf), self.k_proj.bias.index_select(0, uf),
+                    self.v_proj.bias]
+                self._wc_qkvb = torch.cat(bs).detach()
             self._wc_key = key
-        return self._wc_qk, self._wc_qkb
+        return self._wc_qkv, self._wc_qkvb
 
     def forward(self, x, rope=None):
         global _FUSED_DISPATCH_COUNT
@@ -303,23 +307,35 @@ class CausalSelfAttention(nn.Module):
         B, T, C = x.size()
         nh, hd = self.n_head, self.head_dim
         nuf = nh - self._n_frozen
-        v = self.v_proj(x).view(B, T, nh, hd).transpose(1, 2)
         hidx = self._hidx_i32
-        if nuf == 0:
-            qu = ku = v[:, :0]
-        else:
-            if torch.is_grad_enabled():
+        if torch.is_grad_enabled():
+            v = self.v_proj(x).view(B, T, nh, hd).transpose(1, 2)
+            if nuf == 0:
+                qu = ku = v[:, :0]
+            else:
                 qk = _kernel_mod.linear_rows2(x, self.q_proj.weight, self.k_proj.weight,
                                               self.q_proj.bias, self.k_proj.bias, self._uf_cols)
+                qk = qk.view(B, T, 2, nuf, hd)
+                qu, ku = qk[:, :, 0].transpose(1, 2), qk[:, :, 1].transpose(1, 2)
+                if self.position_encoding == "rope":
+                    if rope is None:
+                        raise ValueError("RoPE Q/K requested without a rotary cache")
+                    qu, ku = apply_rotary_pos_emb(qu, ku, *rope)
+        else:
+            # one GEMM for live Q/K and every V; RoPE rotates Q/K in place
+            w, wb = self._infer_weight_cache()
+            qkv = F.linear(x, w, wb)
+            nqk = 2 * nuf * hd
+            v = qkv[..., nqk:].view(B, T, nh, hd).transpose(1, 2)
+            if nuf == 0:
+                qu = ku = v[:, :0]
             else:
-                wqk, wqkb = self._infer_weight_cache()
-                qk = F.linear(x, wqk, wqkb)
-            qk = qk.view(B, T, 2, nuf, hd)
-            qu, ku = qk[:, :, 0].transpose(1, 2), qk[:, :, 1].transpose(1, 2)
-            if self.position_encoding == "rope":
-                if rope is None:
-                    raise ValueError("RoPE Q/K requested without a rotary cache")
-                qu, ku = apply_rotary_pos_emb(qu, ku, *rope)
+                qk = qkv[..., :nqk].view(B, T, 2, nuf, hd)
+                qu, ku = qk[:, :, 0].transpose(1, 2), qk[:, :, 1].transpose(1, 2)
+                if self.position_encoding == "rope":
+                    if rope is None:
+                        raise ValueError("RoPE Q/K requested without a rotary cache")
+                    _kernel_mod.rope_qk_(qu, ku, *rope)
         _FUSED_DISPATCH_COUNT += 1
         dec = self._dec_any
         y = fused_mixed_attn(qu, ku, v, self.dyn_pattern, self._fz_mask_i32, hidx,
