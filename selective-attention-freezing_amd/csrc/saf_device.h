@@ -44,6 +44,7 @@ constexpr float kLog2e = 1.4426950408889634f;  // 1 / ln(2)
 template <typename T> struct Elem;
 
 template <> struct Elem<__bf16> {
+  static constexpr bool is_bf16 = true;
   __device__ static inline f32x16_t mfma(uint4 a, uint4 b, f32x16_t c) {
     return __builtin_amdgcn_mfma_f32_32x32x16_bf16(
         __builtin_bit_cast(bf16x8_t, a), __builtin_bit_cast(bf16x8_t, b), c, 0, 0, 0);
@@ -65,6 +66,7 @@ template <> struct Elem<__bf16> {
 };
 
 template <> struct Elem<_Float16> {
+  static constexpr bool is_bf16 = false;
   __device__ static inline f32x16_t mfma(uint4 a, uint4 b, f32x16_t c) {
     return __builtin_amdgcn_mfma_f32_32x32x16_f16(
         __builtin_bit_cast(f16x8_t, a), __builtin_bit_cast(f16x8_t, b), c, 0, 0, 0);

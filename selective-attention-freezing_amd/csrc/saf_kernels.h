@@ -74,6 +74,7 @@ struct FrozenParams {
   const void* patt;
   int patt_dtype;
   int patt_vec;  // rows contiguous and aligned for 16/32-byte loads
+  int p_cols;    // S: row length of the pattern buffer
   int64_t p_sh, p_si, p_sj;
   // decomposed buffers (H, S) indexed by the natural head
   const void* alpha;
