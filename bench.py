@@ -13,6 +13,11 @@ Prints ONE JSON line: whole-job prefill tokens/s, the roofline of the
 dominant kernel (live-head flash, bf16 MFMA) measured with HIP events over the
 timed region, and a CPU baseline (the oracle's restatement of the reference's
 CPU path, timed on a bounded sample on this host).
+
+--workload c4 --rate r measures BASELINE.json configs[4] instead: the
+Qwen-style GQA model (transformers Qwen3 modules, random init) with
+round(14 r) query heads per layer frozen to the causal mean, B=4, T=4096,
+one step = backbone prefill to the last hidden state.
 """
 import argparse
 import json
@@ -139,41 +144,100 @@ def cpu_baseline(model, x, plan, T, max_layers=2):
                        f"({t_sample:.2f} s per sample)")}
 
 
-def main():
-    ap = argparse.ArgumentParser()
-    ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=10)
-    ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--seq-len", type=int, default=16384)
-    ap.add_argument("--layers", type=int, default=12)
-    ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--cpu-layers", type=int, default=2)
-    ap.add_argument("--no-timer", action="store_true", help="skip per-kernel HIP events")
-    ap.add_argument("--copy-calibration-mib", type=int, default=0,
-                    help="only run device-to-device copies of this many MiB (the known-size "
-                         "kernel that scales rocprofv3 FETCH_SIZE / WRITE_SIZE readings)")
-    args = ap.parse_args()
-    if args.gpus != 1:
-        print(f"bench.py measures one GPU: this build runs the mixed-head prefill on a single "
-              f"MI355X and has no multi-GPU path (asked for --gpus {args.gpus})", file=sys.stderr)
-        sys.exit(2)
+def c4_cpu_baseline(model, sd, masks, B, T, max_layers=1):
+    """The oracle's restatement of the hybrid Qwen3 split path (fp32, torch CPU)
+    on a bounded sample: `max_layers` layers at B=1 and the full T, plus
+    embedding and final norm, extrapolated linearly to all layers and B."""
+    import torch
+    from oracle import qwen_oracle
 
+    threads = len(os.sched_getaffinity(0))
+    torch.set_num_threads(threads)
+    cfg = model.config
+    mean = torch.ones(T, T).tril_()
+    fr = [{"mask": m.numpy(), "dense": mean.expand(cfg.num_attention_heads, T, T)} for m in masks]
+    ocfg = dict(n_layers=cfg.num_hidden_layers, n_heads=cfg.num_attention_heads,
+                n_kv_heads=cfg.num_key_value_heads, head_dim=cfg.head_dim, eps=cfg.rms_norm_eps,
+                rope_theta=1e6)
+    idx = torch.randint(0, cfg.vocab_size, (1, T), generator=torch.Generator().manual_seed(2))
+    layers = list(range(min(max_layers, cfg.num_hidden_layers)))
+    times = []
+    for it in range(2):
+        t0 = time.perf_counter()
+        qwen_oracle.qwen_forward(sd, ocfg, fr, idx, layers=layers)
+        times.append(time.perf_counter() - t0)
+        log(f"cpu baseline sample {it}: {times[-1]:.2f} s on {threads} threads")
+    t_sample = min(times)
+    t_full = t_sample * cfg.num_hidden_layers / len(layers) * B
+    return {"value": round(B * T / t_full, 3), "unit": "tokens/s", "cores": threads, "kind": "port",
+            "sample": (f"oracle hybrid Qwen3 split-path forward (fp32, torch CPU) of {len(layers)} of "
+                       f"{cfg.num_hidden_layers} layers at B=1 T={T}, best of 2, extrapolated "
+                       f"linearly to all layers and B={B} ({t_sample:.2f} s per sample)")}
+
+
+def timed_steps(step, steps, warmup, use_timer):
+    """Warm up, then time exactly `steps` calls of step() with HIP events
+    (and, unless disabled, per-kernel events of the attention operators)."""
     import torch
     import kernel
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    log(f"warmup done; timing {steps} steps")
+    timer = kernel.KernelTimer() if use_timer else None
+    starts = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
+    ends = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
+    kernel.set_kernel_timer(timer)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for s, e in zip(starts, ends):
+        s.record()
+        step()
+        e.record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    kernel.set_kernel_timer(None)
+    step_ms = [s.elapsed_time(e) for s, e in zip(starts, ends)]
+    return step_ms, wall, (timer.summary() if timer is not None else None)
+
+
+def kernel_rooflines(summ, flash_label, traffic, steps):
+    """Roofline of the live-head flash kernel (bf16 MFMA) plus the frozen-head
+    kernels' HBM figures, from the per-launch HIP event times."""
+    roof, extra = None, {}
+    if summ is None:
+        return roof, extra
+    if "flash" in summ:
+        n, ms, work = summ["flash"]
+        per_launch_ms = ms / n
+        achieved = (work / n) / (per_launch_ms / 1000.0) / 1e12
+        roof = {"bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_BF16_TFLOPS,
+                "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
+                "traffic": traffic,
+                "traffic_source": "profiles/flash_fwd_c2_hbm_traffic.txt" if traffic else None,
+                "kernel": flash_label, "launches": n, "avg_launch_ms": round(per_launch_ms, 4),
+                "flop_per_launch": work // n}
+    if "scan" in summ:
+        n, ms, work = summ["scan"]
+        gbs = (work / n) / (ms / n / 1000.0) / 1e9
+        extra["frozen_scan"] = {"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS,
+                                "unit": "GB/s", "frac": round(gbs / PEAK_HBM_GBS, 4),
+                                "launches": n, "avg_launch_ms": round(ms / n, 4),
+                                "bytes_per_launch": work // n}
+    if "dense" in summ:
+        n, ms, work = summ["dense"]
+        extra["frozen_dense_pv"] = {"launches": n, "avg_launch_ms": round(ms / n, 4),
+                                    "flop_per_launch": work // n}
+    extra["attention_ms_per_step"] = round(sum(v[1] for v in summ.values()) / steps, 3)
+    return roof, extra
+
+
+def run_c2(args):
+    import torch
     from nanogpt import model as model_mod
 
-    if args.copy_calibration_mib:
-        n = args.copy_calibration_mib << 20
-        src = torch.ones(n, dtype=torch.uint8, device="cuda")
-        dst = torch.empty_like(src)
-        for _ in range(5):
-            dst.copy_(src)
-        torch.cuda.synchronize()
-        print(json.dumps({"copy_calibration_bytes": n, "copies": 5}), flush=True)
-        return
-
     dev = "cuda"
-    T = args.seq_len
+    T = args.seq_len or 16384
     log(f"building C2 model T={T} layers={args.layers}")
     model, x, plan = build_c2_model(T, dev, torch.bfloat16, n_layer=args.layers)
     log("model built; verifying dispatch")
@@ -188,53 +252,12 @@ def main():
         calls = model_mod.fused_dispatch_count() - before
         if calls != cfg.n_layer:
             raise RuntimeError(f"dispatch verification failed: {calls} != {cfg.n_layer}")
-        for _ in range(args.warmup):
-            model(x)
-        torch.cuda.synchronize()
+        step_ms, wall, summ = timed_steps(lambda: model(x), args.steps, args.warmup, not args.no_timer)
 
-        log(f"warmup done; timing {args.steps} steps")
-        timer = None if args.no_timer else kernel.KernelTimer()
-        starts = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps)]
-        ends = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps)]
-        kernel.set_kernel_timer(timer)
-        torch.cuda.synchronize()
-        t0 = time.perf_counter()
-        for s, e in zip(starts, ends):
-            s.record()
-            model(x)
-            e.record()
-        torch.cuda.synchronize()
-        wall = time.perf_counter() - t0
-        kernel.set_kernel_timer(None)
-
-    step_ms = [s.elapsed_time(e) for s, e in zip(starts, ends)]
     total_ms = sum(step_ms)
     tok_s = x.numel() * args.steps / (total_ms / 1000.0)
-
-    roof = None
-    extra = {}
-    if timer is not None:
-        summ = timer.summary()
-        if "flash" in summ:
-            n, ms, work = summ["flash"]
-            per_launch_ms = ms / n
-            achieved = (work / n) / (per_launch_ms / 1000.0) / 1e12
-            label = "flash_fwd_kernel<bf16,64,2>"
-            roof = {"bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_BF16_TFLOPS,
-                    "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
-                    "traffic": pmc_traffic(label) if T == 16384 else None,
-                    "traffic_source": "profiles/flash_fwd_c2_hbm_traffic.txt", "kernel": label,
-                    "launches": n, "avg_launch_ms": round(per_launch_ms, 4),
-                    "flop_per_launch": work // n}
-        if "scan" in summ:
-            n, ms, work = summ["scan"]
-            gbs = (work / n) / (ms / n / 1000.0) / 1e9
-            extra["frozen_scan"] = {"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS,
-                                    "unit": "GB/s", "frac": round(gbs / PEAK_HBM_GBS, 4),
-                                    "launches": n, "avg_launch_ms": round(ms / n, 4),
-                                    "bytes_per_launch": work // n}
-        extra["attention_ms_per_step"] = round(sum(v[1] for v in summ.values()) / args.steps, 3)
-
+    label = "flash_fwd_kernel<bf16,64,2>"
+    roof, extra = kernel_rooflines(summ, label, pmc_traffic(label) if T == 16384 else None, args.steps)
     log(f"GPU: {tok_s:.0f} tokens/s, {total_ms / args.steps:.2f} ms/step")
     cpu = None
     if not args.no_cpu_baseline:
@@ -256,6 +279,123 @@ def main():
     }
     line.update(extra)
     print(json.dumps(line), flush=True)
+
+
+def run_c4(args):
+    """Qwen-style GQA (24 layers, hidden 896, 14 query /
+    2 KV heads, head_dim 64, RoPE theta 1e6), bf16 random init, B=4, T=4096;
+    round(rate * 14) query heads per layer frozen to the causal mean.  One step
+    = backbone prefill to the last hidden state (bench_qwen_prefill_triton.py
+    of the reference)."""
+    import torch
+    import qwen
+
+    dev = "cuda"
+    T = args.seq_len or 4096
+    B = args.batch or 4
+    cfg = qwen.qwen_config(n_layers=args.layers or 24, max_positions=max(T, 4096))
+    log(f"building C4 model B={B} T={T} rate={args.rate} prior={args.prior_repr}")
+    model = qwen.build_model(cfg, device=dev, dtype=torch.bfloat16, seed=1337)
+    use_sdpa = args.rate == 0 and args.sdpa_live
+    masks = qwen.nested_head_masks(args.rate, cfg.num_hidden_layers, cfg.num_attention_heads)
+    sd = None
+    if not args.no_cpu_baseline:   # the oracle reads the unconverted parameter names
+        sd = {k: v.detach().float().cpu() for k, v in model.state_dict().items()
+              if not k.startswith("lm_head")}
+    if not use_sdpa:
+        _, masks = qwen.convert_with_rate(model, args.rate, T, repr=args.prior_repr,
+                                          fuse_live_only=args.rate == 0)
+    f = int(masks[0].sum())
+    H, L, hd = cfg.num_attention_heads, cfg.num_hidden_layers, cfg.head_dim
+    ids = torch.randint(0, 151643, (B, T), generator=torch.Generator().manual_seed(1337)).to(dev)
+    backbone = model.model
+    with torch.inference_mode():
+        n0 = qwen.fused_dispatch_count()
+        qwen.backbone_forward(backbone, ids)
+        torch.cuda.synchronize()
+        calls = qwen.fused_dispatch_count() - n0
+        if calls != (0 if use_sdpa else L):
+            raise RuntimeError(f"dispatch verification failed: {calls} fused calls for {L} layers")
+        step_ms, wall, summ = timed_steps(lambda: qwen.backbone_forward(backbone, ids), args.steps,
+                                          args.warmup, not args.no_timer and not use_sdpa)
+    total_ms = sum(step_ms)
+    tok_s = B * T * args.steps / (total_ms / 1000.0)
+    roof, extra = kernel_rooflines(summ, "flash_fwd_kernel<bf16,64,2>", None, args.steps)
+    log(f"GPU: {tok_s:.0f} tokens/s, {total_ms / args.steps:.2f} ms/step")
+    cpu = None
+    if not args.no_cpu_baseline:
+        cpu = c4_cpu_baseline(model, sd, masks, B, T, max_layers=args.cpu_layers)
+    attn = "torch SDPA for every head (unconverted model)" if use_sdpa else (
+        f"fused HIP path, frozen heads as {args.prior_repr} priors"
+        + (" (closed-form mean scan)" if args.prior_repr == "decomposed" else " (dense P.V)"))
+    line = {
+        "metric": "prefill tokens/sec (1 GPU), Qwen-style GQA with frozen query heads",
+        "value": round(tok_s, 1), "unit": "tokens/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(total_ms / args.steps, 3),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+        "data": "synthetic (random-init weights seed 1337, uniform random tokens)",
+        "config": {"workload": f"C4: Qwen3-style GQA {L}L hidden 896 14q/2kv hd 64, B={B}, T={T}, "
+                               f"{f}/{H} query heads frozen per layer (rate {args.rate}); {attn}",
+                   "batch": B, "seq_len": T, "frozen_per_layer": f, "live_per_layer": H - f,
+                   "live_flops": (H - f) * L * B * 4 * hd * T * (T + 1) // 2,
+                   "frozen_bytes": f * L * B * 2 * T * hd * 2,
+                   "median_step_ms": round(statistics.median(step_ms), 3),
+                   "wall_s": round(wall, 3)},
+        "roofline": roof,
+        "cpu_baseline": cpu,
+    }
+    line.update(extra)
+    print(json.dumps(line), flush=True)
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=10)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--workload", choices=["c2", "c4"], default="c2",
+                    help="c2: 124M nanoGPT SAF-25%% at 16K (the headline); c4: Qwen-style GQA")
+    ap.add_argument("--seq-len", type=int, default=None)
+    ap.add_argument("--batch", type=int, default=None, help="c4 only (default 4)")
+    ap.add_argument("--layers", type=int, default=None)
+    ap.add_argument("--rate", type=float, default=0.25, help="c4: frozen fraction of query heads")
+    ap.add_argument("--prior-repr", choices=["decomposed", "dense"], default="decomposed",
+                    help="c4: causal-mean prior as alpha = rho = 0 (scan) or a dense (T, T) pattern")
+    ap.add_argument("--sdpa-live", action="store_true",
+                    help="c4 at rate 0: leave the model unconverted (torch SDPA) instead of the HIP flash path")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-layers", type=int, default=None)
+    ap.add_argument("--no-timer", action="store_true", help="skip per-kernel HIP events")
+    ap.add_argument("--copy-calibration-mib", type=int, default=0,
+                    help="only run device-to-device copies of this many MiB (the known-size "
+                         "kernel that scales rocprofv3 FETCH_SIZE / WRITE_SIZE readings)")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU: this build runs the mixed-head prefill on a single "
+              f"MI355X and has no multi-GPU path (asked for --gpus {args.gpus})", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+
+    if args.copy_calibration_mib:
+        n = args.copy_calibration_mib << 20
+        src = torch.ones(n, dtype=torch.uint8, device="cuda")
+        dst = torch.empty_like(src)
+        for _ in range(5):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_calibration_bytes": n, "copies": 5}), flush=True)
+        return
+    if args.workload == "c4":
+        if args.cpu_layers is None:
+            args.cpu_layers = 1
+        run_c4(args)
+    else:
+        if args.layers is None:
+            args.layers = 12
+        if args.cpu_layers is None:
+            args.cpu_layers = 2
+        run_c2(args)
 
 
 if __name__ == "__main__":

@@ -125,6 +125,16 @@ int saf_frozen_pv_fwd(const saf_tensor_t* patt, const saf_tensor_t* v, const int
 int saf_rope_qk_inplace(const saf_tensor_t* q, const saf_tensor_t* k, const saf_tensor_t* cos,
                         const saf_tensor_t* sin, void* stream);
 
+/* Qwen3 attention prologue on the live-head q (B, Uq, T, HD) and the raw key
+ * heads k (B, HKV, T, HD), in place: per-head RMSNorm over HD with the
+ * (HD,) weights (fp32 statistics, x <- w * round(x * rsqrt(mean(x^2) + eps))
+ * rounded to the activation dtype, as Qwen3RMSNorm), then the rotation of
+ * saf_rope_qk_inplace.  Replaces q_norm / k_norm + apply_rotary_pos_emb of the
+ * Qwen3 fused branch (qwen/nanogpt/hybrid_prior_attention.py:543-572). */
+int saf_qk_rmsnorm_rope_inplace(const saf_tensor_t* q, const saf_tensor_t* k, const saf_tensor_t* q_weight,
+                                const saf_tensor_t* k_weight, float eps, const saf_tensor_t* cos,
+                                const saf_tensor_t* sin, void* stream);
+
 /* Workspace needed by saf_frozen_scan_fwd for n_scan_heads closed-form heads
  * (0 bytes when there are none). */
 int64_t saf_workspace_bytes(int32_t B, int32_t T, int32_t head_dim, int32_t n_scan_heads);

@@ -1,0 +1,110 @@
+"""CPU restatement of the hybrid Qwen3 backbone forward (torch fp32).
+
+TEST INFRASTRUCTURE ONLY: the model-level checker of the HIP path for the
+GQA caller.  Only tests/, __graft_entry__.smoke() and bench.py's
+cpu_baseline leg may use it.
+
+Works on a plain state dict with transformers' Qwen3 parameter names and
+restates, without importing any model class:
+  transformers modeling_qwen3 (the installed 5.15.0; the reference pins
+  5.2.0, /root/reference/requirements.txt:7): RMSNorm in fp32 with eps,
+  per-head q_norm / k_norm before RoPE, default RoPE (inv_freq =
+  theta^(-2i/hd), cos/sin of cat(freqs, freqs)), GQA by repeating KV heads,
+  SiLU-gated MLP, pre-norm residual blocks, final norm -> last hidden state;
+  the split path of the reference's hybrid Qwen3 attention
+  (/root/reference/qwen/nanogpt/hybrid_prior_attention.py:586-640): live heads
+  through causal softmax attention with scale hd^-0.5, frozen query heads as
+  P @ V of their KV group, P the dense prior tril'ed and row-renormalised
+  (:146-152) or exp(alpha[j] + rho[i-j] - z[i]) for decomposed priors
+  (:128-140, :187-194).
+Pinned by tests/golden/qwen_forward_small.npz, written by the reference's own
+adapter on CPU (tests/golden/make_golden_qwen.py).
+"""
+import math
+
+import numpy as np
+import torch
+import torch.nn.functional as F
+
+from . import saf_oracle as orc
+
+
+def rms_norm(x, w, eps):
+    x = x.float()
+    return w * (x * torch.rsqrt(x.pow(2).mean(-1, keepdim=True) + eps))
+
+
+def rope_cache(hd, T, theta):
+    inv = 1.0 / (theta ** (torch.arange(0, hd, 2, dtype=torch.int64).float() / hd))
+    freqs = torch.outer(torch.arange(T, dtype=torch.float32), inv)
+    emb = torch.cat((freqs, freqs), dim=-1)
+    return emb.cos(), emb.sin()
+
+
+def _rot(x):
+    x1, x2 = x.chunk(2, dim=-1)
+    return torch.cat((-x2, x1), dim=-1)
+
+
+def apply_rope(x, cos, sin):
+    return x * cos + _rot(x) * sin
+
+
+def dense_prior(p, dtype=torch.float32):
+    """tril + row renormalisation of a dense prior (:146-152)."""
+    p = p.to(dtype).tril()
+    return p / p.sum(-1, keepdim=True).clamp_min(torch.finfo(dtype).tiny)
+
+
+def frozen_patterns(fr, T):
+    """(n_pattern, T, T) fp32 priors of a layer's frozen heads in ascending
+    head order.  fr: {"mask": (H,) bool, "dense": (H, S, S)} or
+    {"mask": ..., "alpha": (H, S), "rho": (H, S)}."""
+    heads = [h for h in range(len(fr["mask"])) if fr["mask"][h]]
+    if "dense" in fr:
+        return dense_prior(torch.from_numpy(np.asarray(fr["dense"])[heads]).float())[:, :T, :T]
+    a = np.asarray(fr["alpha"], dtype=np.float64)[heads]
+    r = np.asarray(fr["rho"], dtype=np.float64)[heads]
+    z = orc.decomposed_logz(a, r)
+    return torch.from_numpy(np.nan_to_num(orc.decomp_pattern(a, r, z, T), nan=0.0)).float()
+
+
+def attention(x, sd, p, cfg, fr, cos, sin):
+    B, T, _ = x.shape
+    H, HKV, hd, eps = cfg["n_heads"], cfg["n_kv_heads"], cfg["head_dim"], cfg["eps"]
+    lin = lambda name, t: F.linear(t, sd[p + name + ".weight"], sd.get(p + name + ".bias"))
+    q = rms_norm(lin("q_proj", x).view(B, T, H, hd), sd[p + "q_norm.weight"], eps).transpose(1, 2)
+    k = rms_norm(lin("k_proj", x).view(B, T, HKV, hd), sd[p + "k_norm.weight"], eps).transpose(1, 2)
+    v = lin("v_proj", x).view(B, T, HKV, hd).transpose(1, 2)
+    q, k = apply_rope(q, cos, sin), apply_rope(k, cos, sin)
+    g = H // HKV
+    k = k.repeat_interleave(g, dim=1)
+    v = v.repeat_interleave(g, dim=1)
+    att = (q @ k.transpose(-2, -1)) * (1.0 / math.sqrt(hd))
+    causal = torch.tril(torch.ones(T, T, dtype=torch.bool))
+    att = att.masked_fill(~causal, float("-inf")).softmax(-1)
+    if fr is not None and bool(np.any(fr["mask"])):
+        heads = [h for h in range(H) if fr["mask"][h]]
+        att[:, heads] = frozen_patterns(fr, T).unsqueeze(0).expand(B, -1, -1, -1)
+    y = (att @ v).transpose(1, 2).reshape(B, T, H * hd)
+    return lin("o_proj", y)
+
+
+@torch.no_grad()
+def qwen_forward(sd, cfg, freeze, idx, layers=None):
+    """Last hidden state (B, T, hidden) of the hybrid Qwen3 backbone.
+
+    sd: float32 state dict (transformers names); cfg: dict with n_layers,
+    n_heads, n_kv_heads, head_dim, eps, rope_theta; freeze: per-layer records
+    for frozen_patterns() or None; layers: run only these layer indices."""
+    x = sd["model.embed_tokens.weight"][idx].float()
+    T = idx.size(1)
+    cos, sin = rope_cache(cfg["head_dim"], T, cfg["rope_theta"])
+    for l in (range(cfg["n_layers"]) if layers is None else layers):
+        p = f"model.layers.{l}."
+        h = rms_norm(x, sd[p + "input_layernorm.weight"], cfg["eps"])
+        x = x + attention(h, sd, p + "self_attn.", cfg, None if freeze is None else freeze[l], cos, sin)
+        h = rms_norm(x, sd[p + "post_attention_layernorm.weight"], cfg["eps"])
+        m = F.silu(F.linear(h, sd[p + "mlp.gate_proj.weight"])) * F.linear(h, sd[p + "mlp.up_proj.weight"])
+        x = x + F.linear(m, sd[p + "mlp.down_proj.weight"])
+    return rms_norm(x, sd["model.norm.weight"], cfg["eps"])

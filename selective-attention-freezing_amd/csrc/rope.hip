@@ -9,22 +9,65 @@
 // the reference's chain of elementwise ops (mul, neg, cat, mul, add per
 // tensor).  A thread owns one chunk pair: 8 columns of the first half and the
 // matching 8 columns of the second half of one row, loaded as 16-byte words.
+// The same kernel optionally applies the Qwen3 per-head q/k RMSNorm first.
 #include "saf_kernels.h"
 
 namespace saf {
 
+// Eight consecutive elements of a cos/sin cache row or a norm weight, as fp32.
+template <typename H>
+__device__ inline void load8_16(const void* src, float (&e)[8]) {
+  const uint4 w = *reinterpret_cast<const uint4*>(src);
+  const uint32_t w4[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+  for (int m = 0; m < 4; ++m) {
+    e[2 * m] = Elem<H>::lo(w4[m]);
+    e[2 * m + 1] = Elem<H>::hi(w4[m]);
+  }
+}
+
+__device__ inline void load8(const void* base, int dtype, int64_t off, float (&e)[8]) {
+  if (dtype == kF32) {
+    const float* f = reinterpret_cast<const float*>(base) + off;
+    const float4 a = *reinterpret_cast<const float4*>(f), b = *reinterpret_cast<const float4*>(f + 4);
+    e[0] = a.x; e[1] = a.y; e[2] = a.z; e[3] = a.w; e[4] = b.x; e[5] = b.y; e[6] = b.z; e[7] = b.w;
+  } else if (dtype == kBF16) {
+    load8_16<__bf16>(reinterpret_cast<const uint16_t*>(base) + off, e);
+  } else {
+    load8_16<_Float16>(reinterpret_cast<const uint16_t*>(base) + off, e);
+  }
+}
+
 template <typename T>
-__global__ __launch_bounds__(256) void rope_kernel(const RopeParams p) {
+__device__ inline float round_to(float x) { return (float)static_cast<T>(x); }
+
+// Lanes per row: the row's chunk pairs rounded up to a power of two, so the
+// lanes of one row are an aligned group inside a wavefront (hd = 96 leaves
+// two of its eight lanes idle).
+inline int rope_lanes(int hd) {
+  int l = 1;
+  while (l < hd / 16) l <<= 1;
+  return l;
+}
+
+// With NORM, each row is first RMS-normalised over the head dimension as
+// Qwen3RMSNorm does (transformers modeling_qwen3, used as q_norm / k_norm at
+// /root/reference/qwen/nanogpt/hybrid_prior_attention.py:543-572):
+//   x <- w * round(x * rsqrt(mean(x^2) + eps)),  rounded to the activation dtype
+// (fp32 statistics; the two roundings of the reference module are kept), then
+// rotated.  The row's sum of squares is reduced across its lane group.
+template <typename T, bool NORM>
+__global__ __launch_bounds__(256) void rope_kernel(const RopeParams p, const int lanes) {
   const int np = p.hd / 16;  // chunk pairs per row
   const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   const int64_t rows_q = (int64_t)p.B * p.Uq * p.T;
   const int64_t rows = rows_q + (int64_t)p.B * p.Uk * p.T;
-  const int64_t row = gid / np;
-  if (row >= rows) return;
-  const int c = (int)(gid % np);
+  const int64_t row = gid / lanes;
+  const int c = (int)(gid & (lanes - 1));
+  const bool active = row < rows && c < np;
   const bool is_k = row >= rows_q;
-  const int64_t rr = is_k ? row - rows_q : row;
-  const int U = is_k ? p.Uk : p.Uq;
+  const int64_t rr = active ? (is_k ? row - rows_q : row) : 0;
+  const int U = max(is_k ? p.Uk : p.Uq, 1);
   const int t = (int)(rr % p.T);
   const int64_t bu = rr / p.T;
   const int u = (int)(bu % U), b = (int)(bu / U);
@@ -34,37 +77,47 @@ __global__ __launch_bounds__(256) void rope_kernel(const RopeParams p) {
   const int d0 = 8 * c, half = p.hd / 2;
   uint4* lo_p = reinterpret_cast<uint4*>(x + d0);
   uint4* hi_p = reinterpret_cast<uint4*>(x + d0 + half);
-  const uint4 lo = *lo_p, hi = *hi_p;
-  float cs[8], sn[8];
-  if (p.cs_dtype == kF32) {
-    const float* cp = reinterpret_cast<const float*>(p.cos) + (int64_t)t * p.cs_st + d0;
-    const float* sp = reinterpret_cast<const float*>(p.sin) + (int64_t)t * p.sn_st + d0;
-    const float4 c0 = *reinterpret_cast<const float4*>(cp), c1 = *reinterpret_cast<const float4*>(cp + 4);
-    const float4 s0 = *reinterpret_cast<const float4*>(sp), s1 = *reinterpret_cast<const float4*>(sp + 4);
-    cs[0] = c0.x; cs[1] = c0.y; cs[2] = c0.z; cs[3] = c0.w; cs[4] = c1.x; cs[5] = c1.y; cs[6] = c1.z; cs[7] = c1.w;
-    sn[0] = s0.x; sn[1] = s0.y; sn[2] = s0.z; sn[3] = s0.w; sn[4] = s1.x; sn[5] = s1.y; sn[6] = s1.z; sn[7] = s1.w;
-  } else {
-    const uint4 cw = *reinterpret_cast<const uint4*>(reinterpret_cast<const uint16_t*>(p.cos) + (int64_t)t * p.cs_st + d0);
-    const uint4 sw = *reinterpret_cast<const uint4*>(reinterpret_cast<const uint16_t*>(p.sin) + (int64_t)t * p.sn_st + d0);
-    const uint32_t cw4[4] = {cw.x, cw.y, cw.z, cw.w}, sw4[4] = {sw.x, sw.y, sw.z, sw.w};
+  float a[8], bv[8];
+  {
+    uint4 lo = make_uint4(0, 0, 0, 0), hi = lo;
+    if (active) {
+      lo = *lo_p;
+      hi = *hi_p;
+    }
+    const uint32_t lw[4] = {lo.x, lo.y, lo.z, lo.w}, hw[4] = {hi.x, hi.y, hi.z, hi.w};
 #pragma unroll
     for (int m = 0; m < 4; ++m) {
-      if (p.cs_dtype == kBF16) {
-        cs[2 * m] = Elem<__bf16>::lo(cw4[m]); cs[2 * m + 1] = Elem<__bf16>::hi(cw4[m]);
-        sn[2 * m] = Elem<__bf16>::lo(sw4[m]); sn[2 * m + 1] = Elem<__bf16>::hi(sw4[m]);
-      } else {
-        cs[2 * m] = Elem<_Float16>::lo(cw4[m]); cs[2 * m + 1] = Elem<_Float16>::hi(cw4[m]);
-        sn[2 * m] = Elem<_Float16>::lo(sw4[m]); sn[2 * m + 1] = Elem<_Float16>::hi(sw4[m]);
+      a[2 * m] = Elem<T>::lo(lw[m]); a[2 * m + 1] = Elem<T>::hi(lw[m]);
+      bv[2 * m] = Elem<T>::lo(hw[m]); bv[2 * m + 1] = Elem<T>::hi(hw[m]);
+    }
+  }
+  if constexpr (NORM) {
+    float ss = 0.f;
+#pragma unroll
+    for (int m = 0; m < 8; ++m) ss = fmaf(a[m], a[m], fmaf(bv[m], bv[m], ss));
+    for (int m = 1; m < lanes; m <<= 1) ss += __shfl_xor(ss, m, lanes);
+    const float r = rsqrtf(ss / (float)p.hd + p.eps);
+    if (active) {
+      float wl[8], wh[8];
+      const void* w = is_k ? p.k_w : p.q_w;
+      load8(w, p.w_dtype, d0, wl);
+      load8(w, p.w_dtype, d0 + half, wh);
+#pragma unroll
+      for (int m = 0; m < 8; ++m) {
+        a[m] = round_to<T>(wl[m] * round_to<T>(a[m] * r));
+        bv[m] = round_to<T>(wh[m] * round_to<T>(bv[m] * r));
       }
     }
   }
+  if (!active) return;
+  float cs[8], sn[8];
+  load8(p.cos, p.cs_dtype, (int64_t)t * p.cs_st + d0, cs);
+  load8(p.sin, p.cs_dtype, (int64_t)t * p.sn_st + d0, sn);
   // the cache repeats its frequencies in both halves (cos[t][d] = cos[t][d + hd/2])
-  const uint32_t lw[4] = {lo.x, lo.y, lo.z, lo.w}, hw[4] = {hi.x, hi.y, hi.z, hi.w};
   uint32_t ol[4], oh[4];
 #pragma unroll
   for (int m = 0; m < 4; ++m) {
-    const float a0 = Elem<T>::lo(lw[m]), a1 = Elem<T>::hi(lw[m]);
-    const float b0 = Elem<T>::lo(hw[m]), b1 = Elem<T>::hi(hw[m]);
+    const float a0 = a[2 * m], a1 = a[2 * m + 1], b0 = bv[2 * m], b1 = bv[2 * m + 1];
     const float c0 = cs[2 * m], c1 = cs[2 * m + 1], s0 = sn[2 * m], s1 = sn[2 * m + 1];
     ol[m] = Elem<T>::pack2(fmaf(a0, c0, -b0 * s0), fmaf(a1, c1, -b1 * s1));
     oh[m] = Elem<T>::pack2(fmaf(b0, c0, a0 * s0), fmaf(b1, c1, a1 * s1));
@@ -73,15 +126,24 @@ __global__ __launch_bounds__(256) void rope_kernel(const RopeParams p) {
   *hi_p = make_uint4(oh[0], oh[1], oh[2], oh[3]);
 }
 
+template <typename T>
+static void launch_rope_t(const RopeParams& p, dim3 grid, int lanes, hipStream_t s) {
+  if (p.q_w != nullptr)
+    hipLaunchKernelGGL((rope_kernel<T, true>), grid, dim3(256), 0, s, p, lanes);
+  else
+    hipLaunchKernelGGL((rope_kernel<T, false>), grid, dim3(256), 0, s, p, lanes);
+}
+
 hipError_t launch_rope(const RopeParams& p, int dtype, hipStream_t s) {
   const int64_t rows = (int64_t)p.B * (p.Uq + p.Uk) * p.T;
-  const int64_t threads = rows * (p.hd / 16);
+  const int lanes = rope_lanes(p.hd);
+  const int64_t threads = rows * lanes;
   if (threads == 0) return hipSuccess;
   const dim3 grid((unsigned)((threads + 255) / 256));
   if (dtype == kBF16)
-    hipLaunchKernelGGL(rope_kernel<__bf16>, grid, dim3(256), 0, s, p);
+    launch_rope_t<__bf16>(p, grid, lanes, s);
   else if (dtype == kF16)
-    hipLaunchKernelGGL(rope_kernel<_Float16>, grid, dim3(256), 0, s, p);
+    launch_rope_t<_Float16>(p, grid, lanes, s);
   else
     return hipErrorInvalidValue;
   return hipGetLastError();

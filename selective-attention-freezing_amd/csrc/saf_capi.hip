@@ -522,8 +522,9 @@ int saf_frozen_pv_fwd(const saf_tensor_t* patt, const saf_tensor_t* v, const int
   return run_dense(*patt, *v, *out, B, T, HD, v->dtype, oh, vh, ph, reinterpret_cast<hipStream_t>(stream));
 }
 
-int saf_rope_qk_inplace(const saf_tensor_t* q, const saf_tensor_t* k, const saf_tensor_t* cos,
-                        const saf_tensor_t* sin, void* stream) {
+static int rope_common(const saf_tensor_t* q, const saf_tensor_t* k, const saf_tensor_t* qw,
+                       const saf_tensor_t* kw, float eps, const saf_tensor_t* cos, const saf_tensor_t* sin,
+                       void* stream) {
   if (q == nullptr || k == nullptr || cos == nullptr || sin == nullptr)
     return fail(SAF_EINVAL, "q, k, cos and sin are required");
   if (!present(*q) || !present(*k) || !present(*cos) || !present(*sin))
@@ -547,6 +548,22 @@ int saf_rope_qk_inplace(const saf_tensor_t* q, const saf_tensor_t* k, const saf_
       return fail(SAF_EALIGN, "cos/sin rows must be contiguous and 16-byte aligned");
   }
   if (cos->dtype != sin->dtype) return fail(SAF_EINVAL, "cos and sin must share a dtype");
+  const bool norm = qw != nullptr || kw != nullptr;
+  if (norm) {
+    if (qw == nullptr || kw == nullptr || !present(*qw) || !present(*kw))
+      return fail(SAF_EINVAL, "q_weight and k_weight are both required for the RMSNorm");
+    const saf_tensor_t* ws[2] = {qw, kw};
+    for (int i = 0; i < 2; ++i) {
+      const saf_tensor_t& w = *ws[i];
+      if (w.ndim != 1 || w.size[0] != hd) return fail(SAF_EINVAL, "norm weights must be (HD,) vectors");
+      if (w.dtype != SAF_F32 && w.dtype != SAF_BF16 && w.dtype != SAF_F16)
+        return fail(SAF_EUNSUPPORTED, "rmsnorm: unsupported weight dtype %s", dtype_name(w.dtype));
+      if (w.stride[0] != 1 || reinterpret_cast<uintptr_t>(w.data) % 16)
+        return fail(SAF_EALIGN, "norm weights must be contiguous and 16-byte aligned");
+    }
+    if (qw->dtype != kw->dtype) return fail(SAF_EINVAL, "q_weight and k_weight must share a dtype");
+    if (!(eps >= 0.f)) return fail(SAF_EINVAL, "eps must be a non-negative number");
+  }
   if (int rc = check_act(*q, "q", 16)) return rc;
   if (int rc = check_act(*k, "k", 16)) return rc;
   RopeParams p{};
@@ -557,7 +574,25 @@ int saf_rope_qk_inplace(const saf_tensor_t* q, const saf_tensor_t* k, const saf_
   p.cs_st = cos->stride[0]; p.sn_st = sin->stride[0];
   p.cs_dtype = cos->dtype;
   p.B = (int)B; p.Uq = (int)q->size[1]; p.Uk = (int)k->size[1]; p.T = (int)T; p.hd = (int)hd;
+  if (norm) {
+    p.q_w = qw->data; p.k_w = kw->data;
+    p.w_dtype = qw->dtype;
+    p.eps = eps;
+  }
   return launched(launch_rope(p, q->dtype, reinterpret_cast<hipStream_t>(stream)), "rope");
+}
+
+int saf_rope_qk_inplace(const saf_tensor_t* q, const saf_tensor_t* k, const saf_tensor_t* cos,
+                        const saf_tensor_t* sin, void* stream) {
+  return rope_common(q, k, nullptr, nullptr, 0.f, cos, sin, stream);
+}
+
+int saf_qk_rmsnorm_rope_inplace(const saf_tensor_t* q, const saf_tensor_t* k, const saf_tensor_t* q_weight,
+                                const saf_tensor_t* k_weight, float eps, const saf_tensor_t* cos,
+                                const saf_tensor_t* sin, void* stream) {
+  if (q_weight == nullptr || k_weight == nullptr)
+    return fail(SAF_EINVAL, "q_weight and k_weight are required");
+  return rope_common(q, k, q_weight, k_weight, eps, cos, sin, stream);
 }
 
 int64_t saf_mixed_attn_workspace_bytes(const saf_mixed_attn_args* args) {

@@ -123,6 +123,11 @@ struct RopeParams {
   int64_t cs_st, sn_st;  // row strides of the (T', hd) caches
   int cs_dtype;
   int B, Uq, Uk, T, hd;
+  // optional per-head RMSNorm of q and k before the rotation (null: none)
+  const void* q_w;
+  const void* k_w;
+  int w_dtype;
+  float eps;
 };
 
 // Rows of one scan chunk for a head dimension (must match the kernel).

@@ -282,10 +282,11 @@ def fused_mixed_attn(q, k, v, patt, frozen, hidx=None, pidx=None,
         q_d = _aligned_view(q, 16)
         k_d = _aligned_view(k, 16)
     v_d = _aligned_view(v, 16)
-    if kv_identity and v_d.stride(2) > v_d.stride(1):
+    if v_d.stride(2) > v_d.stride(1):
         # v is a T-major view (the model's (B, T, H, hd) projection output):
         # keep that layout so the caller's transpose(1, 2).reshape is free,
-        # as the reference's empty_like(v) does for a dense v
+        # as the reference's empty_like(v) does for a dense v (with kvidx the
+        # output still has all H query heads)
         out = torch.empty((B, T, H, HD), device=v.device, dtype=v.dtype).transpose(1, 2)
     elif kv_identity:
         out = torch.empty_like(v_d)
