@@ -139,13 +139,15 @@ int saf_qk_rmsnorm_rope_inplace(const saf_tensor_t* q, const saf_tensor_t* k, co
  * (0 bytes when there are none). */
 int64_t saf_workspace_bytes(int32_t B, int32_t T, int32_t head_dim, int32_t n_scan_heads);
 
-/* Workspace that lets one saf_mixed_attn_fwd / saf_flash_fwd call with these
+/* Workspace that lets one saf_mixed_attn_fwd (or per-kind) call with these
  * arguments (workspace fields ignored) use every optimisation: the closed-form
- * scan's look-back words, then fp32 partials of the live-head kernel's causal
- * load balancing (long query blocks split into key segments and merged by a
- * combine kernel).  A smaller workspace still works if it covers the scan:
- * the live-head kernel then runs unsplit.  Returns -1 on invalid arguments.
- * No counterpart in the reference (its Triton launch needs no workspace). */
+ * scan's look-back words, then one region of fp32 partials shared by the
+ * live-head and the dense P.V kernels' causal load balancing (long query
+ * blocks split into key segments and merged by a combine kernel; the two run
+ * one after the other on the stream).  A smaller workspace still works if it
+ * covers the scan: those kernels then run unsplit.  Partials need a 16-byte
+ * aligned workspace.  Returns -1 on invalid arguments.  No counterpart in the
+ * reference (its Triton launch needs no workspace). */
 int64_t saf_mixed_attn_workspace_bytes(const saf_mixed_attn_args* args);
 
 /* Reads the scan's look-back error word from a workspace after the stream

@@ -247,7 +247,9 @@ void flash_fwd_kernel(const FlashParams p) {
 }
 
 // Merge the key-segment partials of split query blocks (one workgroup per
-// (batch, live slot, split query block); 16 threads x 4 columns per row).
+// (batch, slot, split query block); HD/4 threads x 4 columns per row): the
+// flash partials by their (m, l) rescaling, dense P.V partials (part_ml null)
+// by a plain sum.
 template <typename T, int HD>
 __global__ __launch_bounds__(256) void flash_combine_kernel(const CombineParams p) {
   const int tid = threadIdx.x;
@@ -269,6 +271,21 @@ __global__ __launch_bounds__(256) void flash_combine_kernel(const CombineParams 
   for (int rl = tid / CPR; rl < BM; rl += RPP) {
     const int q = q0 + rl;
     if (q >= p.T) break;
+    if (p.part_ml == nullptr) {  // dense P.V partials: a plain sum
+      float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+      for (int s = 0; s < nseg; ++s) {
+        const float4 v = *reinterpret_cast<const float4*>(p.part_o + ((pbase + s) * BM + rl) * HD + 4 * c4);
+        acc.x += v.x;
+        acc.y += v.y;
+        acc.z += v.z;
+        acc.w += v.w;
+      }
+      uint2 wv;
+      wv.x = Elem<T>::pack2(acc.x, acc.y);
+      wv.y = Elem<T>::pack2(acc.z, acc.w);
+      *reinterpret_cast<uint2*>(obase + (int64_t)q * p.o_st + 4 * c4) = wv;
+      continue;
+    }
     float mmax = -INFINITY;
     for (int s = 0; s < nseg; ++s) mmax = fmaxf(mmax, p.part_ml[((pbase + s) * 2) * BM + rl]);
     const float mref = mmax == -INFINITY ? 0.f : mmax;

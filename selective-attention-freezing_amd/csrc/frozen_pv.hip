@@ -11,13 +11,13 @@
 //     j > i are exactly zero.
 //
 // The P.V half is the same as the live-head kernel: one workgroup = 4 waves
-// x 32*QT query rows; V^T tiles double-buffered in LDS.  Dense: P tiles
-// (BM rows x 64 keys) are staged through LDS as well, loaded with coalesced,
-// prefetched 16-byte reads and rounded to the input dtype once; workgroups
-// that share a P tile (the batch siblings) are placed on the same XCD so the
-// second one reads it from that XCD's L2.  Decomposed: P^T is produced
-// directly in the B-operand lane layout (lane (n, g) owns query n and keys
-// 8g + 0..7 of each 16-key step).
+// x 32*QT query rows; V^T tiles double-buffered in LDS; P^T lives in the
+// B-operand lane layout (lane (n, g) owns query n and keys 8g + 0..7 of each
+// 16-key step).  Dense: each lane reads its P^T operands directly from the
+// pattern rows (16 bytes per operand, rounded to the input dtype once unless
+// already in it), 64 rows per wave, causally balanced work items; workgroups
+// that share P (the batch siblings) are placed on the same XCD so the second
+// one reads it from that XCD's L2.  Decomposed: P^T is rebuilt in registers.
 #include "saf_kernels.h"
 
 namespace saf {
@@ -152,14 +152,6 @@ __global__ __launch_bounds__(256) void frozen_decomp_kernel(const FrozenParams p
 }
 
 
-// LDS tile of P (BM rows x 64 keys, activation dtype): row-major, 16-byte
-// chunks XOR-swizzled by the row so the 32 B-operand lanes of an MFMA (32
-// rows, same chunk) and the 8 writers of a row hit distinct banks.
-template <int BM> struct PLayout {
-  static constexpr int BYTES = BM * 128;
-  __device__ static inline int chunk(int row, int c) { return row * 8 + (c ^ (row & 7)); }
-};
-
 // Pattern element types: 8 consecutive elements -> 8 floats.
 template <typename PT> struct PatVec;
 template <> struct PatVec<float> {
@@ -185,72 +177,82 @@ template <typename H> struct PatVec16 {
 template <> struct PatVec<__bf16> : PatVec16<__bf16> {};
 template <> struct PatVec<_Float16> : PatVec16<_Float16> {};
 
-// Stages P[q0 .. q0+BM)[j0 .. j0+64) rounded to T, zero above the diagonal
-// and beyond T.  Eight consecutive threads read one row's 64 keys.
-template <typename T, typename PT, int BM, int NTHR> struct PStager {
-  static constexpr int PER_THR = BM * 8 / NTHR;
-  uint4 r[PER_THR];
+// Keep the first n (0..8) 16-bit elements of a packed chunk, zero the rest.
+__device__ inline uint4 keep_leading(uint4 w, int n) {
+  uint32_t d[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+  for (int m = 0; m < 4; ++m) d[m] = 2 * m + 1 < n ? d[m] : (2 * m < n ? d[m] & 0xffffu : 0u);
+  return make_uint4(d[0], d[1], d[2], d[3]);
+}
 
-  __device__ inline void load(const FrozenParams& p, const PT* pbase, int q0, int j0, int T_len, int tid) {
-#pragma unroll
-    for (int u = 0; u < PER_THR; ++u) {
-      const int idx = tid + u * NTHR;
-      const int row = idx >> 3, c = idx & 7;
-      const int i = q0 + row, jc = j0 + 8 * c;
-      float e[8];
-      if (i >= T_len || jc > i) {
-#pragma unroll
-        for (int m = 0; m < 8; ++m) e[m] = 0.f;
-      } else {
-        const PT* prow = pbase + (int64_t)i * p.p_si;
-        if (p.patt_vec && jc + 8 <= p.p_cols) {
-          PatVec<PT>::load8(prow + jc, e);
-        } else {
-#pragma unroll
-          for (int m = 0; m < 8; ++m) e[m] = jc + m <= i ? PatVec<PT>::one(prow + (int64_t)(jc + m) * p.p_sj) : 0.f;
-        }
-        if (jc + 7 > i) {  // diagonal chunk: keys past the query are zero
-#pragma unroll
-          for (int m = 0; m < 8; ++m) e[m] = jc + m <= i ? e[m] : 0.f;
-        }
-      }
-      r[u] = make_uint4(Elem<T>::pack2(e[0], e[1]), Elem<T>::pack2(e[2], e[3]), Elem<T>::pack2(e[4], e[5]),
-                        Elem<T>::pack2(e[6], e[7]));
+// One B-operand chunk of P^T: keys kstart .. kstart+7 of one query row in
+// the activation dtype, the first `nvalid` kept (keys past the query and rows
+// past T are zero; nvalid <= 0 loads nothing).  Same-dtype patterns are used
+// as loaded; others are widened and rounded once.  A chunk that would cross
+// the row end, or a pattern not laid out for 16-byte loads, is read element
+// by element (only the kept elements).
+template <typename T, typename PT>
+__device__ inline uint4 p_chunk(const FrozenParams& p, const PT* prow, int kstart, int nvalid) {
+  if (nvalid <= 0) return make_uint4(0, 0, 0, 0);
+  const bool vec = p.patt_vec && kstart + 8 <= p.p_cols;
+  if constexpr (std::is_same<PT, T>::value) {
+    if (vec) {
+      const uint4 w = *reinterpret_cast<const uint4*>(prow + kstart);
+      return nvalid < 8 ? keep_leading(w, nvalid) : w;
     }
   }
-
-  __device__ inline void store(uint4* lds, int tid) const {
+  float e[8];
+  if (vec) {
+    PatVec<PT>::load8(prow + kstart, e);
+  } else {
 #pragma unroll
-    for (int u = 0; u < PER_THR; ++u) {
-      const int idx = tid + u * NTHR;
-      lds[PLayout<BM>::chunk(idx >> 3, idx & 7)] = r[u];
-    }
+    for (int m = 0; m < 8; ++m) e[m] = m < nvalid ? PatVec<PT>::one(prow + (int64_t)(kstart + m) * p.p_sj) : 0.f;
   }
-};
+#pragma unroll
+  for (int m = 0; m < 8; ++m) e[m] = m < nvalid ? e[m] : 0.f;
+  return make_uint4(Elem<T>::pack2(e[0], e[1]), Elem<T>::pack2(e[2], e[3]), Elem<T>::pack2(e[4], e[5]),
+                    Elem<T>::pack2(e[6], e[7]));
+}
 
-// Two resident workgroups per CU double the pattern bytes in flight; the
-// loop is bound by load latency, not by its short MFMA work.
-template <typename T, typename PT, int HD, int QT>
+// Dense P.V.  Each lane loads its own B operands straight from the pattern
+// rows (lane (n, g): query n of a 32-row tile, keys 8g + 0..7 of each 16-key
+// step = one 16-byte read), refilled for the next 64-key block as soon as
+// they are used, so P needs no LDS staging and no barrier; only the V^T tile
+// (shared by the four waves) is double-buffered in LDS.  64 query rows per wave: each V^T operand read from
+// LDS feeds two MFMAs.  Work items cover a key segment of a 256-row query
+// block; split blocks write fp32 partials that the combine kernel sums.  Two
+// resident workgroups per CU overlap one's loads with the other's MFMAs.
+template <typename T, typename PT, int HD>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void frozen_dense_kernel(const FrozenParams p) {
-  constexpr int NW = 4, NTHR = 256;
+  constexpr int QT = 2, NW = 4, NTHR = 256;
   constexpr int BM = NW * 32 * QT;
   constexpr int NDT = HD / 32;
   __shared__ __align__(16) uint4 v_lds[2][VLayout<HD>::BYTES / 16];
-  __shared__ __align__(16) uint4 p_lds[2][PLayout<BM>::BYTES / 16];
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int n = lane & 31, g = lane >> 5;
 
   // XCD-aware order: workgroup i runs on XCD i % 8; the B batch siblings of a
-  // (query block, head) group get ids 8 apart (same XCD, dispatched together)
-  // and groups are numbered heaviest query block first.
+  // (work item, head) group get ids 8 apart (same XCD, dispatched together,
+  // so the second reads the P tiles from that XCD's L2); items heaviest first.
   const int x = blockIdx.x & 7, t8 = blockIdx.x >> 3;
   const int b = t8 % p.B, grp = 8 * (t8 / p.B) + x;
-  if (grp >= p.n_qblk * p.n_slots) return;
-  const int qb = p.n_qblk - 1 - grp / p.n_slots;
-  const int slot = grp % p.n_slots;
+  const int n_work = p.n_items ? p.n_items : p.n_qblk;
+  if (grp >= n_work * p.n_slots) return;
+  const int it = grp / p.n_slots, slot = grp % p.n_slots;
+  int qb, seg;
+  if (p.n_items) {
+    const int w = p.items[it];
+    qb = w >> 8;
+    seg = w & 255;
+  } else {
+    qb = p.n_qblk - 1 - it;
+    seg = 0;
+  }
+  qb = __builtin_amdgcn_readfirstlane(qb);
+  seg = __builtin_amdgcn_readfirstlane(seg);
   const int h = p.out_head[slot];
   const PT* pbase = reinterpret_cast<const PT*>(p.patt) + (int64_t)p.pat_head[slot] * p.p_sh;
   const T* vbase = reinterpret_cast<const T*>(p.v) + b * p.v_sb + (int64_t)p.v_head[slot] * p.v_sh;
@@ -258,10 +260,27 @@ void frozen_dense_kernel(const FrozenParams p) {
 
   const int T_len = p.T;
   const int q0 = qb * BM;
-  const int q0w = q0 + wave * 32 * QT;
   const int nkb = (min(q0 + BM, T_len) + 63) / 64;
+  const bool split = p.n_items != 0 && p.part_base[qb] >= 0;
+  const int kb0 = split ? seg * p.seg_len : 0;
+  const int kb1 = split ? min(nkb, kb0 + p.seg_len) : nkb;
+  const int q0w = q0 + wave * 32 * QT;
   const int kend_w = min(q0w + 32 * QT, T_len);
-  const int nkb_w = kend_w > 0 ? (kend_w + 63) / 64 : 0;
+  const int kb1_w = min(kb1, kend_w > 0 ? (kend_w + 63) / 64 : 0);  // blocks this wave's rows reach
+
+  int row[QT];
+  const PT* prow[QT];
+#pragma unroll
+  for (int qt = 0; qt < QT; ++qt) {
+    row[qt] = q0w + 32 * qt + n;
+    prow[qt] = pbase + (int64_t)min(row[qt], T_len - 1) * p.p_si;
+  }
+  // P^T operand of key step (ks, sh) of block j for query tile qt
+  auto p_op = [&](int j, int ks, int sh, int qt) {
+    const int kstart = 64 * j + 32 * ks + 16 * sh + 8 * g;
+    const int nvalid = row[qt] < T_len ? min(row[qt] - kstart + 1, 8) : 0;
+    return p_chunk<T, PT>(p, prow[qt], kstart, nvalid);
+  };
 
   f32x16_t o[QT][NDT];
 #pragma unroll
@@ -270,57 +289,78 @@ void frozen_dense_kernel(const FrozenParams p) {
     for (int dt = 0; dt < NDT; ++dt) o[qt][dt] = zero16();
 
   VStager<T, HD, NTHR> vst;
-  PStager<T, PT, BM, NTHR> pst;
-  vst.load(vbase, p.v_st, 0, T_len, tid);
-  pst.load(p, pbase, q0, 0, T_len, tid);
+  uint4 pb[2][2][QT];
+  vst.load(vbase, p.v_st, 64 * kb0, T_len, tid);
+  if (kb0 < kb1_w) {
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+      for (int sh = 0; sh < 2; ++sh)
+#pragma unroll
+        for (int qt = 0; qt < QT; ++qt) pb[ks][sh][qt] = p_op(kb0, ks, sh, qt);
+  }
   vst.store(reinterpret_cast<uint32_t*>(v_lds[0]), tid);
-  pst.store(p_lds[0], tid);
   __syncthreads();
 
-  for (int j = 0; j < nkb; ++j) {
-    const int buf = j & 1;
-    const bool more = j + 1 < nkb;
-    if (more) {
-      vst.load(vbase, p.v_st, 64 * (j + 1), T_len, tid);
-      pst.load(p, pbase, q0, 64 * (j + 1), T_len, tid);
-    }
-    if (j < nkb_w) {
-      uint4 pb[2][2][QT];
+  for (int j = kb0; j < kb1; ++j) {
+    const int buf = (j - kb0) & 1;
+    const bool more = j + 1 < kb1;
+    if (more) vst.load(vbase, p.v_st, 64 * (j + 1), T_len, tid);
+    if (j < kb1_w) {
+      const uint4* vt = v_lds[buf];
+      const bool next = j + 1 < kb1_w;
+      // each operand is refilled with block j+1's right after its last use,
+      // so one block of P^T registers keeps a block of loads in flight
 #pragma unroll
-      for (int qt = 0; qt < QT; ++qt) {
-        const int row = 32 * QT * wave + 32 * qt + n;
+      for (int ks = 0; ks < 2; ++ks)
 #pragma unroll
-        for (int ks = 0; ks < 2; ++ks)
+        for (int sh = 0; sh < 2; ++sh) {
 #pragma unroll
-          for (int sh = 0; sh < 2; ++sh) pb[ks][sh][qt] = p_lds[buf][PLayout<BM>::chunk(row, 4 * ks + 2 * sh + g)];
-      }
-      pv_block<T, HD, QT>(o, pb, v_lds[buf], lane);
+          for (int dt = 0; dt < NDT; ++dt) {
+            const uint4 a = vt[VLayout<HD>::chunk(32 * dt + n, 4 * ks + 2 * sh + g)];
+#pragma unroll
+            for (int qt = 0; qt < QT; ++qt) o[qt][dt] = Elem<T>::mfma(a, pb[ks][sh][qt], o[qt][dt]);
+          }
+          if (next) {
+#pragma unroll
+            for (int qt = 0; qt < QT; ++qt) pb[ks][sh][qt] = p_op(j + 1, ks, sh, qt);
+          }
+        }
     }
-    if (more) {
-      vst.store(reinterpret_cast<uint32_t*>(v_lds[buf ^ 1]), tid);
-      pst.store(p_lds[buf ^ 1], tid);
-    }
+    if (more) vst.store(reinterpret_cast<uint32_t*>(v_lds[buf ^ 1]), tid);
     __syncthreads();
   }
 
 #pragma unroll
   for (int qt = 0; qt < QT; ++qt) {
-    const int i = q0w + 32 * qt + n;
-    if (i < T_len) store_out_tile<T, HD>(obase + (int64_t)i * p.o_st, o[qt], 1.f, g);
+    const int i = row[qt];
+    if (i >= T_len) continue;
+    if (split) {
+      const int64_t pidx = ((int64_t)b * p.n_slots + slot) * p.n_part_per_head + p.part_base[qb] + seg;
+      float* po = p.part_o + (pidx * BM + (i - q0)) * HD;
+#pragma unroll
+      for (int dt = 0; dt < NDT; ++dt)
+#pragma unroll
+        for (int r4 = 0; r4 < 4; ++r4)
+          *reinterpret_cast<float4*>(po + 32 * dt + 8 * r4 + 4 * g) =
+              make_float4(o[qt][dt][4 * r4], o[qt][dt][4 * r4 + 1], o[qt][dt][4 * r4 + 2], o[qt][dt][4 * r4 + 3]);
+    } else {
+      store_out_tile<T, HD>(obase + (int64_t)i * p.o_st, o[qt], 1.f, g);
+    }
   }
 }
 
 template <typename T, int HD, int QT>
 static hipError_t launch_frozen_t(const FrozenParams& p, int mode, hipStream_t s) {
   if (mode == 0) {
-    const int64_t groups = (int64_t)p.n_qblk * p.n_slots;
+    const int64_t groups = (int64_t)(p.n_items ? p.n_items : p.n_qblk) * p.n_slots;
     const dim3 grid((unsigned)(8 * p.B * ((groups + 7) / 8)));
     if (p.patt_dtype == kF32)
-      hipLaunchKernelGGL((frozen_dense_kernel<T, float, HD, QT>), grid, dim3(256), 0, s, p);
+      hipLaunchKernelGGL((frozen_dense_kernel<T, float, HD>), grid, dim3(256), 0, s, p);
     else if (p.patt_dtype == kBF16)
-      hipLaunchKernelGGL((frozen_dense_kernel<T, __bf16, HD, QT>), grid, dim3(256), 0, s, p);
+      hipLaunchKernelGGL((frozen_dense_kernel<T, __bf16, HD>), grid, dim3(256), 0, s, p);
     else
-      hipLaunchKernelGGL((frozen_dense_kernel<T, _Float16, HD, QT>), grid, dim3(256), 0, s, p);
+      hipLaunchKernelGGL((frozen_dense_kernel<T, _Float16, HD>), grid, dim3(256), 0, s, p);
   } else {
     const dim3 grid((unsigned)((int64_t)p.n_qblk * p.B * p.n_slots));
     hipLaunchKernelGGL((frozen_decomp_kernel<T, HD, QT>), grid, dim3(256), 0, s, p);
@@ -339,7 +379,6 @@ static hipError_t launch_frozen_hd(const FrozenParams& p, int hd, int mode, hipS
   }
 }
 
-int frozen_qt(int hd) { return hd <= 64 ? 2 : 1; }
 
 hipError_t launch_frozen_pv(const FrozenParams& p, int dtype, int hd, int mode, hipStream_t s) {
   if (dtype == kBF16) return launch_frozen_hd<__bf16>(p, hd, mode, s);

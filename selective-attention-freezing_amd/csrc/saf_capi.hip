@@ -333,7 +333,8 @@ int run_flash(const saf_mixed_attn_args* a, const Plan& pl, hipStream_t s) {
   // split the causal tail when the caller's workspace holds the partials
   FlashPlan fp = plan_flash(pl.B, p.n_slots, pl.T, pl.HD, qt);
   const int64_t part_off = scan_ws_bytes(pl);
-  if (fp.n_items && a->workspace != nullptr && a->workspace_bytes >= part_off + fp.part_bytes) {
+  if (fp.n_items && a->workspace != nullptr && a->workspace_bytes >= part_off + fp.part_bytes &&
+      reinterpret_cast<uintptr_t>(a->workspace) % 16 == 0) {
     char* ws = reinterpret_cast<char*>(a->workspace) + part_off;
     const int64_t nbh = (int64_t)pl.B * p.n_slots;
     p.n_items = fp.n_items;
@@ -382,9 +383,15 @@ void fill_frozen_common(FrozenParams& p, const saf_tensor_t& v, const saf_tensor
 
 int frozen_qtiles(int hd) { return hd <= 64 ? 2 : 1; }
 
+// Query tiles per wave of the dense P.V kernel (256-row query blocks).
+constexpr int kDenseQt = 2;
+
+// Dense P.V over the heads listed; with a workspace large enough for the
+// plan's partials, long query blocks are split into key segments (the flash
+// planner's causal balance) and summed by the combine kernel.
 int run_dense(const saf_tensor_t& patt, const saf_tensor_t& v, const saf_tensor_t& o, int B, int T, int HD,
               int dtype, const std::vector<int>& out_head, const std::vector<int>& v_head,
-              const std::vector<int>& pat_head, hipStream_t s) {
+              const std::vector<int>& pat_head, void* ws, int64_t ws_bytes, hipStream_t s) {
   if (out_head.empty() || T == 0 || B == 0) return SAF_OK;
   FrozenParams p{};
   fill_frozen_common(p, v, o, B, T);
@@ -396,13 +403,36 @@ int run_dense(const saf_tensor_t& patt, const saf_tensor_t& v, const saf_tensor_
   p.patt_vec = patt.stride[2] == 1 && reinterpret_cast<uintptr_t>(patt.data) % 16 == 0 &&
                (patt.stride[1] * es) % 16 == 0 && (patt.stride[0] * es) % 16 == 0;
   p.n_slots = (int)out_head.size();
-  p.n_qblk = (T + block_rows(frozen_qtiles(HD)) - 1) / block_rows(frozen_qtiles(HD));
+  p.n_qblk = (T + block_rows(kDenseQt) - 1) / block_rows(kDenseQt);
   for (int i = 0; i < p.n_slots; ++i) {
     p.out_head[i] = (int16_t)out_head[i];
     p.v_head[i] = (int16_t)v_head[i];
     p.pat_head[i] = (int16_t)pat_head[i];
   }
-  return launched(launch_frozen_pv(p, dtype, HD, 0, s), "dense P.V");
+  FlashPlan fp = plan_flash(B, p.n_slots, T, HD, kDenseQt);
+  if (fp.n_items && ws != nullptr && ws_bytes >= fp.part_bytes && reinterpret_cast<uintptr_t>(ws) % 16 == 0) {
+    p.n_items = fp.n_items;
+    p.seg_len = fp.seg_len;
+    p.n_part_per_head = fp.n_part_per_head;
+    p.part_o = reinterpret_cast<float*>(ws);
+    std::copy(fp.items.begin(), fp.items.end(), p.items);
+    std::copy(fp.part_base.begin(), fp.part_base.end(), p.part_base);
+  } else {
+    fp = FlashPlan();
+  }
+  if (int rc = launched(launch_frozen_pv(p, dtype, HD, 0, s), "dense P.V")) return rc;
+  if (fp.n_split == 0) return SAF_OK;
+  CombineParams c{};
+  c.out = p.out;
+  c.o_sb = p.o_sb; c.o_sh = p.o_sh; c.o_st = p.o_st;
+  c.B = p.B; c.T = p.T; c.n_slots = p.n_slots; c.BM = block_rows(kDenseQt);
+  c.seg_len = fp.seg_len; c.n_part_per_head = fp.n_part_per_head; c.n_split = fp.n_split;
+  c.part_o = p.part_o;
+  c.part_ml = nullptr;
+  std::copy(p.out_head, p.out_head + kMaxHeads, c.out_head);
+  std::copy(fp.split_qb.begin(), fp.split_qb.end(), c.split_qb);
+  std::copy(fp.part_base.begin(), fp.part_base.end(), c.part_base);
+  return launched(launch_flash_combine(c, dtype, HD, s), "dense P.V combine");
 }
 
 int run_decomp(const saf_mixed_attn_args* a, const Plan& pl, hipStream_t s) {
@@ -458,7 +488,16 @@ int run_dense_mixed(const saf_mixed_attn_args* a, const Plan& pl, hipStream_t s)
     vh.push_back(a->kvidx ? a->kvidx[h] : h);
     ph.push_back(a->pidx ? a->pidx[h] : h);
   }
-  return run_dense(a->patt, a->v, a->out, pl.B, pl.T, pl.HD, pl.dtype, pl.dense, vh, ph, s);
+  // the partials share the flash kernel's region: same stream, flash's
+  // combine has consumed it before the dense kernel starts
+  const int64_t part_off = scan_ws_bytes(pl);
+  void* ws = nullptr;
+  int64_t ws_bytes = 0;
+  if (a->workspace != nullptr && a->workspace_bytes > part_off) {
+    ws = reinterpret_cast<char*>(a->workspace) + part_off;
+    ws_bytes = a->workspace_bytes - part_off;
+  }
+  return run_dense(a->patt, a->v, a->out, pl.B, pl.T, pl.HD, pl.dtype, pl.dense, vh, ph, ws, ws_bytes, s);
 }
 
 int run(const saf_mixed_attn_args* a, unsigned which, void* stream) {
@@ -519,7 +558,8 @@ int saf_frozen_pv_fwd(const saf_tensor_t* patt, const saf_tensor_t* v, const int
     vh.push_back(f);
     ph.push_back(fz_idx[f]);
   }
-  return run_dense(*patt, *v, *out, B, T, HD, v->dtype, oh, vh, ph, reinterpret_cast<hipStream_t>(stream));
+  return run_dense(*patt, *v, *out, B, T, HD, v->dtype, oh, vh, ph, nullptr, 0,
+                   reinterpret_cast<hipStream_t>(stream));
 }
 
 static int rope_common(const saf_tensor_t* q, const saf_tensor_t* k, const saf_tensor_t* qw,
@@ -598,11 +638,14 @@ int saf_qk_rmsnorm_rope_inplace(const saf_tensor_t* q, const saf_tensor_t* k, co
 int64_t saf_mixed_attn_workspace_bytes(const saf_mixed_attn_args* args) {
   Plan pl;
   if (plan_and_validate(args, kDoFlash | kDoScan, pl, false)) return -1;
-  int64_t total = scan_ws_bytes(pl);
+  int64_t total = scan_ws_bytes(pl), part = 0;
   if (!pl.live.empty()) {
     const FlashPlan fp = plan_flash(pl.B, (int)pl.live.size(), pl.T, pl.HD, flash_qtiles_for(args, pl.HD));
-    total += fp.part_bytes;
+    part = fp.part_bytes;
   }
+  if (!pl.dense.empty())
+    part = std::max(part, plan_flash(pl.B, (int)pl.dense.size(), pl.T, pl.HD, kDenseQt).part_bytes);
+  total += part;
   return total;
 }
 

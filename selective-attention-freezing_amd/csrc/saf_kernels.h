@@ -57,7 +57,7 @@ struct CombineParams {
   int64_t l_sb, l_sh, l_st;
   int B, T, n_slots, BM, seg_len, n_part_per_head, n_split;
   const float* part_o;
-  const float* part_ml;
+  const float* part_ml;  // null: the partials are plain sums (dense P.V)
   int16_t out_head[kMaxHeads];
   int16_t split_qb[kMaxQblk];    // split query blocks
   int16_t part_base[kMaxQblk];   // indexed by query block
@@ -86,7 +86,15 @@ struct FrozenParams {
   int16_t out_head[kMaxHeads];
   int16_t v_head[kMaxHeads];
   int16_t pat_head[kMaxHeads];  // dense: pattern row; decomposed: buffer row
+  // dense P.V causal balance (as FlashParams): work items (qb << 8) | seg,
+  // fp32 partials of split query blocks summed by the combine kernel;
+  // n_items == 0: one item per query block, heaviest first
+  int n_items, seg_len, n_part_per_head;
+  float* part_o;
+  int32_t items[kMaxItems];
+  int16_t part_base[kMaxQblk];
 };
+static_assert(sizeof(FrozenParams) <= 4096, "FrozenParams must fit the kernel argument segment");
 
 // Closed-form frozen heads (state 2 heads recognised as causal mean,
 // exponential decay or sliding window): a single-pass chunked scan along T

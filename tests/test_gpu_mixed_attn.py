@@ -202,6 +202,35 @@ def test_causal_split_of_long_query_blocks(B, H, T, hd, qt):
         assert np.abs(lse[0, h].cpu().numpy() - ref_lse).max() < 2e-2
 
 
+@pytest.mark.parametrize("T,hd,pdtype", [(2000, 64, torch.bfloat16), (1537, 128, torch.float32),
+                                         (2304, 128, torch.bfloat16), (1111, 32, torch.float16),
+                                         (1300, 96, torch.bfloat16)])
+def test_dense_causal_split(T, hd, pdtype):
+    """Few dense heads at long T: the dense P.V kernel splits the heaviest
+    query blocks into key segments whose fp32 partials the combine kernel
+    sums; both the split (fused operator, workspace given) and the unsplit
+    (frozen_pv, no workspace) paths match the oracle.  S = T + 40 covers both
+    the 16-byte pattern rows and the element-wise path (fp32 rows of 1577)."""
+    K = _kernel()
+    B, H, S = 2, 3, T + 40
+    frozen, hidx, live = routing(H, {0: 1, 2: 1})
+    patt = make_pattern(2, S, seed=T)
+    pidx = torch.tensor([0, 0, 1], dtype=torch.int32)
+    q, k, v = qkv(B, H, T, hd, seed=T + hd, dtype=torch.bfloat16)
+    q, k = q[:, live].contiguous(), k[:, live].contiguous()
+    pd = patt.to(pdtype)
+    y = K.fused_mixed_attn(q.to(DEV), k.to(DEV), v.to(DEV), pd.to(DEV), frozen.to(DEV), hidx.to(DEV),
+                           pidx.to(DEV))
+    torch.cuda.synchronize()
+    ref = orc.eager_mixed_attention(f64(q), f64(k), f64(v), frozen.numpy(), hidx.numpy(), pidx.numpy(),
+                                    patt=f64(pd))
+    compare(y, ref, what=f"dense split T{T} hd{hd} {pdtype}")
+    fz = torch.tensor([0, 1], dtype=torch.int32)
+    yu = K.frozen_pv(pd.to(DEV), v[:, [0, 2]].contiguous().to(DEV), fz.to(DEV), T)
+    torch.cuda.synchronize()
+    compare(yu, ref[:, [0, 2]], what=f"dense unsplit T{T} hd{hd} {pdtype}")
+
+
 def test_gqa_kvidx():
     """Qwen-style map: 14 query heads over 2 KV heads, frozen query heads read
     the shared V of their group (qwen/kernel/fused_attn.py:254-259)."""
