@@ -3,48 +3,283 @@
 // Semantics follow the reference's live-head accumulator
 // (/root/reference/kernel/fused_attn.py:182-226, GQA variant
 // /root/reference/qwen/kernel/fused_attn.py:183-231): base-2 online softmax
-// with qk_scale = sm_scale * log2(e), fp32 running max / sum / accumulator,
-// P rounded to the input dtype before the P.V product, output divided by the
-// row sum, and LSE = m + log2(l) in base-2 units.  Two deliberate changes of
-// bookkeeping, both exact up to rounding: the running max is only moved when
-// a block exceeds it by more than kSlack (lazy rescale), and the row sum adds
-// the rounded P values (v_dot2 on packed pairs), i.e. exactly the weights
-// that multiply V.
+// with qk_scale = sm_scale * log2(e), fp32 running reference / sum /
+// accumulator, P rounded to the input dtype before the P.V product, output
+// divided by the row sum, and LSE = m + log2(l) in base-2 units.  Two
+// deliberate changes of bookkeeping, both exact up to rounding:
+//   - the reference value m of a query is not the running maximum.  P is
+//     computed against the current m, and only when some lane's sum of its 16
+//     P values of a 32-key sub-block exceeds kRedoSum (so some P > 2^16, or
+//     m is still the initial kMinit) is the sub-block recomputed against
+//     max(m, block max), rescaling O and l.  That happens for the first
+//     sub-block of every query and whenever the scores grow by more than 16
+//     (base 2) over the reference; the common sub-block needs no max at all.
+//   - the row sum adds the rounded P values (v_dot2 on packed pairs), i.e.
+//     exactly the weights that multiply V.
 //
 // Work decomposition: one workgroup = 4 waves = (4 * 32 * QT) query rows of
-// one (batch, live head); each wave owns 32*QT queries and walks 64-key
-// blocks up to its own causal limit.  K and V^T tiles are double-buffered in
-// LDS; the next tile's global loads are issued before the current tile's
-// MFMAs.  Workgroups are ordered heaviest query block first.
+// one (batch, live head); each wave owns 32*QT queries.  Keys are walked in
+// 64-key blocks of two 32-key sub-blocks.  K and V tiles arrive by
+// global_load_lds DMA (no staging registers) into three static LDS slots
+// each: block j reads K_j, K_{j+1}, V_{j-1}, V_j while K_{j+2} and V_{j+1}
+// load.  K is stored XOR-swizzled for the ds_read_b128 A operand of
+// S^T = K.Q^T; V stays row-major (32-byte segments XOR-swizzled by key) and
+// its V^T A operands come from ds_read_b64_tr_b16 transposing reads.
+//
+// Software pipeline: iteration u issues the MFMAs of S_{u+1} and of
+// P_{u-1}.V together with the softmax VALU work of S_u, all in one basic
+// block, so the matrix pipe always has independent work while the exps run.
+// Workgroups are ordered heaviest query block first.
 #include <type_traits>
 
 #include "saf_kernels.h"
 
 namespace saf {
 
-// Slack of the lazy rescale (base-2 units): P values stay below 2^8.
-constexpr float kSlack = 8.f;
+// Initial reference value: finite, so masked scores (-inf) give exp2 = 0
+// rather than NaN, and any real score overflows the first sum and forces
+// the recompute against the true maximum.
+constexpr float kMinit = -1.0e30f;
+// A lane whose 16 P values of a sub-block sum above this recomputes them
+// against the true maximum: every P used in a product is <= 2^16.
+constexpr float kRedoSum = 65536.f;
 
-// Two waves per SIMD (one from each of two resident workgroups) lets one
-// wave's softmax VALU work overlap the other's MFMAs; the register budget
-// (256 per lane) fits every variant except hd >= 96 with two query tiles.
+#define SAF_LDS_PTR(p) ((__attribute__((address_space(3))) void*)(p))
+
+// V tile: 64 key rows of HD values; row pitch VSEG 32-byte segments; the
+// logical segment s of key row r is stored at segment s ^ (r & 3), so the
+// four rows a 16-lane group of ds_read_b64_tr_b16 touches fall in four
+// different bank quarters.
+template <int HD> struct VRow {
+  static constexpr int VSEG = HD / 16 <= 4 ? 4 : 8;
+  static constexpr int PITCH = VSEG * 32;
+  static constexpr int CHP = 2 * VSEG;  // 16-byte chunks per row
+  static constexpr int BYTES = 64 * PITCH;
+};
+
+// One 64-key K and V tile copy by DMA: thread (wave w, lane L), load p
+// writes LDS chunk X = (4p + w) * 64 + L of the tile (buffer_load ... lds
+// puts consecutive lanes' 16 bytes at consecutive addresses from a
+// wave-uniform base).  The per-thread source (row in the tile, column) of
+// each chunk is the inverse of the tile's swizzle; padding chunks (hd 96)
+// re-read column 0.  Each tile gets a buffer descriptor starting at its
+// first row and ending after row T-1, so rows past the end read as zero
+// (those keys are masked, and zero V rows meet P = 0).  Buffer loads count
+// only vmcnt, which leaves the compiler's LDS-read waits exact.
+constexpr int kBufferWord3 = 0x00020000;  // gfx9 raw buffer: 32-bit data format, no swizzle
+
+template <typename T, int HD> struct TileDma {
+  static constexpr int KCH = HD / 8;
+  static constexpr int KCHP = KLayout<HD>::KCHP;
+  static constexpr int KN = KCHP / 4;
+  static constexpr int VN = VRow<HD>::CHP / 4;
+  uint32_t koff[KN], voff[VN];  // byte offset of this thread's chunks from the tile's first row
+
+  __device__ __forceinline__ void init(int wave, int lane, int64_t k_st, int64_t v_st) {
+#pragma unroll
+    for (int p = 0; p < KN; ++p) {
+      const int X = (4 * p + wave) * 64 + lane;
+      const int key = X / KCHP, slot = X % KCHP;
+      const int f = (key & 3) | ((key >> 1) & 4);
+      const int c = slot ^ (f & (KCHP - 1));
+      koff[p] = (uint32_t)(key * k_st * (int64_t)sizeof(T)) + 16u * (c < KCH ? c : 0);
+    }
+#pragma unroll
+    for (int p = 0; p < VN; ++p) {
+      const int X = (4 * p + wave) * 64 + lane;
+      const int key = X / VRow<HD>::CHP, pc = X % VRow<HD>::CHP;
+      const int c = 2 * ((pc >> 1) ^ (key & 3)) + (pc & 1);
+      voff[p] = (uint32_t)(key * v_st * (int64_t)sizeof(T)) + 16u * (c < KCH ? c : 0);
+    }
+  }
+
+  __device__ static __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const T* base, int64_t st, int j0, int T_len) {
+    const int64_t bytes = (int64_t)(T_len - j0) * st * (int64_t)sizeof(T);
+    const int num = (int)(bytes < 0 ? 0 : (bytes > 0x7fffffff ? 0x7fffffff : bytes));
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<T*>(base + (int64_t)j0 * st), 0, num, kBufferWord3);
+  }
+  __device__ __forceinline__ void load_k(const T* base, int64_t st, int j0, int T_len, char* tile, int wave) const {
+    const __amdgpu_buffer_rsrc_t r = rsrc(base, st, j0, T_len);
+#pragma unroll
+    for (int p = 0; p < KN; ++p)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(r, SAF_LDS_PTR(tile + (4 * p + wave) * 1024), 16, koff[p], 0, 0, 0);
+  }
+  __device__ __forceinline__ void load_v(const T* base, int64_t st, int j0, int T_len, char* tile, int wave) const {
+    const __amdgpu_buffer_rsrc_t r = rsrc(base, st, j0, T_len);
+#pragma unroll
+    for (int p = 0; p < VN; ++p)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(r, SAF_LDS_PTR(tile + (4 * p + wave) * 1024), 16, voff[p], 0, 0, 0);
+  }
+};
+
+typedef short short4_t __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ uint2 ds_read_tr16(const char* p) {
+  const short4_t r = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+      (__attribute__((address_space(3))) short4_t*)(p));
+  return __builtin_bit_cast(uint2, r);
+}
+
+template <typename T, int HD, int QT>
+struct FlashState {
+  static constexpr int NDT = HD / 32, NKT = HD / 16;
+  static constexpr int KCHP = KLayout<HD>::KCHP;
+  uint4 qf[QT][NKT];          // Q^T as B operand: lane (n, g), step t -> Q[q][16t + 8g + 0..7]
+  f32x16_t o[QT][NDT];        // O^T accumulators
+  float m_run[QT], l_run[QT];
+  int koff[NKT];              // byte offset of this lane's K A operand of step t in a sub-block
+  int voff[NDT];              // byte offset of this lane's V^T tr-read source for d tile dt
+  float c;                    // sm_scale * log2(e)
+  int n, g, q0w;
+
+  __device__ __forceinline__ void init_offsets(int lane) {
+    n = lane & 31;
+    g = lane >> 5;
+    const int key = kperm(n);
+#pragma unroll
+    for (int t = 0; t < NKT; ++t) koff[t] = 16 * KLayout<HD>::chunk(key, 2 * t + g);
+    const int i = lane & 15, gh = (lane >> 4) & 1;
+    const int vkey = 8 * g + (i >> 2);
+#pragma unroll
+    for (int dt = 0; dt < NDT; ++dt)
+      voff[dt] = vkey * VRow<HD>::PITCH + (((2 * dt + gh) ^ (i >> 2)) << 5) + 8 * (i & 3);
+  }
+
+  // S^T of sub-block ks (0/1) of the K tile: s[qt] = K_sub . Q^T
+  __device__ __forceinline__ void scores(f32x16_t (&s)[QT], const char* ktile, int ks) const {
+    uint4 ka[NKT];
+#pragma unroll
+    for (int t = 0; t < NKT; ++t)
+      ka[t] = *reinterpret_cast<const uint4*>(ktile + ks * 32 * KCHP * 16 + koff[t]);
+#pragma unroll
+    for (int qt = 0; qt < QT; ++qt) s[qt] = zero16();
+#pragma unroll
+    for (int t = 0; t < NKT; ++t)
+#pragma unroll
+      for (int qt = 0; qt < QT; ++qt) s[qt] = Elem<T>::mfma(ka[t], qf[qt][t], s[qt]);
+  }
+
+  // O^T += V_sub^T . P^T for sub-block ks of the V tile; P^T (packed) sits in
+  // registers 0..7 of the S tile it was computed from: words 4 s2 + 0..3 are
+  // the B operand of the 16-key step s2
+  __device__ __forceinline__ void pv(const f32x16_t (&pt)[QT], const char* vtile, int ks) {
+#pragma unroll
+    for (int s2 = 0; s2 < 2; ++s2)
+#pragma unroll
+      for (int dt = 0; dt < NDT; ++dt) {
+        const char* src = vtile + (32 * ks + 16 * s2) * VRow<HD>::PITCH + voff[dt];
+        const uint2 lo = ds_read_tr16(src);
+        const uint2 hi = ds_read_tr16(src + 4 * VRow<HD>::PITCH);
+        const uint4 a = make_uint4(lo.x, lo.y, hi.x, hi.y);
+#pragma unroll
+        for (int qt = 0; qt < QT; ++qt) {
+          const uint4 b = make_uint4(__float_as_uint(pt[qt][4 * s2]), __float_as_uint(pt[qt][4 * s2 + 1]),
+                                     __float_as_uint(pt[qt][4 * s2 + 2]), __float_as_uint(pt[qt][4 * s2 + 3]));
+          o[qt][dt] = Elem<T>::mfma(a, b, o[qt][dt]);
+        }
+      }
+  }
+
+  // keys past a query of this wave -> -inf (sub-block starting at key j0):
+  // register i of lane-half g holds key j0 + 8g + (16 (i / 8) + i % 8), so
+  // each element compares a constant against one per-lane limit
+  __device__ __forceinline__ void mask(f32x16_t (&s)[QT], int j0) const {
+#pragma unroll
+    for (int qt = 0; qt < QT; ++qt) {
+      const int lim = q0w + 32 * qt + n - j0 - 8 * g;
+#pragma unroll
+      for (int i = 0; i < 16; ++i)
+        if (16 * (i >> 3) + (i & 7) > lim) s[qt][i] = -INFINITY;
+    }
+  }
+
+  // P = 2^(s c - m) rounded to T, packed in place into registers 0..7 of s
+  // (word 4 sh + u = keys 16 sh + 8g + 2u, 2u + 1); bs = the lane's sum of
+  // its rounded P values
+  __device__ __forceinline__ void exp_pack(f32x16_t (&s)[QT], float (&bs)[QT]) const {
+#pragma unroll
+    for (int qt = 0; qt < QT; ++qt) {
+      const float mneg = -m_run[qt];
+      float sum = 0.f;
+#pragma unroll
+      for (int w = 0; w < 8; ++w) {
+        const float e0 = fast_exp2(fmaf(s[qt][2 * w], c, mneg));
+        const float e1 = fast_exp2(fmaf(s[qt][2 * w + 1], c, mneg));
+        const uint32_t word = Elem<T>::pack2(e0, e1);
+        sum = Elem<T>::sum2(word, sum);
+        s[qt][w] = __uint_as_float(word);
+      }
+      bs[qt] = sum;
+    }
+  }
+
+  // Rare path: S_u is recomputed from its K tile, the reference moves to
+  // max(m, block max) for every query of the wave, O and l are rescaled and
+  // P recomputed.  After it every P of the sub-block is <= 1.
+  __device__ __forceinline__ void redo(f32x16_t (&s)[QT], float (&bs)[QT], const char* ktile, int ks, int j0,
+                                       bool masked) {
+    scores(s, ktile, ks);
+    if (masked) mask(s, j0);
+#pragma unroll
+    for (int qt = 0; qt < QT; ++qt) {
+      float mx = s[qt][0];
+#pragma unroll
+      for (int i = 1; i < 16; ++i) mx = fmaxf(mx, s[qt][i]);
+      mx = half_swap_max(mx);
+      const float m_new = fmaxf(m_run[qt], mx * c);
+      const float alpha = fast_exp2(m_run[qt] - m_new);
+      m_run[qt] = m_new;
+      l_run[qt] *= alpha;
+#pragma unroll
+      for (int dt = 0; dt < NDT; ++dt)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) o[qt][dt][i] *= alpha;
+    }
+    exp_pack(s, bs);
+  }
+
+  // One pipeline step u.  On entry `nxt` holds P_{u-1} (packed) and `cur`
+  // holds S_u.  O += P_{u-1} V (tile vP, sub-block ksP) is issued first, then
+  // S_{u+1} overwrites `nxt` (tile kS, sub-block ksS), and the softmax of
+  // S_u packs P_u into `cur` (tile kR / sub-block ksR for the rare recompute).
+  __device__ __forceinline__ void step(f32x16_t (&cur)[QT], f32x16_t (&nxt)[QT], int u, bool masked, const char* kS,
+                                       int ksS, const char* kR, int ksR, const char* vP, int ksP) {
+    // the mask touches only S_u, complete before the step: applying it first
+    // keeps the MFMAs and the softmax below in one basic block
+    if (masked) mask(cur, 32 * u);
+    pv(nxt, vP, ksP);
+    scores(nxt, kS, ksS);
+    float bs[QT];
+    exp_pack(cur, bs);
+    bool bad = false;
+#pragma unroll
+    for (int qt = 0; qt < QT; ++qt) bad |= bs[qt] > kRedoSum;
+    if (__builtin_amdgcn_ballot_w64(bad)) redo(cur, bs, kR, ksR, 32 * u, masked);
+#pragma unroll
+    for (int qt = 0; qt < QT; ++qt) l_run[qt] += bs[qt];
+  }
+};
+
+// hd <= 64: two waves per SIMD (two resident workgroups) within 256
+// registers; larger heads take the SIMD's whole register file (and one
+// workgroup's LDS slots fill most of the CU).
 template <int HD, int QT>
-constexpr int flash_waves_per_eu() { return (HD <= 64 || QT == 1) ? 2 : 1; }
+constexpr int flash_waves_per_eu() { return HD <= 64 ? 2 : 1; }
 
 template <typename T, int HD, int QT>
 __global__ __launch_bounds__(256)
 __attribute__((amdgpu_waves_per_eu(flash_waves_per_eu<HD, QT>(), flash_waves_per_eu<HD, QT>())))
 void flash_fwd_kernel(const FlashParams p) {
-  constexpr int NW = 4, NTHR = 256;
+  using St = FlashState<T, HD, QT>;
+  constexpr int NW = 4;
   constexpr int BM = NW * 32 * QT;
-  constexpr int NDT = HD / 32;   // 32-wide d tiles of O^T
-  constexpr int NKT = HD / 16;   // 16-deep k steps of Q.K
-  __shared__ __align__(16) uint4 k_lds[2][KLayout<HD>::BYTES / 16];
-  __shared__ __align__(16) uint4 v_lds[2][VLayout<HD>::BYTES / 16];
+  constexpr int NDT = St::NDT, NKT = St::NKT;
+  constexpr int KB = KLayout<HD>::BYTES, VB = VRow<HD>::BYTES;
+  __shared__ __align__(16) char k0[KB], k1[KB], k2[KB];
+  __shared__ __align__(16) char v0[VB], v1[VB], v2[VB];
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (SGPR)
-  const int n = lane & 31, g = lane >> 5;
 
   // work item: query block (and key segment) of one (batch, live slot);
   // items are ordered heaviest first, (batch, live slot) fastest
@@ -67,157 +302,92 @@ void flash_fwd_kernel(const FlashParams p) {
 
   const int T_len = p.T;
   const int q0 = qb * BM;
-  const int q0w = q0 + wave * 32 * QT;
   const int nkb_qb = (min(q0 + BM, T_len) + 63) / 64;  // key blocks of the query block
   const int kb0 = p.n_items ? seg * p.seg_len : 0;     // this item's key-block range
   const int nkb = p.n_items ? min(kb0 + p.seg_len, nkb_qb) : nkb_qb;
   const bool split = p.n_items && p.part_base[qb] >= 0;
-  const int kend_w = min(q0w + 32 * QT, T_len);
-  const int nkb_w = kend_w > 0 ? (kend_w + 63) / 64 : 0;
+  // blocks wholly below the workgroup's first query need no causal mask
+  const int jd = min(nkb, max(kb0, q0 / 64));
 
-  // Q as the B operand: lane (n, g), step t -> Q[q][16t + 8g .. +7]
-  uint4 qf[QT][NKT];
+  St st;
+  st.init_offsets(lane);
+  st.q0w = q0 + wave * 32 * QT;
+  st.c = p.scale_log2;
+  TileDma<T, HD> dma;
+  dma.init(wave, lane, p.k_st, p.v_st);
+
+  // prologue DMA: K_kb0, K_kb0+1, V_kb0 into slot 0 / 1 / 0; slot 2 of V
+  // (the "V_{kb0-1}" of the first step, multiplied by P = 0) gets finite
+  // data too, since 0 * NaN from stale LDS would poison O
+  dma.load_k(kbase, p.k_st, 64 * kb0, T_len, k0, wave);
+  if (kb0 + 1 < nkb) dma.load_k(kbase, p.k_st, 64 * (kb0 + 1), T_len, k1, wave);
+  dma.load_v(vbase, p.v_st, 64 * kb0, T_len, v0, wave);
+  dma.load_v(vbase, p.v_st, 64 * kb0, T_len, v2, wave);
+
 #pragma unroll
   for (int qt = 0; qt < QT; ++qt) {
-    const int q = q0w + 32 * qt + n;
+    const int q = st.q0w + 32 * qt + st.n;
 #pragma unroll
     for (int t = 0; t < NKT; ++t)
-      qf[qt][t] = q < T_len ? *reinterpret_cast<const uint4*>(qbase + (int64_t)q * p.q_st + 16 * t + 8 * g)
-                            : make_uint4(0, 0, 0, 0);
-  }
-
-  f32x16_t o[QT][NDT];
-  float m_run[QT], l_run[QT];
+      st.qf[qt][t] = q < T_len ? *reinterpret_cast<const uint4*>(qbase + (int64_t)q * p.q_st + 16 * t + 8 * st.g)
+                               : make_uint4(0, 0, 0, 0);
+    st.m_run[qt] = kMinit;
+    st.l_run[qt] = 0.f;
 #pragma unroll
-  for (int qt = 0; qt < QT; ++qt) {
-    m_run[qt] = -INFINITY;
-    l_run[qt] = 0.f;
-#pragma unroll
-    for (int dt = 0; dt < NDT; ++dt) o[qt][dt] = zero16();
+    for (int dt = 0; dt < NDT; ++dt) st.o[qt][dt] = zero16();
   }
-  const float c = p.scale_log2;
-
-  KStager<T, HD, NTHR> kst;
-  VStager<T, HD, NTHR> vst;
-  kst.load(kbase, p.k_st, 64 * kb0, T_len, tid);
-  vst.load(vbase, p.v_st, 64 * kb0, T_len, tid);
-  kst.store(k_lds[0], tid);
-  vst.store(reinterpret_cast<uint32_t*>(v_lds[0]), tid);
   __syncthreads();
 
-  auto block = [&](const int j, auto masked) {
-    const int buf = (j - kb0) & 1;
-    const bool more = j + 1 < nkb;
-    if (more) {
-      kst.load(kbase, p.k_st, 64 * (j + 1), T_len, tid);
-      vst.load(vbase, p.v_st, 64 * (j + 1), T_len, tid);
-    }
-    if (j < nkb_w) {
-      const uint4* kt = k_lds[buf];
-      const uint4* vt = v_lds[buf];
-      // two 32-key sub-blocks: S^T, softmax and P.V per sub-block keeps the
-      // live S / P registers at 16 + 8 per query tile
+  // pipeline registers: sA / sB alternate between S_u and P_{u-1} / S_{u+1};
+  // P_{-1} = 0 makes the first P.V a no-op
+  f32x16_t sA[QT], sB[QT];
 #pragma unroll
-      for (int ks = 0; ks < 2; ++ks) {
-        const int j0 = 64 * j + 32 * ks;
-        f32x16_t sacc[QT];
-#pragma unroll
-        for (int qt = 0; qt < QT; ++qt) sacc[qt] = zero16();
-        const int key = 32 * ks + kperm(n);
-        // all A operands of the sub-block are read from LDS up front, so only
-        // the first MFMA waits for LDS latency
-        uint4 ka[NKT];
-#pragma unroll
-        for (int t = 0; t < NKT; ++t) ka[t] = kt[KLayout<HD>::chunk(key, 2 * t + g)];
-        // MFMA phases run at raised wave priority so that, of the two waves
-        // sharing a SIMD, the one with matrix work ready issues it first and
-        // the other fills the VALU with its softmax
-        __builtin_amdgcn_s_setprio(1);
-#pragma unroll
-        for (int t = 0; t < NKT; ++t)
-#pragma unroll
-          for (int qt = 0; qt < QT; ++qt) sacc[qt] = Elem<T>::mfma(ka[t], qf[qt][t], sacc[qt]);
-        __builtin_amdgcn_s_setprio(0);
-        // V^T operands of this sub-block arrive while the softmax runs
-        uint4 va[2][NDT];
-#pragma unroll
-        for (int sh = 0; sh < 2; ++sh)
-#pragma unroll
-          for (int dt = 0; dt < NDT; ++dt) va[sh][dt] = vt[VLayout<HD>::chunk(32 * dt + n, 4 * ks + 2 * sh + g)];
-        if (decltype(masked)::value && j0 + 31 > q0w) {  // keys past a query of this wave
-#pragma unroll
-          for (int qt = 0; qt < QT; ++qt) {
-            const int q = q0w + 32 * qt + n;
-#pragma unroll
-            for (int i = 0; i < 16; ++i)
-              if (j0 + acc_key(i, g) > q) sacc[qt][i] = -INFINITY;
-          }
-        }
-        uint4 pb[2][QT];
-#pragma unroll
-        for (int qt = 0; qt < QT; ++qt) {
-          float mx = sacc[qt][0];
-#pragma unroll
-          for (int i = 1; i < 16; ++i) mx = fmaxf(mx, sacc[qt][i]);
-          mx = half_swap_max(mx);
-          // Lazy rescaling: a query's reference max only moves when the block
-          // max exceeds it by more than kSlack (base-2 units), so P stays
-          // <= 2^kSlack and most blocks skip the O rescale.  Exact: O and l
-          // always share the same reference max.
-          const float mb = mx * c;
-          const bool up = mb > m_run[qt] + kSlack;
-          if (__builtin_amdgcn_ballot_w64(up)) {
-            const float m_new = up ? mb : m_run[qt];
-            const float alpha = up ? fast_exp2(m_run[qt] - m_new) : 1.f;
-            m_run[qt] = m_new;
-            l_run[qt] *= alpha;
-#pragma unroll
-            for (int dt = 0; dt < NDT; ++dt)
-#pragma unroll
-              for (int i = 0; i < 16; ++i) o[qt][dt][i] *= alpha;
-          }
-          const float mneg = -m_run[qt];
-          float psum = l_run[qt];
-#pragma unroll
-          for (int sh = 0; sh < 2; ++sh) {
-            uint32_t w[4];
-#pragma unroll
-            for (int u = 0; u < 4; ++u) {
-              const float e0 = fast_exp2(fmaf(sacc[qt][8 * sh + 2 * u], c, mneg));
-              const float e1 = fast_exp2(fmaf(sacc[qt][8 * sh + 2 * u + 1], c, mneg));
-              w[u] = Elem<T>::pack2(e0, e1);
-              psum = Elem<T>::sum2(w[u], psum);
-            }
-            pb[sh][qt] = make_uint4(w[0], w[1], w[2], w[3]);
-          }
-          l_run[qt] = psum;
-        }
-        __builtin_amdgcn_s_setprio(1);
-#pragma unroll
-        for (int sh = 0; sh < 2; ++sh)
-#pragma unroll
-          for (int dt = 0; dt < NDT; ++dt)
-#pragma unroll
-            for (int qt = 0; qt < QT; ++qt) o[qt][dt] = Elem<T>::mfma(va[sh][dt], pb[sh][qt], o[qt][dt]);
-        __builtin_amdgcn_s_setprio(0);
-      }
-    }
-    if (more) {
-      kst.store(k_lds[buf ^ 1], tid);
-      vst.store(reinterpret_cast<uint32_t*>(v_lds[buf ^ 1]), tid);
-    }
-    __syncthreads();
+  for (int qt = 0; qt < QT; ++qt) sB[qt] = zero16();
+  st.scores(sA, k0, 0);
+
+  // block j in phase R (slots: K_j = R, K_{j+1} = R+1, K_{j+2} = R+2 (loading),
+  // V_{j-1} = R+2, V_j = R, V_{j+1} = R+1 (loading), all mod 3); blocks at
+  // or past jd hold the diagonal and run the masked steps
+  auto block = [&](const int j, auto phase) {
+    constexpr int R = decltype(phase)::value;
+    char* const ks[3] = {k0, k1, k2};
+    char* const vs[3] = {v0, v1, v2};
+    char* const kJ = ks[R];
+    char* const kJ1 = ks[(R + 1) % 3];
+    char* const kJ2 = ks[(R + 2) % 3];
+    char* const vJm = vs[(R + 2) % 3];
+    char* const vJ = vs[R];
+    char* const vJ1 = vs[(R + 1) % 3];
+    if (j + 2 < nkb) dma.load_k(kbase, p.k_st, 64 * (j + 2), T_len, kJ2, wave);
+    if (j + 1 < nkb) dma.load_v(vbase, p.v_st, 64 * (j + 1), T_len, vJ1, wave);
+    const bool masked = j >= jd;
+    // u = 2j: S_{2j+1} from K_j sub 1, P_{2j-1} V_{j-1} sub 1, softmax S_{2j}
+    st.step(sA, sB, 2 * j, masked, kJ, 1, kJ, 0, vJm, 1);
+    // u = 2j+1: S_{2j+2} from K_{j+1} sub 0, P_{2j} V_j sub 0, softmax S_{2j+1}
+    st.step(sB, sA, 2 * j + 1, masked, kJ1, 0, kJ, 1, vJ, 0);
+    __syncthreads();  // waits for this block's DMA (vmcnt 0) before any wave moves on
   };
-  // blocks wholly below the workgroup's first query need no causal mask; the
-  // masked variant runs only for the last BM/64 blocks of a query block
-  const int jd = min(nkb, max(kb0, q0 / 64));
-  for (int j = kb0; j < jd; ++j) block(j, std::false_type());
-  for (int j = jd; j < nkb; ++j) block(j, std::true_type());
+  using P0 = std::integral_constant<int, 0>;
+  using P1 = std::integral_constant<int, 1>;
+  using P2 = std::integral_constant<int, 2>;
+  // blocks run as a chain of phases 0 -> 1 -> 2 -> 0, so every DMA target and
+  // every read names a static LDS slot
+  int j = kb0, ph;
+  for (;;) {
+    if (j >= nkb) { ph = 0; break; }
+    block(j++, P0());
+    if (j >= nkb) { ph = 1; break; }
+    block(j++, P1());
+    if (j >= nkb) { ph = 2; break; }
+    block(j++, P2());
+  }
+  // P_{2 nkb - 1} . V_{nkb-1} sub 1 (V_{nkb-1} sits in the slot of phase ph - 1)
+  st.pv(sB, ph == 1 ? v0 : (ph == 2 ? v1 : v2), 1);
 
 #pragma unroll
   for (int qt = 0; qt < QT; ++qt) {
-    const int q = q0w + 32 * qt + n;
-    const float l_tot = half_swap_sum(l_run[qt]);
+    const int q = st.q0w + 32 * qt + st.n;
+    const float l_tot = half_swap_sum(st.l_run[qt]);
     if (split) {
       // unnormalised partial of this key segment, merged by flash_combine_kernel
       const int64_t pidx = (int64_t)r * p.n_part_per_head + p.part_base[qb] + seg;
@@ -227,21 +397,20 @@ void flash_fwd_kernel(const FlashParams p) {
       for (int dt = 0; dt < NDT; ++dt)
 #pragma unroll
         for (int r4 = 0; r4 < 4; ++r4)
-          *reinterpret_cast<float4*>(po + 32 * dt + 8 * r4 + 4 * g) =
-              make_float4(o[qt][dt][4 * r4], o[qt][dt][4 * r4 + 1], o[qt][dt][4 * r4 + 2], o[qt][dt][4 * r4 + 3]);
-      if (g == 0) {
-        p.part_ml[(pidx * 2) * BM + rl] = m_run[qt];
+          *reinterpret_cast<float4*>(po + 32 * dt + 8 * r4 + 4 * st.g) =
+              make_float4(st.o[qt][dt][4 * r4], st.o[qt][dt][4 * r4 + 1], st.o[qt][dt][4 * r4 + 2],
+                          st.o[qt][dt][4 * r4 + 3]);
+      if (st.g == 0) {
+        p.part_ml[(pidx * 2) * BM + rl] = st.m_run[qt];
         p.part_ml[(pidx * 2 + 1) * BM + rl] = l_tot;
       }
       continue;
     }
     const float l_safe = l_tot == 0.f ? 1.f : l_tot;
     if (q < T_len) {
-      store_out_tile<T, HD>(obase + (int64_t)q * p.o_st, o[qt], 1.f / l_safe, g);
-      if (p.lse != nullptr && g == 0) {
-        const float m_store = m_run[qt] == -INFINITY ? 0.f : m_run[qt];
-        p.lse[b * p.l_sb + (int64_t)h * p.l_sh + (int64_t)q * p.l_st] = m_store + __log2f(l_safe);
-      }
+      store_out_tile<T, HD>(obase + (int64_t)q * p.o_st, st.o[qt], 1.f / l_safe, st.g);
+      if (p.lse != nullptr && st.g == 0)
+        p.lse[b * p.l_sb + (int64_t)h * p.l_sh + (int64_t)q * p.l_st] = st.m_run[qt] + __log2f(l_safe);
     }
   }
 }
@@ -309,6 +478,17 @@ __global__ __launch_bounds__(256) void flash_combine_kernel(const CombineParams 
       p.lse[b * p.l_sb + (int64_t)h * p.l_sh + (int64_t)q * p.l_st] = mref + __log2f(l == 0.f ? 1.f : l);
   }
 }
+
+// Explicit instantiations: every (dtype, head_dim, query tiles) the
+// launcher dispatches to gets its host stub emitted.
+#define SAF_FLASH_INST(T, HD, QT) template __global__ void flash_fwd_kernel<T, HD, QT>(const FlashParams);
+#define SAF_FLASH_INST_HD(T) \
+  SAF_FLASH_INST(T, 32, 1) SAF_FLASH_INST(T, 32, 2) SAF_FLASH_INST(T, 64, 1) SAF_FLASH_INST(T, 64, 2) \
+  SAF_FLASH_INST(T, 96, 1) SAF_FLASH_INST(T, 96, 2) SAF_FLASH_INST(T, 128, 1) SAF_FLASH_INST(T, 128, 2)
+SAF_FLASH_INST_HD(__bf16)
+SAF_FLASH_INST_HD(_Float16)
+#undef SAF_FLASH_INST_HD
+#undef SAF_FLASH_INST
 
 template <typename T, int HD, int QT>
 static hipError_t launch_flash_t(const FlashParams& p, hipStream_t s) {
