@@ -135,6 +135,16 @@ int saf_qk_rmsnorm_rope_inplace(const saf_tensor_t* q, const saf_tensor_t* k, co
                                 const saf_tensor_t* k_weight, float eps, const saf_tensor_t* cos,
                                 const saf_tensor_t* sin, void* stream);
 
+/* Residual add + LayerNorm of the GPT block, in place on the residual x
+ * (rows, C): x += delta when delta is present (one rounding to x's dtype),
+ * then out = (x - mean) * rsqrt(var + eps) * weight + bias over C, computed
+ * in fp32 from the rounded x (bias may be absent).  x, delta and out are 2-D
+ * bf16 / fp16 with unit channel stride; weight and bias (C,) in fp32, bf16
+ * or fp16.  C is even and at most 2048.  Replaces LayerNorm.forward (nanogpt/model.py:45-54) and the
+ * residual additions of Block.forward (:1214-1240) on the prefill path. */
+int saf_add_layernorm(const saf_tensor_t* x, const saf_tensor_t* delta, const saf_tensor_t* weight,
+                      const saf_tensor_t* bias, float eps, const saf_tensor_t* out, void* stream);
+
 /* Workspace needed by saf_frozen_scan_fwd for n_scan_heads closed-form heads
  * (0 bytes when there are none). */
 int64_t saf_workspace_bytes(int32_t B, int32_t T, int32_t head_dim, int32_t n_scan_heads);

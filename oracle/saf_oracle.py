@@ -20,9 +20,12 @@ Each function restates the reference's algorithm from its source
                           nanogpt/test_prior_flash.py:47-59 (exp(-dist/scale))
   refresh_routing         nanogpt/model.py:846-898 (_refresh_freeze_cache)
   rope                    nanogpt/model.py:57-99
+  add_layernorm           nanogpt/model.py:45-54 (LayerNorm, eps 1e-5) with the
+                          residual additions of Block.forward (:1214-1240)
 
 How each is pinned (tests/test_oracle.py): torch SDPA as the library special
-case of the all-live case; brute-force pure-Python loops on tiny inputs;
+case of the all-live case (torch.nn.functional.layer_norm likewise for
+add_layernorm); brute-force pure-Python loops on tiny inputs;
 closed forms (prefix sums, IIR recurrences, box filters) against the dense
 patterns; invariants (rows sum to 1, T = 1 gives y = v, frozen heads ignore
 Q/K, head-permutation equivariance); routing tables brute-forced over every
@@ -284,3 +287,19 @@ def apply_rope(x, cos, sin):
     half = x.shape[-1] // 2
     rot = np.concatenate([-x[..., half:], x[..., :half]], axis=-1)
     return x * cos + rot * sin
+
+
+def add_layernorm(x, delta, weight, bias=None, eps=1e-5, round_fn=None):
+    """Residual update and LayerNorm of the GPT block (nanogpt/model.py:45-54,
+    :1214-1240): x' = x + delta, rounded by round_fn to the activation dtype
+    (torch's bf16/fp16 add); y = (x' - mean) / sqrt(var + eps) * w + b over
+    the last axis, var the biased variance.  Returns (x', y) in float64."""
+    xn = _f64(x) if delta is None else _f64(x) + _f64(delta)
+    if round_fn is not None and delta is not None:
+        xn = round_fn(xn)
+    mean = xn.mean(-1, keepdims=True)
+    var = ((xn - mean) ** 2).mean(-1, keepdims=True)
+    y = (xn - mean) / np.sqrt(var + eps) * _f64(weight)
+    if bias is not None:
+        y = y + _f64(bias)
+    return xn, y

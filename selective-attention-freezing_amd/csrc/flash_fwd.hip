@@ -416,7 +416,8 @@ void flash_fwd_kernel(const FlashParams p) {
 }
 
 // Merge the key-segment partials of split query blocks (one workgroup per
-// (batch, slot, split query block); HD/4 threads x 4 columns per row): the
+// (batch, slot, split query block) and 64-row chunk; HD/4 threads x 4
+// columns per row): the
 // flash partials by their (m, l) rescaling, dense P.V partials (part_ml null)
 // by a plain sum.
 template <typename T, int HD>
@@ -437,7 +438,10 @@ __global__ __launch_bounds__(256) void flash_combine_kernel(const CombineParams 
   const int c4 = tid % CPR;
   T* obase = reinterpret_cast<T*>(p.out) + b * p.o_sb + (int64_t)h * p.o_sh;
   if (tid >= RPP * CPR) return;
-  for (int rl = tid / CPR; rl < BM; rl += RPP) {
+  // blockIdx.y picks a 64-row chunk of the query block: four times the
+  // workgroups of one per query block, for the latency of the partial reads
+  const int r_end = min(BM, 64 * ((int)blockIdx.y + 1));
+  for (int rl = 64 * (int)blockIdx.y + tid / CPR; rl < r_end; rl += RPP) {
     const int q = q0 + rl;
     if (q >= p.T) break;
     if (p.part_ml == nullptr) {  // dense P.V partials: a plain sum
@@ -521,7 +525,7 @@ hipError_t launch_flash(const FlashParams& p, int dtype, int hd, int qt, hipStre
 
 template <typename T>
 static hipError_t launch_combine_t(const CombineParams& p, int hd, hipStream_t s) {
-  const dim3 grid((unsigned)((int64_t)p.n_split * p.B * p.n_slots));
+  const dim3 grid((unsigned)((int64_t)p.n_split * p.B * p.n_slots), (unsigned)((p.BM + 63) / 64));
   switch (hd) {
     case 32: hipLaunchKernelGGL((flash_combine_kernel<T, 32>), grid, dim3(256), 0, s, p); break;
     case 64: hipLaunchKernelGGL((flash_combine_kernel<T, 64>), grid, dim3(256), 0, s, p); break;

@@ -1,0 +1,153 @@
+// Residual add + LayerNorm of the GPT block on gfx950 (the caller side of
+// the attention path: /root/reference/nanogpt/model.py:45-54 LayerNorm with
+// eps 1e-5 and optional bias, applied as in Block.forward :1214-1240,
+// x = x + attn(ln_1(x)); x = x + mlp(ln_2(x))).
+//
+// One wave per row: x += delta (one rounding to the activation dtype, as
+// torch's bf16/fp16 add), then y = (x - mean) * rsqrt(var + eps) * w + b
+// from the rounded x in fp32 (two passes over registers: mean, then the
+// centred sum of squares), one rounding of y.  Each lane holds NCH chunks of
+// VEC consecutive channels, chunk k at channel VEC * (64 k + lane), so every
+// load and store of the wave is one coalesced run; chunks past C are idle.
+#include "saf_kernels.h"
+
+namespace saf {
+
+template <typename T, int VEC> struct Vec;
+template <typename T> struct Vec<T, 4> {
+  using raw = uint2;
+  __device__ static inline void unpack(raw r, float (&f)[4]) {
+    f[0] = Elem<T>::lo(r.x); f[1] = Elem<T>::hi(r.x); f[2] = Elem<T>::lo(r.y); f[3] = Elem<T>::hi(r.y);
+  }
+  __device__ static inline raw pack(const float (&f)[4]) {
+    raw r;
+    r.x = Elem<T>::pack2(f[0], f[1]);
+    r.y = Elem<T>::pack2(f[2], f[3]);
+    return r;
+  }
+};
+template <typename T> struct Vec<T, 2> {
+  using raw = uint32_t;
+  __device__ static inline void unpack(raw r, float (&f)[2]) { f[0] = Elem<T>::lo(r); f[1] = Elem<T>::hi(r); }
+  __device__ static inline raw pack(const float (&f)[2]) { return Elem<T>::pack2(f[0], f[1]); }
+};
+
+__device__ inline float wave_sum(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+
+template <typename T, int VEC, int NCH>
+__global__ __launch_bounds__(256) void add_layernorm_kernel(const AddLnParams p) {
+  using V = Vec<T, VEC>;
+  using raw = typename V::raw;
+  const int lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= p.rows) return;
+  const int C = (int)p.C;
+  T* xr = reinterpret_cast<T*>(p.x) + row * p.x_rs;
+  const T* dr = p.delta ? reinterpret_cast<const T*>(p.delta) + row * p.d_rs : nullptr;
+  T* yr = reinterpret_cast<T*>(p.y) + row * p.y_rs;
+  float v[NCH][VEC];
+#pragma unroll
+  for (int k = 0; k < NCH; ++k) {
+    const int c = VEC * (64 * k + lane);
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) v[k][e] = 0.f;
+    if (c < C) {  // C is a multiple of VEC: a chunk is wholly in or out
+      V::unpack(*reinterpret_cast<const raw*>(xr + c), v[k]);
+      if (dr) {
+        float d[VEC];
+        V::unpack(*reinterpret_cast<const raw*>(dr + c), d);
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) v[k][e] += d[e];
+        const raw r = V::pack(v[k]);
+        *reinterpret_cast<raw*>(xr + c) = r;
+        V::unpack(r, v[k]);  // the statistics see the rounded residual, as torch's LayerNorm of it does
+      }
+    }
+  }
+  float s = 0.f;
+#pragma unroll
+  for (int k = 0; k < NCH; ++k)
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) s += v[k][e];
+  const float inv_c = 1.f / (float)C;
+  const float mean = wave_sum(s) * inv_c;
+  float q = 0.f;
+#pragma unroll
+  for (int k = 0; k < NCH; ++k)
+    if (VEC * (64 * k + lane) < C)
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) {
+        const float t = v[k][e] - mean;
+        q = fmaf(t, t, q);
+      }
+  const float rstd = rsqrtf(wave_sum(q) * inv_c + p.eps);
+#pragma unroll
+  for (int k = 0; k < NCH; ++k) {
+    const int c = VEC * (64 * k + lane);
+    if (c >= C) continue;
+    float o[VEC];
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) {
+      const float w = load_as_f32(p.w, c + e, p.wb_dtype);
+      const float b = p.b ? load_as_f32(p.b, c + e, p.wb_dtype) : 0.f;
+      o[e] = fmaf((v[k][e] - mean) * rstd, w, b);
+    }
+    *reinterpret_cast<raw*>(yr + c) = V::pack(o);
+  }
+}
+
+template <typename T, int VEC, int NCH>
+static hipError_t launch_ln_t(const AddLnParams& p, hipStream_t s) {
+  hipLaunchKernelGGL((add_layernorm_kernel<T, VEC, NCH>), dim3((unsigned)((p.rows + 3) / 4)), dim3(256), 0, s, p);
+  return hipGetLastError();
+}
+
+// Channel layouts: multiples of 256 use 8-byte chunks (VEC 4), other even C
+// up to 2048 4-byte chunks (VEC 2) with the tail lanes idle.
+template <typename T>
+static hipError_t launch_ln_dt(const AddLnParams& p, hipStream_t s) {
+  if (p.C % 256 == 0) {
+    switch (p.C / 256) {
+      case 1: return launch_ln_t<T, 4, 1>(p, s);
+      case 2: return launch_ln_t<T, 4, 2>(p, s);
+      case 3: return launch_ln_t<T, 4, 3>(p, s);
+      case 4: return launch_ln_t<T, 4, 4>(p, s);
+      case 5: return launch_ln_t<T, 4, 5>(p, s);
+      case 6: return launch_ln_t<T, 4, 6>(p, s);
+      case 7: return launch_ln_t<T, 4, 7>(p, s);
+      case 8: return launch_ln_t<T, 4, 8>(p, s);
+      default: return hipErrorInvalidValue;
+    }
+  }
+  switch ((p.C + 127) / 128) {
+    case 1: return launch_ln_t<T, 2, 1>(p, s);
+    case 2: return launch_ln_t<T, 2, 2>(p, s);
+    case 3: return launch_ln_t<T, 2, 3>(p, s);
+    case 4: return launch_ln_t<T, 2, 4>(p, s);
+    case 5: return launch_ln_t<T, 2, 5>(p, s);
+    case 6: return launch_ln_t<T, 2, 6>(p, s);
+    case 7: return launch_ln_t<T, 2, 7>(p, s);
+    case 8: return launch_ln_t<T, 2, 8>(p, s);
+    case 9: return launch_ln_t<T, 2, 9>(p, s);
+    case 10: return launch_ln_t<T, 2, 10>(p, s);
+    case 11: return launch_ln_t<T, 2, 11>(p, s);
+    case 12: return launch_ln_t<T, 2, 12>(p, s);
+    case 13: return launch_ln_t<T, 2, 13>(p, s);
+    case 14: return launch_ln_t<T, 2, 14>(p, s);
+    case 15: return launch_ln_t<T, 2, 15>(p, s);
+    case 16: return launch_ln_t<T, 2, 16>(p, s);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+hipError_t launch_add_layernorm(const AddLnParams& p, int dtype, hipStream_t s) {
+  if (dtype == kBF16) return launch_ln_dt<__bf16>(p, s);
+  if (dtype == kF16) return launch_ln_dt<_Float16>(p, s);
+  return hipErrorInvalidValue;
+}
+
+}  // namespace saf

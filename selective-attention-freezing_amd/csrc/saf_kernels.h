@@ -138,6 +138,20 @@ struct RopeParams {
   float eps;
 };
 
+// Residual add + LayerNorm of (rows, C) activations: x += delta (when
+// present), y = LayerNorm(x) * w + b.
+struct AddLnParams {
+  void* x;
+  const void* delta;  // may be null: plain LayerNorm of x
+  void* y;
+  const void* w;
+  const void* b;      // may be null
+  int64_t rows, C;
+  int64_t x_rs, d_rs, y_rs;  // row strides in elements
+  float eps;
+  int wb_dtype;
+};
+
 // Rows of one scan chunk for a head dimension (must match the kernel).
 inline int scan_chunk_rows(int hd) { return hd <= 64 ? 32 * 16 : 16 * 16; }
 
@@ -148,6 +162,7 @@ hipError_t launch_frozen_pv(const FrozenParams& p, int dtype, int hd, int mode, 
 hipError_t launch_scan(const ScanParams& p, int dtype, int hd, hipStream_t s);
 hipError_t launch_zero_u32(uint32_t* ptr, int64_t n, hipStream_t s);
 hipError_t launch_rope(const RopeParams& p, int dtype, hipStream_t s);
+hipError_t launch_add_layernorm(const AddLnParams& p, int dtype, hipStream_t s);
 
 // Queries per flash / frozen workgroup for a query-tile count.
 inline int block_rows(int qt) { return 4 * 32 * qt; }

@@ -424,7 +424,23 @@ class GPT(nn.Module):
 
     def forward_hidden(self, idx):
         x, rope = self.prepare_inputs(idx)
-        for block in self.transformer.h:
+        blocks = self.transformer.h
+        if (x.is_cuda and not torch.is_grad_enabled()
+                and x.dtype in (torch.bfloat16, torch.float16)):
+            # prefill: each residual add of Block.forward runs fused with the
+            # LayerNorm after it (ln_2, then the next block's ln_1 or ln_f);
+            # x is the embedding output, updated in place
+            x = x.contiguous()
+            ln = blocks[0].ln_1
+            h = _kernel_mod.add_layernorm_(x, None, ln.weight, ln.bias)
+            for i, block in enumerate(blocks):
+                a = block.attn(h, rope=rope)
+                h = _kernel_mod.add_layernorm_(x, a, block.ln_2.weight, block.ln_2.bias)
+                m = block.mlp(h)
+                ln = blocks[i + 1].ln_1 if i + 1 < len(blocks) else self.transformer.ln_f
+                h = _kernel_mod.add_layernorm_(x, m, ln.weight, ln.bias)
+            return h
+        for block in blocks:
             x = block(x, rope=rope)
         return self.transformer.ln_f(x)
 

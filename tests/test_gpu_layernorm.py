@@ -1,0 +1,60 @@
+"""GPU parity of the fused residual add + LayerNorm (saf_add_layernorm)
+against the oracle's restatement of the reference's LayerNorm and residual
+update (nanogpt/model.py:45-54, :1214-1240): the updated residual is bit-exact
+with torch's bf16/fp16 add, the normalised output within half-precision
+rounding of the float64 result."""
+import numpy as np
+import pytest
+import torch
+
+from oracle import saf_oracle as orc
+
+pytestmark = pytest.mark.gpu
+
+
+def _round(dtype):
+    return lambda a: torch.from_numpy(a).to(dtype).double().numpy()
+
+
+@pytest.mark.parametrize("C", [64, 130, 256, 768, 896, 1152, 2048])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("with_delta,with_bias,wdtype",
+                         [(True, False, "act"), (False, False, "act"), (True, True, "f32"), (True, True, "act")])
+def test_add_layernorm_matches_oracle(C, dtype, with_delta, with_bias, wdtype):
+    import kernel
+    g = torch.Generator().manual_seed(C + (7 if with_delta else 0))
+    rows = 37 if C > 1000 else 1000
+    x = (torch.randn(rows, C, generator=g) * 2 + 0.5).to(dtype)
+    d = torch.randn(rows, C, generator=g).to(dtype) if with_delta else None
+    wt = torch.float32 if wdtype == "f32" else dtype
+    w = (1 + 0.1 * torch.randn(C, generator=g)).to(wt)
+    b = (0.1 * torch.randn(C, generator=g)).to(wt) if with_bias else None
+    xd = x.cuda()
+    y = kernel.add_layernorm_(xd, None if d is None else d.cuda(), w.cuda(), None if b is None else b.cuda())
+    torch.cuda.synchronize()
+    ref_x = (x.cuda() + d.cuda()).cpu() if with_delta else x
+    assert torch.equal(xd.cpu(), ref_x), "residual update must be bit-exact with torch's add"
+    xn, yr = orc.add_layernorm(x.double().numpy(), None if d is None else d.double().numpy(), w.double().numpy(),
+                               None if b is None else b.double().numpy(), round_fn=_round(dtype))
+    err = np.abs(y.double().cpu().numpy() - yr).max()
+    tol = 3e-2 if dtype == torch.bfloat16 else 4e-3   # one rounding of O(1) values
+    assert err <= tol, f"C={C} {dtype}: max-abs {err:.3e} > {tol}"
+
+
+def test_add_layernorm_3d_view_and_rejections():
+    import kernel
+    x = torch.randn(2, 50, 768, dtype=torch.bfloat16, device="cuda")
+    d = torch.randn(2, 50, 768, dtype=torch.bfloat16, device="cuda")
+    w = torch.ones(768, dtype=torch.bfloat16, device="cuda")
+    ref = torch.nn.functional.layer_norm((x + d).float(), (768,), w.float(), None, 1e-5)
+    y = kernel.add_layernorm_(x, d, w)
+    assert y.shape == (2, 50, 768)
+    assert (y.float() - ref).abs().max().item() < 3e-2
+    with pytest.raises(NotImplementedError, match="not supported"):
+        kernel.add_layernorm_(torch.zeros(4, 2050, dtype=torch.bfloat16, device="cuda"), None,
+                              torch.ones(2050, device="cuda"))
+    with pytest.raises(NotImplementedError, match="bf16 / fp16"):
+        kernel.add_layernorm_(torch.zeros(4, 768, device="cuda"), None, torch.ones(768, device="cuda"))
+    with pytest.raises(ValueError, match="weight and bias"):
+        kernel.add_layernorm_(torch.zeros(4, 768, dtype=torch.bfloat16, device="cuda"), None,
+                              torch.ones(767, device="cuda"))

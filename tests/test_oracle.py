@@ -215,6 +215,22 @@ def test_rope_is_a_rotation():
         np.testing.assert_allclose(y[t, half:], zc.imag, atol=1e-12)
 
 
+def test_add_layernorm_matches_torch_layer_norm():
+    # the library special case: torch's LayerNorm of x + delta (float64)
+    g = torch.Generator().manual_seed(7)
+    x, d = torch.randn(5, 96, generator=g, dtype=torch.float64), torch.randn(5, 96, generator=g, dtype=torch.float64)
+    w, b = torch.randn(96, generator=g, dtype=torch.float64), torch.randn(96, generator=g, dtype=torch.float64)
+    xn, y = orc.add_layernorm(x.numpy(), d.numpy(), w.numpy(), b.numpy())
+    ref = torch.nn.functional.layer_norm(x + d, (96,), w, b, 1e-5)
+    assert np.allclose(xn, (x + d).numpy())
+    assert np.allclose(y, ref.numpy(), atol=1e-12)
+    _, y0 = orc.add_layernorm(x.numpy(), None, w.numpy(), None)
+    assert np.allclose(y0, torch.nn.functional.layer_norm(x, (96,), w, None, 1e-5).numpy(), atol=1e-12)
+    # a mean-free, unit-variance output before the affine map
+    _, y1 = orc.add_layernorm(x.numpy(), d.numpy(), np.ones(96), None)
+    assert np.allclose(y1.mean(-1), 0, atol=1e-12) and np.allclose(y1.var(-1), 1 / (1 + 1e-5 / (x + d).numpy().var(-1)))
+
+
 def test_planted_oracle_mistake_is_caught():
     """A transposed pattern (a plausible slip) breaks the causal-mean check."""
     T = 12
