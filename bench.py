@@ -27,6 +27,8 @@ import statistics
 import sys
 import time
 
+import numpy as np
+
 REPO = os.path.dirname(os.path.abspath(__file__))
 PKG = os.path.join(REPO, "selective-attention-freezing_amd")
 for _p in (PKG, REPO):
@@ -348,13 +350,63 @@ def run_c4(args):
     print(json.dumps(line), flush=True)
 
 
+def run_scan(args):
+    """Frozen-only sizing run of the closed-form scan (the HBM-bound frozen-head
+    kernel): every head of B=8, H=12, T=16384, hd=64 bf16 frozen to a seeded
+    mix of causal mean, exponential decay (rate ~U(0.001, 0.1)) and sliding
+    window (w ~U{64..1024}), i.e. 96 sequences of V read once and Y written
+    once (403 MB).  One step = one fused_mixed_attn call (the scan and its
+    workspace clear)."""
+    import torch
+    import kernel
+
+    B = args.batch or 8
+    T = args.seq_len or 16384
+    H, hd = 12, 64
+    g = torch.Generator().manual_seed(1337)
+    v = torch.randn(B, H, T, hd, generator=g).bfloat16().cuda()
+    kind = np.zeros(H, dtype=np.int32)
+    param = np.zeros(H, dtype=np.float32)
+    for h in range(H):
+        k = int(torch.randint(0, 3, (1,), generator=g))
+        if k == 0:
+            kind[h] = kernel.CLOSED_MEAN
+        elif k == 1:
+            kind[h], param[h] = kernel.CLOSED_DECAY, 0.001 + 0.099 * float(torch.rand(1, generator=g))
+        else:
+            kind[h], param[h] = kernel.CLOSED_WINDOW, float(int(torch.randint(64, 1025, (1,), generator=g)))
+    frozen = torch.full((H,), 2, dtype=torch.int32, device="cuda")
+    step = lambda: kernel.fused_mixed_attn(None, None, v, None, frozen, closed_form=(kind, param),
+                                           validate=False)
+    with torch.inference_mode():
+        step_ms, wall, summ = timed_steps(step, args.steps, args.warmup, True)
+    _, extra = kernel_rooflines(summ, None, None, args.steps)
+    scan = extra["frozen_scan"]
+    nbytes = scan["bytes_per_launch"]
+    total_ms = sum(step_ms)
+    line = {
+        "metric": "closed-form frozen-head scan throughput (1 GPU), HBM GB/s",
+        "value": round(nbytes * args.steps / (total_ms / 1000.0) / 1e9, 1), "unit": "GB/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(total_ms / args.steps, 4),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+        "data": "synthetic (V ~ N(0, 1), seed 1337)",
+        "config": {"workload": f"frozen-only sizing run: B={B}, H={H} all frozen (mean/decay/window), T={T}, "
+                               f"hd={hd}; V read once + Y written once = {nbytes} bytes per step",
+                   "kinds": [int(k) for k in kind], "params": [float(x) for x in param]},
+        "roofline": scan,
+        "cpu_baseline": None,
+    }
+    print(json.dumps(line), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=10)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--workload", choices=["c2", "c4"], default="c2",
-                    help="c2: 124M nanoGPT SAF-25%% at 16K (the headline); c4: Qwen-style GQA")
+    ap.add_argument("--workload", choices=["c2", "c4", "scan"], default="c2",
+                    help="c2: 124M nanoGPT SAF-25%% at 16K (the headline); c4: Qwen-style GQA; "
+                         "scan: frozen-only sizing run of the closed-form scan (HBM roofline)")
     ap.add_argument("--seq-len", type=int, default=None)
     ap.add_argument("--batch", type=int, default=None, help="c4 only (default 4)")
     ap.add_argument("--layers", type=int, default=None)
@@ -385,6 +437,9 @@ def main():
             dst.copy_(src)
         torch.cuda.synchronize()
         print(json.dumps({"copy_calibration_bytes": n, "copies": 5}), flush=True)
+        return
+    if args.workload == "scan":
+        run_scan(args)
         return
     if args.workload == "c4":
         if args.cpu_layers is None:

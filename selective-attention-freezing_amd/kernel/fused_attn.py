@@ -204,6 +204,16 @@ class KernelTimer:
 
 
 _TIMER = None
+_SIDE_STREAMS = {}
+
+
+def _side_stream(device):
+    """A second stream per device (default priority) for the closed-form scan,
+    which runs beside the MFMA-bound kernels of the same call."""
+    idx = device.index if device.index is not None else torch.cuda.current_device()
+    if idx not in _SIDE_STREAMS:
+        _SIDE_STREAMS[idx] = torch.cuda.Stream(device=idx)
+    return _SIDE_STREAMS[idx]
 
 
 def set_kernel_timer(timer):
@@ -329,29 +339,47 @@ def fused_mixed_attn(q, k, v, patt, frozen, hidx=None, pidx=None,
     args.workspace = None if ws is None else ws.data_ptr()
     args.workspace_bytes = ws_bytes
 
+    n_dense = int((frozen_h == 1).sum())
+    n_dec = int((frozen_h == 2).sum()) - n_scan
+
+    work = {"flash": (L.saf_flash_fwd, n_live * B * 4 * HD * T * (T + 1) // 2),
+            "scan": (L.saf_frozen_scan_fwd, n_scan * B * 2 * T * HD * v.element_size()),
+            "dense": (L.saf_frozen_dense_pv_fwd, n_dense * B * 2 * HD * T * (T + 1) // 2),
+            "decomp": (L.saf_frozen_decomp_fwd, n_dec * B * 2 * HD * T * (T + 1) // 2)}
+
     def run():
-        stream = _ext.current_stream_ptr(v.device)
         timer = _TIMER
-        if timer is None:
-            _ext.check(L.saf_mixed_attn_fwd(args, stream))
-            return out
-        n_dense = int((frozen_h == 1).sum())
-        n_dec = int((frozen_h == 2).sum()) - n_scan
-        work = {"flash": (L.saf_flash_fwd, n_live * B * 4 * HD * T * (T + 1) // 2),
-                "scan": (L.saf_frozen_scan_fwd, n_scan * B * 2 * T * HD * v.element_size()),
-                "dense": (L.saf_frozen_dense_pv_fwd, n_dense * B * 2 * HD * T * (T + 1) // 2),
-                "decomp": (L.saf_frozen_decomp_fwd, n_dec * B * 2 * HD * T * (T + 1) // 2)}
         cur = torch.cuda.current_stream(v.device)
-        for kind in KernelTimer.KINDS:
+
+        def launch(kind, strm):
             fn, w = work[kind]
-            if w == 0:
-                continue
+            if timer is None:
+                _ext.check(fn(args, strm.cuda_stream))
+                return
             e0 = torch.cuda.Event(enable_timing=True)
             e1 = torch.cuda.Event(enable_timing=True)
-            e0.record(cur)
-            _ext.check(fn(args, stream))
-            e1.record(cur)
+            e0.record(strm)
+            _ext.check(fn(args, strm.cuda_stream))
+            e1.record(strm)
             timer.records[kind].append((e0, e1, w))
+
+        if n_scan and (n_live or n_dense or n_dec):
+            # the HBM-bound scan of the closed-form heads on a side stream
+            # beside the MFMA-bound kernels: disjoint output rows and disjoint
+            # workspace regions; joined before returning
+            side = _side_stream(v.device)
+            side.wait_stream(cur)
+            launch("scan", side)
+            for kind in ("flash", "dense", "decomp"):
+                if work[kind][1]:
+                    launch(kind, cur)
+            cur.wait_stream(side)
+        elif timer is not None:
+            for kind in KernelTimer.KINDS:
+                if work[kind][1]:
+                    launch(kind, cur)
+        else:
+            _ext.check(L.saf_mixed_attn_fwd(args, cur.cuda_stream))
         return out
 
     if torch.is_grad_enabled() and any(
