@@ -164,6 +164,15 @@ int64_t saf_mixed_attn_workspace_bytes(const saf_mixed_attn_args* args);
  * has been synchronised: 1 if a wait hit its spin limit, else 0. */
 int saf_workspace_error(const void* workspace, void* stream, int32_t* error_out);
 
+/* Kernel timing: the next main kernel this host thread launches through an
+ * attention entry point (the flash, dense P.V, decomposed P.V or scan kernel;
+ * not the workspace clear or the merge of split query blocks) is bracketed by
+ * hipEventRecord(begin_event) and hipEventRecord(end_event) on its stream, so
+ * hipEventElapsedTime gives that kernel's own duration.  One-shot; two NULLs
+ * cancel.  No counterpart in the reference (profiling hook for the roofline
+ * measurement). */
+int saf_time_next_kernel(void* begin_event, void* end_event);
+
 const char* saf_last_error(void);
 const char* saf_version(void);
 

@@ -66,7 +66,6 @@ template <int HD> struct VRow {
 // first row and ending after row T-1, so rows past the end read as zero
 // (those keys are masked, and zero V rows meet P = 0).  Buffer loads count
 // only vmcnt, which leaves the compiler's LDS-read waits exact.
-constexpr int kBufferWord3 = 0x00020000;  // gfx9 raw buffer: 32-bit data format, no swizzle
 
 template <typename T, int HD> struct TileDma {
   static constexpr int KCH = HD / 8;

@@ -13,13 +13,27 @@
 // u_i = v_i - v_{i-w} for the window, and Z_i = i + 1, (1 - r^{i+1})/(1 - r)
 // or min(i + 1, w).  Reads V once and writes Y once, in fp32 arithmetic.
 //
-// Parallelisation: each (batch, head) sequence is cut into chunks of CH rows;
-// a workgroup takes a ticket from an atomic counter (chunk-major order, so a
-// chunk's predecessors always hold smaller tickets and are already running),
-// scans its chunk in registers (threads = column groups x row lanes, R rows
-// per thread), publishes its chunk aggregate, and obtains the carry from its
-// predecessors by decoupled look-back over tagged 64-bit words.  Every wait is
-// bounded by spin_limit.
+// Parallelisation: each (batch, head) sequence is cut into chunks of
+// NRL * R rows (32 KB of V for hd 64 / 128).  Workgroup g takes chunk
+// g / n_seq of sequence g % n_seq (chunk-major), so every predecessor of a
+// chunk has a lower workgroup index and was dispatched before it.  A
+// workgroup loads its chunk into registers (threads = column groups x row
+// lanes, R rows per thread, buffer loads whose range check zero-fills rows
+// >= T), scans it, publishes its chunk aggregate, obtains the carry from its
+// predecessors by decoupled look-back over one tagged 64-bit status word per
+// (sequence, chunk, column), and streams Y out with non-temporal stores.
+// Every wait is bounded by spin_limit.  There is no global ticket counter: a
+// single-address device-scope atomic per workgroup serialises at about one
+// per 30 ns on this chip, which alone bounded an earlier version to 45% of
+// HBM bandwidth.
+//
+// Window heads also load the lagged rows v_{i-w} (mostly L2 hits: chunk c of
+// a sequence runs on the same XCD as chunk c - 1 when n_seq is a multiple of
+// 8, and Y's non-temporal stores leave L2 to V).
+//
+// The look-back's sum order depends on which predecessors have published
+// their inclusive prefix, so results can differ between runs in the last
+// fp32 bit of the carry (well below one bf16 / fp16 rounding step).
 #include "saf_kernels.h"
 
 namespace saf {
@@ -29,53 +43,89 @@ __device__ inline uint64_t pack_word(uint32_t tag, float v) {
 }
 __device__ inline float word_value(uint64_t w) { return __uint_as_float((uint32_t)(w & 0xffffffffu)); }
 
-template <typename T, int HD, int R>
-__global__ __launch_bounds__(256) void scan_kernel(const ScanParams p) {
-  constexpr int NCG = HD / 8;                 // 16-byte column groups
-  constexpr int NRL = HD <= 64 ? 32 : 16;     // row lanes
-  constexpr int NTHR = NCG * NRL;
-  constexpr int CH = NRL * R;
-  constexpr int LOG_NRL = NRL == 32 ? 5 : 4;
-  __shared__ float sh_x[NRL][HD];
-  __shared__ float sh_carry[HD];
-  __shared__ uint32_t sh_ticket;
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 
+// Threads of a scan workgroup: NCG 16-byte column groups x NRL row lanes.
+template <int HD> struct ScanShape {
+  static constexpr int NCG = HD / 8;
+  static constexpr int NRL = HD == 32 ? 64 : (HD == 64 ? 32 : 16);
+  static constexpr int LOG_NRL = NRL == 64 ? 6 : (NRL == 32 ? 5 : 4);
+  static constexpr int NTHR = NCG * NRL;
+  static constexpr int R = 8;  // rows per thread
+  static constexpr int CH = NRL * R;
+};
+static_assert(ScanShape<32>::CH == 512 && ScanShape<64>::CH == 256 && ScanShape<96>::CH == 128 &&
+                  ScanShape<128>::CH == 128,
+              "scan_chunk_rows() must match ScanShape");
+
+// Predecessor status words read per look-back round trip.
+constexpr int kLookBack = 4;
+
+__device__ __forceinline__ uint4 buf_load(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  const u32x4_t x = __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0);
+  return make_uint4(x[0], x[1], x[2], x[3]);
+}
+
+template <typename T, int HD, int KIND, bool WS>
+__device__ __forceinline__ void scan_body(const ScanParams& p, int chunk, int seq, int slot, float (*sh_x)[HD],
+                                          float* sh_carry) {
+  using S = ScanShape<HD>;
+  constexpr int NCG = S::NCG, NRL = S::NRL, R = S::R, CH = S::CH;
   const int tid = threadIdx.x;
   const int cg = tid % NCG, rl = tid / NCG;
-  if (tid == 0) sh_ticket = atomicAdd(p.counter, 1u);
-  __syncthreads();
-  const int ticket = (int)sh_ticket;
-  const int nseq = p.B * p.n_slots;
-  const int chunk = ticket / nseq, seq = ticket % nseq;
-  const int b = seq / p.n_slots, slot = seq % p.n_slots;
-  const int kind = p.kind[slot];
+  const int b = seq / p.n_slots;
   const float prm = p.param[slot];
-  const float rate = kind == kScanDecay ? prm : 0.f;
-  const float rr = kind == kScanDecay ? expf(-rate) : 1.f;
-  const int win = kind == kScanWindow ? (int)prm : 0;
-  auto rpow = [&](float k) { return kind == kScanDecay ? expf(-rate * k) : 1.f; };
+  const float rate = KIND == kScanDecay ? prm : 0.f;
+  const float rr = KIND == kScanDecay ? expf(-rate) : 1.f;
+  const int win = KIND == kScanWindow ? (int)prm : 0;
+  auto rpow = [&](float k) { return KIND == kScanDecay ? expf(-rate * k) : 1.f; };
 
-  const T* vbase = reinterpret_cast<const T*>(p.v) + b * p.v_sb + (int64_t)p.v_head[slot] * p.v_sh + 8 * cg;
-  T* obase = reinterpret_cast<T*>(p.out) + b * p.o_sb + (int64_t)p.out_head[slot] * p.o_sh + 8 * cg;
+  // Buffer resources (uniform): V and Y rows of this chunk, and the lagged
+  // rows [c0 - win, c0 + CH - win) clipped to [0, T).  Offsets stay below
+  // CH row strides (< 2 GiB, checked by the host).
+  const int64_t vst = p.v_st * (int64_t)sizeof(T), ost = p.o_st * (int64_t)sizeof(T);
   const int T_len = p.T;
-  const int row0 = chunk * CH + rl * R;
+  const int c0 = chunk * CH;
+  const int nrow = min(CH, T_len - c0);
+  const char* vseq =
+      reinterpret_cast<const char*>(p.v) + (b * p.v_sb + (int64_t)p.v_head[slot] * p.v_sh) * (int64_t)sizeof(T);
+  char* oseq = reinterpret_cast<char*>(p.out) + (b * p.o_sb + (int64_t)p.out_head[slot] * p.o_sh) * (int64_t)sizeof(T);
+  const __amdgpu_buffer_rsrc_t vr =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(vseq) + c0 * vst, 0, (int)(nrow * vst), kBufferWord3);
+  const __amdgpu_buffer_rsrc_t orr = __builtin_amdgcn_make_buffer_rsrc(oseq + c0 * ost, 0, (int)(nrow * ost), kBufferWord3);
+  const int l0 = max(c0 - win, 0);
+  const int lrows = KIND == kScanWindow ? max(min(c0 + CH - win, T_len) - l0, 0) : 0;
+  const __amdgpu_buffer_rsrc_t lr =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(vseq) + l0 * vst, 0, (int)(lrows * vst), kBufferWord3);
+  const int r0 = rl * R;  // this thread's first row within the chunk
+  const uint32_t voff = (uint32_t)(r0 * vst) + 16u * cg;
+  const uint32_t ooff = (uint32_t)(r0 * ost) + 16u * cg;
 
-  uint4 raw[R], lag[R];
+  uint4 raw[R];
+#pragma unroll
+  for (int i = 0; i < R; ++i) raw[i] = buf_load(vr, voff + (uint32_t)(i * vst));
+  uint4 lag[R];  // window: v_{row - win} (zero before row 0 and past T)
 #pragma unroll
   for (int i = 0; i < R; ++i) {
-    const int row = row0 + i;
-    raw[i] = row < T_len ? *reinterpret_cast<const uint4*>(vbase + (int64_t)row * p.v_st) : make_uint4(0, 0, 0, 0);
-    lag[i] = make_uint4(0, 0, 0, 0);
-    if (kind == kScanWindow && row < T_len && row - win >= 0)
-      lag[i] = *reinterpret_cast<const uint4*>(vbase + (int64_t)(row - win) * p.v_st);
+    const int row = c0 + r0 + i, lrow = row - win;
+    const uint32_t off = (row < T_len && lrow >= 0) ? (uint32_t)((lrow - l0) * vst) + 16u * cg : 0x80000000u;
+    lag[i] = KIND == kScanWindow ? buf_load(lr, off) : make_uint4(0, 0, 0, 0);
   }
   auto unpack = [&](int i, float (&u)[8]) {
     const uint32_t w[4] = {raw[i].x, raw[i].y, raw[i].z, raw[i].w};
-    const uint32_t x[4] = {lag[i].x, lag[i].y, lag[i].z, lag[i].w};
 #pragma unroll
     for (int m = 0; m < 4; ++m) {
-      u[2 * m] = Elem<T>::lo(w[m]) - Elem<T>::lo(x[m]);
-      u[2 * m + 1] = Elem<T>::hi(w[m]) - Elem<T>::hi(x[m]);
+      u[2 * m] = Elem<T>::lo(w[m]);
+      u[2 * m + 1] = Elem<T>::hi(w[m]);
+    }
+    if (KIND == kScanWindow) {
+      const uint4 l = lag[i];
+      const uint32_t x[4] = {l.x, l.y, l.z, l.w};
+#pragma unroll
+      for (int m = 0; m < 4; ++m) {
+        u[2 * m] -= Elem<T>::lo(x[m]);
+        u[2 * m + 1] -= Elem<T>::hi(x[m]);
+      }
     }
   };
 
@@ -88,71 +138,141 @@ __global__ __launch_bounds__(256) void scan_kernel(const ScanParams p) {
     float u[8];
     unpack(i, u);
 #pragma unroll
-    for (int c = 0; c < 8; ++c) agg[c] = fmaf(agg[c], rr, u[c]);
+    for (int c = 0; c < 8; ++c) agg[c] = KIND == kScanDecay ? fmaf(agg[c], rr, u[c]) : agg[c] + u[c];
   }
+  // Keep the tile packed across the look-back: otherwise the compiler keeps
+  // the fp32 unpack of this phase alive for the output phase (2x the VGPRs).
 #pragma unroll
-  for (int c = 0; c < 8; ++c) sh_x[rl][8 * cg + c] = agg[c];
-  __syncthreads();
-
-  // inclusive scan over row lanes: X_rl = sum_{k <= rl} r^{R (rl - k)} agg_k
+  for (int i = 0; i < R; ++i) {
+    asm volatile("" : "+v"(raw[i].x), "+v"(raw[i].y), "+v"(raw[i].z), "+v"(raw[i].w));
+    if (KIND == kScanWindow) asm volatile("" : "+v"(lag[i].x), "+v"(lag[i].y), "+v"(lag[i].z), "+v"(lag[i].w));
+  }
+  // Scan over row lanes.  X_rl = sum_{k <= rl} r^{R (rl - k)} agg_k is the
+  // chunk-local state at row lane rl's last row; excl = X_{rl-1}.
+  constexpr bool kWaveScan = WS && 64 % NCG == 0;  // every wave holds whole row lanes
+  constexpr int RLW = kWaveScan ? 64 / NCG : 1;     // row lanes per wave
+  constexpr int NW = NRL / RLW;
+  float excl[8];
+  if constexpr (kWaveScan) {
+    // within the wave by shuffles, then one exchange of the wave totals
+    const int lr = rl % RLW, wv = rl / RLW;
+    float x[8];
 #pragma unroll
-  for (int st = 0; st < LOG_NRL; ++st) {
-    const int off = 1 << st;
-    const float f = rpow((float)(R * off));
-    float t[8];
+    for (int c = 0; c < 8; ++c) x[c] = agg[c];
 #pragma unroll
-    for (int c = 0; c < 8; ++c) t[c] = rl >= off ? sh_x[rl - off][8 * cg + c] * f : 0.f;
+    for (int off = 1; off < RLW; off <<= 1) {
+      const float f = rpow((float)(R * off));
+#pragma unroll
+      for (int c = 0; c < 8; ++c) {
+        const float y = __shfl_up(x[c], NCG * off, 64);
+        if (lr >= off) x[c] = fmaf(y, f, x[c]);
+      }
+    }
+    if (lr == RLW - 1)
+#pragma unroll
+      for (int c = 0; c < 8; ++c) sh_x[wv][8 * cg + c] = x[c];
+    __syncthreads();
+    // P = state at the last row before this wave's rows
+    const float fw = rpow((float)(R * RLW));
+    float P[8];
+#pragma unroll
+    for (int c = 0; c < 8; ++c) P[c] = 0.f;
+#pragma unroll
+    for (int w2 = 0; w2 < NW - 1; ++w2)
+      if (w2 < wv)
+#pragma unroll
+        for (int c = 0; c < 8; ++c) P[c] = fmaf(P[c], fw, sh_x[w2][8 * cg + c]);
+    const float fl = rpow((float)(R * lr));
+#pragma unroll
+    for (int c = 0; c < 8; ++c) {
+      const float y = __shfl_up(x[c], NCG, 64);
+      excl[c] = fmaf(P[c], fl, lr > 0 ? y : 0.f);
+    }
+  } else {
+    // Hillis-Steele over LDS
+#pragma unroll
+    for (int c = 0; c < 8; ++c) sh_x[rl][8 * cg + c] = agg[c];
     __syncthreads();
 #pragma unroll
-    for (int c = 0; c < 8; ++c) sh_x[rl][8 * cg + c] += t[c];
-    __syncthreads();
+    for (int st = 0; st < S::LOG_NRL; ++st) {
+      const int off = 1 << st;
+      const float f = rpow((float)(R * off));
+      float t[8];
+#pragma unroll
+      for (int c = 0; c < 8; ++c) t[c] = rl >= off ? sh_x[rl - off][8 * cg + c] * f : 0.f;
+      __syncthreads();
+#pragma unroll
+      for (int c = 0; c < 8; ++c) sh_x[rl][8 * cg + c] += t[c];
+      __syncthreads();
+    }
+#pragma unroll
+    for (int c = 0; c < 8; ++c) excl[c] = rl > 0 ? sh_x[rl - 1][8 * cg + c] : 0.f;
   }
 
-  // Decoupled look-back (wave 0; lane owns columns lane, lane + 64).  Each
-  // published value is one 64-bit word: tag in the high half (1 = chunk
-  // aggregate, 2 = inclusive prefix, 0 = not yet written), fp32 value in the
-  // low half, so a single relaxed device-scope atomic store publishes it and
-  // no fence (L2 write-back / invalidate) is needed on either side.  Columns
-  // are independent, so lanes may look back to different depths.
+  // Decoupled look-back (wave 0; lane owns columns lane, lane + 64).  The
+  // status word of (sequence, chunk, column) holds tag << 32 | fp32 value:
+  // tag 1 = chunk aggregate, 2 = inclusive prefix, 0 = not yet written, so a
+  // single relaxed device-scope atomic store publishes it and no fence (L2
+  // write-back / invalidate) is needed on either side.  Each round trip reads
+  // kLookBack predecessors, nearest first; chunk -1 reads as an inclusive
+  // prefix of 0.  Columns are independent, so lanes may look back to
+  // different depths.
   if (tid < 64) {
     const int lane = tid;
     constexpr int NC = (HD + 63) / 64;
-    const int64_t idx = (int64_t)seq * p.n_chunks + chunk;
     const float r_ch = rpow((float)CH);
+    uint64_t* sw_seq = p.status + (int64_t)seq * p.n_chunks * HD;
 #pragma unroll
     for (int u = 0; u < NC; ++u) {
       const int col = lane + 64 * u;
       if (col >= HD) continue;
-      const float a_wg = sh_x[NRL - 1][col];
+      float a_wg;  // chunk aggregate of the column
+      if constexpr (kWaveScan) {
+        const float fw = rpow((float)(R * RLW));
+        a_wg = 0.f;
+#pragma unroll
+        for (int w2 = 0; w2 < NW; ++w2) a_wg = fmaf(a_wg, fw, sh_x[w2][col]);
+      } else {
+        a_wg = sh_x[NRL - 1][col];
+      }
+      uint64_t* sw = sw_seq + col;
       float carry = 0.f;
       if (chunk > 0) {
-        __hip_atomic_store(p.agg + idx * HD + col, pack_word(1u, a_wg), __ATOMIC_RELAXED,
-                           __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(sw + (int64_t)chunk * HD, pack_word(1u, a_wg), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         float factor = 1.f;
         int k = chunk - 1;
         int spins = 0;
-        while (k >= 0) {
-          const int64_t kc = ((int64_t)seq * p.n_chunks + k) * HD + col;
-          const uint64_t wi = __hip_atomic_load(p.incl + kc, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-          if (wi >> 32) {
-            carry = fmaf(factor, word_value(wi), carry);
-            break;
+        for (;;) {
+          uint64_t w[kLookBack];
+#pragma unroll
+          for (int j = 0; j < kLookBack; ++j)
+            w[j] = k - j >= 0 ? __hip_atomic_load(sw + (int64_t)(k - j) * HD, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
+                              : pack_word(2u, 0.f);
+          bool open = true, done = false;
+          int used = 0;
+#pragma unroll
+          for (int j = 0; j < kLookBack; ++j) {
+            const uint32_t tag = (uint32_t)(w[j] >> 32);
+            if (open && tag != 0u) {
+              carry = fmaf(factor, word_value(w[j]), carry);
+              factor *= r_ch;
+              ++used;
+              done = done || tag == 2u;
+            }
+            open = open && tag == 1u;
           }
-          const uint64_t wa = __hip_atomic_load(p.agg + kc, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-          if (wa >> 32) {
-            carry = fmaf(factor, word_value(wa), carry);
-            factor *= r_ch;
-            --k;
-            continue;
+          if (done) break;
+          k -= used;
+          if (used == 0) {
+            if (++spins > p.spin_limit) {  // give up: carry incomplete, kernel still drains
+              atomicOr(p.error, 1u);
+              break;
+            }
+            __builtin_amdgcn_s_sleep(1);
           }
-          if (++spins > p.spin_limit) {  // give up: carry incomplete, kernel still drains
-            atomicOr(p.error, 1u);
-            break;
-          }
-          __builtin_amdgcn_s_sleep(1);
         }
       }
-      __hip_atomic_store(p.incl + idx * HD + col, pack_word(2u, fmaf(carry, r_ch, a_wg)), __ATOMIC_RELAXED,
+      __hip_atomic_store(sw + (int64_t)chunk * HD, pack_word(2u, fmaf(carry, r_ch, a_wg)), __ATOMIC_RELAXED,
                          __HIP_MEMORY_SCOPE_AGENT);
       sh_carry[col] = carry;
     }
@@ -164,35 +284,49 @@ __global__ __launch_bounds__(256) void scan_kernel(const ScanParams p) {
   {
     const float f = rpow((float)(R * rl));
 #pragma unroll
-    for (int c = 0; c < 8; ++c) {
-      const float prev = rl > 0 ? sh_x[rl - 1][8 * cg + c] : 0.f;
-      s[c] = fmaf(sh_carry[8 * cg + c], f, prev);
-    }
+    for (int c = 0; c < 8; ++c) s[c] = fmaf(sh_carry[8 * cg + c], f, excl[c]);
   }
-  const float em1 = kind == kScanDecay ? expm1f(-rate) : 0.f;
+  const float em1 = KIND == kScanDecay ? expm1f(-rate) : 0.f;
 #pragma unroll
   for (int i = 0; i < R; ++i) {
-    const int row = row0 + i;
+    const int row = c0 + r0 + i;
     float u[8];
     unpack(i, u);
 #pragma unroll
-    for (int c = 0; c < 8; ++c) s[c] = fmaf(s[c], rr, u[c]);
-    if (row < T_len) {
-      float inv;
-      if (kind == kScanDecay)
-        inv = em1 / expm1f(-rate * (float)(row + 1));
-      else if (kind == kScanWindow)
-        inv = 1.f / (float)min(row + 1, win);
-      else
-        inv = 1.f / (float)(row + 1);
-      uint4 w;
-      w.x = Elem<T>::pack2(s[0] * inv, s[1] * inv);
-      w.y = Elem<T>::pack2(s[2] * inv, s[3] * inv);
-      w.z = Elem<T>::pack2(s[4] * inv, s[5] * inv);
-      w.w = Elem<T>::pack2(s[6] * inv, s[7] * inv);
-      *reinterpret_cast<uint4*>(obase + (int64_t)row * p.o_st) = w;
-    }
+    for (int c = 0; c < 8; ++c) s[c] = KIND == kScanDecay ? fmaf(s[c], rr, u[c]) : s[c] + u[c];
+    float inv;
+    if (KIND == kScanDecay)
+      inv = em1 / expm1f(-rate * (float)(row + 1));
+    else if (KIND == kScanWindow)
+      inv = 1.f / (float)min(row + 1, win);
+    else
+      inv = 1.f / (float)(row + 1);
+    u32x4_t w;
+    w[0] = Elem<T>::pack2(s[0] * inv, s[1] * inv);
+    w[1] = Elem<T>::pack2(s[2] * inv, s[3] * inv);
+    w[2] = Elem<T>::pack2(s[4] * inv, s[5] * inv);
+    w[3] = Elem<T>::pack2(s[6] * inv, s[7] * inv);
+    // non-temporal: Y is not re-read, keep L2 for V (the window's lagged rows)
+    __builtin_amdgcn_raw_buffer_store_b128(w, orr, ooff + (uint32_t)(i * ost), 0, kBufferNT);
+    __builtin_amdgcn_sched_barrier(0);  // store as soon as the row is ready (frees its VGPRs)
   }
+}
+
+template <typename T, int HD, bool WS = true>
+__global__ __launch_bounds__(ScanShape<HD>::NTHR) __attribute__((amdgpu_waves_per_eu(4, 8))) void scan_kernel(
+    const ScanParams p) {
+  __shared__ float sh_x[ScanShape<HD>::NRL][HD];
+  __shared__ float sh_carry[HD];
+  const int nseq = p.B * p.n_slots;
+  const int chunk = (int)blockIdx.x / nseq, seq = (int)blockIdx.x % nseq;
+  const int slot = seq % p.n_slots;
+  const int kind = p.kind[slot];
+  if (kind == kScanDecay)
+    scan_body<T, HD, kScanDecay, WS>(p, chunk, seq, slot, sh_x, sh_carry);
+  else if (kind == kScanWindow)
+    scan_body<T, HD, kScanWindow, WS>(p, chunk, seq, slot, sh_x, sh_carry);
+  else
+    scan_body<T, HD, kScanMean, WS>(p, chunk, seq, slot, sh_x, sh_carry);
 }
 
 __global__ void zero_u32_kernel(uint32_t* ptr, int64_t n) {
@@ -208,9 +342,8 @@ hipError_t launch_zero_u32(uint32_t* ptr, int64_t n, hipStream_t s) {
 
 template <typename T, int HD>
 static hipError_t launch_scan_t(const ScanParams& p, hipStream_t s) {
-  constexpr int NTHR = (HD / 8) * (HD <= 64 ? 32 : 16);
   const dim3 grid((unsigned)((int64_t)p.n_chunks * p.B * p.n_slots));
-  hipLaunchKernelGGL((scan_kernel<T, HD, 16>), grid, dim3(NTHR), 0, s, p);
+  hipLaunchKernelGGL((scan_kernel<T, HD>), grid, dim3(ScanShape<HD>::NTHR), 0, s, p);
   return hipGetLastError();
 }
 

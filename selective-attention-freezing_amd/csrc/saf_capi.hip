@@ -69,19 +69,18 @@ bool supported_hd(int64_t hd) { return hd == 32 || hd == 64 || hd == 96 || hd ==
 
 int n_scan_chunks(int T, int hd) { return (T + scan_chunk_rows(hd) - 1) / scan_chunk_rows(hd); }
 
-// Workspace: [counter u32, error u32, pad to 256] [agg u64 x n] [incl u64 x n]
-// with n = n_seq * n_chunks * hd; the whole block is cleared before a scan.
+// Workspace: [reserved u32, error u32, pad to 256] [status u64 x n] with
+// n = n_seq * n_chunks * hd; the whole block is cleared before a scan.
 struct WsLayout {
-  int64_t agg_off, incl_off, total;
+  int64_t status_off, total;
 };
 
 WsLayout ws_layout(int64_t B, int64_t T, int hd, int64_t n_scan) {
-  WsLayout w{0, 0, 0};
+  WsLayout w{0, 0};
   if (n_scan <= 0 || T <= 0 || B <= 0) return w;
   const int64_t n = B * n_scan * n_scan_chunks((int)T, hd) * hd;
-  w.agg_off = 256;
-  w.incl_off = w.agg_off + 8 * n;
-  w.total = w.incl_off + 8 * n;
+  w.status_off = 256;
+  w.total = w.status_off + 8 * n;
   return w;
 }
 
@@ -205,6 +204,13 @@ int plan_and_validate(const saf_mixed_attn_args* a, unsigned which, Plan& pl, bo
         return fail(SAF_EUNSUPPORTED, "unsupported %s dtype %s", names[i], dtype_name(t.dtype));
     }
   }
+  if ((which & kDoScan) && !pl.scan.empty()) {
+    // the scan addresses one chunk of rows with 32-bit buffer offsets
+    const int64_t lim = (int64_t)1 << 31, es = 2, ch = scan_chunk_rows(pl.HD);
+    if (v.stride[2] * es * ch >= lim || o.stride[2] * es * ch >= lim)
+      return fail(SAF_EUNSUPPORTED, "closed-form heads: row stride of v or out too large (%lld x %lld rows >= 2 GiB)",
+                  (long long)std::max(v.stride[2], o.stride[2]) * es, (long long)ch);
+  }
   if (need_workspace && (which & kDoScan) && !pl.scan.empty()) {
     const WsLayout w = ws_layout(pl.B, pl.T, pl.HD, (int64_t)pl.scan.size());
     if (a->workspace == nullptr || a->workspace_bytes < w.total)
@@ -305,6 +311,22 @@ int launched(hipError_t e, const char* what) {
   return SAF_OK;
 }
 
+// Pending events of saf_time_next_kernel (per host thread, consumed by the
+// next main kernel).
+thread_local hipEvent_t g_time_begin = nullptr, g_time_end = nullptr;
+
+// Runs launch() between the pending timing events, if any, on stream s.
+template <class F>
+hipError_t timed(F&& launch, hipStream_t s) {
+  hipEvent_t b = g_time_begin, e = g_time_end;
+  if (b == nullptr) return launch();
+  g_time_begin = g_time_end = nullptr;
+  hipError_t rc = hipEventRecord(b, s);
+  if (rc == hipSuccess) rc = launch();
+  if (rc == hipSuccess) rc = hipEventRecord(e, s);
+  return rc;
+}
+
 int run_flash(const saf_mixed_attn_args* a, const Plan& pl, hipStream_t s) {
   if (pl.live.empty() || pl.T == 0 || pl.B == 0) return SAF_OK;
   FlashParams p{};
@@ -355,7 +377,7 @@ int run_flash(const saf_mixed_attn_args* a, const Plan& pl, hipStream_t s) {
     p.k_head[i] = (int16_t)(a->kvidx ? a->kvidx[h] : slot);
     p.v_head[i] = (int16_t)(a->kvidx ? a->kvidx[h] : h);
   }
-  if (int rc = launched(launch_flash(p, pl.dtype, pl.HD, qt, s), "flash")) return rc;
+  if (int rc = launched(timed([&] { return launch_flash(p, pl.dtype, pl.HD, qt, s); }, s), "flash")) return rc;
   if (fp.n_split == 0) return SAF_OK;
   CombineParams c{};
   c.out = p.out;
@@ -420,7 +442,7 @@ int run_dense(const saf_tensor_t& patt, const saf_tensor_t& v, const saf_tensor_
   } else {
     fp = FlashPlan();
   }
-  if (int rc = launched(launch_frozen_pv(p, dtype, HD, 0, s), "dense P.V")) return rc;
+  if (int rc = launched(timed([&] { return launch_frozen_pv(p, dtype, HD, 0, s); }, s), "dense P.V")) return rc;
   if (fp.n_split == 0) return SAF_OK;
   CombineParams c{};
   c.out = p.out;
@@ -450,7 +472,7 @@ int run_decomp(const saf_mixed_attn_args* a, const Plan& pl, hipStream_t s) {
     p.v_head[i] = (int16_t)(a->kvidx ? a->kvidx[h] : h);
     p.pat_head[i] = (int16_t)h;
   }
-  return launched(launch_frozen_pv(p, pl.dtype, pl.HD, 1, s), "decomposed P.V");
+  return launched(timed([&] { return launch_frozen_pv(p, pl.dtype, pl.HD, 1, s); }, s), "decomposed P.V");
 }
 
 int run_scan(const saf_mixed_attn_args* a, const Plan& pl, hipStream_t s) {
@@ -466,10 +488,8 @@ int run_scan(const saf_mixed_attn_args* a, const Plan& pl, hipStream_t s) {
   p.T = pl.T;
   p.n_slots = (int)pl.scan.size();
   p.n_chunks = n_scan_chunks(pl.T, pl.HD);
-  p.counter = reinterpret_cast<uint32_t*>(ws);
   p.error = reinterpret_cast<uint32_t*>(ws + 4);
-  p.agg = reinterpret_cast<uint64_t*>(ws + w.agg_off);
-  p.incl = reinterpret_cast<uint64_t*>(ws + w.incl_off);
+  p.status = reinterpret_cast<uint64_t*>(ws + w.status_off);
   p.spin_limit = a->scan_spin_limit > 0 ? a->scan_spin_limit : (1 << 20);
   for (int i = 0; i < p.n_slots; ++i) {
     const int h = pl.scan[i];
@@ -478,8 +498,8 @@ int run_scan(const saf_mixed_attn_args* a, const Plan& pl, hipStream_t s) {
     p.kind[i] = (int8_t)a->closed_kind[h];
     p.param[i] = a->closed_param[h];
   }
-  if (int rc = launched(launch_zero_u32(p.counter, w.total / 4, s), "workspace clear")) return rc;
-  return launched(launch_scan(p, pl.dtype, pl.HD, s), "closed-form scan");
+  if (int rc = launched(launch_zero_u32(reinterpret_cast<uint32_t*>(ws), w.total / 4, s), "workspace clear")) return rc;
+  return launched(timed([&] { return launch_scan(p, pl.dtype, pl.HD, s); }, s), "closed-form scan");
 }
 
 int run_dense_mixed(const saf_mixed_attn_args* a, const Plan& pl, hipStream_t s) {
@@ -709,6 +729,14 @@ int saf_workspace_error(const void* workspace, void* stream, int32_t* error_out)
   if (rc == hipSuccess) rc = hipStreamSynchronize(s);
   if (rc != hipSuccess) return fail(SAF_ELAUNCH, "reading the workspace failed: %s", hipGetErrorString(rc));
   *error_out = (int32_t)e;
+  return SAF_OK;
+}
+
+int saf_time_next_kernel(void* begin_event, void* end_event) {
+  if ((begin_event == nullptr) != (end_event == nullptr))
+    return fail(SAF_EINVAL, "saf_time_next_kernel takes two events or none");
+  g_time_begin = reinterpret_cast<hipEvent_t>(begin_event);
+  g_time_end = reinterpret_cast<hipEvent_t>(end_event);
   return SAF_OK;
 }
 

@@ -39,6 +39,11 @@ typedef float f32x16_t __attribute__((ext_vector_type(16)));
 
 constexpr float kLog2e = 1.4426950408889634f;  // 1 / ln(2)
 
+// Word 3 of a raw gfx9 buffer resource: 32-bit data format, no swizzle.
+constexpr int kBufferWord3 = 0x00020000;
+// Cache-policy operand of buffer stores: non-temporal (streaming) store.
+constexpr int kBufferNT = 2;
+
 // ---- element types: bf16 and fp16 storage, fp32 arithmetic -----------------
 
 template <typename T> struct Elem;

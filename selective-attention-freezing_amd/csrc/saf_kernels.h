@@ -98,7 +98,8 @@ static_assert(sizeof(FrozenParams) <= 4096, "FrozenParams must fit the kernel ar
 
 // Closed-form frozen heads (state 2 heads recognised as causal mean,
 // exponential decay or sliding window): a single-pass chunked scan along T
-// with decoupled look-back between chunks.
+// with decoupled look-back between chunks (workgroup g = chunk g / n_seq of
+// sequence g % n_seq).
 enum : int { kScanMean = 1, kScanDecay = 2, kScanWindow = 3 };
 
 struct ScanParams {
@@ -107,12 +108,10 @@ struct ScanParams {
   int64_t v_sb, v_sh, v_st;
   int64_t o_sb, o_sh, o_st;
   int B, T, n_slots, n_chunks;
-  uint32_t* counter;  // ticket counter (zeroed before launch)
-  uint32_t* error;    // set to 1 if a look-back wait hit the spin limit
-  // [n_seq * n_chunks * HD] tagged words (tag << 32 | fp32 bits), zeroed
-  // before launch: chunk aggregates and inclusive prefixes
-  uint64_t* agg;
-  uint64_t* incl;
+  uint32_t* error;  // set to 1 if a look-back wait hit the spin limit
+  // [n_seq][n_chunks][HD] status words (tag << 32 | fp32 bits), zeroed before
+  // launch: tag 1 = chunk aggregate, 2 = inclusive prefix
+  uint64_t* status;
   int spin_limit;
   int16_t out_head[kMaxHeads];
   int16_t v_head[kMaxHeads];
@@ -152,8 +151,9 @@ struct AddLnParams {
   int wb_dtype;
 };
 
-// Rows of one scan chunk for a head dimension (must match the kernel).
-inline int scan_chunk_rows(int hd) { return hd <= 64 ? 32 * 16 : 16 * 16; }
+// Rows of one scan chunk for a head dimension (must match ScanShape in the
+// kernel): 8 rows per thread, 32 KB of V per chunk for hd 64 / 128.
+inline int scan_chunk_rows(int hd) { return hd == 32 ? 512 : (hd == 64 ? 256 : 128); }
 
 // Launchers: return hipSuccess or the launch error.  dtype is kBF16 / kF16.
 hipError_t launch_flash(const FlashParams& p, int dtype, int hd, int qt, hipStream_t s);

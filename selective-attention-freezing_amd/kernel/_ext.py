@@ -24,7 +24,7 @@ EXPORTS = ("saf_mixed_attn_fwd", "saf_flash_fwd", "saf_frozen_dense_pv_fwd",
            "saf_frozen_decomp_fwd", "saf_frozen_scan_fwd", "saf_frozen_pv_fwd",
            "saf_rope_qk_inplace", "saf_qk_rmsnorm_rope_inplace", "saf_add_layernorm",
            "saf_workspace_bytes", "saf_mixed_attn_workspace_bytes",
-           "saf_workspace_error", "saf_last_error", "saf_version")
+           "saf_workspace_error", "saf_time_next_kernel", "saf_last_error", "saf_version")
 
 
 class SafTensor(ctypes.Structure):
@@ -92,6 +92,8 @@ def lib():
         L.saf_mixed_attn_workspace_bytes.restype = ctypes.c_int64
         L.saf_workspace_error.argtypes = [ctypes.c_void_p, ctypes.c_void_p, P(ctypes.c_int32)]
         L.saf_workspace_error.restype = ctypes.c_int
+        L.saf_time_next_kernel.argtypes = [ctypes.c_void_p, ctypes.c_void_p]
+        L.saf_time_next_kernel.restype = ctypes.c_int
         L.saf_last_error.argtypes = []
         L.saf_last_error.restype = ctypes.c_char_p
         L.saf_version.argtypes = []

@@ -183,8 +183,11 @@ def _aligned_view(t, align=16):
 
 
 class KernelTimer:
-    """Brackets each per-kind launch of fused_mixed_attn with HIP events on the
-    launch stream and records the algorithmic work of that launch:
+    """Times the main kernel of each per-kind launch of fused_mixed_attn with
+    HIP events that the library records on the launch stream right around
+    that kernel (saf_time_next_kernel: the flash, dense P.V, decomposed P.V or
+    scan kernel alone, without the workspace clear or the merge of split
+    query blocks), and records the algorithmic work of that launch:
     flash: 4*hd*T(T+1)/2 flops per (batch, live head); scan: V read once and
     Y written once, 2*T*hd*elem bytes per (batch, closed-form head)."""
 
@@ -358,9 +361,12 @@ def fused_mixed_attn(q, k, v, patt, frozen, hidx=None, pidx=None,
                 return
             e0 = torch.cuda.Event(enable_timing=True)
             e1 = torch.cuda.Event(enable_timing=True)
-            e0.record(strm)
-            _ext.check(fn(args, strm.cuda_stream))
+            e0.record(strm)  # creates the HIP events; the library re-records them
             e1.record(strm)
+            _ext.check(L.saf_time_next_kernel(e0.cuda_event, e1.cuda_event))
+            rc = fn(args, strm.cuda_stream)
+            L.saf_time_next_kernel(None, None)  # never left pending for a later call
+            _ext.check(rc)
             timer.records[kind].append((e0, e1, w))
 
         if n_scan and (n_live or n_dense or n_dec):

@@ -32,9 +32,12 @@ def test_library_loads_and_exports_header_symbols():
 def test_workspace_bytes():
     L = _ext.lib()
     assert L.saf_workspace_bytes(8, 16384, 64, 0) == 0
+    # 256-byte header (error word) + one 8-byte status word per (sequence,
+    # 256-row chunk, column) at hd 64
     n = L.saf_workspace_bytes(8, 16384, 64, 12)
-    nseq, nch = 8 * 12, 16384 // 512
-    assert n >= 8 + 4 * nseq * nch + 2 * 4 * nseq * nch * 64
+    nseq, nch = 8 * 12, 16384 // 256
+    assert n == 256 + 8 * nseq * nch * 64
+    assert L.saf_workspace_bytes(1, 1000, 128, 1) == 256 + 8 * 8 * 128   # 128-row chunks at hd 128
     assert L.saf_workspace_bytes(1, 1000, 80, 3) == 0   # unsupported head dim
 
 
