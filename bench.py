@@ -85,14 +85,15 @@ def build_c2_model(T, device, dtype, seed=1337, n_layer=12):
 
 
 TRAFFIC_FILE = os.path.join(REPO, "profiles", "flash_fwd_c2_hbm_traffic.txt")
+SCAN_TRAFFIC_FILE = os.path.join(REPO, "profiles", "frozen_scan_sizing_hbm_traffic.txt")
 
 
-def pmc_traffic(kernel_label):
-    """HBM bytes per dispatch of a kernel from the committed rocprofv3
+def pmc_traffic(kernel_label, path=TRAFFIC_FILE):
+    """HBM bytes per dispatch of a kernel from a committed rocprofv3
     FETCH_SIZE / WRITE_SIZE summary (copy-calibrated), or None."""
-    if not os.path.exists(TRAFFIC_FILE):
+    if not os.path.exists(path):
         return None
-    for line in open(TRAFFIC_FILE):
+    for line in open(path):
         if line.startswith(kernel_label + ":"):
             for part in line.split(","):
                 k, _, v = part.partition("=")
@@ -382,6 +383,10 @@ def run_scan(args):
         step_ms, wall, summ = timed_steps(step, args.steps, args.warmup, True)
     _, extra = kernel_rooflines(summ, None, None, args.steps)
     scan = extra["frozen_scan"]
+    if (B, T) == (8, 16384):
+        scan["traffic"] = pmc_traffic("scan_kernel<bf16,64>", SCAN_TRAFFIC_FILE)
+        scan["traffic_source"] = os.path.relpath(SCAN_TRAFFIC_FILE, REPO)
+    scan["kernel"] = "scan_kernel<bf16,64>"
     nbytes = scan["bytes_per_launch"]
     total_ms = sum(step_ms)
     line = {
