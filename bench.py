@@ -351,6 +351,92 @@ def run_c4(args):
     print(json.dumps(line), flush=True)
 
 
+def build_c3_model(T, L, device, seed=1337):
+    """1B-class SAF model (24 layers, d_model 2048, 16
+    heads, hd 128, vocab 50304, RoPE, no bias), bf16 random init; per layer
+    the heads randperm(16, seed + layer)[:4] are frozen to dense
+    lower-triangular row-stochastic patterns softmax(N(0,1) logits masked
+    causally), stored compactly in bf16 as (4, T, T)."""
+    import torch
+    from nanogpt.model import GPT, GPTConfig
+
+    torch.manual_seed(seed)
+    cfg = GPTConfig(block_size=T, vocab_size=50304, n_layer=L, n_head=16, n_embd=2048, bias=False,
+                    position_encoding="rope", rand_attn_prior_repr="dense", freeze_pattern_dtype="bfloat16",
+                    rand_seed=seed)
+    model = GPT(cfg).to(device=device, dtype=torch.bfloat16).eval()
+    causal = torch.ones(T, T, dtype=torch.bool, device=device).tril()
+    plan = {}
+    for layer in range(L):
+        heads = torch.randperm(cfg.n_head, generator=torch.Generator().manual_seed(seed + layer))[:4].tolist()
+        g = torch.Generator(device=device).manual_seed(seed + layer)
+        logits = torch.randn(len(heads), T, T, generator=g, device=device)
+        logits.masked_fill_(~causal, float("-inf"))
+        model.transformer.h[layer].attn.freeze_heads(heads, torch.softmax(logits, dim=-1))
+        del logits
+        plan[layer] = [(h, "dense", 0.0) for h in heads]
+    x = torch.randint(0, 50257, (2, T), generator=torch.Generator().manual_seed(seed + 1)).to(device)
+    return model, x, plan
+
+
+def run_c3(args):
+    """C3 prefill: last-position logits of the 1B-class model at B=2,
+    T=8192, with the live-head flash (hd 128) and the dense P.V rooflines."""
+    import torch
+    from nanogpt import model as model_mod
+
+    dev = "cuda"
+    T = args.seq_len or 8192
+    L = args.layers or 24
+    log(f"building C3 model T={T} layers={L}")
+    model, x, plan = build_c3_model(T, L, dev)
+    B = x.size(0)
+    H, hd = 16, 128
+    n_dense = sum(len(v) for v in plan.values())
+    n_live = L * H - n_dense
+    with torch.inference_mode():
+        before = model_mod.fused_dispatch_count()
+        model(x)
+        torch.cuda.synchronize()
+        if model_mod.fused_dispatch_count() - before != L:
+            raise RuntimeError("dispatch verification failed")
+        step_ms, wall, summ = timed_steps(lambda: model(x), args.steps, args.warmup, not args.no_timer)
+    total_ms = sum(step_ms)
+    tok_s = x.numel() * args.steps / (total_ms / 1000.0)
+    roof, extra = kernel_rooflines(summ, "flash_fwd_kernel<bf16,128,1>", None, args.steps)
+    if summ is not None and "dense" in summ:
+        n, ms, flops = summ["dense"]
+        per_ms = ms / n
+        # pattern causal half read once per head (batch innermost), V read and Y written per (b, h)
+        nbytes = (n_dense // L) * (T * (T + 1) // 2 * 2 + B * 2 * T * hd * 2)
+        gbs = nbytes / (per_ms / 1000.0) / 1e9
+        tfs = (flops / n) / (per_ms / 1000.0) / 1e12
+        t_hbm, t_mfma = nbytes / (PEAK_HBM_GBS * 1e9), (flops / n) / (PEAK_BF16_TFLOPS * 1e12)
+        extra["frozen_dense_pv"] = {
+            "bound": "hbm" if t_hbm >= t_mfma else "mfma", "kernel": "frozen_pv_kernel<bf16,128,dense>",
+            "achieved_gbs": round(gbs, 1), "achieved_tflops": round(tfs, 1),
+            "frac": round(max(t_hbm, t_mfma) / (per_ms / 1000.0), 4),
+            "bytes_per_launch": nbytes, "flop_per_launch": flops // n,
+            "launches": n, "avg_launch_ms": round(per_ms, 4)}
+    log(f"GPU: {tok_s:.0f} tokens/s, {total_ms / args.steps:.2f} ms/step")
+    line = {
+        "metric": "prefill tokens/sec (1 GPU), 1B-class SAF model with dense frozen patterns",
+        "value": round(tok_s, 1), "unit": "tokens/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(total_ms / args.steps, 3),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+        "data": "synthetic (random-init weights and patterns seed 1337, uniform random tokens)",
+        "config": {"workload": f"C3: 1B-class SAF prefill, {L}L d2048 16H hd128, B={B}, T={T}, "
+                               f"{n_dense}/{L * H} heads frozen to dense bf16 patterns, {n_live} live",
+                   "batch": B, "seq_len": T,
+                   "live_flops": n_live * B * 4 * hd * T * (T + 1) // 2,
+                   "median_step_ms": round(statistics.median(step_ms), 3), "wall_s": round(wall, 3)},
+        "roofline": roof,
+        "cpu_baseline": None,
+    }
+    line.update(extra)
+    print(json.dumps(line), flush=True)
+
+
 def run_scan(args):
     """Frozen-only sizing run of the closed-form scan (the HBM-bound frozen-head
     kernel): every head of B=8, H=12, T=16384, hd=64 bf16 frozen to a seeded
@@ -409,8 +495,9 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=10)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--workload", choices=["c2", "c4", "scan"], default="c2",
-                    help="c2: 124M nanoGPT SAF-25%% at 16K (the headline); c4: Qwen-style GQA; "
+    ap.add_argument("--workload", choices=["c2", "c3", "c4", "scan"], default="c2",
+                    help="c2: 124M nanoGPT SAF-25%% at 16K (the headline); c3: 1B-class with dense "
+                         "frozen patterns; c4: Qwen-style GQA; "
                          "scan: frozen-only sizing run of the closed-form scan (HBM roofline)")
     ap.add_argument("--seq-len", type=int, default=None)
     ap.add_argument("--batch", type=int, default=None, help="c4 only (default 4)")
@@ -445,6 +532,9 @@ def main():
         return
     if args.workload == "scan":
         run_scan(args)
+        return
+    if args.workload == "c3":
+        run_c3(args)
         return
     if args.workload == "c4":
         if args.cpu_layers is None:
