@@ -259,7 +259,7 @@ def run_c2(args):
 
     total_ms = sum(step_ms)
     tok_s = x.numel() * args.steps / (total_ms / 1000.0)
-    label = "flash_fwd_kernel<bf16,64,2>"
+    label = "flash_fwd_kernel<bf16,64,1>"
     roof, extra = kernel_rooflines(summ, label, pmc_traffic(label) if T == 16384 else None, args.steps)
     log(f"GPU: {tok_s:.0f} tokens/s, {total_ms / args.steps:.2f} ms/step")
     cpu = None
@@ -323,7 +323,7 @@ def run_c4(args):
                                           args.warmup, not args.no_timer and not use_sdpa)
     total_ms = sum(step_ms)
     tok_s = B * T * args.steps / (total_ms / 1000.0)
-    roof, extra = kernel_rooflines(summ, "flash_fwd_kernel<bf16,64,2>", None, args.steps)
+    roof, extra = kernel_rooflines(summ, "flash_fwd_kernel<bf16,64,1>", None, args.steps)
     log(f"GPU: {tok_s:.0f} tokens/s, {total_ms / args.steps:.2f} ms/step")
     cpu = None
     if not args.no_cpu_baseline:

@@ -259,11 +259,12 @@ struct FlashState {
   }
 };
 
-// hd <= 64: two waves per SIMD (two resident workgroups) within 256
-// registers; larger heads take the SIMD's whole register file (and one
-// workgroup's LDS slots fill most of the CU).
+// hd <= 64: three waves per SIMD (three resident 128-query workgroups,
+// within 170 registers) or two of 256 queries (within 256 registers);
+// larger heads take the SIMD's whole register file (and one workgroup's LDS
+// slots fill most of the CU).  The host's flash_resident() mirrors this.
 template <int HD, int QT>
-constexpr int flash_waves_per_eu() { return HD <= 64 ? 2 : 1; }
+constexpr int flash_waves_per_eu() { return HD <= 64 ? (QT == 1 ? 3 : 2) : 1; }
 
 template <typename T, int HD, int QT>
 __global__ __launch_bounds__(256)

@@ -223,20 +223,25 @@ int plan_and_validate(const saf_mixed_attn_args* a, unsigned which, Plan& pl, bo
 }
 
 // ---- causal load balancing of the live-head kernel ------------------------
-// Resident flash workgroups per device (2 per CU), cached per device per thread.
-int flash_slots() {
-  thread_local int cached_dev = -1, cached_slots = 0;
+// Compute units of the current device, cached per device per thread.
+int cu_count() {
+  thread_local int cached_dev = -1, cached_cus = 0;
   int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess) return 512;
+  if (hipGetDevice(&dev) != hipSuccess) return 256;
   if (dev != cached_dev) {
     int cus = 0;
     if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
       cus = 256;
     cached_dev = dev;
-    cached_slots = 2 * cus;
+    cached_cus = cus;
   }
-  return cached_slots;
+  return cached_cus;
 }
+
+// Resident live-head workgroups per CU (flash_waves_per_eu in the kernel:
+// three 128-query workgroups at hd <= 64, two of 256 queries; one at larger
+// head dims, where one workgroup's LDS slots fill most of the CU).
+int flash_resident(int HD, int qt) { return HD <= 64 ? (qt == 1 ? 3 : 2) : 1; }
 
 struct FlashPlan {
   int n_items = 0, seg_len = 0, n_part_per_head = 0, n_split = 0;
@@ -248,7 +253,7 @@ struct FlashPlan {
 // Splits the key range of the heaviest query blocks into segments of about
 // the average per-slot work, so the causal tail (the last query block walks
 // every key) does not outlast the rest of the grid.
-FlashPlan plan_flash(int B, int n_slots, int T, int HD, int qt) {
+FlashPlan plan_flash(int B, int n_slots, int T, int HD, int qt, int per_cu) {
   FlashPlan fp;
   const int BM = block_rows(qt), BMb = BM / 64;
   const int nqb = (T + BM - 1) / BM;
@@ -260,7 +265,7 @@ FlashPlan plan_flash(int B, int n_slots, int T, int HD, int qt) {
     per_head += nkb[qb];
   }
   const int64_t nbh = (int64_t)B * n_slots;
-  const int64_t slots = flash_slots();
+  const int64_t slots = (int64_t)cu_count() * per_cu;
   int64_t L = (nbh * per_head + slots - 1) / slots;
   L = std::max<int64_t>(L, 4 * BMb);
   L = (L + BMb - 1) / BMb * BMb;
@@ -297,7 +302,7 @@ FlashPlan plan_flash(int B, int n_slots, int T, int HD, int qt) {
 
 int flash_qtiles_for(const saf_mixed_attn_args* a, int HD) {
   int qt = a->flash_qtiles;
-  if (qt == 0) qt = HD <= 64 ? 2 : 1;
+  if (qt == 0) qt = 1;
   return qt;
 }
 
@@ -353,7 +358,7 @@ int run_flash(const saf_mixed_attn_args* a, const Plan& pl, hipStream_t s) {
   p.n_qblk = (pl.T + block_rows(qt) - 1) / block_rows(qt);
   p.scale_log2 = a->sm_scale * kLog2e;
   // split the causal tail when the caller's workspace holds the partials
-  FlashPlan fp = plan_flash(pl.B, p.n_slots, pl.T, pl.HD, qt);
+  FlashPlan fp = plan_flash(pl.B, p.n_slots, pl.T, pl.HD, qt, flash_resident(pl.HD, qt));
   const int64_t part_off = scan_ws_bytes(pl);
   if (fp.n_items && a->workspace != nullptr && a->workspace_bytes >= part_off + fp.part_bytes &&
       reinterpret_cast<uintptr_t>(a->workspace) % 16 == 0) {
@@ -431,7 +436,7 @@ int run_dense(const saf_tensor_t& patt, const saf_tensor_t& v, const saf_tensor_
     p.v_head[i] = (int16_t)v_head[i];
     p.pat_head[i] = (int16_t)pat_head[i];
   }
-  FlashPlan fp = plan_flash(B, p.n_slots, T, HD, kDenseQt);
+  FlashPlan fp = plan_flash(B, p.n_slots, T, HD, kDenseQt, 2);
   if (fp.n_items && ws != nullptr && ws_bytes >= fp.part_bytes && reinterpret_cast<uintptr_t>(ws) % 16 == 0) {
     p.n_items = fp.n_items;
     p.seg_len = fp.seg_len;
@@ -707,11 +712,12 @@ int64_t saf_mixed_attn_workspace_bytes(const saf_mixed_attn_args* args) {
   if (plan_and_validate(args, kDoFlash | kDoScan, pl, false)) return -1;
   int64_t total = scan_ws_bytes(pl), part = 0;
   if (!pl.live.empty()) {
-    const FlashPlan fp = plan_flash(pl.B, (int)pl.live.size(), pl.T, pl.HD, flash_qtiles_for(args, pl.HD));
+    const int qt = flash_qtiles_for(args, pl.HD);
+    const FlashPlan fp = plan_flash(pl.B, (int)pl.live.size(), pl.T, pl.HD, qt, flash_resident(pl.HD, qt));
     part = fp.part_bytes;
   }
   if (!pl.dense.empty())
-    part = std::max(part, plan_flash(pl.B, (int)pl.dense.size(), pl.T, pl.HD, kDenseQt).part_bytes);
+    part = std::max(part, plan_flash(pl.B, (int)pl.dense.size(), pl.T, pl.HD, kDenseQt, 2).part_bytes);
   total += part;
   return total;
 }
