@@ -98,7 +98,7 @@ typedef struct saf_mixed_attn_args {
   float sm_scale;               /* softmax scale (1/sqrt(HD) by default) */
   void* workspace;              /* device scratch, saf_workspace_bytes() bytes */
   int64_t workspace_bytes;
-  int32_t flash_qtiles;         /* 0 = auto; 1 or 2 query tiles per wave */
+  int32_t flash_qtiles;         /* 0 = auto (1); 1 or 2 query tiles per wave (2 only up to hd 64) */
   int32_t scan_spin_limit;      /* 0 = default bound of each look-back wait */
 } saf_mixed_attn_args;
 

@@ -68,16 +68,18 @@ template <int HD> struct VRow {
 // only vmcnt, which leaves the compiler's LDS-read waits exact.
 
 template <typename T, int HD> struct TileDma {
+  static constexpr int NW = flash_waves(HD);
   static constexpr int KCH = HD / 8;
   static constexpr int KCHP = KLayout<HD>::KCHP;
-  static constexpr int KN = KCHP / 4;
-  static constexpr int VN = VRow<HD>::CHP / 4;
+  static constexpr int KN = KCHP / NW;
+  static constexpr int VN = VRow<HD>::CHP / NW;
+  static_assert(KCHP % NW == 0 && VRow<HD>::CHP % NW == 0, "tile chunks must split evenly over the waves");
   uint32_t koff[KN], voff[VN];  // byte offset of this thread's chunks from the tile's first row
 
   __device__ __forceinline__ void init(int wave, int lane, int64_t k_st, int64_t v_st) {
 #pragma unroll
     for (int p = 0; p < KN; ++p) {
-      const int X = (4 * p + wave) * 64 + lane;
+      const int X = (NW * p + wave) * 64 + lane;
       const int key = X / KCHP, slot = X % KCHP;
       const int f = (key & 3) | ((key >> 1) & 4);
       const int c = slot ^ (f & (KCHP - 1));
@@ -85,7 +87,7 @@ template <typename T, int HD> struct TileDma {
     }
 #pragma unroll
     for (int p = 0; p < VN; ++p) {
-      const int X = (4 * p + wave) * 64 + lane;
+      const int X = (NW * p + wave) * 64 + lane;
       const int key = X / VRow<HD>::CHP, pc = X % VRow<HD>::CHP;
       const int c = 2 * ((pc >> 1) ^ (key & 3)) + (pc & 1);
       voff[p] = (uint32_t)(key * v_st * (int64_t)sizeof(T)) + 16u * (c < KCH ? c : 0);
@@ -101,13 +103,13 @@ template <typename T, int HD> struct TileDma {
     const __amdgpu_buffer_rsrc_t r = rsrc(base, st, j0, T_len);
 #pragma unroll
     for (int p = 0; p < KN; ++p)
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(r, SAF_LDS_PTR(tile + (4 * p + wave) * 1024), 16, koff[p], 0, 0, 0);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(r, SAF_LDS_PTR(tile + (NW * p + wave) * 1024), 16, koff[p], 0, 0, 0);
   }
   __device__ __forceinline__ void load_v(const T* base, int64_t st, int j0, int T_len, char* tile, int wave) const {
     const __amdgpu_buffer_rsrc_t r = rsrc(base, st, j0, T_len);
 #pragma unroll
     for (int p = 0; p < VN; ++p)
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(r, SAF_LDS_PTR(tile + (4 * p + wave) * 1024), 16, voff[p], 0, 0, 0);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(r, SAF_LDS_PTR(tile + (NW * p + wave) * 1024), 16, voff[p], 0, 0, 0);
   }
 };
 
@@ -259,19 +261,20 @@ struct FlashState {
   }
 };
 
-// hd <= 64: three waves per SIMD (three resident 128-query workgroups,
-// within 170 registers) or two of 256 queries (within 256 registers);
-// larger heads take the SIMD's whole register file (and one workgroup's LDS
-// slots fill most of the CU).  The host's flash_resident() mirrors this.
+// hd <= 64: three waves per SIMD (three resident 4-wave workgroups of 128
+// queries, within 170 registers) or two of 256 queries (within 256
+// registers).  Larger heads: one workgroup's three K and V slots fill most of
+// the CU's LDS, so the workgroup has 8 waves (two per SIMD) sharing them.
+// The host's flash_resident() and flash_block_rows() mirror this.
 template <int HD, int QT>
-constexpr int flash_waves_per_eu() { return HD <= 64 ? (QT == 1 ? 3 : 2) : 1; }
+constexpr int flash_waves_per_eu() { return HD <= 64 ? (QT == 1 ? 3 : 2) : (QT == 1 ? 2 : 1); }
 
 template <typename T, int HD, int QT>
-__global__ __launch_bounds__(256)
+__global__ __launch_bounds__(64 * flash_waves(HD))
 __attribute__((amdgpu_waves_per_eu(flash_waves_per_eu<HD, QT>(), flash_waves_per_eu<HD, QT>())))
 void flash_fwd_kernel(const FlashParams p) {
   using St = FlashState<T, HD, QT>;
-  constexpr int NW = 4;
+  constexpr int NW = flash_waves(HD);
   constexpr int BM = NW * 32 * QT;
   constexpr int NDT = St::NDT, NKT = St::NKT;
   constexpr int KB = KLayout<HD>::BYTES, VB = VRow<HD>::BYTES;
@@ -488,7 +491,7 @@ __global__ __launch_bounds__(256) void flash_combine_kernel(const CombineParams 
 #define SAF_FLASH_INST(T, HD, QT) template __global__ void flash_fwd_kernel<T, HD, QT>(const FlashParams);
 #define SAF_FLASH_INST_HD(T) \
   SAF_FLASH_INST(T, 32, 1) SAF_FLASH_INST(T, 32, 2) SAF_FLASH_INST(T, 64, 1) SAF_FLASH_INST(T, 64, 2) \
-  SAF_FLASH_INST(T, 96, 1) SAF_FLASH_INST(T, 96, 2) SAF_FLASH_INST(T, 128, 1) SAF_FLASH_INST(T, 128, 2)
+  SAF_FLASH_INST(T, 96, 1) SAF_FLASH_INST(T, 128, 1)
 SAF_FLASH_INST_HD(__bf16)
 SAF_FLASH_INST_HD(_Float16)
 #undef SAF_FLASH_INST_HD
@@ -498,7 +501,7 @@ template <typename T, int HD, int QT>
 static hipError_t launch_flash_t(const FlashParams& p, hipStream_t s) {
   const int64_t items = p.n_items ? p.n_items : p.n_qblk;
   const dim3 grid((unsigned)(items * p.B * p.n_slots));
-  hipLaunchKernelGGL((flash_fwd_kernel<T, HD, QT>), grid, dim3(256), 0, s, p);
+  hipLaunchKernelGGL((flash_fwd_kernel<T, HD, QT>), grid, dim3(64 * flash_waves(HD)), 0, s, p);
   return hipGetLastError();
 }
 
@@ -510,9 +513,7 @@ static hipError_t launch_flash_hd(const FlashParams& p, int hd, int qt, hipStrea
     case 64 * 4 + 1: return launch_flash_t<T, 64, 1>(p, s);
     case 64 * 4 + 2: return launch_flash_t<T, 64, 2>(p, s);
     case 96 * 4 + 1: return launch_flash_t<T, 96, 1>(p, s);
-    case 96 * 4 + 2: return launch_flash_t<T, 96, 2>(p, s);
     case 128 * 4 + 1: return launch_flash_t<T, 128, 1>(p, s);
-    case 128 * 4 + 2: return launch_flash_t<T, 128, 2>(p, s);
     default: return hipErrorInvalidValue;
   }
 }

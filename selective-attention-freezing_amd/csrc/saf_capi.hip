@@ -239,8 +239,8 @@ int cu_count() {
 }
 
 // Resident live-head workgroups per CU (flash_waves_per_eu in the kernel:
-// three 128-query workgroups at hd <= 64, two of 256 queries; one at larger
-// head dims, where one workgroup's LDS slots fill most of the CU).
+// three 128-query workgroups at hd <= 64, two of 256 queries; one 8-wave
+// workgroup at larger head dims, where its LDS slots fill most of the CU).
 int flash_resident(int HD, int qt) { return HD <= 64 ? (qt == 1 ? 3 : 2) : 1; }
 
 struct FlashPlan {
@@ -253,9 +253,9 @@ struct FlashPlan {
 // Splits the key range of the heaviest query blocks into segments of about
 // the average per-slot work, so the causal tail (the last query block walks
 // every key) does not outlast the rest of the grid.
-FlashPlan plan_flash(int B, int n_slots, int T, int HD, int qt, int per_cu) {
+FlashPlan plan_flash(int B, int n_slots, int T, int HD, int BM, int per_cu) {
   FlashPlan fp;
-  const int BM = block_rows(qt), BMb = BM / 64;
+  const int BMb = BM / 64;
   const int nqb = (T + BM - 1) / BM;
   if (nqb <= 1 || nqb > kMaxQblk) return fp;
   std::vector<int> nkb(nqb);
@@ -302,7 +302,9 @@ FlashPlan plan_flash(int B, int n_slots, int T, int HD, int qt, int per_cu) {
 
 int flash_qtiles_for(const saf_mixed_attn_args* a, int HD) {
   int qt = a->flash_qtiles;
-  if (qt == 0) qt = 1;
+  // one query tile per wave by default; two (256-query workgroups) only up
+  // to hd 64, where they fit two waves per SIMD
+  if (qt == 0 || (qt == 2 && HD > 64)) qt = 1;
   return qt;
 }
 
@@ -355,10 +357,11 @@ int run_flash(const saf_mixed_attn_args* a, const Plan& pl, hipStream_t s) {
   p.B = pl.B;
   p.T = pl.T;
   p.n_slots = (int)pl.live.size();
-  p.n_qblk = (pl.T + block_rows(qt) - 1) / block_rows(qt);
+  const int BM = flash_block_rows(pl.HD, qt);
+  p.n_qblk = (pl.T + BM - 1) / BM;
   p.scale_log2 = a->sm_scale * kLog2e;
   // split the causal tail when the caller's workspace holds the partials
-  FlashPlan fp = plan_flash(pl.B, p.n_slots, pl.T, pl.HD, qt, flash_resident(pl.HD, qt));
+  FlashPlan fp = plan_flash(pl.B, p.n_slots, pl.T, pl.HD, BM, flash_resident(pl.HD, qt));
   const int64_t part_off = scan_ws_bytes(pl);
   if (fp.n_items && a->workspace != nullptr && a->workspace_bytes >= part_off + fp.part_bytes &&
       reinterpret_cast<uintptr_t>(a->workspace) % 16 == 0) {
@@ -368,7 +371,7 @@ int run_flash(const saf_mixed_attn_args* a, const Plan& pl, hipStream_t s) {
     p.seg_len = fp.seg_len;
     p.n_part_per_head = fp.n_part_per_head;
     p.part_o = reinterpret_cast<float*>(ws);
-    p.part_ml = reinterpret_cast<float*>(ws + nbh * fp.n_part_per_head * (int64_t)block_rows(qt) * pl.HD * 4);
+    p.part_ml = reinterpret_cast<float*>(ws + nbh * fp.n_part_per_head * (int64_t)BM * pl.HD * 4);
     std::copy(fp.items.begin(), fp.items.end(), p.items);
     std::copy(fp.part_base.begin(), fp.part_base.end(), p.part_base);
   } else {
@@ -389,7 +392,7 @@ int run_flash(const saf_mixed_attn_args* a, const Plan& pl, hipStream_t s) {
   c.lse = p.lse;
   c.o_sb = p.o_sb; c.o_sh = p.o_sh; c.o_st = p.o_st;
   c.l_sb = p.l_sb; c.l_sh = p.l_sh; c.l_st = p.l_st;
-  c.B = p.B; c.T = p.T; c.n_slots = p.n_slots; c.BM = block_rows(qt);
+  c.B = p.B; c.T = p.T; c.n_slots = p.n_slots; c.BM = BM;
   c.seg_len = fp.seg_len; c.n_part_per_head = fp.n_part_per_head; c.n_split = fp.n_split;
   c.part_o = p.part_o;
   c.part_ml = p.part_ml;
@@ -436,7 +439,7 @@ int run_dense(const saf_tensor_t& patt, const saf_tensor_t& v, const saf_tensor_
     p.v_head[i] = (int16_t)v_head[i];
     p.pat_head[i] = (int16_t)pat_head[i];
   }
-  FlashPlan fp = plan_flash(B, p.n_slots, T, HD, kDenseQt, 2);
+  FlashPlan fp = plan_flash(B, p.n_slots, T, HD, block_rows(kDenseQt), 2);
   if (fp.n_items && ws != nullptr && ws_bytes >= fp.part_bytes && reinterpret_cast<uintptr_t>(ws) % 16 == 0) {
     p.n_items = fp.n_items;
     p.seg_len = fp.seg_len;
@@ -713,11 +716,12 @@ int64_t saf_mixed_attn_workspace_bytes(const saf_mixed_attn_args* args) {
   int64_t total = scan_ws_bytes(pl), part = 0;
   if (!pl.live.empty()) {
     const int qt = flash_qtiles_for(args, pl.HD);
-    const FlashPlan fp = plan_flash(pl.B, (int)pl.live.size(), pl.T, pl.HD, qt, flash_resident(pl.HD, qt));
+    const FlashPlan fp = plan_flash(pl.B, (int)pl.live.size(), pl.T, pl.HD, flash_block_rows(pl.HD, qt),
+                                    flash_resident(pl.HD, qt));
     part = fp.part_bytes;
   }
   if (!pl.dense.empty())
-    part = std::max(part, plan_flash(pl.B, (int)pl.dense.size(), pl.T, pl.HD, kDenseQt, 2).part_bytes);
+    part = std::max(part, plan_flash(pl.B, (int)pl.dense.size(), pl.T, pl.HD, block_rows(kDenseQt), 2).part_bytes);
   total += part;
   return total;
 }

@@ -164,7 +164,13 @@ hipError_t launch_zero_u32(uint32_t* ptr, int64_t n, hipStream_t s);
 hipError_t launch_rope(const RopeParams& p, int dtype, hipStream_t s);
 hipError_t launch_add_layernorm(const AddLnParams& p, int dtype, hipStream_t s);
 
-// Queries per flash / frozen workgroup for a query-tile count.
+// Queries per frozen-head workgroup (4 waves) for a query-tile count.
 inline int block_rows(int qt) { return 4 * 32 * qt; }
+
+// Waves of a live-head workgroup: 8 above hd 64 (two per SIMD sharing one
+// set of LDS tiles), else 4.
+constexpr int flash_waves(int hd) { return hd > 64 ? 8 : 4; }
+// Queries per live-head workgroup.
+inline int flash_block_rows(int hd, int qt) { return flash_waves(hd) * 32 * qt; }
 
 }  // namespace saf

@@ -262,7 +262,8 @@ def fused_mixed_attn(q, k, v, patt, frozen, hidx=None, pidx=None,
                classify_closed_form(): state-2 heads with a non-zero kind run
                the closed-form scan instead of the in-register rebuild
       lse      optional (B, H, T) fp32 output for the live heads' base-2 LSE
-      flash_qtiles 0 (auto) / 1 / 2 query tiles per wave of the flash kernel
+      flash_qtiles 0 (auto: 1) / 1 / 2 query tiles per wave of the flash kernel
+               (2 applies up to hd 64; larger heads use 1)
     Returns (B, H, T, HD) in natural head order, strided like v (like the
     reference's empty_like(v)).
     """
