@@ -351,6 +351,111 @@ def run_c4(args):
     print(json.dumps(line), flush=True)
 
 
+def run_c1(args):
+    """the isolated mixed-head attention op at the 124M
+    shape, B=8, H=12, T=4096, hd=64, bf16 Q/K/V ~ N(0, 1) from a CPU
+    generator (seed 1337); heads randperm(12)[:3] frozen to exponential-decay
+    patterns, rate ~U(0.001, 0.1), rows renormalised.  The same op runs with
+    the decay heads as closed forms (the O(T) scan; the primary run), as
+    generic decomposed heads (the in-register rebuild kernel) and
+    materialised as dense bf16 patterns (the MFMA P.V kernel); frozen_pv (the
+    split path) is timed on the same dense patterns."""
+    import torch
+    import kernel
+
+    B, H, hd = args.batch or 8, 12, 64
+    T = args.seq_len or 4096
+    g = torch.Generator().manual_seed(1337)
+    fz = sorted(torch.randperm(H, generator=g)[:3].tolist())
+    rates = [0.001 + 0.099 * float(x) for x in torch.rand(3, generator=g)]
+    live = [h for h in range(H) if h not in fz]
+    q = torch.randn(B, len(live), T, hd, generator=g).bfloat16().cuda()
+    k = torch.randn(B, len(live), T, hd, generator=g).bfloat16().cuda()
+    v = torch.randn(B, H, T, hd, generator=g).bfloat16().cuda()
+    hidx = torch.zeros(H, dtype=torch.int32)
+    for slot, h in enumerate(live):
+        hidx[h] = slot
+    d = torch.arange(T, dtype=torch.float32)
+    alpha = torch.zeros(H, T)
+    rho = torch.zeros(H, T)
+    for f, c in zip(fz, rates):
+        rho[f] = -c * d
+    alpha, rho = alpha.cuda(), rho.cuda()
+    z = kernel.decomposed_logz(alpha, rho)
+    cf = kernel.classify_closed_form(alpha, rho, z)
+    frozen2 = torch.zeros(H, dtype=torch.int32)
+    frozen2[fz] = 2
+    frozen1 = torch.zeros(H, dtype=torch.int32)
+    frozen1[fz] = 1
+    pidx = torch.zeros(H, dtype=torch.int32)
+    for slot, f in enumerate(fz):
+        pidx[f] = slot
+    # the decay patterns materialised: P[i, j] = e^{-c (i - j)} / Z_i for j <= i
+    ii = torch.arange(T, device="cuda", dtype=torch.float32)
+    dist = (ii[:, None] - ii[None, :]).clamp_min(0)
+    patt = torch.empty(len(fz), T, T, device="cuda", dtype=torch.bfloat16)
+    for slot, c in enumerate(rates):
+        pm = torch.exp(-c * dist).tril_()
+        patt[slot] = (pm / pm.sum(-1, keepdim=True)).bfloat16()
+        del pm
+    del dist
+    dev = lambda t: t.cuda()
+    runs = {
+        "scan": lambda: kernel.fused_mixed_attn(q, k, v, None, dev(frozen2), dev(hidx), alpha=alpha, rho=rho, z=z,
+                                                 closed_form=cf, validate=False),
+        "decomp": lambda: kernel.fused_mixed_attn(q, k, v, None, dev(frozen2), dev(hidx), alpha=alpha, rho=rho, z=z,
+                                                   validate=False),
+        "dense": lambda: kernel.fused_mixed_attn(q, k, v, patt, dev(frozen1), dev(hidx), dev(pidx), validate=False),
+    }
+    n_live, nf = len(live), len(fz)
+    flops_live = n_live * B * 4 * hd * T * (T + 1) // 2
+    res = {}
+    with torch.inference_mode():
+        for name, fn in runs.items():
+            step_ms, wall, summ = timed_steps(fn, args.steps, args.warmup, not args.no_timer)
+            roof, extra = kernel_rooflines(summ, "flash_fwd_kernel<bf16,64,1>", None, args.steps)
+            entry = {"ms_per_op": round(sum(step_ms) / args.steps, 4)}
+            if roof:
+                entry["flash"] = {k2: roof[k2] for k2 in ("achieved", "frac", "avg_launch_ms")}
+            if summ and "dense" in summ:
+                n, ms, fl = summ["dense"]
+                nbytes = nf * T * (T + 1) // 2 * 2 + nf * B * 2 * T * hd * 2
+                entry["frozen_dense_pv"] = {"avg_launch_ms": round(ms / n, 4), "bytes_per_launch": nbytes,
+                                            "achieved_gbs": round(nbytes / (ms / n / 1000) / 1e9, 1),
+                                            "frac_hbm": round(nbytes / (ms / n / 1000) / 1e9 / PEAK_HBM_GBS, 4)}
+            if summ and "decomp" in summ:
+                n, ms, fl = summ["decomp"]
+                entry["frozen_decomp_pv"] = {"avg_launch_ms": round(ms / n, 4), "flop_per_launch": fl // n,
+                                             "achieved_tflops": round(fl / n / (ms / n / 1000) / 1e12, 1),
+                                             "frac_mfma": round(fl / n / (ms / n / 1000) / 1e12 / PEAK_BF16_TFLOPS, 4)}
+            if "frozen_scan" in extra:
+                entry["frozen_scan"] = {k2: extra["frozen_scan"][k2] for k2 in ("achieved", "frac", "avg_launch_ms")}
+            res[name] = entry
+        vf = v[:, fz].contiguous()
+        fz_idx = torch.arange(nf, dtype=torch.int32, device="cuda")
+        step_ms, _, _ = timed_steps(lambda: kernel.frozen_pv(patt, vf, fz_idx, T), args.steps, args.warmup, False)
+        res["frozen_pv_split"] = {"ms_per_op": round(sum(step_ms) / args.steps, 4)}
+    prim = res["scan"]
+    log(f"GPU: C1 op {prim['ms_per_op']:.3f} ms (scan), {res['decomp']['ms_per_op']:.3f} (rebuild), "
+        f"{res['dense']['ms_per_op']:.3f} (dense)")
+    roof, _ = None, None
+    line = {
+        "metric": "isolated mixed-head attention op (C1), tokens/s through the op",
+        "value": round(B * T / (prim["ms_per_op"] / 1000.0), 1), "unit": "tokens/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": prim["ms_per_op"],
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+        "data": "synthetic (Q/K/V ~ N(0, 1), seed 1337)",
+        "config": {"workload": f"C1: B={B}, H={H}, T={T}, hd={hd}; heads {fz} frozen to decay rates "
+                               f"{[round(c, 4) for c in rates]}; primary run: closed-form scan",
+                   "live_flops": flops_live},
+        "roofline": dict(prim.get("flash", {}), bound="mfma", peak=PEAK_BF16_TFLOPS, unit="TFLOP/s",
+                         kernel="flash_fwd_kernel<bf16,64,1>"),
+        "cpu_baseline": None,
+        "runs": res,
+    }
+    print(json.dumps(line), flush=True)
+
+
 def build_c3_model(T, L, device, seed=1337):
     """1B-class SAF model (24 layers, d_model 2048, 16
     heads, hd 128, vocab 50304, RoPE, no bias), bf16 random init; per layer
@@ -495,8 +600,9 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=10)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--workload", choices=["c2", "c3", "c4", "scan"], default="c2",
-                    help="c2: 124M nanoGPT SAF-25%% at 16K (the headline); c3: 1B-class with dense "
+    ap.add_argument("--workload", choices=["c1", "c2", "c3", "c4", "scan"], default="c2",
+                    help="c1: the isolated op (decay heads as scan / rebuild / dense); "
+                         "c2: 124M nanoGPT SAF-25%% at 16K (the headline); c3: 1B-class with dense "
                          "frozen patterns; c4: Qwen-style GQA; "
                          "scan: frozen-only sizing run of the closed-form scan (HBM roofline)")
     ap.add_argument("--seq-len", type=int, default=None)
@@ -535,6 +641,9 @@ def main():
         return
     if args.workload == "c3":
         run_c3(args)
+        return
+    if args.workload == "c1":
+        run_c1(args)
         return
     if args.workload == "c4":
         if args.cpu_layers is None:
