@@ -22,8 +22,17 @@
 
 namespace saf {
 
+// Resident rebuild workgroups per CU (decomp_resident() on the host).
+constexpr int decomp_waves_per_eu(int) { return 3; }
+
+// Decomposed frozen heads: P^T rebuilt in registers, one 16-key operand at a
+// time and consumed by its MFMAs right away (building a whole 64-key block of
+// operands first pushed the accumulators into AGPR copies at one wave per
+// SIMD).  alpha, rho and z are staged pre-multiplied by log2(e), so a cell
+// costs one add, one subtract and one exp2.
 template <typename T, int HD, int QT>
-__global__ __launch_bounds__(256) void frozen_decomp_kernel(const FrozenParams p) {
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(decomp_waves_per_eu(HD), decomp_waves_per_eu(HD))))
+void frozen_decomp_kernel(const FrozenParams p) {
   constexpr int MODE = 1;
   constexpr int NW = 4, NTHR = 256;
   constexpr int BM = NW * 32 * QT;
@@ -37,9 +46,18 @@ __global__ __launch_bounds__(256) void frozen_decomp_kernel(const FrozenParams p
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (SGPR)
   const int n = lane & 31, g = lane >> 5;
 
+  // work item (query block, key segment) of one (batch, head), heaviest
+  // first, (batch, head) fastest; without items one per query block
   const int nbh = p.B * p.n_slots;
-  const int qb = p.n_qblk - 1 - (int)(blockIdx.x / nbh);
   const int r = blockIdx.x % nbh;
+  int qb, seg = 0;
+  if (p.n_items) {
+    const int w = p.items[blockIdx.x / nbh];
+    qb = w >> 8;
+    seg = w & 255;
+  } else {
+    qb = p.n_qblk - 1 - (int)(blockIdx.x / nbh);
+  }
   const int b = r / p.n_slots, slot = r % p.n_slots;
   const int h = p.out_head[slot];
   const int ph = p.pat_head[slot];
@@ -51,9 +69,12 @@ __global__ __launch_bounds__(256) void frozen_decomp_kernel(const FrozenParams p
   const int q0 = qb * BM;
   const int q0w = q0 + wave * 32 * QT;
   const int kend_wg = min(q0 + BM, T_len);
-  const int nkb = (kend_wg + 63) / 64;
+  const int nkb_qb = (kend_wg + 63) / 64;
+  const bool split = p.n_items != 0 && p.part_base[qb] >= 0;
+  const int kb0 = split ? seg * p.seg_len : 0;
+  const int nkb = split ? min(nkb_qb, kb0 + p.seg_len) : nkb_qb;
   const int kend_w = min(q0w + 32 * QT, T_len);
-  const int nkb_w = kend_w > 0 ? (kend_w + 63) / 64 : 0;
+  const int nkb_w = min(nkb, kend_w > 0 ? (kend_w + 63) / 64 : 0);  // blocks this wave's rows reach
 
   // per-lane row normaliser (decomposed); rows >= T get +inf -> exact zeros
   float zq[QT];
@@ -61,7 +82,8 @@ __global__ __launch_bounds__(256) void frozen_decomp_kernel(const FrozenParams p
   for (int qt = 0; qt < QT; ++qt) {
     const int i = q0w + 32 * qt + n;
     zq[qt] = INFINITY;
-    if (MODE == 1 && i < T_len) zq[qt] = load_as_f32(p.z, (int64_t)ph * p.z_sh + (int64_t)i * p.z_ss, p.z_dtype);
+    if (MODE == 1 && i < T_len)
+      zq[qt] = load_as_f32(p.z, (int64_t)ph * p.z_sh + (int64_t)i * p.z_ss, p.z_dtype) * kLog2e;
   }
 
   f32x16_t o[QT][NDT];
@@ -77,7 +99,7 @@ __global__ __launch_bounds__(256) void frozen_decomp_kernel(const FrozenParams p
     if (MODE != 1) return;
     if (tid < 64) {
       const int j = j0 + tid;
-      a_reg = j < T_len ? load_as_f32(p.alpha, (int64_t)ph * p.a_sh + (int64_t)j * p.a_ss, p.a_dtype) : 0.f;
+      a_reg = j < T_len ? load_as_f32(p.alpha, (int64_t)ph * p.a_sh + (int64_t)j * p.a_ss, p.a_dtype) * kLog2e : 0.f;
     }
     const int dmin = q0 - j0 - 63;
 #pragma unroll
@@ -85,7 +107,7 @@ __global__ __launch_bounds__(256) void frozen_decomp_kernel(const FrozenParams p
       const int t = tid + u * NTHR;
       const int d = dmin + t;
       r_reg[u] = (t < RW && d >= 0 && d < T_len)
-                     ? load_as_f32(p.rho, (int64_t)ph * p.r_sh + (int64_t)d * p.r_ss, p.r_dtype)
+                     ? load_as_f32(p.rho, (int64_t)ph * p.r_sh + (int64_t)d * p.r_ss, p.r_dtype) * kLog2e
                      : -INFINITY;
     }
   };
@@ -100,14 +122,14 @@ __global__ __launch_bounds__(256) void frozen_decomp_kernel(const FrozenParams p
   };
 
   VStager<T, HD, NTHR> vst;
-  vst.load(vbase, p.v_st, 0, T_len, tid);
-  stage_params(0);
+  vst.load(vbase, p.v_st, 64 * kb0, T_len, tid);
+  stage_params(64 * kb0);
   vst.store(reinterpret_cast<uint32_t*>(v_lds[0]), tid);
   store_params(0);
   __syncthreads();
 
-  for (int j = 0; j < nkb; ++j) {
-    const int buf = j & 1;
+  for (int j = kb0; j < nkb; ++j) {
+    const int buf = (j - kb0) & 1;
     const bool more = j + 1 < nkb;
     if (more) {
       vst.load(vbase, p.v_st, 64 * (j + 1), T_len, tid);
@@ -115,27 +137,31 @@ __global__ __launch_bounds__(256) void frozen_decomp_kernel(const FrozenParams p
     }
     if (j < nkb_w) {
       const int j0 = 64 * j;
-      uint4 pb[2][2][QT];
+      const uint4* vt = v_lds[buf];
 #pragma unroll
-      for (int qt = 0; qt < QT; ++qt) {
-        const int i = q0w + 32 * qt + n;
+      for (int ks = 0; ks < 2; ++ks)
 #pragma unroll
-        for (int ks = 0; ks < 2; ++ks)
+        for (int sh = 0; sh < 2; ++sh) {
+          const int jb = j0 + 32 * ks + 16 * sh + 8 * g;
+          uint4 pb[QT];
 #pragma unroll
-          for (int sh = 0; sh < 2; ++sh) {
-            const int jb = j0 + 32 * ks + 16 * sh + 8 * g;
-            float e[8];
+          for (int qt = 0; qt < QT; ++qt) {
+            const int i = q0w + 32 * qt + n;
             const int dbase = i - jb - (q0 - j0 - 63);  // index of d = i - jb in r_lds
+            float e[8];
 #pragma unroll
-            for (int u = 0; u < 8; ++u) {
-              const float lg = a_lds[buf][jb - j0 + u] + r_lds[buf][dbase - u];
-              e[u] = fast_exp2((lg - zq[qt]) * kLog2e);
-            }
-            pb[ks][sh][qt] = make_uint4(Elem<T>::pack2(e[0], e[1]), Elem<T>::pack2(e[2], e[3]),
-                                        Elem<T>::pack2(e[4], e[5]), Elem<T>::pack2(e[6], e[7]));
+            for (int u = 0; u < 8; ++u)
+              e[u] = fast_exp2(a_lds[buf][jb - j0 + u] + r_lds[buf][dbase - u] - zq[qt]);
+            pb[qt] = make_uint4(Elem<T>::pack2(e[0], e[1]), Elem<T>::pack2(e[2], e[3]),
+                                Elem<T>::pack2(e[4], e[5]), Elem<T>::pack2(e[6], e[7]));
           }
-      }
-      pv_block<T, HD, QT>(o, pb, v_lds[buf], lane);
+#pragma unroll
+          for (int dt = 0; dt < NDT; ++dt) {
+            const uint4 a = vt[VLayout<HD>::chunk(32 * dt + n, 4 * ks + 2 * sh + g)];
+#pragma unroll
+            for (int qt = 0; qt < QT; ++qt) o[qt][dt] = Elem<T>::mfma(a, pb[qt], o[qt][dt]);
+          }
+        }
     }
     if (more) {
       vst.store(reinterpret_cast<uint32_t*>(v_lds[buf ^ 1]), tid);
@@ -147,7 +173,19 @@ __global__ __launch_bounds__(256) void frozen_decomp_kernel(const FrozenParams p
 #pragma unroll
   for (int qt = 0; qt < QT; ++qt) {
     const int i = q0w + 32 * qt + n;
-    if (i < T_len) store_out_tile<T, HD>(obase + (int64_t)i * p.o_st, o[qt], 1.f, g);
+    if (i >= T_len) continue;
+    if (split) {  // plain-sum partial of this key segment, added up by the combine kernel
+      const int64_t pidx = (int64_t)r * p.n_part_per_head + p.part_base[qb] + seg;
+      float* po = p.part_o + (pidx * BM + (i - q0)) * HD;
+#pragma unroll
+      for (int dt = 0; dt < NDT; ++dt)
+#pragma unroll
+        for (int r4 = 0; r4 < 4; ++r4)
+          *reinterpret_cast<float4*>(po + 32 * dt + 8 * r4 + 4 * g) =
+              make_float4(o[qt][dt][4 * r4], o[qt][dt][4 * r4 + 1], o[qt][dt][4 * r4 + 2], o[qt][dt][4 * r4 + 3]);
+    } else {
+      store_out_tile<T, HD>(obase + (int64_t)i * p.o_st, o[qt], 1.f, g);
+    }
   }
 }
 
@@ -362,7 +400,7 @@ static hipError_t launch_frozen_t(const FrozenParams& p, int mode, hipStream_t s
     else
       hipLaunchKernelGGL((frozen_dense_kernel<T, _Float16, HD>), grid, dim3(256), 0, s, p);
   } else {
-    const dim3 grid((unsigned)((int64_t)p.n_qblk * p.B * p.n_slots));
+    const dim3 grid((unsigned)((int64_t)(p.n_items ? p.n_items : p.n_qblk) * p.B * p.n_slots));
     hipLaunchKernelGGL((frozen_decomp_kernel<T, HD, QT>), grid, dim3(256), 0, s, p);
   }
   return hipGetLastError();

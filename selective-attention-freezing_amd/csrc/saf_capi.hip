@@ -412,6 +412,8 @@ void fill_frozen_common(FrozenParams& p, const saf_tensor_t& v, const saf_tensor
 }
 
 int frozen_qtiles(int hd) { return hd <= 64 ? 2 : 1; }
+// Resident rebuild workgroups per CU (decomp_waves_per_eu in the kernel).
+int decomp_resident(int) { return 3; }
 
 // Query tiles per wave of the dense P.V kernel (256-row query blocks).
 constexpr int kDenseQt = 2;
@@ -465,6 +467,9 @@ int run_dense(const saf_tensor_t& patt, const saf_tensor_t& v, const saf_tensor_
   return launched(launch_flash_combine(c, dtype, HD, s), "dense P.V combine");
 }
 
+// Decomposed P.V (rebuilt in registers), causally balanced like run_dense
+// when the workspace holds the plan's partials (same region as the flash and
+// dense partials: the kernels run one after the other on the stream).
 int run_decomp(const saf_mixed_attn_args* a, const Plan& pl, hipStream_t s) {
   if (pl.decomp.empty() || pl.T == 0 || pl.B == 0) return SAF_OK;
   FrozenParams p{};
@@ -480,7 +485,34 @@ int run_decomp(const saf_mixed_attn_args* a, const Plan& pl, hipStream_t s) {
     p.v_head[i] = (int16_t)(a->kvidx ? a->kvidx[h] : h);
     p.pat_head[i] = (int16_t)h;
   }
-  return launched(timed([&] { return launch_frozen_pv(p, pl.dtype, pl.HD, 1, s); }, s), "decomposed P.V");
+  const int BM = block_rows(frozen_qtiles(pl.HD));
+  FlashPlan fp = plan_flash(pl.B, p.n_slots, pl.T, pl.HD, BM, decomp_resident(pl.HD));
+  const int64_t part_off = scan_ws_bytes(pl);
+  if (fp.n_items && a->workspace != nullptr && a->workspace_bytes >= part_off + fp.part_bytes &&
+      reinterpret_cast<uintptr_t>(a->workspace) % 16 == 0) {
+    p.n_items = fp.n_items;
+    p.seg_len = fp.seg_len;
+    p.n_part_per_head = fp.n_part_per_head;
+    p.part_o = reinterpret_cast<float*>(reinterpret_cast<char*>(a->workspace) + part_off);
+    std::copy(fp.items.begin(), fp.items.end(), p.items);
+    std::copy(fp.part_base.begin(), fp.part_base.end(), p.part_base);
+  } else {
+    fp = FlashPlan();
+  }
+  if (int rc = launched(timed([&] { return launch_frozen_pv(p, pl.dtype, pl.HD, 1, s); }, s), "decomposed P.V"))
+    return rc;
+  if (fp.n_split == 0) return SAF_OK;
+  CombineParams c{};
+  c.out = p.out;
+  c.o_sb = p.o_sb; c.o_sh = p.o_sh; c.o_st = p.o_st;
+  c.B = p.B; c.T = p.T; c.n_slots = p.n_slots; c.BM = BM;
+  c.seg_len = fp.seg_len; c.n_part_per_head = fp.n_part_per_head; c.n_split = fp.n_split;
+  c.part_o = p.part_o;
+  c.part_ml = nullptr;
+  std::copy(p.out_head, p.out_head + kMaxHeads, c.out_head);
+  std::copy(fp.split_qb.begin(), fp.split_qb.end(), c.split_qb);
+  std::copy(fp.part_base.begin(), fp.part_base.end(), c.part_base);
+  return launched(launch_flash_combine(c, pl.dtype, pl.HD, s), "decomposed P.V combine");
 }
 
 int run_scan(const saf_mixed_attn_args* a, const Plan& pl, hipStream_t s) {
@@ -722,6 +754,9 @@ int64_t saf_mixed_attn_workspace_bytes(const saf_mixed_attn_args* args) {
   }
   if (!pl.dense.empty())
     part = std::max(part, plan_flash(pl.B, (int)pl.dense.size(), pl.T, pl.HD, block_rows(kDenseQt), 2).part_bytes);
+  if (!pl.decomp.empty())
+    part = std::max(part, plan_flash(pl.B, (int)pl.decomp.size(), pl.T, pl.HD, block_rows(frozen_qtiles(pl.HD)),
+                                     decomp_resident(pl.HD)).part_bytes);
   total += part;
   return total;
 }
