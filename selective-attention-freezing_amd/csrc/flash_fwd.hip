@@ -246,8 +246,13 @@ struct FlashState {
   __device__ __forceinline__ void step(f32x16_t (&cur)[QT], f32x16_t (&nxt)[QT], int u, bool masked, const char* kS,
                                        int ksS, const char* kR, int ksR, const char* vP, int ksP) {
     // the mask touches only S_u, complete before the step: applying it first
-    // keeps the MFMAs and the softmax below in one basic block
-    if (masked) mask(cur, 32 * u);
+    // keeps the MFMAs and the softmax below in one basic block.  The empty
+    // volatile asm makes the (uniform) branch real: if-converted, every step
+    // paid ~48 compares and selects for the mask of the diagonal blocks.
+    if (masked) {
+      asm volatile("" ::: "memory");
+      mask(cur, 32 * u);
+    }
     pv(nxt, vP, ksP);
     scores(nxt, kS, ksS);
     float bs[QT];
