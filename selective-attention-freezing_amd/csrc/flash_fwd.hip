@@ -247,8 +247,9 @@ struct FlashState {
                                        int ksS, const char* kR, int ksR, const char* vP, int ksP) {
     // the mask touches only S_u, complete before the step: applying it first
     // keeps the MFMAs and the softmax below in one basic block.  The empty
-    // volatile asm makes the (uniform) branch real: if-converted, every step
-    // paid ~48 compares and selects for the mask of the diagonal blocks.
+    // volatile asm keeps the (uniform) branch a real scalar branch, so the
+    // mask's selects stay out of the step's schedule: 140 VGPRs instead of
+    // 152 at hd 64, 198 instead of 228 at hd 128.
     if (masked) {
       asm volatile("" ::: "memory");
       mask(cur, 32 * u);
