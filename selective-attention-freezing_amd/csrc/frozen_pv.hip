@@ -255,28 +255,35 @@ __device__ inline uint4 p_chunk(const FrozenParams& p, const PT* prow, int kstar
 // Dense P.V.  Each lane loads its own B operands straight from the pattern
 // rows (lane (n, g): query n of a 32-row tile, keys 8g + 0..7 of each 16-key
 // step = one 16-byte read), refilled for the next 64-key block as soon as
-// they are used, so P needs no LDS staging and no barrier; only the V^T tile
-// (shared by the four waves) is double-buffered in LDS.  64 query rows per wave: each V^T operand read from
-// LDS feeds two MFMAs.  Work items cover a key segment of a 256-row query
-// block; split blocks write fp32 partials that the combine kernel sums.  Two
-// resident workgroups per CU overlap one's loads with the other's MFMAs.
-template <typename T, typename PT, int HD>
+// they are used, so P needs no LDS staging and no barrier.  A workgroup
+// serves NB batch elements of one head: every P^T operand feeds the MFMAs of
+// all NB of them, so the pattern (the dominant traffic) is read from HBM once
+// per NB sequences instead of once per sequence.  The V^T tiles of the NB
+// sequences (shared by the four waves) are double-buffered in LDS; with QT = 2
+// each V^T operand read from LDS feeds two MFMAs.  Work items cover a key
+// segment of a query block; split blocks write fp32 partials that the combine
+// kernel sums.  Two resident workgroups per CU overlap one's loads with the
+// other's MFMAs.
+template <typename T, typename PT, int HD, int QT, int NB>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void frozen_dense_kernel(const FrozenParams p) {
-  constexpr int QT = 2, NW = 4, NTHR = 256;
+  constexpr int NW = 4, NTHR = 256;
   constexpr int BM = NW * 32 * QT;
   constexpr int NDT = HD / 32;
-  __shared__ __align__(16) uint4 v_lds[2][VLayout<HD>::BYTES / 16];
+  static_assert(NB * QT * NDT <= 8, "accumulators must fit two waves per SIMD");
+  __shared__ __align__(16) uint4 v_lds[2][NB][VLayout<HD>::BYTES / 16];
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int n = lane & 31, g = lane >> 5;
 
-  // XCD-aware order: workgroup i runs on XCD i % 8; the B batch siblings of a
-  // (work item, head) group get ids 8 apart (same XCD, dispatched together,
-  // so the second reads the P tiles from that XCD's L2); items heaviest first.
+  // XCD-aware order: workgroup i runs on XCD i % 8; the batch-group siblings
+  // of a (work item, head) group get ids 8 apart (same XCD, dispatched
+  // together, so later ones read the P tiles from that XCD's L2); items
+  // heaviest first.
+  const int nbg = p.B / NB;
   const int x = blockIdx.x & 7, t8 = blockIdx.x >> 3;
-  const int b = t8 % p.B, grp = 8 * (t8 / p.B) + x;
+  const int bg = t8 % nbg, grp = 8 * (t8 / nbg) + x;
   const int n_work = p.n_items ? p.n_items : p.n_qblk;
   if (grp >= n_work * p.n_slots) return;
   const int it = grp / p.n_slots, slot = grp % p.n_slots;
@@ -293,8 +300,10 @@ void frozen_dense_kernel(const FrozenParams p) {
   seg = __builtin_amdgcn_readfirstlane(seg);
   const int h = p.out_head[slot];
   const PT* pbase = reinterpret_cast<const PT*>(p.patt) + (int64_t)p.pat_head[slot] * p.p_sh;
-  const T* vbase = reinterpret_cast<const T*>(p.v) + b * p.v_sb + (int64_t)p.v_head[slot] * p.v_sh;
-  T* obase = reinterpret_cast<T*>(p.out) + b * p.o_sb + (int64_t)h * p.o_sh;
+  const T* vbase[NB];
+#pragma unroll
+  for (int nb = 0; nb < NB; ++nb)
+    vbase[nb] = reinterpret_cast<const T*>(p.v) + (int64_t)(bg * NB + nb) * p.v_sb + (int64_t)p.v_head[slot] * p.v_sh;
 
   const int T_len = p.T;
   const int q0 = qb * BM;
@@ -320,15 +329,18 @@ void frozen_dense_kernel(const FrozenParams p) {
     return p_chunk<T, PT>(p, prow[qt], kstart, nvalid);
   };
 
-  f32x16_t o[QT][NDT];
+  f32x16_t o[NB][QT][NDT];
 #pragma unroll
-  for (int qt = 0; qt < QT; ++qt)
+  for (int nb = 0; nb < NB; ++nb)
 #pragma unroll
-    for (int dt = 0; dt < NDT; ++dt) o[qt][dt] = zero16();
+    for (int qt = 0; qt < QT; ++qt)
+#pragma unroll
+      for (int dt = 0; dt < NDT; ++dt) o[nb][qt][dt] = zero16();
 
-  VStager<T, HD, NTHR> vst;
+  VStager<T, HD, NTHR> vst[NB];
   uint4 pb[2][2][QT];
-  vst.load(vbase, p.v_st, 64 * kb0, T_len, tid);
+#pragma unroll
+  for (int nb = 0; nb < NB; ++nb) vst[nb].load(vbase[nb], p.v_st, 64 * kb0, T_len, tid);
   if (kb0 < kb1_w) {
 #pragma unroll
     for (int ks = 0; ks < 2; ++ks)
@@ -337,15 +349,18 @@ void frozen_dense_kernel(const FrozenParams p) {
 #pragma unroll
         for (int qt = 0; qt < QT; ++qt) pb[ks][sh][qt] = p_op(kb0, ks, sh, qt);
   }
-  vst.store(reinterpret_cast<uint32_t*>(v_lds[0]), tid);
+#pragma unroll
+  for (int nb = 0; nb < NB; ++nb) vst[nb].store(reinterpret_cast<uint32_t*>(v_lds[0][nb]), tid);
   __syncthreads();
 
   for (int j = kb0; j < kb1; ++j) {
     const int buf = (j - kb0) & 1;
     const bool more = j + 1 < kb1;
-    if (more) vst.load(vbase, p.v_st, 64 * (j + 1), T_len, tid);
+    if (more) {
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb) vst[nb].load(vbase[nb], p.v_st, 64 * (j + 1), T_len, tid);
+    }
     if (j < kb1_w) {
-      const uint4* vt = v_lds[buf];
       const bool next = j + 1 < kb1_w;
       // each operand is refilled with block j+1's right after its last use,
       // so one block of P^T registers keeps a block of loads in flight
@@ -354,10 +369,14 @@ void frozen_dense_kernel(const FrozenParams p) {
 #pragma unroll
         for (int sh = 0; sh < 2; ++sh) {
 #pragma unroll
-          for (int dt = 0; dt < NDT; ++dt) {
-            const uint4 a = vt[VLayout<HD>::chunk(32 * dt + n, 4 * ks + 2 * sh + g)];
+          for (int nb = 0; nb < NB; ++nb) {
+            const uint4* vt = v_lds[buf][nb];
 #pragma unroll
-            for (int qt = 0; qt < QT; ++qt) o[qt][dt] = Elem<T>::mfma(a, pb[ks][sh][qt], o[qt][dt]);
+            for (int dt = 0; dt < NDT; ++dt) {
+              const uint4 a = vt[VLayout<HD>::chunk(32 * dt + n, 4 * ks + 2 * sh + g)];
+#pragma unroll
+              for (int qt = 0; qt < QT; ++qt) o[nb][qt][dt] = Elem<T>::mfma(a, pb[ks][sh][qt], o[nb][qt][dt]);
+            }
           }
           if (next) {
 #pragma unroll
@@ -365,40 +384,63 @@ void frozen_dense_kernel(const FrozenParams p) {
           }
         }
     }
-    if (more) vst.store(reinterpret_cast<uint32_t*>(v_lds[buf ^ 1]), tid);
+    if (more) {
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb) vst[nb].store(reinterpret_cast<uint32_t*>(v_lds[buf ^ 1][nb]), tid);
+    }
     __syncthreads();
   }
 
 #pragma unroll
-  for (int qt = 0; qt < QT; ++qt) {
-    const int i = row[qt];
-    if (i >= T_len) continue;
-    if (split) {
-      const int64_t pidx = ((int64_t)b * p.n_slots + slot) * p.n_part_per_head + p.part_base[qb] + seg;
-      float* po = p.part_o + (pidx * BM + (i - q0)) * HD;
+  for (int nb = 0; nb < NB; ++nb) {
+    const int b = bg * NB + nb;
+    T* obase = reinterpret_cast<T*>(p.out) + b * p.o_sb + (int64_t)h * p.o_sh;
 #pragma unroll
-      for (int dt = 0; dt < NDT; ++dt)
+    for (int qt = 0; qt < QT; ++qt) {
+      const int i = row[qt];
+      if (i >= T_len) continue;
+      if (split) {
+        const int64_t pidx = ((int64_t)b * p.n_slots + slot) * p.n_part_per_head + p.part_base[qb] + seg;
+        float* po = p.part_o + (pidx * BM + (i - q0)) * HD;
 #pragma unroll
-        for (int r4 = 0; r4 < 4; ++r4)
-          *reinterpret_cast<float4*>(po + 32 * dt + 8 * r4 + 4 * g) =
-              make_float4(o[qt][dt][4 * r4], o[qt][dt][4 * r4 + 1], o[qt][dt][4 * r4 + 2], o[qt][dt][4 * r4 + 3]);
-    } else {
-      store_out_tile<T, HD>(obase + (int64_t)i * p.o_st, o[qt], 1.f, g);
+        for (int dt = 0; dt < NDT; ++dt)
+#pragma unroll
+          for (int r4 = 0; r4 < 4; ++r4)
+            *reinterpret_cast<float4*>(po + 32 * dt + 8 * r4 + 4 * g) =
+                make_float4(o[nb][qt][dt][4 * r4], o[nb][qt][dt][4 * r4 + 1], o[nb][qt][dt][4 * r4 + 2],
+                            o[nb][qt][dt][4 * r4 + 3]);
+      } else {
+        store_out_tile<T, HD>(obase + (int64_t)i * p.o_st, o[nb][qt], 1.f, g);
+      }
     }
   }
+}
+
+template <typename T, typename PT, int HD, int NB>
+static void launch_dense_t(const FrozenParams& p, hipStream_t s) {
+  constexpr int QT = dense_qtiles(HD, NB);
+  const int64_t groups = (int64_t)(p.n_items ? p.n_items : p.n_qblk) * p.n_slots;
+  const dim3 grid((unsigned)(8 * (p.B / NB) * ((groups + 7) / 8)));
+  hipLaunchKernelGGL((frozen_dense_kernel<T, PT, HD, QT, NB>), grid, dim3(256), 0, s, p);
+}
+
+template <typename T, typename PT, int HD>
+static void launch_dense_nb(const FrozenParams& p, hipStream_t s) {
+  if (dense_batch_group(p.B) == 2)
+    launch_dense_t<T, PT, HD, 2>(p, s);
+  else
+    launch_dense_t<T, PT, HD, 1>(p, s);
 }
 
 template <typename T, int HD, int QT>
 static hipError_t launch_frozen_t(const FrozenParams& p, int mode, hipStream_t s) {
   if (mode == 0) {
-    const int64_t groups = (int64_t)(p.n_items ? p.n_items : p.n_qblk) * p.n_slots;
-    const dim3 grid((unsigned)(8 * p.B * ((groups + 7) / 8)));
     if (p.patt_dtype == kF32)
-      hipLaunchKernelGGL((frozen_dense_kernel<T, float, HD>), grid, dim3(256), 0, s, p);
+      launch_dense_nb<T, float, HD>(p, s);
     else if (p.patt_dtype == kBF16)
-      hipLaunchKernelGGL((frozen_dense_kernel<T, __bf16, HD>), grid, dim3(256), 0, s, p);
+      launch_dense_nb<T, __bf16, HD>(p, s);
     else
-      hipLaunchKernelGGL((frozen_dense_kernel<T, _Float16, HD>), grid, dim3(256), 0, s, p);
+      launch_dense_nb<T, _Float16, HD>(p, s);
   } else {
     const dim3 grid((unsigned)((int64_t)(p.n_items ? p.n_items : p.n_qblk) * p.B * p.n_slots));
     hipLaunchKernelGGL((frozen_decomp_kernel<T, HD, QT>), grid, dim3(256), 0, s, p);

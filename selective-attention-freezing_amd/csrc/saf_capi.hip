@@ -252,8 +252,9 @@ struct FlashPlan {
 
 // Splits the key range of the heaviest query blocks into segments of about
 // the average per-slot work, so the causal tail (the last query block walks
-// every key) does not outlast the rest of the grid.
-FlashPlan plan_flash(int B, int n_slots, int T, int HD, int BM, int per_cu) {
+// every key) does not outlast the rest of the grid.  B counts the work units
+// per slot; each writes part_mult sequences' partials.
+FlashPlan plan_flash(int B, int n_slots, int T, int HD, int BM, int per_cu, int part_mult = 1) {
   FlashPlan fp;
   const int BMb = BM / 64;
   const int nqb = (T + BM - 1) / BM;
@@ -296,7 +297,7 @@ FlashPlan plan_flash(int B, int n_slots, int T, int HD, int BM, int per_cu) {
   fp.seg_len = (int)L;
   fp.n_part_per_head = parts;
   fp.n_split = (int)fp.split_qb.size();
-  fp.part_bytes = nbh * parts * (int64_t)BM * (HD + 2) * 4;
+  fp.part_bytes = nbh * part_mult * parts * (int64_t)BM * (HD + 2) * 4;
   return fp;
 }
 
@@ -415,8 +416,13 @@ int frozen_qtiles(int hd) { return hd <= 64 ? 2 : 1; }
 // Resident rebuild workgroups per CU (decomp_waves_per_eu in the kernel).
 int decomp_resident(int) { return 3; }
 
-// Query tiles per wave of the dense P.V kernel (256-row query blocks).
-constexpr int kDenseQt = 2;
+// Dense P.V work plan: query blocks of the kernel's shape, balanced over the
+// batch groups that share a pattern (dense_batch_group).
+int dense_block_rows(int B, int HD) { return block_rows(dense_qtiles(HD, dense_batch_group(B))); }
+FlashPlan plan_dense(int B, int n_slots, int T, int HD) {
+  const int nb = dense_batch_group(B);
+  return plan_flash(B / nb, n_slots, T, HD, dense_block_rows(B, HD), 2, nb);
+}
 
 // Dense P.V over the heads listed; with a workspace large enough for the
 // plan's partials, long query blocks are split into key segments (the flash
@@ -435,13 +441,14 @@ int run_dense(const saf_tensor_t& patt, const saf_tensor_t& v, const saf_tensor_
   p.patt_vec = patt.stride[2] == 1 && reinterpret_cast<uintptr_t>(patt.data) % 16 == 0 &&
                (patt.stride[1] * es) % 16 == 0 && (patt.stride[0] * es) % 16 == 0;
   p.n_slots = (int)out_head.size();
-  p.n_qblk = (T + block_rows(kDenseQt) - 1) / block_rows(kDenseQt);
+  const int BM = dense_block_rows(B, HD);
+  p.n_qblk = (T + BM - 1) / BM;
   for (int i = 0; i < p.n_slots; ++i) {
     p.out_head[i] = (int16_t)out_head[i];
     p.v_head[i] = (int16_t)v_head[i];
     p.pat_head[i] = (int16_t)pat_head[i];
   }
-  FlashPlan fp = plan_flash(B, p.n_slots, T, HD, block_rows(kDenseQt), 2);
+  FlashPlan fp = plan_dense(B, p.n_slots, T, HD);
   if (fp.n_items && ws != nullptr && ws_bytes >= fp.part_bytes && reinterpret_cast<uintptr_t>(ws) % 16 == 0) {
     p.n_items = fp.n_items;
     p.seg_len = fp.seg_len;
@@ -457,7 +464,7 @@ int run_dense(const saf_tensor_t& patt, const saf_tensor_t& v, const saf_tensor_
   CombineParams c{};
   c.out = p.out;
   c.o_sb = p.o_sb; c.o_sh = p.o_sh; c.o_st = p.o_st;
-  c.B = p.B; c.T = p.T; c.n_slots = p.n_slots; c.BM = block_rows(kDenseQt);
+  c.B = p.B; c.T = p.T; c.n_slots = p.n_slots; c.BM = BM;
   c.seg_len = fp.seg_len; c.n_part_per_head = fp.n_part_per_head; c.n_split = fp.n_split;
   c.part_o = p.part_o;
   c.part_ml = nullptr;
@@ -753,7 +760,7 @@ int64_t saf_mixed_attn_workspace_bytes(const saf_mixed_attn_args* args) {
     part = fp.part_bytes;
   }
   if (!pl.dense.empty())
-    part = std::max(part, plan_flash(pl.B, (int)pl.dense.size(), pl.T, pl.HD, block_rows(kDenseQt), 2).part_bytes);
+    part = std::max(part, plan_dense(pl.B, (int)pl.dense.size(), pl.T, pl.HD).part_bytes);
   if (!pl.decomp.empty())
     part = std::max(part, plan_flash(pl.B, (int)pl.decomp.size(), pl.T, pl.HD, block_rows(frozen_qtiles(pl.HD)),
                                      decomp_resident(pl.HD)).part_bytes);

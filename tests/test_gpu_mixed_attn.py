@@ -104,6 +104,9 @@ CASES = [
     (1, 8, 1000, 128, 1024, [1, 6]),
     (2, 4, 333, 32, 512, [2]),
     (1, 4, 1, 64, 64, [1]),
+    (3, 6, 777, 128, 1024, [1, 4]),
+    (6, 4, 1500, 128, 1536, [0, 3]),
+    (4, 5, 1200, 64, 1280, [2, 4]),
 ]
 
 
