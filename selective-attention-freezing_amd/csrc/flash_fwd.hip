@@ -44,18 +44,6 @@ constexpr float kMinit = -1.0e30f;
 // against the true maximum: every P used in a product is <= 2^16.
 constexpr float kRedoSum = 65536.f;
 
-#define SAF_LDS_PTR(p) ((__attribute__((address_space(3))) void*)(p))
-
-// V tile: 64 key rows of HD values; row pitch VSEG 32-byte segments; the
-// logical segment s of key row r is stored at segment s ^ (r & 3), so the
-// four rows a 16-lane group of ds_read_b64_tr_b16 touches fall in four
-// different bank quarters.
-template <int HD> struct VRow {
-  static constexpr int VSEG = HD / 16 <= 4 ? 4 : 8;
-  static constexpr int PITCH = VSEG * 32;
-  static constexpr int CHP = 2 * VSEG;  // 16-byte chunks per row
-  static constexpr int BYTES = 64 * PITCH;
-};
 
 // One 64-key K and V tile copy by DMA: thread (wave w, lane L), load p
 // writes LDS chunk X = (4p + w) * 64 + L of the tile (buffer_load ... lds
@@ -86,40 +74,23 @@ template <typename T, int HD> struct TileDma {
       koff[p] = (uint32_t)(key * k_st * (int64_t)sizeof(T)) + 16u * (c < KCH ? c : 0);
     }
 #pragma unroll
-    for (int p = 0; p < VN; ++p) {
-      const int X = (NW * p + wave) * 64 + lane;
-      const int key = X / VRow<HD>::CHP, pc = X % VRow<HD>::CHP;
-      const int c = 2 * ((pc >> 1) ^ (key & 3)) + (pc & 1);
-      voff[p] = (uint32_t)(key * v_st * (int64_t)sizeof(T)) + 16u * (c < KCH ? c : 0);
-    }
+    for (int p = 0; p < VN; ++p) voff[p] = vrow_dma_offset<T, HD>((NW * p + wave) * 64 + lane, v_st);
   }
 
-  __device__ static __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const T* base, int64_t st, int j0, int T_len) {
-    const int64_t bytes = (int64_t)(T_len - j0) * st * (int64_t)sizeof(T);
-    const int num = (int)(bytes < 0 ? 0 : (bytes > 0x7fffffff ? 0x7fffffff : bytes));
-    return __builtin_amdgcn_make_buffer_rsrc(const_cast<T*>(base + (int64_t)j0 * st), 0, num, kBufferWord3);
-  }
   __device__ __forceinline__ void load_k(const T* base, int64_t st, int j0, int T_len, char* tile, int wave) const {
-    const __amdgpu_buffer_rsrc_t r = rsrc(base, st, j0, T_len);
+    const __amdgpu_buffer_rsrc_t r = rows_rsrc(base, st, j0, T_len);
 #pragma unroll
     for (int p = 0; p < KN; ++p)
       __builtin_amdgcn_raw_ptr_buffer_load_lds(r, SAF_LDS_PTR(tile + (NW * p + wave) * 1024), 16, koff[p], 0, 0, 0);
   }
   __device__ __forceinline__ void load_v(const T* base, int64_t st, int j0, int T_len, char* tile, int wave) const {
-    const __amdgpu_buffer_rsrc_t r = rsrc(base, st, j0, T_len);
+    const __amdgpu_buffer_rsrc_t r = rows_rsrc(base, st, j0, T_len);
 #pragma unroll
     for (int p = 0; p < VN; ++p)
       __builtin_amdgcn_raw_ptr_buffer_load_lds(r, SAF_LDS_PTR(tile + (NW * p + wave) * 1024), 16, voff[p], 0, 0, 0);
   }
 };
 
-typedef short short4_t __attribute__((ext_vector_type(4)));
-
-__device__ __forceinline__ uint2 ds_read_tr16(const char* p) {
-  const short4_t r = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-      (__attribute__((address_space(3))) short4_t*)(p));
-  return __builtin_bit_cast(uint2, r);
-}
 
 template <typename T, int HD, int QT>
 struct FlashState {
@@ -139,11 +110,8 @@ struct FlashState {
     const int key = kperm(n);
 #pragma unroll
     for (int t = 0; t < NKT; ++t) koff[t] = 16 * KLayout<HD>::chunk(key, 2 * t + g);
-    const int i = lane & 15, gh = (lane >> 4) & 1;
-    const int vkey = 8 * g + (i >> 2);
 #pragma unroll
-    for (int dt = 0; dt < NDT; ++dt)
-      voff[dt] = vkey * VRow<HD>::PITCH + (((2 * dt + gh) ^ (i >> 2)) << 5) + 8 * (i & 3);
+    for (int dt = 0; dt < NDT; ++dt) voff[dt] = vt_read_offset<HD>(lane, dt);
   }
 
   // S^T of sub-block ks (0/1) of the K tile: s[qt] = K_sub . Q^T

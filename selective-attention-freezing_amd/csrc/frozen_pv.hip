@@ -18,6 +18,8 @@
 // already in it), 64 rows per wave, causally balanced work items; workgroups
 // that share P (the batch siblings) are placed on the same XCD so the second
 // one reads it from that XCD's L2.  Decomposed: P^T is rebuilt in registers.
+#include <type_traits>
+
 #include "saf_kernels.h"
 
 namespace saf {
@@ -252,26 +254,157 @@ __device__ inline uint4 p_chunk(const FrozenParams& p, const PT* prow, int kstar
                     Elem<T>::pack2(e[6], e[7]));
 }
 
+// s_waitcnt immediate that waits for vmcnt <= n alone (expcnt and lgkmcnt
+// left at their maxima; gfx9 encoding: vmcnt bits 3:0 and 15:14).
+constexpr int waitcnt_vm(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8); }
+
+// Per-wave state of the dense P.V kernel (below): the lane's pattern rows,
+// the V DMA and V^T read offsets, and the O^T accumulators of NB sequences.
+template <typename T, typename PT, int HD, int QT, int NB, bool FAST>
+struct DenseState {
+  static constexpr int NW = 4;
+  static constexpr int NDT = HD / 32;
+  static constexpr int VB = VRow<HD>::BYTES;
+  static constexpr int PITCH = VRow<HD>::PITCH;
+  static constexpr int VN = VRow<HD>::CHP / NW;  // DMA chunks per thread per V tile
+  const T* vbase[NB];
+  int64_t v_st;
+  int T_len, wave, g, q0w;
+  int row[QT];
+  const PT* prow[QT];    // general path: the lane's pattern rows
+  uint32_t poff[QT];     // fast path: their byte offsets in the descriptor
+  __amdgpu_buffer_rsrc_t prs;
+  uint32_t voff[VN];
+  int vro[NDT];
+  f32x16_t o[NB][QT][NDT];
+
+  // DMA of the 64-key V tiles of block j of the NB sequences into `tile`:
+  // load pp of a wave writes chunk (NW pp + wave) * 64 + lane of each tile
+  __device__ __forceinline__ void load_v(int j, char* tile) const {
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) {
+      const __amdgpu_buffer_rsrc_t r = rows_rsrc(vbase[nb], v_st, 64 * j, T_len);
+#pragma unroll
+      for (int pp = 0; pp < VN; ++pp)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(r, SAF_LDS_PTR(tile + nb * VB + (NW * pp + wave) * 1024), 16,
+                                                 voff[pp], 0, 0, 0);
+    }
+  }
+
+  // P^T operand of key step (ks, sh) of block j for query tile qt.  Fast
+  // path: one raw buffer load; keys past the row and rows past T are
+  // cleared at use (mask_p).  General path: masked and widened here.
+  __device__ __forceinline__ uint4 p_op(const FrozenParams& p, int j, int ks, int sh, int qt) const {
+    const int kstart = 64 * j + 32 * ks + 16 * sh + 8 * g;
+    if constexpr (FAST) {
+      return __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(
+                                           prs, poff[qt] + 2u * (uint32_t)kstart, 0, 0));
+    } else {
+      const int nvalid = row[qt] < T_len ? min(row[qt] - kstart + 1, 8) : 0;
+      return p_chunk<T, PT>(p, prow[qt], kstart, nvalid);
+    }
+  }
+  __device__ __forceinline__ void load_p(const FrozenParams& p, uint4 (&pb)[2][2][QT], int j) const {
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+      for (int sh = 0; sh < 2; ++sh)
+#pragma unroll
+        for (int qt = 0; qt < QT; ++qt) pb[ks][sh][qt] = p_op(p, j, ks, sh, qt);
+  }
+  __device__ __forceinline__ void mask_p(uint4 (&pb)[2][2][QT], int j) const {
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+      for (int sh = 0; sh < 2; ++sh)
+#pragma unroll
+        for (int qt = 0; qt < QT; ++qt) {
+          const int kstart = 64 * j + 32 * ks + 16 * sh + 8 * g;
+          const int nvalid = row[qt] < T_len ? min(row[qt] - kstart + 1, 8) : 0;
+          pb[ks][sh][qt] = keep_leading(pb[ks][sh][qt], nvalid);
+        }
+  }
+
+  // O^T += V^T P^T for one 64-key block (V tiles at `cur`)
+  __device__ __forceinline__ void mma_block(const char* cur, const uint4 (&pb)[2][2][QT]) {
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+      for (int sh = 0; sh < 2; ++sh)
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+          for (int dt = 0; dt < NDT; ++dt) {
+            const char* src = cur + nb * VB + (32 * ks + 16 * sh) * PITCH + vro[dt];
+            const uint2 lo = ds_read_tr16(src);
+            const uint2 hi = ds_read_tr16(src + 4 * PITCH);
+            const uint4 a = make_uint4(lo.x, lo.y, hi.x, hi.y);
+#pragma unroll
+            for (int qt = 0; qt < QT; ++qt) o[nb][qt][dt] = Elem<T>::mfma(a, pb[ks][sh][qt], o[nb][qt][dt]);
+          }
+  }
+
+  // Block j of the key range [kb0, kb1) (this wave's rows reach blocks
+  // < kb1_w): V_j in `cur`, P_j in `pc`; V_{j+1} -> `nxt`, P_{j+1} -> `pn`.
+  // In the fast path the loads of block j+1 are issued unconditionally (past
+  // the end they read zeros or data that is never used), so the compiler's
+  // own waits before the MFMAs count exactly the loads issued after P_j.
+  __device__ __forceinline__ void block(const FrozenParams& p, int j, int kb1, int kb1_w, char* cur, char* nxt,
+                                        uint4 (&pc)[2][2][QT], uint4 (&pn)[2][2][QT]) {
+    // end-of-block wait: this wave's V_{j+1} DMA has landed (fast path: the
+    // 4 QT pattern loads issued after it may stay in flight)
+    constexpr int kWaitV = waitcnt_vm(FAST ? 4 * QT : 0);
+    const bool next = j + 1 < kb1_w;
+    if (FAST || j + 1 < kb1) load_v(j + 1, nxt);
+    asm volatile("" ::: "memory");
+    if (FAST || next) load_p(p, pn, j + 1);
+    asm volatile("" ::: "memory");
+    if (j < kb1_w) {
+      if (FAST && (64 * j + 63 > q0w || q0w + 32 * QT > T_len)) {
+        // a diagonal block or the last rows: clear keys past each row and rows past T
+        asm volatile("" ::: "memory");
+        mask_p(pc, j);
+      }
+      mma_block(cur, pc);
+    }
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_waitcnt(kWaitV);
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+  }
+};
+
 // Dense P.V.  Each lane loads its own B operands straight from the pattern
 // rows (lane (n, g): query n of a 32-row tile, keys 8g + 0..7 of each 16-key
-// step = one 16-byte read), refilled for the next 64-key block as soon as
-// they are used, so P needs no LDS staging and no barrier.  A workgroup
-// serves NB batch elements of one head: every P^T operand feeds the MFMAs of
-// all NB of them, so the pattern (the dominant traffic) is read from HBM once
-// per NB sequences instead of once per sequence.  The V^T tiles of the NB
-// sequences (shared by the four waves) are double-buffered in LDS; with QT = 2
-// each V^T operand read from LDS feeds two MFMAs.  Work items cover a key
-// segment of a query block; split blocks write fp32 partials that the combine
-// kernel sums.  Two resident workgroups per CU overlap one's loads with the
-// other's MFMAs.
-template <typename T, typename PT, int HD, int QT, int NB>
+// step = one 16-byte read), so P needs no LDS staging.  A workgroup serves NB
+// batch elements of one head: every P^T operand feeds the MFMAs of all NB of
+// them, so the pattern (the dominant traffic) is read from HBM once per NB
+// sequences.  The V tiles of the NB sequences (shared by the four waves)
+// arrive by buffer_load ... lds DMA into two static LDS slots (the VRow
+// layout of the live-head kernel) and their V^T operands come from
+// transposing ds_read_b64_tr_b16 reads.
+//
+// Block j issues the DMA of V_{j+1}, then the P^T operands of block j+1 into
+// the other register set, then the MFMAs of block j.  When the pattern is in
+// the activation dtype with 16-byte rows (FAST), every P load is one
+// unconditional buffer load (rows and keys past the data read zero or are
+// masked), so a wave knows that exactly the 4 QT loads of block j+1 were
+// issued after its DMA: it waits for vmcnt <= 4 QT (its V_{j+1} chunks have
+// landed, the pattern loads stay in flight) and meets the others at a bare
+// s_barrier.  A __syncthreads here would drain the pattern loads at every
+// block.  Other pattern dtypes wait for vmcnt 0.  Work items cover a key
+// segment of a query block; split blocks write fp32 partials that the
+// combine kernel sums.  Two resident workgroups per CU.
+template <typename T, typename PT, int HD, int QT, int NB, bool FAST>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void frozen_dense_kernel(const FrozenParams p) {
-  constexpr int NW = 4, NTHR = 256;
+  using St = DenseState<T, PT, HD, QT, NB, FAST>;
+  constexpr int NW = St::NW;
   constexpr int BM = NW * 32 * QT;
-  constexpr int NDT = HD / 32;
+  constexpr int NDT = St::NDT;
   static_assert(NB * QT * NDT <= 8, "accumulators must fit two waves per SIMD");
-  __shared__ __align__(16) uint4 v_lds[2][NB][VLayout<HD>::BYTES / 16];
+  static_assert(!FAST || std::is_same<T, PT>::value, "the fast path loads the pattern in the activation dtype");
+  __shared__ __align__(16) char vs0[NB * St::VB], vs1[NB * St::VB];
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -299,11 +432,8 @@ void frozen_dense_kernel(const FrozenParams p) {
   qb = __builtin_amdgcn_readfirstlane(qb);
   seg = __builtin_amdgcn_readfirstlane(seg);
   const int h = p.out_head[slot];
-  const PT* pbase = reinterpret_cast<const PT*>(p.patt) + (int64_t)p.pat_head[slot] * p.p_sh;
-  const T* vbase[NB];
-#pragma unroll
-  for (int nb = 0; nb < NB; ++nb)
-    vbase[nb] = reinterpret_cast<const T*>(p.v) + (int64_t)(bg * NB + nb) * p.v_sb + (int64_t)p.v_head[slot] * p.v_sh;
+  const int64_t pat_off = (int64_t)p.pat_head[slot] * p.p_sh;
+  const PT* pbase = reinterpret_cast<const PT*>(p.patt) + pat_off;
 
   const int T_len = p.T;
   const int q0 = qb * BM;
@@ -311,84 +441,49 @@ void frozen_dense_kernel(const FrozenParams p) {
   const bool split = p.n_items != 0 && p.part_base[qb] >= 0;
   const int kb0 = split ? seg * p.seg_len : 0;
   const int kb1 = split ? min(nkb, kb0 + p.seg_len) : nkb;
-  const int q0w = q0 + wave * 32 * QT;
-  const int kend_w = min(q0w + 32 * QT, T_len);
-  const int kb1_w = min(kb1, kend_w > 0 ? (kend_w + 63) / 64 : 0);  // blocks this wave's rows reach
 
-  int row[QT];
-  const PT* prow[QT];
+  St st;
+#pragma unroll
+  for (int nb = 0; nb < NB; ++nb)
+    st.vbase[nb] = reinterpret_cast<const T*>(p.v) + (int64_t)(bg * NB + nb) * p.v_sb + (int64_t)p.v_head[slot] * p.v_sh;
+  st.v_st = p.v_st;
+  st.T_len = T_len;
+  st.wave = wave;
+  st.g = g;
+  st.q0w = q0 + wave * 32 * QT;
+  const int kend_w = min(st.q0w + 32 * QT, T_len);
+  const int kb1_w = min(kb1, kend_w > 0 ? (kend_w + 63) / 64 : 0);  // blocks this wave's rows reach
+#pragma unroll
+  for (int pp = 0; pp < St::VN; ++pp) st.voff[pp] = vrow_dma_offset<T, HD>((NW * pp + wave) * 64 + lane, p.v_st);
+#pragma unroll
+  for (int dt = 0; dt < NDT; ++dt) st.vro[dt] = vt_read_offset<HD>(lane, dt);
+  // pattern rows of this lane (rows past T read row T-1 and are masked); the
+  // descriptor runs from the workgroup's first pattern row to the end of the
+  // buffer
 #pragma unroll
   for (int qt = 0; qt < QT; ++qt) {
-    row[qt] = q0w + 32 * qt + n;
-    prow[qt] = pbase + (int64_t)min(row[qt], T_len - 1) * p.p_si;
+    st.row[qt] = st.q0w + 32 * qt + n;
+    const int rc = min(st.row[qt], T_len - 1);
+    st.prow[qt] = pbase + (int64_t)rc * p.p_si;
+    st.poff[qt] = (uint32_t)((int64_t)(rc - q0) * p.p_si * (int64_t)sizeof(PT));
   }
-  // P^T operand of key step (ks, sh) of block j for query tile qt
-  auto p_op = [&](int j, int ks, int sh, int qt) {
-    const int kstart = 64 * j + 32 * ks + 16 * sh + 8 * g;
-    const int nvalid = row[qt] < T_len ? min(row[qt] - kstart + 1, 8) : 0;
-    return p_chunk<T, PT>(p, prow[qt], kstart, nvalid);
-  };
-
-  f32x16_t o[NB][QT][NDT];
+  const int64_t pfirst = pat_off + (int64_t)q0 * p.p_si;
+  st.prs = span_rsrc(reinterpret_cast<const PT*>(p.patt) + pfirst, (p.patt_elems - pfirst) * (int64_t)sizeof(PT));
 #pragma unroll
   for (int nb = 0; nb < NB; ++nb)
 #pragma unroll
     for (int qt = 0; qt < QT; ++qt)
 #pragma unroll
-      for (int dt = 0; dt < NDT; ++dt) o[nb][qt][dt] = zero16();
+      for (int dt = 0; dt < NDT; ++dt) st.o[nb][qt][dt] = zero16();
 
-  VStager<T, HD, NTHR> vst[NB];
-  uint4 pb[2][2][QT];
-#pragma unroll
-  for (int nb = 0; nb < NB; ++nb) vst[nb].load(vbase[nb], p.v_st, 64 * kb0, T_len, tid);
-  if (kb0 < kb1_w) {
-#pragma unroll
-    for (int ks = 0; ks < 2; ++ks)
-#pragma unroll
-      for (int sh = 0; sh < 2; ++sh)
-#pragma unroll
-        for (int qt = 0; qt < QT; ++qt) pb[ks][sh][qt] = p_op(kb0, ks, sh, qt);
-  }
-#pragma unroll
-  for (int nb = 0; nb < NB; ++nb) vst[nb].store(reinterpret_cast<uint32_t*>(v_lds[0][nb]), tid);
-  __syncthreads();
-
-  for (int j = kb0; j < kb1; ++j) {
-    const int buf = (j - kb0) & 1;
-    const bool more = j + 1 < kb1;
-    if (more) {
-#pragma unroll
-      for (int nb = 0; nb < NB; ++nb) vst[nb].load(vbase[nb], p.v_st, 64 * (j + 1), T_len, tid);
-    }
-    if (j < kb1_w) {
-      const bool next = j + 1 < kb1_w;
-      // each operand is refilled with block j+1's right after its last use,
-      // so one block of P^T registers keeps a block of loads in flight
-#pragma unroll
-      for (int ks = 0; ks < 2; ++ks)
-#pragma unroll
-        for (int sh = 0; sh < 2; ++sh) {
-#pragma unroll
-          for (int nb = 0; nb < NB; ++nb) {
-            const uint4* vt = v_lds[buf][nb];
-#pragma unroll
-            for (int dt = 0; dt < NDT; ++dt) {
-              const uint4 a = vt[VLayout<HD>::chunk(32 * dt + n, 4 * ks + 2 * sh + g)];
-#pragma unroll
-              for (int qt = 0; qt < QT; ++qt) o[nb][qt][dt] = Elem<T>::mfma(a, pb[ks][sh][qt], o[nb][qt][dt]);
-            }
-          }
-          if (next) {
-#pragma unroll
-            for (int qt = 0; qt < QT; ++qt) pb[ks][sh][qt] = p_op(j + 1, ks, sh, qt);
-          }
-        }
-    }
-    if (more) {
-#pragma unroll
-      for (int nb = 0; nb < NB; ++nb) vst[nb].store(reinterpret_cast<uint32_t*>(v_lds[buf ^ 1][nb]), tid);
-    }
-    __syncthreads();
+  uint4 pA[2][2][QT], pB[2][2][QT];
+  st.load_v(kb0, vs0);
+  if (FAST || kb0 < kb1_w) st.load_p(p, pA, kb0);
+  __syncthreads();  // prologue: V_kb0 in LDS for every wave
+  // two blocks per iteration, so every DMA target and read names a static slot
+  for (int j = kb0; j < kb1; j += 2) {
+    st.block(p, j, kb1, kb1_w, vs0, vs1, pA, pB);
+    if (j + 1 < kb1) st.block(p, j + 1, kb1, kb1_w, vs1, vs0, pB, pA);
   }
 
 #pragma unroll
@@ -397,7 +492,7 @@ void frozen_dense_kernel(const FrozenParams p) {
     T* obase = reinterpret_cast<T*>(p.out) + b * p.o_sb + (int64_t)h * p.o_sh;
 #pragma unroll
     for (int qt = 0; qt < QT; ++qt) {
-      const int i = row[qt];
+      const int i = st.row[qt];
       if (i >= T_len) continue;
       if (split) {
         const int64_t pidx = ((int64_t)b * p.n_slots + slot) * p.n_part_per_head + p.part_base[qb] + seg;
@@ -407,10 +502,10 @@ void frozen_dense_kernel(const FrozenParams p) {
 #pragma unroll
           for (int r4 = 0; r4 < 4; ++r4)
             *reinterpret_cast<float4*>(po + 32 * dt + 8 * r4 + 4 * g) =
-                make_float4(o[nb][qt][dt][4 * r4], o[nb][qt][dt][4 * r4 + 1], o[nb][qt][dt][4 * r4 + 2],
-                            o[nb][qt][dt][4 * r4 + 3]);
+                make_float4(st.o[nb][qt][dt][4 * r4], st.o[nb][qt][dt][4 * r4 + 1], st.o[nb][qt][dt][4 * r4 + 2],
+                            st.o[nb][qt][dt][4 * r4 + 3]);
       } else {
-        store_out_tile<T, HD>(obase + (int64_t)i * p.o_st, o[nb][qt], 1.f, g);
+        store_out_tile<T, HD>(obase + (int64_t)i * p.o_st, st.o[nb][qt], 1.f, g);
       }
     }
   }
@@ -421,7 +516,13 @@ static void launch_dense_t(const FrozenParams& p, hipStream_t s) {
   constexpr int QT = dense_qtiles(HD, NB);
   const int64_t groups = (int64_t)(p.n_items ? p.n_items : p.n_qblk) * p.n_slots;
   const dim3 grid((unsigned)(8 * (p.B / NB) * ((groups + 7) / 8)));
-  hipLaunchKernelGGL((frozen_dense_kernel<T, PT, HD, QT, NB>), grid, dim3(256), 0, s, p);
+  if constexpr (std::is_same<T, PT>::value) {
+    if (p.patt_vec) {
+      hipLaunchKernelGGL((frozen_dense_kernel<T, PT, HD, QT, NB, true>), grid, dim3(256), 0, s, p);
+      return;
+    }
+  }
+  hipLaunchKernelGGL((frozen_dense_kernel<T, PT, HD, QT, NB, false>), grid, dim3(256), 0, s, p);
 }
 
 template <typename T, typename PT, int HD>

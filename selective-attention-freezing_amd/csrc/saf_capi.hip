@@ -437,6 +437,8 @@ int run_dense(const saf_tensor_t& patt, const saf_tensor_t& v, const saf_tensor_
   p.patt_dtype = patt.dtype;
   p.p_sh = patt.stride[0]; p.p_si = patt.stride[1]; p.p_sj = patt.stride[2];
   p.p_cols = (int)patt.size[2];
+  p.patt_elems = 1 + (patt.size[0] - 1) * patt.stride[0] + (patt.size[1] - 1) * patt.stride[1] +
+                 (patt.size[2] - 1) * patt.stride[2];
   const int es = elem_size(patt.dtype);
   p.patt_vec = patt.stride[2] == 1 && reinterpret_cast<uintptr_t>(patt.data) % 16 == 0 &&
                (patt.stride[1] * es) % 16 == 0 && (patt.stride[0] * es) % 16 == 0;

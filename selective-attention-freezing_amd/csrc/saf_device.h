@@ -158,6 +158,68 @@ template <int HD> struct VLayout {
   }
 };
 
+#define SAF_LDS_PTR(p) ((__attribute__((address_space(3))) void*)(p))
+
+// V tile: 64 key rows of HD values; row pitch VSEG 32-byte segments; the
+// logical segment s of key row r is stored at segment s ^ (r & 3), so the
+// four rows a 16-lane group of ds_read_b64_tr_b16 touches fall in four
+// different bank quarters.
+template <int HD> struct VRow {
+  static constexpr int VSEG = HD / 16 <= 4 ? 4 : 8;
+  static constexpr int PITCH = VSEG * 32;
+  static constexpr int CHP = 2 * VSEG;  // 16-byte chunks per row
+  static constexpr int BYTES = 64 * PITCH;
+};
+
+typedef short short4_t __attribute__((ext_vector_type(4)));
+
+// ds_read_b64_tr_b16: a transposing LDS read (16-bit elements).
+__device__ __forceinline__ uint2 ds_read_tr16(const char* p) {
+  const short4_t r = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+      (__attribute__((address_space(3))) short4_t*)(p));
+  return __builtin_bit_cast(uint2, r);
+}
+
+// Lane offset (within a V tile in the VRow layout) of the ds_read_tr16 pair
+// that builds the V^T A operand of rows d = 32 dt + (lane % 32) for keys
+// 8 (lane / 32) + 0..7 of a 16-key step: the operand is
+// (tr16(base + off), tr16(base + off + 4 PITCH)) with base at the step's
+// first key row.
+template <int HD>
+__device__ inline int vt_read_offset(int lane, int dt) {
+  const int i = lane & 15, gh = (lane >> 4) & 1, g = lane >> 5;
+  const int vkey = 8 * g + (i >> 2);
+  return vkey * VRow<HD>::PITCH + (((2 * dt + gh) ^ (i >> 2)) << 5) + 8 * (i & 3);
+}
+
+// Source offset of DMA chunk X of a 64-key V tile in the VRow layout:
+// buffer_load ... lds writes chunk X (16 bytes) at tile + 16 X; the chunk
+// holds logical 16-byte column c of key row X / CHP.  Padding chunks (hd 32,
+// 96) re-read column 0.
+template <typename T, int HD>
+__device__ inline uint32_t vrow_dma_offset(int X, int64_t v_st) {
+  constexpr int KCH = HD / 8;
+  const int key = X / VRow<HD>::CHP, pc = X % VRow<HD>::CHP;
+  const int c = 2 * ((pc >> 1) ^ (key & 3)) + (pc & 1);
+  return (uint32_t)(key * v_st * (int64_t)sizeof(T)) + 16u * (c < KCH ? c : 0);
+}
+
+// Buffer descriptor over `bytes` bytes from base (clamped to [0, 2^31)):
+// loads past the end return zero.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t span_rsrc(const void* base, int64_t bytes) {
+  const int num = (int)(bytes < 0 ? 0 : (bytes > 0x7fffffff ? 0x7fffffff : bytes));
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, num, kBufferWord3);
+}
+
+// Buffer descriptor over rows j0.. of a (rows, st) tensor ending after row
+// T_len - 1: loads past the end return zero.
+template <typename T>
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t rows_rsrc(const T* base, int64_t st, int j0, int T_len) {
+  const int64_t bytes = (int64_t)(T_len - j0) * st * (int64_t)sizeof(T);
+  const int num = (int)(bytes < 0 ? 0 : (bytes > 0x7fffffff ? 0x7fffffff : bytes));
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<T*>(base + (int64_t)j0 * st), 0, num, kBufferWord3);
+}
+
 // Stage a 64-key V tile (rows j0..j0+63 of one head) into registers:
 // item idx covers keys 2kp, 2kp+1 and columns 8c..8c+7.  Rows >= T are zero.
 template <typename T, int HD, int NTHR> struct VStager {

@@ -76,6 +76,7 @@ struct FrozenParams {
   int patt_vec;  // rows contiguous and aligned for 16/32-byte loads
   int p_cols;    // S: row length of the pattern buffer
   int64_t p_sh, p_si, p_sj;
+  int64_t patt_elems;  // elements from patt to the end of its last row
   // decomposed buffers (H, S) indexed by the natural head
   const void* alpha;
   const void* rho;

@@ -234,6 +234,34 @@ def test_dense_causal_split(T, hd, pdtype):
     compare(yu, ref[:, [0, 2]], what=f"dense unsplit T{T} hd{hd} {pdtype}")
 
 
+@pytest.mark.parametrize("B,T,hd,dtype", [(1, 8, 64, torch.bfloat16), (2, 72, 32, torch.bfloat16),
+                                          (3, 1000, 128, torch.bfloat16), (2, 1544, 64, torch.float16),
+                                          (4, 520, 96, torch.bfloat16), (1, 2048, 128, torch.float16)])
+def test_dense_pattern_in_activation_dtype(B, T, hd, dtype):
+    """Dense patterns stored in the activation dtype with 16-byte rows (the
+    kernel's unconditional buffer-load path) and S = T, so the last rows'
+    loads run past the end of the pattern buffer: both the fused operator
+    (causal split with a workspace) and frozen_pv match the oracle; the last
+    head's pattern is the last slab of the buffer."""
+    K = _kernel()
+    H = 3
+    frozen, hidx, live = routing(H, {0: 1, 2: 1})
+    patt = make_pattern(2, T, seed=T + hd).to(dtype)
+    pidx = torch.tensor([1, 0, 0], dtype=torch.int32)
+    q, k, v = qkv(B, H, T, hd, seed=T * 3 + hd, dtype=dtype)
+    q, k = q[:, live].contiguous(), k[:, live].contiguous()
+    y = K.fused_mixed_attn(q.to(DEV), k.to(DEV), v.to(DEV), patt.to(DEV), frozen.to(DEV), hidx.to(DEV),
+                           pidx.to(DEV))
+    torch.cuda.synchronize()
+    ref = orc.eager_mixed_attention(f64(q), f64(k), f64(v), frozen.numpy(), hidx.numpy(), pidx.numpy(),
+                                    patt=f64(patt))
+    compare(y, ref, what=f"dense {dtype} patterns B{B} T{T} hd{hd}")
+    fz = torch.tensor([1, 0], dtype=torch.int32)
+    yu = K.frozen_pv(patt.to(DEV), v[:, [0, 2]].contiguous().to(DEV), fz.to(DEV), T)
+    torch.cuda.synchronize()
+    compare(yu, ref[:, [0, 2]], what=f"frozen_pv {dtype} patterns B{B} T{T} hd{hd}")
+
+
 def test_gqa_kvidx():
     """Qwen-style map: 14 query heads over 2 KV heads, frozen query heads read
     the shared V of their group (qwen/kernel/fused_attn.py:254-259)."""
