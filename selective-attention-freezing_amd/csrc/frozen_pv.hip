@@ -260,19 +260,22 @@ constexpr int waitcnt_vm(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4) 
 
 // Per-wave state of the dense P.V kernel (below): the lane's pattern rows,
 // the V DMA and V^T read offsets, and the O^T accumulators of NB sequences.
-template <typename T, typename PT, int HD, int QT, int NB, bool FAST>
+template <typename T, typename PT, int HD, int QT, int NB, int NW, bool FAST>
 struct DenseState {
-  static constexpr int NW = 4;
   static constexpr int NDT = HD / 32;
   static constexpr int VB = VRow<HD>::BYTES;
   static constexpr int PITCH = VRow<HD>::PITCH;
   static constexpr int VN = VRow<HD>::CHP / NW;  // DMA chunks per thread per V tile
+  static_assert(VRow<HD>::CHP % NW == 0, "V tile chunks must split evenly over the waves");
+  // end-of-block wait: this wave's V_{j+1} DMA has landed.  Fast path: the
+  // loads issued after it (P_{j+1}, V_{j+2}, P_{j+2}) may stay in flight.
+  static constexpr int kWaitV = waitcnt_vm(FAST ? 8 * QT + NB * VN : 0);
   const T* vbase[NB];
   int64_t v_st;
   int T_len, wave, g, q0w;
   int row[QT];
   const PT* prow[QT];    // general path: the lane's pattern rows
-  uint32_t poff[QT];     // fast path: their byte offsets in the descriptor
+  uint32_t poff[QT];     // fast path: byte offset of key 8g of the row in the descriptor
   __amdgpu_buffer_rsrc_t prs;
   uint32_t voff[VN];
   int vro[NDT];
@@ -295,11 +298,13 @@ struct DenseState {
   // path: one raw buffer load; keys past the row and rows past T are
   // cleared at use (mask_p).  General path: masked and widened here.
   __device__ __forceinline__ uint4 p_op(const FrozenParams& p, int j, int ks, int sh, int qt) const {
-    const int kstart = 64 * j + 32 * ks + 16 * sh + 8 * g;
     if constexpr (FAST) {
+      // per-lane part in the VGPR offset (row, 8g, step), the block in the
+      // scalar offset: no per-block address arithmetic in vector registers
       return __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(
-                                           prs, poff[qt] + 2u * (uint32_t)kstart, 0, 0));
+                                           prs, poff[qt] + (uint32_t)(64 * ks + 32 * sh), 128 * j, 0));
     } else {
+      const int kstart = 64 * j + 32 * ks + 16 * sh + 8 * g;
       const int nvalid = row[qt] < T_len ? min(row[qt] - kstart + 1, 8) : 0;
       return p_chunk<T, PT>(p, prow[qt], kstart, nvalid);
     }
@@ -345,19 +350,16 @@ struct DenseState {
   }
 
   // Block j of the key range [kb0, kb1) (this wave's rows reach blocks
-  // < kb1_w): V_j in `cur`, P_j in `pc`; V_{j+1} -> `nxt`, P_{j+1} -> `pn`.
-  // In the fast path the loads of block j+1 are issued unconditionally (past
-  // the end they read zeros or data that is never used), so the compiler's
-  // own waits before the MFMAs count exactly the loads issued after P_j.
-  __device__ __forceinline__ void block(const FrozenParams& p, int j, int kb1, int kb1_w, char* cur, char* nxt,
-                                        uint4 (&pc)[2][2][QT], uint4 (&pn)[2][2][QT]) {
-    // end-of-block wait: this wave's V_{j+1} DMA has landed (fast path: the
-    // 4 QT pattern loads issued after it may stay in flight)
-    constexpr int kWaitV = waitcnt_vm(FAST ? 4 * QT : 0);
-    const bool next = j + 1 < kb1_w;
-    if (FAST || j + 1 < kb1) load_v(j + 1, nxt);
+  // < kb1_w): V_j in `cur` and P_j in `pc` (loaded two blocks earlier);
+  // V_{j+2} -> `fut`, P_{j+2} -> `pf`.  In the fast path the loads are issued
+  // unconditionally (past the end they read zeros or data that is never
+  // used), so the compiler's own waits before the MFMAs count exactly the
+  // loads issued after P_j.
+  __device__ __forceinline__ void block(const FrozenParams& p, int j, int kb1, int kb1_w, const char* cur,
+                                        char* fut, uint4 (&pc)[2][2][QT], uint4 (&pf)[2][2][QT]) {
+    if (FAST || j + 2 < kb1) load_v(j + 2, fut);
     asm volatile("" ::: "memory");
-    if (FAST || next) load_p(p, pn, j + 1);
+    if (FAST || j + 2 < kb1_w) load_p(p, pf, j + 2);
     asm volatile("" ::: "memory");
     if (j < kb1_w) {
       if (FAST && (64 * j + 63 > q0w || q0w + 32 * QT > T_len)) {
@@ -376,35 +378,35 @@ struct DenseState {
 
 // Dense P.V.  Each lane loads its own B operands straight from the pattern
 // rows (lane (n, g): query n of a 32-row tile, keys 8g + 0..7 of each 16-key
-// step = one 16-byte read), so P needs no LDS staging.  A workgroup serves NB
-// batch elements of one head: every P^T operand feeds the MFMAs of all NB of
-// them, so the pattern (the dominant traffic) is read from HBM once per NB
-// sequences.  The V tiles of the NB sequences (shared by the four waves)
-// arrive by buffer_load ... lds DMA into two static LDS slots (the VRow
-// layout of the live-head kernel) and their V^T operands come from
-// transposing ds_read_b64_tr_b16 reads.
+// step = one 16-byte read), so P needs no LDS staging.  A workgroup of NW = 8
+// waves (256 query rows, two waves per SIMD) serves NB batch elements of one
+// head: every P^T operand feeds the MFMAs of all NB of them, so the pattern
+// (the dominant traffic) is read from HBM once per NB sequences, and each V
+// tile is shared by 256 rows.  The V tiles of the NB sequences arrive by
+// buffer_load ... lds DMA into three static LDS slots (the VRow layout of the
+// live-head kernel); their V^T operands come from transposing
+// ds_read_b64_tr_b16 reads.
 //
-// Block j issues the DMA of V_{j+1}, then the P^T operands of block j+1 into
-// the other register set, then the MFMAs of block j.  When the pattern is in
-// the activation dtype with 16-byte rows (FAST), every P load is one
-// unconditional buffer load (rows and keys past the data read zero or are
-// masked), so a wave knows that exactly the 4 QT loads of block j+1 were
-// issued after its DMA: it waits for vmcnt <= 4 QT (its V_{j+1} chunks have
-// landed, the pattern loads stay in flight) and meets the others at a bare
-// s_barrier.  A __syncthreads here would drain the pattern loads at every
-// block.  Other pattern dtypes wait for vmcnt 0.  Work items cover a key
-// segment of a query block; split blocks write fp32 partials that the
-// combine kernel sums.  Two resident workgroups per CU.
+// The kernel is latency-bound unless enough bytes are in flight, so V and P
+// run two blocks ahead: block j issues the DMA of V_{j+2} and the P^T loads
+// of block j+2 (a third register set), then the MFMAs of block j.  When the
+// pattern is in the activation dtype with 16-byte rows (FAST) every P load is
+// one unconditional buffer load, so a wave knows how many loads were issued
+// after its V_{j+1} DMA: it waits for exactly those to remain (vmcnt) and
+// meets the others at a bare s_barrier; a __syncthreads would drain the
+// pattern loads at every block.  Other pattern dtypes wait for vmcnt 0.
+// Work items cover a key segment of a query block; split blocks write fp32
+// partials that the combine kernel sums.
 template <typename T, typename PT, int HD, int QT, int NB, bool FAST>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))
+__global__ __launch_bounds__(64 * kDenseWaves) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void frozen_dense_kernel(const FrozenParams p) {
-  using St = DenseState<T, PT, HD, QT, NB, FAST>;
-  constexpr int NW = St::NW;
+  constexpr int NW = kDenseWaves;
+  using St = DenseState<T, PT, HD, QT, NB, NW, FAST>;
   constexpr int BM = NW * 32 * QT;
   constexpr int NDT = St::NDT;
   static_assert(NB * QT * NDT <= 8, "accumulators must fit two waves per SIMD");
   static_assert(!FAST || std::is_same<T, PT>::value, "the fast path loads the pattern in the activation dtype");
-  __shared__ __align__(16) char vs0[NB * St::VB], vs1[NB * St::VB];
+  __shared__ __align__(16) char vs0[NB * St::VB], vs1[NB * St::VB], vs2[NB * St::VB];
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -465,7 +467,7 @@ void frozen_dense_kernel(const FrozenParams p) {
     st.row[qt] = st.q0w + 32 * qt + n;
     const int rc = min(st.row[qt], T_len - 1);
     st.prow[qt] = pbase + (int64_t)rc * p.p_si;
-    st.poff[qt] = (uint32_t)((int64_t)(rc - q0) * p.p_si * (int64_t)sizeof(PT));
+    st.poff[qt] = (uint32_t)((int64_t)(rc - q0) * p.p_si * (int64_t)sizeof(PT)) + 16u * g;
   }
   const int64_t pfirst = pat_off + (int64_t)q0 * p.p_si;
   st.prs = span_rsrc(reinterpret_cast<const PT*>(p.patt) + pfirst, (p.patt_elems - pfirst) * (int64_t)sizeof(PT));
@@ -476,14 +478,27 @@ void frozen_dense_kernel(const FrozenParams p) {
 #pragma unroll
       for (int dt = 0; dt < NDT; ++dt) st.o[nb][qt][dt] = zero16();
 
-  uint4 pA[2][2][QT], pB[2][2][QT];
+  // prologue: blocks kb0 and kb0+1 in flight, then V_kb0 landed everywhere
+  uint4 pA[2][2][QT], pB[2][2][QT], pC[2][2][QT];
   st.load_v(kb0, vs0);
+  asm volatile("" ::: "memory");
   if (FAST || kb0 < kb1_w) st.load_p(p, pA, kb0);
-  __syncthreads();  // prologue: V_kb0 in LDS for every wave
-  // two blocks per iteration, so every DMA target and read names a static slot
-  for (int j = kb0; j < kb1; j += 2) {
-    st.block(p, j, kb1, kb1_w, vs0, vs1, pA, pB);
-    if (j + 1 < kb1) st.block(p, j + 1, kb1, kb1_w, vs1, vs0, pB, pA);
+  asm volatile("" ::: "memory");
+  if (FAST || kb0 + 1 < kb1) st.load_v(kb0 + 1, vs1);
+  asm volatile("" ::: "memory");
+  if (FAST || kb0 + 1 < kb1_w) st.load_p(p, pB, kb0 + 1);
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_waitcnt(St::kWaitV);
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+  // three blocks per iteration, so every DMA target and read names a static
+  // slot and register set.  The iteration is straight-line (blocks past kb1
+  // issue their loads and barrier but no MFMAs): the compiler then counts
+  // the loads in flight across the back edge exactly.
+  for (int j = kb0; j < kb1; j += 3) {
+    st.block(p, j, kb1, kb1_w, vs0, vs2, pA, pC);
+    st.block(p, j + 1, kb1, kb1_w, vs1, vs0, pB, pA);
+    st.block(p, j + 2, kb1, kb1_w, vs2, vs1, pC, pB);
   }
 
 #pragma unroll
@@ -518,11 +533,11 @@ static void launch_dense_t(const FrozenParams& p, hipStream_t s) {
   const dim3 grid((unsigned)(8 * (p.B / NB) * ((groups + 7) / 8)));
   if constexpr (std::is_same<T, PT>::value) {
     if (p.patt_vec) {
-      hipLaunchKernelGGL((frozen_dense_kernel<T, PT, HD, QT, NB, true>), grid, dim3(256), 0, s, p);
+      hipLaunchKernelGGL((frozen_dense_kernel<T, PT, HD, QT, NB, true>), grid, dim3(64 * kDenseWaves), 0, s, p);
       return;
     }
   }
-  hipLaunchKernelGGL((frozen_dense_kernel<T, PT, HD, QT, NB, false>), grid, dim3(256), 0, s, p);
+  hipLaunchKernelGGL((frozen_dense_kernel<T, PT, HD, QT, NB, false>), grid, dim3(64 * kDenseWaves), 0, s, p);
 }
 
 template <typename T, typename PT, int HD>

@@ -418,10 +418,9 @@ int decomp_resident(int) { return 3; }
 
 // Dense P.V work plan: query blocks of the kernel's shape, balanced over the
 // batch groups that share a pattern (dense_batch_group).
-int dense_block_rows(int B, int HD) { return block_rows(dense_qtiles(HD, dense_batch_group(B))); }
 FlashPlan plan_dense(int B, int n_slots, int T, int HD) {
   const int nb = dense_batch_group(B);
-  return plan_flash(B / nb, n_slots, T, HD, dense_block_rows(B, HD), 2, nb);
+  return plan_flash(B / nb, n_slots, T, HD, dense_block_rows(B, HD), kDenseResident, nb);
 }
 
 // Dense P.V over the heads listed; with a workspace large enough for the

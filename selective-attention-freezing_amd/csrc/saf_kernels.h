@@ -168,12 +168,15 @@ hipError_t launch_add_layernorm(const AddLnParams& p, int dtype, hipStream_t s);
 // Queries per frozen-head workgroup (4 waves) for a query-tile count.
 inline int block_rows(int qt) { return 4 * 32 * qt; }
 
-// Dense P.V shape: a workgroup serves a group of NB batch elements (2 when
-// the batch is even, else 1) that share every pattern operand, with QT query
-// tiles per wave, so that the NB * QT * HD/32 accumulator tiles fit two
-// waves per SIMD.
+// Dense P.V shape: a workgroup of kDenseWaves waves (two per SIMD, one
+// query tile of 32 rows each) serves a group of NB batch elements (2 when
+// the batch is even, else 1) that share every pattern operand; one workgroup
+// per CU (its three V slots fill most of the LDS at hd 128).
+constexpr int kDenseWaves = 8;
 constexpr int dense_batch_group(int B) { return B % 2 == 0 ? 2 : 1; }
-constexpr int dense_qtiles(int hd, int nb) { return (hd > 64 && nb > 1) ? 1 : 2; }
+constexpr int dense_qtiles(int, int) { return 1; }
+constexpr int dense_block_rows(int, int) { return kDenseWaves * 32; }
+constexpr int kDenseResident = 1;
 
 // Waves of a live-head workgroup: 8 above hd 64 (two per SIMD sharing one
 // set of LDS tiles), else 4.
