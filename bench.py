@@ -518,7 +518,7 @@ def run_c3(args):
         tfs = (flops / n) / (per_ms / 1000.0) / 1e12
         t_hbm, t_mfma = nbytes / (PEAK_HBM_GBS * 1e9), (flops / n) / (PEAK_BF16_TFLOPS * 1e12)
         extra["frozen_dense_pv"] = {
-            "bound": "hbm" if t_hbm >= t_mfma else "mfma", "kernel": "frozen_pv_kernel<bf16,128,dense>",
+            "bound": "hbm" if t_hbm >= t_mfma else "mfma", "kernel": f"frozen_dense_kernel<bf16,bf16,128,nb{2 if B % 2 == 0 else 1}>",
             "achieved_gbs": round(gbs, 1), "achieved_tflops": round(tfs, 1),
             "frac": round(max(t_hbm, t_mfma) / (per_ms / 1000.0), 4),
             "bytes_per_launch": nbytes, "flop_per_launch": flops // n,
