@@ -243,17 +243,15 @@ struct FlashState {
 template <int HD, int QT>
 constexpr int flash_waves_per_eu() { return HD <= 64 ? (QT == 1 ? 3 : 2) : (QT == 1 ? 2 : 1); }
 
-template <typename T, int HD, int QT>
-__global__ __launch_bounds__(64 * flash_waves(HD))
-__attribute__((amdgpu_waves_per_eu(flash_waves_per_eu<HD, QT>(), flash_waves_per_eu<HD, QT>())))
-void flash_fwd_kernel(const FlashParams p) {
+// One work unit of the live-head kernel: unit = item * (B * n_slots) + r,
+// item = a query block (and key segment), r = (batch, live slot).
+template <typename T, int HD, int QT, typename Params>
+__device__ __forceinline__ void flash_unit(Params& p, const int unit, char* k0, char* k1, char* k2, char* v0,
+                                           char* v1, char* v2) {
   using St = FlashState<T, HD, QT>;
   constexpr int NW = flash_waves(HD);
   constexpr int BM = NW * 32 * QT;
   constexpr int NDT = St::NDT, NKT = St::NKT;
-  constexpr int KB = KLayout<HD>::BYTES, VB = VRow<HD>::BYTES;
-  __shared__ __align__(16) char k0[KB], k1[KB], k2[KB];
-  __shared__ __align__(16) char v0[VB], v1[VB], v2[VB];
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (SGPR)
@@ -261,16 +259,16 @@ void flash_fwd_kernel(const FlashParams p) {
   // work item: query block (and key segment) of one (batch, live slot);
   // items are ordered heaviest first, (batch, live slot) fastest
   const int nbh = p.B * p.n_slots;
-  const int r = blockIdx.x % nbh;
+  const int r = unit % nbh;
   const int b = r / p.n_slots, slot = r % p.n_slots;
   const int h = p.out_head[slot];
   int qb, seg = 0;
   if (p.n_items) {
-    const int it = p.items[blockIdx.x / nbh];
+    const int it = p.items[unit / nbh];
     qb = it >> 8;
     seg = it & 255;
   } else {
-    qb = p.n_qblk - 1 - (int)(blockIdx.x / nbh);
+    qb = p.n_qblk - 1 - unit / nbh;
   }
   const T* qbase = reinterpret_cast<const T*>(p.q) + b * p.q_sb + (int64_t)p.q_head[slot] * p.q_sh;
   const T* kbase = reinterpret_cast<const T*>(p.k) + b * p.k_sb + (int64_t)p.k_head[slot] * p.k_sh;
@@ -392,6 +390,45 @@ void flash_fwd_kernel(const FlashParams p) {
   }
 }
 
+// hd <= 64: three waves per SIMD (three resident 4-wave workgroups of 128
+// queries) or two of 256 queries; larger heads: one 8-wave workgroup per CU.
+// PERSIST (with a queue word p.queue, zeroed before the launch): the grid
+// holds only the resident workgroups, and each takes its next unit from the
+// queue when it finishes one (units in heaviest-first order), so a CU or XCD
+// that runs faster takes more units instead of each XCD working through a
+// fixed 1/8 of the grid.  Otherwise one workgroup per unit.
+template <typename T, int HD, int QT, bool PERSIST>
+__global__ __launch_bounds__(64 * flash_waves(HD))
+__attribute__((amdgpu_waves_per_eu(flash_waves_per_eu<HD, QT>(), flash_waves_per_eu<HD, QT>())))
+void flash_fwd_kernel(const FlashParams p) {
+  constexpr int KB = KLayout<HD>::BYTES, VB = VRow<HD>::BYTES;
+  __shared__ __align__(16) char k0[KB], k1[KB], k2[KB];
+  __shared__ __align__(16) char v0[VB], v1[VB], v2[VB];
+  if constexpr (!PERSIST) {
+    flash_unit<T, HD, QT>(p, blockIdx.x, k0, k1, k2, v0, v1, v2);
+  } else {
+    __shared__ int next_unit;
+    const int n_units = (p.n_items ? p.n_items : p.n_qblk) * p.B * p.n_slots;
+    int unit = blockIdx.x;
+    for (;;) {
+      // claim the next unit now, so the atomic's latency hides behind this one
+      if (threadIdx.x == 0) next_unit = (int)atomicAdd(p.queue, 1u) + (int)gridDim.x;
+      // the parameter block is read through a kernarg-segment pointer that
+      // the compiler cannot follow across iterations: its fields are loaded
+      // (scalar loads) per unit instead of being kept live in SGPRs across
+      // units, which spilled
+      const __attribute__((address_space(4))) FlashParams* pk =
+          (const __attribute__((address_space(4))) FlashParams*)__builtin_amdgcn_kernarg_segment_ptr();
+      asm volatile("" : "+s"(pk));
+      flash_unit<T, HD, QT>(*pk, unit, k0, k1, k2, v0, v1, v2);
+      __syncthreads();
+      unit = __builtin_amdgcn_readfirstlane(next_unit);
+      __syncthreads();  // every wave has read next_unit before it is claimed again
+      if (unit >= n_units) break;
+    }
+  }
+}
+
 // Merge the key-segment partials of split query blocks (one workgroup per
 // (batch, slot, split query block) and 64-row chunk; HD/4 threads x 4
 // columns per row): the
@@ -462,7 +499,9 @@ __global__ __launch_bounds__(256) void flash_combine_kernel(const CombineParams 
 
 // Explicit instantiations: every (dtype, head_dim, query tiles) the
 // launcher dispatches to gets its host stub emitted.
-#define SAF_FLASH_INST(T, HD, QT) template __global__ void flash_fwd_kernel<T, HD, QT>(const FlashParams);
+#define SAF_FLASH_INST(T, HD, QT) \
+  template __global__ void flash_fwd_kernel<T, HD, QT, false>(const FlashParams); \
+  template __global__ void flash_fwd_kernel<T, HD, QT, true>(const FlashParams);
 #define SAF_FLASH_INST_HD(T) \
   SAF_FLASH_INST(T, 32, 1) SAF_FLASH_INST(T, 32, 2) SAF_FLASH_INST(T, 64, 1) SAF_FLASH_INST(T, 64, 2) \
   SAF_FLASH_INST(T, 96, 1) SAF_FLASH_INST(T, 128, 1)
@@ -473,9 +512,14 @@ SAF_FLASH_INST_HD(_Float16)
 
 template <typename T, int HD, int QT>
 static hipError_t launch_flash_t(const FlashParams& p, hipStream_t s) {
-  const int64_t items = p.n_items ? p.n_items : p.n_qblk;
-  const dim3 grid((unsigned)(items * p.B * p.n_slots));
-  hipLaunchKernelGGL((flash_fwd_kernel<T, HD, QT>), grid, dim3(64 * flash_waves(HD)), 0, s, p);
+  const int64_t units = (int64_t)(p.n_items ? p.n_items : p.n_qblk) * p.B * p.n_slots;
+  if (p.queue != nullptr) {
+    const int64_t g = p.max_grid > 0 && units > p.max_grid ? p.max_grid : units;
+    hipLaunchKernelGGL((flash_fwd_kernel<T, HD, QT, true>), dim3((unsigned)g), dim3(64 * flash_waves(HD)), 0, s, p);
+  } else {
+    hipLaunchKernelGGL((flash_fwd_kernel<T, HD, QT, false>), dim3((unsigned)units), dim3(64 * flash_waves(HD)), 0, s,
+                       p);
+  }
   return hipGetLastError();
 }
 

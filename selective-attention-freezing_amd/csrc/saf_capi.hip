@@ -301,6 +301,9 @@ FlashPlan plan_flash(int B, int n_slots, int T, int HD, int BM, int per_cu, int 
   return fp;
 }
 
+// Workspace bytes of the live-head kernel's work queue (one word used).
+constexpr int64_t kQueueBytes = 256;
+
 int flash_qtiles_for(const saf_mixed_attn_args* a, int HD) {
   int qt = a->flash_qtiles;
   // one query tile per wave by default; two (256-query workgroups) only up
@@ -361,11 +364,19 @@ int run_flash(const saf_mixed_attn_args* a, const Plan& pl, hipStream_t s) {
   const int BM = flash_block_rows(pl.HD, qt);
   p.n_qblk = (pl.T + BM - 1) / BM;
   p.scale_log2 = a->sm_scale * kLog2e;
-  // split the causal tail when the caller's workspace holds the partials
+  // split the causal tail when the caller's workspace holds the partials;
+  // the workspace's first 256 bytes after the scan region hold the queue word
   FlashPlan fp = plan_flash(pl.B, p.n_slots, pl.T, pl.HD, BM, flash_resident(pl.HD, qt));
-  const int64_t part_off = scan_ws_bytes(pl);
-  if (fp.n_items && a->workspace != nullptr && a->workspace_bytes >= part_off + fp.part_bytes &&
-      reinterpret_cast<uintptr_t>(a->workspace) % 16 == 0) {
+  const int64_t queue_off = scan_ws_bytes(pl), part_off = queue_off + kQueueBytes;
+  const bool have_ws = a->workspace != nullptr && reinterpret_cast<uintptr_t>(a->workspace) % 16 == 0;
+  // the work queue pays off for the one-workgroup-per-CU kernel above hd 64
+  // (C3 flash 458 -> 426 us); at hd <= 64 the three resident workgroups per
+  // CU keep the CUs fed and the queue measured 4% slower
+  if (pl.HD > 64 && have_ws && a->workspace_bytes >= part_off) {
+    p.queue = reinterpret_cast<unsigned*>(reinterpret_cast<char*>(a->workspace) + queue_off);
+    p.max_grid = cu_count() * flash_resident(pl.HD, qt);
+  }
+  if (fp.n_items && have_ws && a->workspace_bytes >= part_off + fp.part_bytes) {
     char* ws = reinterpret_cast<char*>(a->workspace) + part_off;
     const int64_t nbh = (int64_t)pl.B * p.n_slots;
     p.n_items = fp.n_items;
@@ -386,6 +397,8 @@ int run_flash(const saf_mixed_attn_args* a, const Plan& pl, hipStream_t s) {
     p.k_head[i] = (int16_t)(a->kvidx ? a->kvidx[h] : slot);
     p.v_head[i] = (int16_t)(a->kvidx ? a->kvidx[h] : h);
   }
+  if (p.queue != nullptr)
+    if (int rc = launched(launch_zero_u32(p.queue, 1, s), "flash queue clear")) return rc;
   if (int rc = launched(timed([&] { return launch_flash(p, pl.dtype, pl.HD, qt, s); }, s), "flash")) return rc;
   if (fp.n_split == 0) return SAF_OK;
   CombineParams c{};
@@ -758,7 +771,7 @@ int64_t saf_mixed_attn_workspace_bytes(const saf_mixed_attn_args* args) {
     const int qt = flash_qtiles_for(args, pl.HD);
     const FlashPlan fp = plan_flash(pl.B, (int)pl.live.size(), pl.T, pl.HD, flash_block_rows(pl.HD, qt),
                                     flash_resident(pl.HD, qt));
-    part = fp.part_bytes;
+    part = kQueueBytes + fp.part_bytes;
   }
   if (!pl.dense.empty())
     part = std::max(part, plan_dense(pl.B, (int)pl.dense.size(), pl.T, pl.HD).part_bytes);

@@ -47,6 +47,10 @@ struct FlashParams {
   float* part_ml;       // [bh][part][2][BM]: running max (base 2), row sum
   int32_t items[kMaxItems];      // (qb << 8) | segment
   int16_t part_base[kMaxQblk];   // first partial slot of a split query block, -1 if not split
+  // work queue (null: one workgroup per unit): a word zeroed before the
+  // launch, from which the resident workgroups claim their next unit
+  unsigned* queue;
+  int max_grid;  // with a queue: the resident workgroups (grid = min(units, max_grid))
 };
 
 // Merge of split query blocks: out = sum_s 2^(m_s - M) O_s / sum_s 2^(m_s - M) l_s.
