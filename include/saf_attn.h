@@ -111,6 +111,21 @@ int saf_frozen_dense_pv_fwd(const saf_mixed_attn_args* args, void* stream);
 int saf_frozen_decomp_fwd(const saf_mixed_attn_args* args, void* stream);
 int saf_frozen_scan_fwd(const saf_mixed_attn_args* args, void* stream);
 
+/* Backward of saf_mixed_attn_fwd (replaces _bwd and _FusedMixedAttn.backward,
+ * kernel/fused_attn.py:593-648, with _bwd_preprocess / _bwd_dkdv / _bwd_dq
+ * :291-591).  args is the forward's argument block, with args->lse the
+ * forward's (B, H, T) base-2 LSE (required when a head is live) and a
+ * workspace of saf_mixed_attn_bwd_workspace_bytes() bytes.  Writes dq, dk
+ * (shaped like the compact q, k; only the slots of live heads) and dv (shaped
+ * like v, every head): live heads get the gradients of causal softmax
+ * attention, frozen heads only dV = P^T dO (closed-form heads through their
+ * decomposed buffers, which must be passed); patterns and decomposed buffers
+ * get no gradient.  kvidx (GQA) is refused as in the reference
+ * (qwen/kernel/fused_attn.py:605-609). */
+int saf_mixed_attn_bwd(const saf_mixed_attn_args* args, const saf_tensor_t* dout, const saf_tensor_t* dq,
+                       const saf_tensor_t* dk, const saf_tensor_t* dv, void* stream);
+int64_t saf_mixed_attn_bwd_workspace_bytes(const saf_mixed_attn_args* args);
+
 /* frozen_pv: out[b, f] = patt[fz_idx[f], :T, :T] @ v[b, f] for compact
  * frozen-head values v (B, nf, T, HD); fz_idx is a host array of nf entries. */
 int saf_frozen_pv_fwd(const saf_tensor_t* patt, const saf_tensor_t* v, const int32_t* fz_idx,

@@ -222,6 +222,54 @@ def eager_mixed_attention(q, k, v, frozen, hidx=None, pidx=None, kvidx=None,
     return out
 
 
+def eager_mixed_attention_grads(q, k, v, frozen, dout, hidx=None, pidx=None, patt=None, alpha=None,
+                                rho=None, z=None, sm_scale=None):
+    """Gradients of eager_mixed_attention with respect to q, k (compact live
+    slots) and v, for the upstream gradient dout (B, H, T, HD): the backward
+    of /root/reference/kernel/fused_attn.py:593-648 in closed form.  Live
+    heads: P = softmax(scale q k^T) (causal), dV = P^T dO,
+    dS = P (dO V^T - rowsum(dO * O)), dQ = scale dS K, dK = scale dS^T Q.
+    Frozen heads: dV = P^T dO, and no q/k gradient.  float64."""
+    q = None if q is None else _f64(q)
+    k = None if k is None else _f64(k)
+    v = _f64(v)
+    dout = _f64(dout)
+    frozen = np.asarray(frozen)
+    H = frozen.shape[0]
+    B, _, T, HD = v.shape
+    if sm_scale is None:
+        sm_scale = 1.0 / math.sqrt(HD)
+    dq = None if q is None else np.zeros_like(q)
+    dk = None if k is None else np.zeros_like(k)
+    dv = np.zeros_like(v)
+    mask = np.tril(np.ones((T, T), dtype=bool))
+    for h in range(H):
+        st = int(frozen[h])
+        if st == 0:
+            qs = h if hidx is None else int(hidx[h])
+            for b in range(B):
+                s = (q[b, qs] @ k[b, qs].T) * sm_scale
+                s = np.where(mask, s, -np.inf)
+                P = np.exp(s - s.max(-1, keepdims=True))
+                P /= P.sum(-1, keepdims=True)
+                o = P @ v[b, h]
+                dv[b, h] += P.T @ dout[b, h]
+                dP = dout[b, h] @ v[b, h].T
+                delta = (dout[b, h] * o).sum(-1, keepdims=True)
+                dS = P * (dP - delta)
+                dq[b, qs] += sm_scale * dS @ k[b, qs]
+                dk[b, qs] += sm_scale * dS.T @ q[b, qs]
+            continue
+        if st == 1:
+            row = h if pidx is None else int(pidx[h])
+            P = _f64(patt[row, :T, :T])
+        else:
+            P = decomp_pattern(np.asarray(alpha)[h:h + 1], np.asarray(rho)[h:h + 1], np.asarray(z)[h:h + 1], T)[0]
+        for b in range(B):
+            dv[b, h] += P.T @ dout[b, h]
+    return dq, dk, dv
+
+
 def frozen_pv(patt, v, fz_idx, T):
     """y[b, f] = patt[fz_idx[f], :T, :T] @ v[b, f]."""
     v = _f64(v)

@@ -763,6 +763,130 @@ int saf_add_layernorm(const saf_tensor_t* x, const saf_tensor_t* delta, const sa
   return launched(launch_add_layernorm(p, x->dtype, reinterpret_cast<hipStream_t>(stream)), "add_layernorm");
 }
 
+// ---- backward -------------------------------------------------------------
+
+static int64_t bwd_delta_bytes(const Plan& pl) {
+  return ((int64_t)pl.B * (int64_t)pl.live.size() * pl.T * 4 + 255) / 256 * 256;
+}
+
+int64_t saf_mixed_attn_bwd_workspace_bytes(const saf_mixed_attn_args* args) {
+  Plan pl;
+  if (plan_and_validate(args, kDoFlash, pl, false)) return -1;
+  return bwd_delta_bytes(pl);
+}
+
+int saf_mixed_attn_bwd(const saf_mixed_attn_args* a, const saf_tensor_t* dout, const saf_tensor_t* dq,
+                       const saf_tensor_t* dk, const saf_tensor_t* dv, void* stream) {
+  Plan pl;
+  if (int rc = plan_and_validate(a, kDoFlash | kDoDense | kDoDecomp, pl, false)) return rc;
+  if (a->kvidx != nullptr)
+    return fail(SAF_EUNSUPPORTED, "backward with kvidx (GQA) is not implemented (forward / prefill only)");
+  if (dout == nullptr || dv == nullptr) return fail(SAF_EINVAL, "dout and dv are required");
+  auto same4 = [](const saf_tensor_t& t, const saf_tensor_t& ref) {
+    for (int i = 0; i < 4; ++i)
+      if (t.size[i] != ref.size[i]) return false;
+    return t.ndim == 4 && t.dtype == ref.dtype;
+  };
+  if (!present(*dout) || !same4(*dout, a->out)) return fail(SAF_EINVAL, "dout must match out's shape and dtype");
+  if (!present(*dv) || !same4(*dv, a->v)) return fail(SAF_EINVAL, "dv must match v's shape and dtype");
+  if (int rc = check_act(*dout, "dout", 16)) return rc;
+  if (int rc = check_act(*dv, "dv", 8)) return rc;
+  // closed-form heads run as decomposed heads here: their alpha/rho/z are needed
+  std::vector<int> fz_dec = pl.decomp;
+  fz_dec.insert(fz_dec.end(), pl.scan.begin(), pl.scan.end());
+  if (!pl.scan.empty()) {
+    const saf_tensor_t* bufs[3] = {&a->alpha, &a->rho, &a->z};
+    for (int i = 0; i < 3; ++i) {
+      const saf_tensor_t& t = *bufs[i];
+      if (!present(t) || t.ndim != 2 || t.size[0] != pl.H || t.size[1] < pl.T)
+        return fail(SAF_EINVAL, "the backward of closed-form heads needs their (H, S) alpha/rho/z buffers");
+      if (t.dtype != SAF_F32 && t.dtype != SAF_BF16 && t.dtype != SAF_F16)
+        return fail(SAF_EUNSUPPORTED, "unsupported decomposed buffer dtype %s", dtype_name(t.dtype));
+    }
+  }
+  const int nf = (int)(pl.dense.size() + fz_dec.size());
+  if (pl.T == 0 || pl.B == 0) return SAF_OK;
+
+  BwdParams p{};
+  p.v = a->v.data;
+  p.out = a->out.data;
+  p.dout = dout->data;
+  p.dv = dv->data;
+  p.v_sb = a->v.stride[0]; p.v_sh = a->v.stride[1]; p.v_st = a->v.stride[2];
+  p.o_sb = a->out.stride[0]; p.o_sh = a->out.stride[1]; p.o_st = a->out.stride[2];
+  p.do_sb = dout->stride[0]; p.do_sh = dout->stride[1]; p.do_st = dout->stride[2];
+  p.dv_sb = dv->stride[0]; p.dv_sh = dv->stride[1]; p.dv_st = dv->stride[2];
+  p.B = pl.B;
+  p.T = pl.T;
+  p.scale_log2 = a->sm_scale * kLog2e;
+  p.sm_scale = a->sm_scale;
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+
+  if (!pl.live.empty()) {
+    if (dq == nullptr || dk == nullptr || !present(*dq) || !present(*dk) || !same4(*dq, a->q) || !same4(*dk, a->k))
+      return fail(SAF_EINVAL, "live heads require dq and dk shaped like q and k");
+    if (int rc = check_act(*dq, "dq", 8)) return rc;
+    if (int rc = check_act(*dk, "dk", 8)) return rc;
+    if (int rc = check_act(a->out, "out", 16)) return rc;
+    const saf_tensor_t& l = a->lse;
+    if (!present(l) || l.ndim != 3 || l.size[0] != pl.B || l.size[1] != pl.H || l.size[2] != pl.T || l.dtype != SAF_F32)
+      return fail(SAF_EINVAL, "live heads require the forward's lse, (B, H, T) float32");
+    const int64_t need = bwd_delta_bytes(pl);
+    if (a->workspace == nullptr || a->workspace_bytes < need || reinterpret_cast<uintptr_t>(a->workspace) % 16 != 0)
+      return fail(SAF_EWORKSPACE, "the backward needs a 16-byte aligned %lld-byte workspace (got %lld)",
+                  (long long)need, (long long)a->workspace_bytes);
+    p.q = a->q.data;
+    p.k = a->k.data;
+    p.dq = dq->data;
+    p.dk = dk->data;
+    p.lse = reinterpret_cast<const float*>(l.data);
+    p.delta = reinterpret_cast<float*>(a->workspace);
+    p.q_sb = a->q.stride[0]; p.q_sh = a->q.stride[1]; p.q_st = a->q.stride[2];
+    p.k_sb = a->k.stride[0]; p.k_sh = a->k.stride[1]; p.k_st = a->k.stride[2];
+    p.dq_sb = dq->stride[0]; p.dq_sh = dq->stride[1]; p.dq_st = dq->stride[2];
+    p.dk_sb = dk->stride[0]; p.dk_sh = dk->stride[1]; p.dk_st = dk->stride[2];
+    p.l_sb = l.stride[0]; p.l_sh = l.stride[1]; p.l_st = l.stride[2];
+    p.n_live = (int)pl.live.size();
+    for (int i = 0; i < p.n_live; ++i) {
+      const int h = pl.live[i];
+      p.out_head[i] = (int16_t)h;
+      p.q_head[i] = (int16_t)(a->hidx ? a->hidx[h] : h);
+    }
+    if (int rc = launched(launch_bwd_delta(p, pl.dtype, pl.HD, s), "backward delta")) return rc;
+    if (int rc = launched(launch_bwd_dq(p, pl.dtype, pl.HD, s), "backward dq")) return rc;
+    if (int rc = launched(launch_bwd_dkdv(p, pl.dtype, pl.HD, s), "backward dk/dv")) return rc;
+  }
+  if (nf > 0) {
+    p.n_frozen = nf;
+    int i = 0;
+    for (int h : pl.dense) {
+      p.f_head[i] = (int16_t)h;
+      p.pat_head[i] = (int16_t)(a->pidx ? a->pidx[h] : h);
+      p.f_kind[i++] = 1;
+    }
+    for (int h : fz_dec) {
+      p.f_head[i] = (int16_t)h;
+      p.pat_head[i] = (int16_t)h;
+      p.f_kind[i++] = 2;
+    }
+    if (!pl.dense.empty()) {
+      const saf_tensor_t& pt = a->patt;
+      p.patt = pt.data;
+      p.patt_dtype = pt.dtype;
+      p.p_sh = pt.stride[0]; p.p_si = pt.stride[1]; p.p_sj = pt.stride[2];
+    }
+    if (!fz_dec.empty()) {
+      p.alpha = a->alpha.data; p.rho = a->rho.data; p.z = a->z.data;
+      p.a_dtype = a->alpha.dtype; p.r_dtype = a->rho.dtype; p.z_dtype = a->z.dtype;
+      p.a_sh = a->alpha.stride[0]; p.a_ss = a->alpha.stride[1];
+      p.r_sh = a->rho.stride[0]; p.r_ss = a->rho.stride[1];
+      p.z_sh = a->z.stride[0]; p.z_ss = a->z.stride[1];
+    }
+    if (int rc = launched(launch_bwd_frozen_dv(p, pl.dtype, pl.HD, s), "backward frozen dv")) return rc;
+  }
+  return SAF_OK;
+}
+
 int64_t saf_mixed_attn_workspace_bytes(const saf_mixed_attn_args* args) {
   Plan pl;
   if (plan_and_validate(args, kDoFlash | kDoScan, pl, false)) return -1;

@@ -169,6 +169,57 @@ hipError_t launch_zero_u32(uint32_t* ptr, int64_t n, hipStream_t s);
 hipError_t launch_rope(const RopeParams& p, int dtype, hipStream_t s);
 hipError_t launch_add_layernorm(const AddLnParams& p, int dtype, hipStream_t s);
 
+// Backward of the mixed-head operator (gradients of out = attention(q, k, v)
+// with respect to q, k, v; patterns and decomposed buffers are constants).
+// Live slots index the compact q/k (q_head) and the natural head (out_head);
+// frozen slots list the dense / decomposed heads.
+struct BwdParams {
+  const void* q;
+  const void* k;
+  const void* v;
+  const void* out;
+  const void* dout;
+  void* dq;
+  void* dk;
+  void* dv;
+  const float* lse;  // (B, H, T) base-2 log-sum-exp of the forward
+  float* delta;      // (B, n_live, T) workspace: rowsum(out * dout) per live row
+  int64_t q_sb, q_sh, q_st;
+  int64_t k_sb, k_sh, k_st;
+  int64_t v_sb, v_sh, v_st;
+  int64_t o_sb, o_sh, o_st;
+  int64_t do_sb, do_sh, do_st;
+  int64_t dq_sb, dq_sh, dq_st;
+  int64_t dk_sb, dk_sh, dk_st;
+  int64_t dv_sb, dv_sh, dv_st;
+  int64_t l_sb, l_sh, l_st;
+  int B, T, n_live, n_frozen;
+  float scale_log2;  // sm_scale * log2(e)
+  float sm_scale;
+  int16_t out_head[kMaxHeads];   // live slot -> natural head
+  int16_t q_head[kMaxHeads];     // live slot -> compact q/k slot
+  // frozen slots
+  int16_t f_head[kMaxHeads];     // frozen slot -> natural head
+  int16_t pat_head[kMaxHeads];   // dense: pattern row; decomposed: buffer row
+  int8_t f_kind[kMaxHeads];      // 1 dense, 2 decomposed
+  const void* patt;
+  int patt_dtype, patt_vec;
+  int64_t p_sh, p_si, p_sj, patt_elems;
+  const void* alpha;
+  const void* rho;
+  const void* z;
+  int a_dtype, r_dtype, z_dtype;
+  int64_t a_sh, a_ss, r_sh, r_ss, z_sh, z_ss;
+};
+static_assert(sizeof(BwdParams) <= 4096, "BwdParams must fit the kernel argument segment");
+
+// Backward: delta = rowsum(out * dout) of the live rows; dQ; dK and dV of the
+// live heads; dV of the frozen heads.
+hipError_t launch_bwd_delta(const BwdParams& p, int dtype, int hd, hipStream_t s);
+hipError_t launch_bwd_dq(const BwdParams& p, int dtype, int hd, hipStream_t s);
+hipError_t launch_bwd_dkdv(const BwdParams& p, int dtype, int hd, hipStream_t s);
+hipError_t launch_bwd_frozen_dv(const BwdParams& p, int dtype, int hd, hipStream_t s);
+
 // Queries per frozen-head workgroup (4 waves) for a query-tile count.
 inline int block_rows(int qt) { return 4 * 32 * qt; }
 

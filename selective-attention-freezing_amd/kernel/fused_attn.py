@@ -226,19 +226,22 @@ def set_kernel_timer(timer):
 
 
 class _MixedAttnFn(torch.autograd.Function):
-    """Forward-only autograd node: prefill runs under inference_mode; the
-    backward kernels (dQ/dK/dV with exactly-zero frozen Q/K grads) are not
-    part of this library yet."""
+    """Autograd node of fused_mixed_attn (kernel/fused_attn.py:621-647 of the
+    reference): the forward runs the HIP forward and keeps what the backward
+    needs (out, the base-2 LSE of the live heads, the routing tables and the
+    fixed pattern buffers); the backward runs saf_mixed_attn_bwd.  Frozen
+    heads have no q/k slot, so they get no Q/K gradient; patterns and the
+    decomposed buffers are constants (no gradient, ever)."""
 
     @staticmethod
-    def forward(ctx, q, k, v, run):
+    def forward(ctx, q, k, v, run, bwd):
+        ctx.bwd = bwd
         return run()
 
     @staticmethod
     def backward(ctx, dout):
-        raise NotImplementedError(
-            "fused_mixed_attn backward is not implemented in the MI355X build "
-            "(forward / prefill only)")
+        dq, dk, dv = ctx.bwd(dout)
+        return dq, dk, dv, None, None
 
 
 def fused_mixed_attn(q, k, v, patt, frozen, hidx=None, pidx=None,
@@ -291,6 +294,11 @@ def fused_mixed_attn(q, k, v, patt, frozen, hidx=None, pidx=None,
 
     B, HV, T, HD = v.shape
     n_live = int((frozen_h == 0).sum())
+    needs_grad = torch.is_grad_enabled() and any(
+        t is not None and t.requires_grad for t in (q, k, v))
+    if needs_grad and n_live and lse is None:
+        # the backward recomputes P from the forward's base-2 LSE
+        lse = torch.empty((B, H, T), device=v.device, dtype=torch.float32)
     q_d = k_d = None
     if n_live:
         q_d = _aligned_view(q, 16)
@@ -316,6 +324,8 @@ def fused_mixed_attn(q, k, v, patt, frozen, hidx=None, pidx=None,
 
     need_dec = alpha is not None and bool(
         ((frozen_h == 2) & ((ck == 0) if ck is not None else True)).any())
+    # the backward runs closed-form heads through their decomposed buffers
+    need_dec = need_dec or (needs_grad and alpha is not None and bool((frozen_h == 2).any()))
 
     args = _ext.SafMixedAttnArgs()
     args.q = _ext.tensor_desc(q_d)
@@ -389,9 +399,40 @@ def fused_mixed_attn(q, k, v, patt, frozen, hidx=None, pidx=None,
             _ext.check(L.saf_mixed_attn_fwd(args, cur.cuda_stream))
         return out
 
-    if torch.is_grad_enabled() and any(
-            t is not None and t.requires_grad for t in (q, k, v)):
-        return _MixedAttnFn.apply(q, k, v, run)
+    # every tensor the argument block points to stays alive until the backward
+    held = (q_d, k_d, v_d, out, lse, patt, alpha if need_dec else None,
+            rho if need_dec else None, z if need_dec else None)
+
+    def bwd(dout):
+        """dq, dk (compact, contiguous; zero for slots no live head uses) and
+        dv (contiguous) through saf_mixed_attn_bwd."""
+        if kvidx is not None:
+            raise NotImplementedError(
+                "fused_mixed_attn backward with kvidx (GQA) is not implemented "
+                "(as in qwen/kernel/fused_attn.py:605-609 of the reference)")
+        if bool((frozen_h == 2).any()) and alpha is None:
+            raise ValueError("the backward of decomposed heads needs alpha/rho/z")
+        do = dout.contiguous()
+        dq = torch.zeros(q_d.shape, device=v.device, dtype=v.dtype) if n_live else None
+        dk = torch.zeros(k_d.shape, device=v.device, dtype=v.dtype) if n_live else None
+        dv = torch.empty(v_d.shape, device=v.device, dtype=v.dtype)
+        bws = int(L.saf_mixed_attn_bwd_workspace_bytes(args))
+        if bws < 0:
+            bws = 0
+        bw = torch.empty(max(bws, 1), dtype=torch.uint8, device=v.device)
+        bargs = _ext.SafMixedAttnArgs.from_buffer_copy(args)
+        bargs.workspace = bw.data_ptr()
+        bargs.workspace_bytes = bws
+        cur = torch.cuda.current_stream(v.device)
+        _ext.check(L.saf_mixed_attn_bwd(bargs, _ext.tensor_desc(do), _ext.tensor_desc(dq),
+                                        _ext.tensor_desc(dk), _ext.tensor_desc(dv), cur.cuda_stream))
+        _ = (keep, held)  # the host tables and tensors the argument block points to
+        gq = dq.to(q.dtype) if dq is not None and q is not None else None
+        gk = dk.to(k.dtype) if dk is not None and k is not None else None
+        return gq, gk, dv
+
+    if needs_grad:
+        return _MixedAttnFn.apply(q, k, v, run, bwd)
     return run()
 
 

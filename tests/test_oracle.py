@@ -238,3 +238,41 @@ def test_planted_oracle_mistake_is_caught():
     v = _rand((T, 3), 26)
     assert not np.allclose(wrong @ v, orc.mean_apply(v))
     assert np.allclose(orc.mean_pattern(T) @ v, orc.mean_apply(v))
+
+
+def test_backward_oracle_matches_finite_differences():
+    """eager_mixed_attention_grads (the closed-form backward of live, dense and
+    decomposed heads) equals central differences of the pinned forward
+    eager_mixed_attention on a tiny case."""
+    rng = np.random.default_rng(3)
+    B, H, T, HD = 1, 4, 6, 4
+    frozen = np.array([0, 1, 2, 0], dtype=np.int32)
+    hidx = np.array([1, 0, 0, 0], dtype=np.int32)   # live heads 0 -> slot 1, 3 -> slot 0
+    q = rng.normal(size=(B, 2, T, HD))
+    k = rng.normal(size=(B, 2, T, HD))
+    v = rng.normal(size=(B, H, T, HD))
+    p = np.tril(rng.random((H, T, T)))
+    patt = p / p.sum(-1, keepdims=True)
+    alpha = rng.normal(size=(H, T)) * 0.5
+    rho = rng.normal(size=(H, T)) * 0.5
+    z = orc.decomposed_logz(alpha, rho)
+    do = rng.normal(size=(B, H, T, HD))
+    kw = dict(patt=patt, alpha=alpha, rho=rho, z=z, sm_scale=0.7)
+
+    def loss(qq, kk, vv):
+        return float((orc.eager_mixed_attention(qq, kk, vv, frozen, hidx, **kw) * do).sum())
+
+    dq, dk, dv = orc.eager_mixed_attention_grads(q, k, v, frozen, do, hidx, **kw)
+    eps = 1e-6
+    for which, (x, g) in enumerate(((q, dq), (k, dk), (v, dv))):
+        num = np.zeros_like(x)
+        for idx in np.ndindex(x.shape):
+            xp, xm = x.copy(), x.copy()
+            xp[idx] += eps
+            xm[idx] -= eps
+            a = [q, k, v]
+            a[which] = xp
+            fp = loss(*a)
+            a[which] = xm
+            num[idx] = (fp - loss(*a)) / (2 * eps)
+        assert np.abs(num - g).max() < 1e-6, f"gradient {which}"
