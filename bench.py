@@ -542,6 +542,79 @@ def run_c3(args):
     print(json.dumps(line), flush=True)
 
 
+def run_bwd(args):
+    """Backward of the isolated op at the C1 shape (B=8, H=12, T=4096, hd 64,
+    bf16; heads randperm(12)[:3] frozen to exponential decays, installed as
+    decomposed buffers): one step = forward + backward of sum(out * w) with
+    respect to q, k, v (saf_mixed_attn_bwd: delta, dQ, dK/dV of the live
+    heads, dV of the frozen heads).  Reports the backward alone, with the live
+    heads' work counted in the FlashAttention convention (2.5x the forward's
+    4 hd T(T+1)/2 flops per (batch, live head))."""
+    import torch
+    import kernel
+
+    B, H, hd = args.batch or 8, 12, 64
+    T = args.seq_len or 4096
+    g = torch.Generator().manual_seed(1337)
+    fz = sorted(torch.randperm(H, generator=g)[:3].tolist())
+    rates = [0.001 + 0.099 * float(x) for x in torch.rand(3, generator=g)]
+    live = [h for h in range(H) if h not in fz]
+    q = torch.randn(B, len(live), T, hd, generator=g).bfloat16().cuda().requires_grad_(True)
+    k = torch.randn(B, len(live), T, hd, generator=g).bfloat16().cuda().requires_grad_(True)
+    v = torch.randn(B, H, T, hd, generator=g).bfloat16().cuda().requires_grad_(True)
+    hidx = torch.zeros(H, dtype=torch.int32)
+    for slot, h in enumerate(live):
+        hidx[h] = slot
+    d = torch.arange(T, dtype=torch.float32)
+    alpha = torch.zeros(H, T)
+    rho = torch.zeros(H, T)
+    for f, c in zip(fz, rates):
+        rho[f] = -c * d
+    alpha, rho = alpha.cuda(), rho.cuda()
+    z = kernel.decomposed_logz(alpha, rho)
+    cf = kernel.classify_closed_form(alpha, rho, z)
+    frozen = torch.zeros(H, dtype=torch.int32)
+    frozen[fz] = 2
+    frozen, hidx = frozen.cuda(), hidx.cuda()
+    w = torch.randn(B, H, T, hd, generator=g).bfloat16().cuda()
+
+    def fwd():
+        return kernel.fused_mixed_attn(q, k, v, None, frozen, hidx, alpha=alpha, rho=rho, z=z, closed_form=cf,
+                                       validate=False)
+
+    for _ in range(args.warmup):
+        fwd().backward(w)
+    torch.cuda.synchronize()
+    e = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True),
+          torch.cuda.Event(enable_timing=True)) for _ in range(args.steps)]
+    for e0, e1, e2 in e:
+        q.grad = k.grad = v.grad = None
+        e0.record()
+        y = fwd()
+        e1.record()
+        y.backward(w)
+        e2.record()
+    torch.cuda.synchronize()
+    fwd_ms = statistics.median(a.elapsed_time(b) for a, b, _ in e)
+    bwd_ms = statistics.median(b.elapsed_time(c) for _, b, c in e)
+    flops_bwd = 2.5 * len(live) * B * 4 * hd * T * (T + 1) / 2
+    tfs = flops_bwd / (bwd_ms / 1000.0) / 1e12
+    line = {
+        "metric": "backward of the mixed-head op (live-head FLOP/s, FlashAttention convention)",
+        "value": round(tfs, 2), "unit": "TFLOP/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(fwd_ms + bwd_ms, 3), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "bf16", "data": "synthetic (N(0,1) q/k/v seed 1337)",
+        "config": {"workload": f"C1 op backward: B={B}, H={H}, T={T}, hd={hd}, 3 decay heads (decomposed in the "
+                               f"backward, closed-form scan in the forward), {len(live)} live",
+                   "fwd_ms": round(fwd_ms, 4), "bwd_ms": round(bwd_ms, 4)},
+        "roofline": {"bound": "mfma", "achieved": round(tfs, 2), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
+                     "frac": round(tfs / PEAK_BF16_TFLOPS, 4), "traffic": None,
+                     "kernel": "bwd_dq_kernel + bwd_dkdv_kernel + bwd_frozen_dv_kernel (whole backward)"},
+        "cpu_baseline": None,
+    }
+    print(json.dumps(line), flush=True)
+
+
 def run_scan(args):
     """Frozen-only sizing run of the closed-form scan (the HBM-bound frozen-head
     kernel): every head of B=8, H=12, T=16384, hd=64 bf16 frozen to a seeded
@@ -600,7 +673,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=10)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--workload", choices=["c1", "c2", "c3", "c4", "scan"], default="c2",
+    ap.add_argument("--workload", choices=["c1", "c2", "c3", "c4", "scan", "bwd"], default="c2",
                     help="c1: the isolated op (decay heads as scan / rebuild / dense); "
                          "c2: 124M nanoGPT SAF-25%% at 16K (the headline); c3: 1B-class with dense "
                          "frozen patterns; c4: Qwen-style GQA; "
@@ -638,6 +711,9 @@ def main():
         return
     if args.workload == "scan":
         run_scan(args)
+        return
+    if args.workload == "bwd":
+        run_bwd(args)
         return
     if args.workload == "c3":
         run_c3(args)

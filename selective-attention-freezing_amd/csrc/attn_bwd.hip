@@ -312,6 +312,9 @@ template <typename T, int HD, int KIND>
 __global__ __launch_bounds__(256) void bwd_frozen_dv_kernel(const BwdParams p) {
   constexpr int BN = kBwdWaves * 32, NDT = HD / 32, VB = VRow<HD>::BYTES;
   __shared__ __align__(16) char o0[VB], o1[VB];
+  // decomposed heads: z_q log2 e of the block's 64 queries and rho_d log2 e
+  // for every distance d = q - key the block meets (64 + 128 - 1 values)
+  __shared__ float zs[64], rs[64 + BN];
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int n = lane & 31, g = lane >> 5;
@@ -339,7 +342,22 @@ __global__ __launch_bounds__(256) void bwd_frozen_dv_kernel(const BwdParams p) {
   if (ib0 < nqb) oo.load(dobase, p.do_st, 64 * ib0, T_len, o0, wave);
   for (int i = ib0; i < nqb; ++i) {
     const char* ot = ((i - ib0) & 1) ? o1 : o0;
-    __syncthreads();  // this block's dO tile is in LDS
+    const int dmin = 64 * i - kb * BN - (BN - 1);  // smallest q - key of the block
+    if (KIND == 2) {
+      // (the previous block's readers passed the barrier at its end)
+      if (tid < 64) {
+        const int qq = 64 * i + tid;
+        zs[tid] = qq < T_len ? load_as_f32(p.z, (int64_t)ph * p.z_sh + (int64_t)qq * p.z_ss, p.z_dtype) * kLog2e
+                             : 0.f;
+      }
+      if (tid < 64 + BN - 1) {
+        const int dd = dmin + tid;
+        rs[tid] = (dd >= 0 && dd < T_len)
+                      ? load_as_f32(p.rho, (int64_t)ph * p.r_sh + (int64_t)dd * p.r_ss, p.r_dtype) * kLog2e
+                      : 0.f;
+      }
+    }
+    __syncthreads();  // this block's dO tile (and z / rho window) is in LDS
     if (i + 1 < nqb) oo.load(dobase, p.do_st, 64 * (i + 1), T_len, ((i - ib0) & 1) ? o0 : o1, wave);
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks) {
@@ -355,9 +373,7 @@ __global__ __launch_bounds__(256) void bwd_frozen_dv_kernel(const BwdParams p) {
           if (KIND == 1) {
             v = load_as_f32(p.patt, (int64_t)ph * p.p_sh + (int64_t)qq * p.p_si + (int64_t)kk * p.p_sj, p.patt_dtype);
           } else {
-            const float rh = load_as_f32(p.rho, (int64_t)ph * p.r_sh + (int64_t)(qq - kk) * p.r_ss, p.r_dtype);
-            const float zz = load_as_f32(p.z, (int64_t)ph * p.z_sh + (int64_t)qq * p.z_ss, p.z_dtype);
-            v = fast_exp2(alpha_k + (rh - zz) * kLog2e);
+            v = fast_exp2(alpha_k + rs[qq - kk - dmin] - zs[qq - 64 * i]);
           }
         }
         e8[e] = v;
