@@ -37,6 +37,9 @@ for _p in (PKG, REPO):
 
 METRIC = "prefill tokens/sec (1 GPU) + % bf16 MFMA / HBM roofline, 124M SAF-25 @16K ctx"
 PEAK_BF16_TFLOPS = 2500.0      # MI355X dense bf16 MFMA
+# v_exp_f32 issue ceiling: 256 CUs x 4 SIMDs x 64 lanes per 4-cycle
+# transcendental issue x 2.4 GHz
+EXP_ISSUE_PEAK = 256 * 4 * 64 / 4 * 2.4e9
 PEAK_HBM_GBS = 8000.0          # MI355X HBM3E
 
 
@@ -668,16 +671,80 @@ def run_scan(args):
     print(json.dumps(line), flush=True)
 
 
+def run_logz(args):
+    """Freeze-time precompute: row normalisers z = logsumexp_{j<=i}(alpha_j +
+    rho_{i-j}) of a C2 layer's decomposed buffers (H = 12, S = 16384, fp32),
+    one step = one kernel.decomposed_logz call (saf_decomposed_logz).  Beside
+    it, the reference's row-chunked torch definition on the same GPU and the
+    float64 oracle on the host cores (H = 1, S = 4096 sample)."""
+    import torch
+    import kernel
+    from kernel.fused_attn import decomp_logits
+
+    H = 12
+    S = args.seq_len or 16384
+    g = torch.Generator().manual_seed(1337)
+    alpha = (torch.randn(H, S, generator=g) * 0.5).cuda()
+    rho = (-torch.rand(H, S, generator=g) * 0.01 * torch.arange(S)).cuda()
+    step = lambda: kernel.decomposed_logz(alpha, rho)
+    step_ms, wall, _ = timed_steps(step, args.steps, args.warmup, False)
+    total_ms = sum(step_ms)
+    logits = H * S * (S + 1) // 2
+    rate = logits * args.steps / (total_ms / 1000.0)
+
+    def torch_chunked():  # kernel/fused_attn.py:101-116 on device tensors
+        chunk = max(1, (1 << 27) // (H * S))
+        z = torch.empty_like(alpha)
+        for r0 in range(0, S, chunk):
+            r1 = min(r0 + chunk, S)
+            z[:, r0:r1] = decomp_logits(alpha, rho, rows=(r0, r1)).logsumexp(-1)
+        return z
+
+    ref = torch_chunked()
+    err = float((step() - ref).abs().max())
+    t_ms, _, _ = timed_steps(torch_chunked, 2, 0, False)
+    torch_ms = sum(t_ms) / len(t_ms)
+    cpu = None
+    if not args.no_cpu_baseline:
+        from oracle import saf_oracle as orc
+        Sc = min(S, 4096)
+        a64 = alpha[:1, :Sc].double().cpu().numpy()
+        r64 = rho[:1, :Sc].double().cpu().numpy()
+        t0 = time.perf_counter()
+        orc.decomposed_logz(a64, r64)
+        dt = time.perf_counter() - t0
+        cpu = {"value": round(Sc * (Sc + 1) / 2 / dt / 1e9, 4), "unit": "G logits/s", "cores": 1, "kind": "port",
+               "sample": f"oracle decomposed_logz (numpy float64), H=1, S={Sc}, {dt:.2f} s"}
+    peak = EXP_ISSUE_PEAK
+    line = {
+        "metric": "decomposed-pattern row normalisers (freeze-time precompute, 1 GPU), G logits/s",
+        "value": round(rate / 1e9, 1), "unit": "G logits/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(total_ms / args.steps, 4),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f32",
+        "data": "synthetic (alpha ~ N(0, 0.25), rho_d = -U(0, 0.01) d, seed 1337)",
+        "config": {"workload": f"decomposed_logz of one C2 layer: H={H}, S={S} fp32, {logits} logits per step"},
+        "roofline": {"bound": "exp", "achieved": round(rate / 1e9, 1), "peak": round(peak / 1e9, 1),
+                     "unit": "G exp/s", "frac": round(rate / peak, 4), "traffic": None,
+                     "kernel": "decomp_logz_kernel", "avg_launch_ms": round(total_ms / args.steps, 4)},
+        "torch_chunked_gpu_ms": round(torch_ms, 3),
+        "speedup_vs_torch_chunked": round(torch_ms / (total_ms / args.steps), 1),
+        "max_abs_diff_vs_torch_chunked": err,
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=10)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--workload", choices=["c1", "c2", "c3", "c4", "scan", "bwd"], default="c2",
+    ap.add_argument("--workload", choices=["c1", "c2", "c3", "c4", "scan", "bwd", "logz"], default="c2",
                     help="c1: the isolated op (decay heads as scan / rebuild / dense); "
                          "c2: 124M nanoGPT SAF-25%% at 16K (the headline); c3: 1B-class with dense "
                          "frozen patterns; c4: Qwen-style GQA; "
-                         "scan: frozen-only sizing run of the closed-form scan (HBM roofline)")
+                         "scan: frozen-only sizing run of the closed-form scan (HBM roofline); "
+                         "bwd: the C1 op forward + backward; logz: freeze-time row normalisers")
     ap.add_argument("--seq-len", type=int, default=None)
     ap.add_argument("--batch", type=int, default=None, help="c4 only (default 4)")
     ap.add_argument("--layers", type=int, default=None)
@@ -714,6 +781,9 @@ def main():
         return
     if args.workload == "bwd":
         run_bwd(args)
+        return
+    if args.workload == "logz":
+        run_logz(args)
         return
     if args.workload == "c3":
         run_c3(args)

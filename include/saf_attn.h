@@ -160,6 +160,15 @@ int saf_qk_rmsnorm_rope_inplace(const saf_tensor_t* q, const saf_tensor_t* k, co
 int saf_add_layernorm(const saf_tensor_t* x, const saf_tensor_t* delta, const saf_tensor_t* weight,
                       const saf_tensor_t* bias, float eps, const saf_tensor_t* out, void* stream);
 
+/* Row normalisers of decomposed patterns: z[h, i] = logsumexp over j <= i of
+ * alpha[h, j] + rho[h, i - j], for (H, S) fp32 alpha, rho and z with unit
+ * column stride (any row stride).  Rows whose logits are all -inf get -inf.
+ * One pass, no workspace.  Replaces decomposed_logz
+ * (kernel/fused_attn.py:101-116), which the reference computes in row chunks
+ * of materialised (H, rows, S) logits at freeze time (nanogpt/model.py) and
+ * per call when alpha comes without z (kernel/fused_attn.py:690-694). */
+int saf_decomposed_logz(const saf_tensor_t* alpha, const saf_tensor_t* rho, const saf_tensor_t* z, void* stream);
+
 /* Workspace needed by saf_frozen_scan_fwd for n_scan_heads closed-form heads
  * (0 bytes when there are none). */
 int64_t saf_workspace_bytes(int32_t B, int32_t T, int32_t head_dim, int32_t n_scan_heads);

@@ -763,6 +763,34 @@ int saf_add_layernorm(const saf_tensor_t* x, const saf_tensor_t* delta, const sa
   return launched(launch_add_layernorm(p, x->dtype, reinterpret_cast<hipStream_t>(stream)), "add_layernorm");
 }
 
+int saf_decomposed_logz(const saf_tensor_t* alpha, const saf_tensor_t* rho, const saf_tensor_t* z, void* stream) {
+  if (alpha == nullptr || rho == nullptr || z == nullptr || !present(*alpha) || !present(*rho) || !present(*z))
+    return fail(SAF_EINVAL, "alpha, rho and z are required");
+  const saf_tensor_t* ts[3] = {alpha, rho, z};
+  const char* names[3] = {"alpha", "rho", "z"};
+  for (int i = 0; i < 3; ++i) {
+    const saf_tensor_t& t = *ts[i];
+    if (t.ndim != 2 || t.size[0] != alpha->size[0] || t.size[1] != alpha->size[1])
+      return fail(SAF_EINVAL, "%s must be 2-D (H, S) like alpha", names[i]);
+    if (t.dtype != SAF_F32) return fail(SAF_EUNSUPPORTED, "%s must be fp32 (got %s)", names[i], dtype_name(t.dtype));
+    if (t.size[1] > 1 && t.stride[1] != 1) return fail(SAF_EALIGN, "%s needs a unit column stride", names[i]);
+  }
+  const int64_t H = alpha->size[0], S = alpha->size[1];
+  if (H > 65535 || S > (int64_t(1) << 30))
+    return fail(SAF_EUNSUPPORTED, "decomposed_logz: H = %lld, S = %lld out of range", (long long)H, (long long)S);
+  if (H == 0 || S == 0) return SAF_OK;
+  LogzParams p{};
+  p.alpha = static_cast<const float*>(alpha->data);
+  p.rho = static_cast<const float*>(rho->data);
+  p.z = static_cast<float*>(z->data);
+  p.a_hs = alpha->stride[0];
+  p.r_hs = rho->stride[0];
+  p.z_hs = z->stride[0];
+  p.H = (int)H;
+  p.S = (int)S;
+  return launched(launch_decomp_logz(p, reinterpret_cast<hipStream_t>(stream)), "decomposed_logz");
+}
+
 // ---- backward -------------------------------------------------------------
 
 static int64_t bwd_delta_bytes(const Plan& pl) {

@@ -169,6 +169,18 @@ hipError_t launch_zero_u32(uint32_t* ptr, int64_t n, hipStream_t s);
 hipError_t launch_rope(const RopeParams& p, int dtype, hipStream_t s);
 hipError_t launch_add_layernorm(const AddLnParams& p, int dtype, hipStream_t s);
 
+// Row normalisers of decomposed patterns, z[h, i] = logsumexp_{j<=i}(alpha[h, j]
+// + rho[h, i - j]) for i < S; (H, S) fp32 rows with unit column stride.
+struct LogzParams {
+  const float* alpha;
+  const float* rho;
+  float* z;
+  int64_t a_hs, r_hs, z_hs;  // head (row) strides, elements
+  int H, S;
+};
+
+hipError_t launch_decomp_logz(const LogzParams& p, hipStream_t s);
+
 // Backward of the mixed-head operator (gradients of out = attention(q, k, v)
 // with respect to q, k, v; patterns and decomposed buffers are constants).
 // Live slots index the compact q/k (q_head) and the natural head (out_head);

@@ -24,7 +24,7 @@ EXPORTS = ("saf_mixed_attn_fwd", "saf_flash_fwd", "saf_frozen_dense_pv_fwd",
            "saf_frozen_decomp_fwd", "saf_frozen_scan_fwd", "saf_mixed_attn_bwd",
            "saf_mixed_attn_bwd_workspace_bytes", "saf_frozen_pv_fwd",
            "saf_rope_qk_inplace", "saf_qk_rmsnorm_rope_inplace", "saf_add_layernorm",
-           "saf_workspace_bytes", "saf_mixed_attn_workspace_bytes",
+           "saf_decomposed_logz", "saf_workspace_bytes", "saf_mixed_attn_workspace_bytes",
            "saf_workspace_error", "saf_time_next_kernel", "saf_last_error", "saf_version")
 
 
@@ -91,6 +91,8 @@ def lib():
         L.saf_qk_rmsnorm_rope_inplace.restype = ctypes.c_int
         L.saf_add_layernorm.argtypes = [P(SafTensor)] * 4 + [ctypes.c_float, P(SafTensor), ctypes.c_void_p]
         L.saf_add_layernorm.restype = ctypes.c_int
+        L.saf_decomposed_logz.argtypes = [P(SafTensor)] * 3 + [ctypes.c_void_p]
+        L.saf_decomposed_logz.restype = ctypes.c_int
         L.saf_workspace_bytes.argtypes = [ctypes.c_int32] * 4
         L.saf_workspace_bytes.restype = ctypes.c_int64
         L.saf_mixed_attn_workspace_bytes.argtypes = [P(SafMixedAttnArgs)]

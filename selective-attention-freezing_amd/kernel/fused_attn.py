@@ -15,8 +15,9 @@ exponential decay or a sliding window (``closed_form=``), a single-pass scan
 that reads V once.  Output is in natural head order.
 
 Pattern helpers (``make_rho_band``, ``decomp_logits``, ``decomposed_logz``)
-follow the reference's definitions (/root/reference/kernel/fused_attn.py:50-116)
-and run as ordinary torch ops at freeze time.
+follow the reference's definitions (/root/reference/kernel/fused_attn.py:50-116).
+``decomposed_logz`` of device tensors runs one HIP kernel
+(``saf_decomposed_logz``); the other two are single torch ops.
 """
 import math
 
@@ -73,10 +74,28 @@ def decomp_logits(alpha, rho, rows=None):
 
 @torch.no_grad()
 def decomposed_logz(alpha, rho, chunk=None):
-    """z[h, i] = logsumexp_{j <= i}(alpha[h, j] + rho[h, i - j]), row-chunked so
-    the (H, chunk, S) workspace stays near 2^27 elements
-    (/root/reference/kernel/fused_attn.py:101-116)."""
+    """z[h, i] = logsumexp_{j <= i}(alpha[h, j] + rho[h, i - j])
+    (/root/reference/kernel/fused_attn.py:101-116).
+
+    Device tensors: one pass of libsafattn.so ``saf_decomposed_logz`` on the
+    current stream (fp32 arithmetic, no (H, rows, S) logits materialised;
+    ``chunk`` is ignored).  Host tensors (freeze-time set-up on the CPU, as
+    the reference's helper allows): the reference's row-chunked definition,
+    the (H, chunk, S) workspace near 2^27 elements.  Returns alpha's dtype."""
     H, S = alpha.shape
+    if alpha.is_cuda:
+        z = torch.empty(H, S, device=alpha.device, dtype=torch.float32)
+        if H * S == 0:
+            return z.to(alpha.dtype)
+        a32 = alpha.float()
+        r32 = rho.to(device=alpha.device, dtype=torch.float32)
+        if S > 1:
+            a32 = a32 if a32.stride(1) == 1 else a32.contiguous()
+            r32 = r32 if r32.stride(1) == 1 else r32.contiguous()
+        rc = _ext.lib().saf_decomposed_logz(_ext.tensor_desc(a32), _ext.tensor_desc(r32), _ext.tensor_desc(z),
+                                            _ext.current_stream_ptr(alpha.device))
+        _ext.check(rc)
+        return z if alpha.dtype == torch.float32 else z.to(alpha.dtype)
     if chunk is None:
         chunk = max(1, (1 << 27) // max(H * S, 1))
     z = torch.empty_like(alpha)
