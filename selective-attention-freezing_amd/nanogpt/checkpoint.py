@@ -1,0 +1,156 @@
+"""Load the reference's nanoGPT checkpoints (the released SAF exports) into
+this build's GPT.
+
+Follows /root/reference/nanogpt/eval_nanogpt_logprobs.py:51-104
+(``build_config_from_ckpt``, ``load_model``) and the lazy-buffer handling of
+/root/reference/nanogpt/model.py:900-911, with three differences that follow
+from this build:
+
+* the file is read with ``torch.load(weights_only=True)``: tensors, dicts,
+  lists, strings and numbers load; a checkpoint that pickles other objects
+  is refused by torch with an error rather than executed;
+* dense frozen patterns are stored compactly here: the reference's
+  ``dyn_pattern`` is (n_head, S, S) with zero rows for live heads (or absent
+  in decomposed mode until a dense freeze); this build keeps one (S, S) slot
+  per dense-frozen head (``dyn_pattern`` (n_slots, S, S) + ``dyn_pattern_slot``),
+  so the loader moves each dense-frozen head's matrix, bit for bit, into its
+  slot, in head order;
+* ``dyn_rho_band`` (the reference's (n_head, 64, S) derived band) is dropped:
+  the HIP kernels read rho directly.
+
+Only the architecture this build implements loads: standard softmax heads
+with dynamic per-head freezing (any fraction frozen, dense or decomposed
+priors).  Checkpoints of the reference's randomisation ablations (random
+heads or layers, projection masks, attention masks, packed prune / uniform
+layouts, state blocks) raise NotImplementedError naming the field.
+"""
+from __future__ import annotations
+
+import dataclasses
+
+import torch
+
+from .model import GPT, GPTConfig
+
+# GPTConfig defaults of the reference (/root/reference/nanogpt/model.py:1248-1285)
+# for the fields this build reads; a checkpoint's model_args override them.
+REFERENCE_DEFAULTS = {
+    "block_size": 1024, "vocab_size": 50304, "n_layer": 12, "n_head": 12, "n_embd": 768,
+    "dropout": 0.0, "bias": True, "position_encoding": "learned_absolute", "rope_base": 10000.0,
+    "rand_attn_dynamic": False, "rand_attn_prior_repr": "dense", "freeze_pattern_dtype": "float32",
+    "rand_seed": 42,
+}
+
+# Reference fields whose non-default values select architectures outside the
+# prefill hot path (randomisation ablations A-G, state blocks); the value
+# listed is the one this build implements.
+_REQUIRED = {
+    "state_size": 0, "shared_weights": False, "rand_head_rate": 0.0, "rand_layer_rate": 0.0,
+    "rand_components": "none", "rand_attn_mask_rate": 0.0, "rand_attn_head_rate": 0.0,
+    "rand_attn_pattern": "none", "random_proj": False, "block_type": "selfattention",
+}
+
+_PREFIX = "_orig_mod."
+
+
+def build_config_from_ckpt(ckpt) -> GPTConfig:
+    """GPTConfig from a checkpoint's ``model_args`` (or ``model_config``),
+    tolerant of the reference's renamed fields, with the reference's defaults
+    for absent ones (eval_nanogpt_logprobs.py:51-74)."""
+    ma = dict(ckpt.get("model_args", ckpt.get("model_config", {})) or {})
+    if not ma:
+        raise ValueError("Checkpoint has neither model_args nor model_config")
+    if "rand_mask_rate" in ma:  # renamed field of older exports
+        ma["rand_proj_mask_rate"] = ma.pop("rand_mask_rate")
+    cfg_dict = ckpt.get("config", {}) or {}
+    for k in ("rand_attn_pattern", "rand_attn_head_rate"):
+        if k not in ma and cfg_dict.get(k) is not None:
+            ma[k] = cfg_dict[k]
+    for k, want in _REQUIRED.items():
+        if k in ma and ma[k] is not None and ma[k] != want:
+            raise NotImplementedError(f"checkpoint field {k}={ma[k]!r} selects an architecture this build "
+                                      f"does not implement (needs {want!r})")
+    if ma.get("rand_components", "none") != "none" and ma.get("rand_proj_mask_rate", 1.0) != 0.0:
+        raise NotImplementedError("checkpoints with randomised projections are not supported")
+    fields = {f.name for f in dataclasses.fields(GPTConfig)}
+    args = dict(REFERENCE_DEFAULTS)
+    args.update({k: v for k, v in ma.items() if k in fields})
+    # a non-dynamic reference model has no freeze buffers; this build always
+    # carries them (all heads live), in the cheaper decomposed layout
+    if not args.pop("rand_attn_dynamic"):
+        args["rand_attn_prior_repr"] = "decomposed" if args["block_size"] % 64 == 0 else "dense"
+    return GPTConfig(**args)
+
+
+def _layout_check(ckpt):
+    layout = ckpt.get("attention_layout")
+    if layout is None and ckpt.get("intervention"):
+        iv = ckpt["intervention"]
+        mode = iv.get("physical_mode", iv.get("mode"))
+        layout = {"mode": {"prune_gate_taylor": "prune", "random_mean": "mean"}.get(mode, mode)}
+    if layout is not None and layout.get("mode") not in ("ordinary", "mean"):
+        raise NotImplementedError(f"attention layout {layout.get('mode')!r} (packed heads) is not supported")
+
+
+@torch.no_grad()
+def convert_state_dict(state_dict, model: GPT):
+    """Reference state dict -> this build's, in place on ``model``'s pattern
+    slots.  Returns the dict to pass to ``model.load_state_dict``."""
+    sd = {(k[len(_PREFIX):] if k.startswith(_PREFIX) else k): v for k, v in state_dict.items()}
+    out = {}
+    for name, v in sd.items():
+        if name.endswith(".attn.dyn_rho_band") or name.endswith(".attn.bias"):
+            continue
+        if not name.endswith(".attn.dyn_pattern"):
+            out[name] = v
+    for i, blk in enumerate(model.transformer.h):
+        a = blk.attn
+        pre = f"transformer.h.{i}.attn."
+        H, S = a.n_head, a.block_size
+        frozen = sd.get(pre + "dyn_frozen")
+        if frozen is None:  # non-dynamic reference model: every head live
+            out[pre + "dyn_frozen"] = torch.zeros(H, dtype=torch.bool)
+            out[pre + "dyn_decomp"] = torch.zeros(H, dtype=torch.bool)
+            if a.dyn_alpha is not None:
+                for n in ("dyn_alpha", "dyn_rho", "dyn_z"):
+                    out[pre + n] = torch.zeros(H, S)
+            out[pre + "dyn_pattern_slot"] = torch.full((H,), -1, dtype=torch.int32)
+            continue
+        decomp = sd.get(pre + "dyn_decomp", torch.zeros(H, dtype=torch.bool))
+        out[pre + "dyn_decomp"] = decomp
+        if a.dyn_alpha is not None and pre + "dyn_alpha" not in sd:
+            for n in ("dyn_alpha", "dyn_rho", "dyn_z"):
+                out[pre + n] = torch.zeros(H, S)
+        dense = [h for h in range(H) if bool(frozen[h]) and not bool(decomp[h])]
+        slot = torch.full((H,), -1, dtype=torch.int32)
+        if dense:
+            full = sd.get(pre + "dyn_pattern")
+            if full is None or full.dim() != 3 or full.size(0) != H:
+                raise ValueError(f"layer {i}: dense-frozen heads {dense} need a (n_head, S, S) dyn_pattern")
+            compact = torch.empty(len(dense), S, S, dtype=a._pattern_dtype)
+            for s, h in enumerate(dense):
+                compact[s] = full[h]
+                slot[h] = s
+            a.dyn_pattern = compact.to(a.dyn_frozen.device)
+            out[pre + "dyn_pattern"] = compact
+        else:
+            a.dyn_pattern = None
+        out[pre + "dyn_pattern_slot"] = slot
+        a._fz_dirty = True
+    return out
+
+
+def load_model(ckpt_path, device, dtype=None):
+    """(model, cfg, ckpt) for a reference checkpoint file, in eval mode on
+    ``device`` (and ``dtype`` if given; alpha / rho / z stay fp32)
+    (eval_nanogpt_logprobs.py:77-104)."""
+    ckpt = torch.load(ckpt_path, map_location="cpu", weights_only=True)
+    _layout_check(ckpt)
+    cfg = build_config_from_ckpt(ckpt)
+    model = GPT(cfg)
+    model.load_state_dict(convert_state_dict(ckpt["model"], model), strict=True)
+    model.eval()
+    model.to(device)
+    if dtype is not None:
+        model.to(dtype=dtype)
+    return model, cfg, ckpt
