@@ -27,6 +27,14 @@ HIPCC_FLAGS = [
 ]
 
 
+# Per-source flags.  The backward kernels keep four MFMA accumulator sets
+# alive across their loops; with the default AGPR form the compiler parks
+# them in VGPRs and copies every one into AGPRs and back around each product
+# (hundreds of v_accvgpr moves per query block).  The VGPR form of the MFMA
+# instructions removes the copies and lowers register use.
+SOURCE_FLAGS = {"attn_bwd.hip": ("-mllvm", "-amdgpu-mfma-vgpr-form")}
+
+
 def _hipcc():
     for cand in (os.environ.get("HIPCC"), "/opt/rocm/bin/hipcc", "hipcc"):
         if cand and (os.path.sep not in cand or os.path.exists(cand)):
@@ -52,7 +60,7 @@ def build(verbose=False, jobs=None):
     for src in SOURCES:
         obj = os.path.join(BUILD, src.replace(".hip", ".o"))
         objs.append(obj)
-        cmds.append([hipcc, *HIPCC_FLAGS, "-c", os.path.join(CSRC, src), "-o", obj])
+        cmds.append([hipcc, *HIPCC_FLAGS, *SOURCE_FLAGS.get(src, ()), "-c", os.path.join(CSRC, src), "-o", obj])
     jobs = jobs or min(len(cmds), max(1, os.cpu_count() or 1))
     with ThreadPoolExecutor(max_workers=jobs) as ex:
         for out in ex.map(_run, cmds):

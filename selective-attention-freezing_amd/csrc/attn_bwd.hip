@@ -166,7 +166,8 @@ __global__ __launch_bounds__(256) void bwd_dq_kernel(const BwdParams p) {
           for (int u = 0; u < 2; ++u) {
             const int i = 2 * e + u;
             const int key = 64 * j + 32 * ks + acc_key(i, g);
-            const float pr = (qv && key <= q) ? fast_exp2(s[i] * c - lse2) : 0.f;
+            // masked scores go through exp2(-inf) = 0: no branch per element
+            const float pr = fast_exp2((qv && key <= q) ? s[i] * c - lse2 : -__builtin_inff());
             ds2[u] = pr * (dp[i] - dl);
           }
           w[e] = Elem<T>::pack2(ds2[0], ds2[1]);
@@ -193,7 +194,7 @@ __global__ __launch_bounds__(256) void bwd_dq_kernel(const BwdParams p) {
 // key), P = 2^(S c - lse_q), dS = P (dP - delta_q), and accumulates
 // dV^T += dO^T P and dK^T += Q^T dS (dO^T, Q^T from transposing tile reads).
 template <typename T, int HD>
-__global__ __launch_bounds__(256) void bwd_dkdv_kernel(const BwdParams p) {
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void bwd_dkdv_kernel(const BwdParams p) {
   constexpr int BN = kBwdWaves * 32, NKT = HD / 16, NDT = HD / 32, VB = VRow<HD>::BYTES;
   __shared__ __align__(16) char q0[VB], q1[VB], o0[VB], o1[VB];
   __shared__ float ls0[128], ls1[128];  // lse (0..63) and delta (64..127) of the tile's queries
@@ -237,24 +238,33 @@ __global__ __launch_bounds__(256) void bwd_dkdv_kernel(const BwdParams p) {
   oo.init(wave, lane, p.do_st);
   const int ib0 = (kb * BN) / 64, nqb = (T_len + 63) / 64;
 
-  // query block i lives in slot i & 1: Q tile, dO tile, and lse / delta
+  // query block i lives in slot i & 1: Q tile, dO tile, and lse / delta.
+  // The next block's tiles go out by DMA and its lse / delta into registers
+  // right after the barrier; the registers land in the idle slot after the
+  // block's products, so no load latency sits in front of a barrier.
   if (ib0 < nqb) {
     qo.load(qbase, p.q_st, 64 * ib0, T_len, q0, wave);
     oo.load(dobase, p.do_st, 64 * ib0, T_len, o0, wave);
+    if (tid < 64) {
+      const int qq = 64 * ib0 + tid;
+      ls0[tid] = qq < T_len ? lsebase[(int64_t)qq * p.l_st] : 0.f;
+      ls0[64 + tid] = qq < T_len ? dlbase[qq] : 0.f;
+    }
   }
   for (int i = ib0; i < nqb; ++i) {
     const char* qt = ((i - ib0) & 1) ? q1 : q0;
     const char* ot = ((i - ib0) & 1) ? o1 : o0;
-    float* ls = ((i - ib0) & 1) ? ls1 : ls0;
-    if (tid < 64) {
-      const int qq = 64 * i + tid;
-      ls[tid] = qq < T_len ? lsebase[(int64_t)qq * p.l_st] : 0.f;
-      ls[64 + tid] = qq < T_len ? dlbase[qq] : 0.f;
-    }
+    const float* ls = ((i - ib0) & 1) ? ls1 : ls0;
     __syncthreads();  // this block's tiles and statistics are in LDS
+    float nlse = 0.f, ndel = 0.f;
     if (i + 1 < nqb) {
       qo.load(qbase, p.q_st, 64 * (i + 1), T_len, ((i - ib0) & 1) ? q0 : q1, wave);
       oo.load(dobase, p.do_st, 64 * (i + 1), T_len, ((i - ib0) & 1) ? o0 : o1, wave);
+      const int qq = 64 * (i + 1) + tid;
+      if (tid < 64 && qq < T_len) {
+        nlse = lsebase[(int64_t)qq * p.l_st];
+        ndel = dlbase[qq];
+      }
     }
 #pragma unroll
     for (int qs2 = 0; qs2 < 2; ++qs2) {
@@ -275,7 +285,7 @@ __global__ __launch_bounds__(256) void bwd_dkdv_kernel(const BwdParams p) {
           const int i2 = 2 * e + u;
           const int ql = 32 * qs2 + acc_key(i2, g);  // query within the tile
           const int qq = 64 * i + ql;
-          const float pr = (kv && qq >= kk && qq < T_len) ? fast_exp2(s[i2] * c - ls[ql]) : 0.f;
+          const float pr = fast_exp2((kv && qq >= kk && qq < T_len) ? s[i2] * c - ls[ql] : -__builtin_inff());
           pr2[u] = pr;
           ds2[u] = pr * (dp[i2] - ls[64 + ql]);
         }
@@ -292,6 +302,11 @@ __global__ __launch_bounds__(256) void bwd_dkdv_kernel(const BwdParams p) {
           dka[dt] = Elem<T>::mfma(tile_col_op<HD>(qt, 2 * qs2 + s2, dt, lane), bd, dka[dt]);
         }
       }
+    }
+    if (tid < 64) {  // the idle slot's readers finished before the previous barrier
+      float* ln = ((i - ib0) & 1) ? ls0 : ls1;
+      ln[tid] = nlse;
+      ln[64 + tid] = ndel;
     }
     __syncthreads();  // every wave is done with this slot before it is refilled
   }
@@ -314,7 +329,7 @@ __global__ __launch_bounds__(256) void bwd_frozen_dv_kernel(const BwdParams p) {
   __shared__ __align__(16) char o0[VB], o1[VB];
   // decomposed heads: z_q log2 e of the block's 64 queries and rho_d log2 e
   // for every distance d = q - key the block meets (64 + 128 - 1 values)
-  __shared__ float zs[64], rs[64 + BN];
+  __shared__ float zs2[2][64], rs2[2][64 + BN];
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int n = lane & 31, g = lane >> 5;
@@ -339,26 +354,37 @@ __global__ __launch_bounds__(256) void bwd_frozen_dv_kernel(const BwdParams p) {
   TileOffsets<T, HD> oo;
   oo.init(wave, lane, p.do_st);
   const int ib0 = (kb * BN) / 64, nqb = (T_len + 63) / 64;
-  if (ib0 < nqb) oo.load(dobase, p.do_st, 64 * ib0, T_len, o0, wave);
+  // z (per query) and the rho window of query block i, pre-scaled by log2 e;
+  // the next block's are loaded into registers while this one is computed
+  auto z_of = [&](int qq) {
+    return qq < T_len ? load_as_f32(p.z, (int64_t)ph * p.z_sh + (int64_t)qq * p.z_ss, p.z_dtype) * kLog2e : 0.f;
+  };
+  auto rho_of = [&](int dd) {
+    return (dd >= 0 && dd < T_len)
+               ? load_as_f32(p.rho, (int64_t)ph * p.r_sh + (int64_t)dd * p.r_ss, p.r_dtype) * kLog2e
+               : 0.f;
+  };
+  if (ib0 < nqb) {
+    oo.load(dobase, p.do_st, 64 * ib0, T_len, o0, wave);
+    if (KIND == 2) {
+      if (tid < 64) zs2[0][tid] = z_of(64 * ib0 + tid);
+      if (tid < 64 + BN - 1) rs2[0][tid] = rho_of(64 * ib0 - kb * BN - (BN - 1) + tid);
+    }
+  }
   for (int i = ib0; i < nqb; ++i) {
     const char* ot = ((i - ib0) & 1) ? o1 : o0;
     const int dmin = 64 * i - kb * BN - (BN - 1);  // smallest q - key of the block
-    if (KIND == 2) {
-      // (the previous block's readers passed the barrier at its end)
-      if (tid < 64) {
-        const int qq = 64 * i + tid;
-        zs[tid] = qq < T_len ? load_as_f32(p.z, (int64_t)ph * p.z_sh + (int64_t)qq * p.z_ss, p.z_dtype) * kLog2e
-                             : 0.f;
-      }
-      if (tid < 64 + BN - 1) {
-        const int dd = dmin + tid;
-        rs[tid] = (dd >= 0 && dd < T_len)
-                      ? load_as_f32(p.rho, (int64_t)ph * p.r_sh + (int64_t)dd * p.r_ss, p.r_dtype) * kLog2e
-                      : 0.f;
+    const float* zs = zs2[(i - ib0) & 1];
+    const float* rs = rs2[(i - ib0) & 1];
+    __syncthreads();  // this block's dO tile (and z / rho window) is in LDS
+    float nz = 0.f, nr = 0.f;
+    if (i + 1 < nqb) {
+      oo.load(dobase, p.do_st, 64 * (i + 1), T_len, ((i - ib0) & 1) ? o0 : o1, wave);
+      if (KIND == 2) {
+        if (tid < 64) nz = z_of(64 * (i + 1) + tid);
+        if (tid < 64 + BN - 1) nr = rho_of(dmin + 64 + tid);
       }
     }
-    __syncthreads();  // this block's dO tile (and z / rho window) is in LDS
-    if (i + 1 < nqb) oo.load(dobase, p.do_st, 64 * (i + 1), T_len, ((i - ib0) & 1) ? o0 : o1, wave);
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks) {
       const int q0 = 64 * i + 16 * ks;
@@ -368,13 +394,15 @@ __global__ __launch_bounds__(256) void bwd_frozen_dv_kernel(const BwdParams p) {
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
         const int qq = q0 + 8 * g + e;
+        const bool ok = kv && qq >= kk && qq < T_len;
         float v = 0.f;
-        if (kv && qq >= kk && qq < T_len) {
-          if (KIND == 1) {
-            v = load_as_f32(p.patt, (int64_t)ph * p.p_sh + (int64_t)qq * p.p_si + (int64_t)kk * p.p_sj, p.patt_dtype);
-          } else {
-            v = fast_exp2(alpha_k + rs[qq - kk - dmin] - zs[qq - 64 * i]);
-          }
+        if (KIND == 1) {
+          if (ok) v = load_as_f32(p.patt, (int64_t)ph * p.p_sh + (int64_t)qq * p.p_si + (int64_t)kk * p.p_sj, p.patt_dtype);
+        } else {
+          // every (query, key) pair of the block indexes inside the staged
+          // rho window and z row, so the reads need no guard; masked pairs
+          // take exp2(-inf) = 0
+          v = fast_exp2(ok ? alpha_k + rs[qq - kk - dmin] - zs[qq - 64 * i] : -__builtin_inff());
         }
         e8[e] = v;
       }
@@ -382,6 +410,11 @@ __global__ __launch_bounds__(256) void bwd_frozen_dv_kernel(const BwdParams p) {
                                    Elem<T>::pack2(e8[4], e8[5]), Elem<T>::pack2(e8[6], e8[7]));
 #pragma unroll
       for (int dt = 0; dt < NDT; ++dt) dva[dt] = Elem<T>::mfma(tile_col_op<HD>(ot, ks, dt, lane), bop, dva[dt]);
+    }
+    if (KIND == 2) {  // the idle slot's readers finished before the previous barrier
+      const int nx = ((i - ib0) & 1) ^ 1;
+      if (tid < 64) zs2[nx][tid] = nz;
+      if (tid < 64 + BN - 1) rs2[nx][tid] = nr;
     }
     __syncthreads();  // every wave is done with this slot before it is refilled
   }
