@@ -87,6 +87,31 @@ def build_c2_model(T, device, dtype, seed=1337, n_layer=12):
     return model, x, plan
 
 
+def build_c0_model(device, dtype, T=1024, seed=1337, n_layer=12):
+    """the 124M nanoGPT (random-init fp32 weights, seed
+    1337), 3 of 12 heads per layer frozen to the causal mean (heads
+    randperm(12) of a generator seeded 1337 + layer), installed as decomposed
+    heads with alpha = rho = 0 (the reference's own statement that zero
+    logits are the causal-uniform prior, nanogpt/bench_inference_triton.py:92-97);
+    tokens uniform in [0, 50257), B = 1."""
+    import torch
+    from nanogpt.model import GPT, GPTConfig
+
+    torch.manual_seed(seed)
+    cfg = GPTConfig(block_size=T, vocab_size=50304, n_layer=n_layer, n_head=12, n_embd=768,
+                    bias=False, position_encoding="rope", rand_attn_prior_repr="decomposed",
+                    rand_seed=seed)
+    model = GPT(cfg).to(device=device, dtype=dtype).eval()
+    plan = {}
+    for layer, blk in enumerate(model.transformer.h):
+        heads = torch.randperm(12, generator=torch.Generator().manual_seed(seed + layer))[:3].tolist()
+        z = torch.zeros(3, T, device=device)
+        blk.attn.freeze_heads_decomposed(heads, z, z)
+        plan[layer] = [(h, "mean", 0.0) for h in heads]
+    x = torch.randint(0, 50257, (1, T), generator=torch.Generator().manual_seed(seed + 1)).to(device)
+    return model, x, plan
+
+
 TRAFFIC_FILE = os.path.join(REPO, "profiles", "flash_fwd_c2_hbm_traffic.txt")
 SCAN_TRAFFIC_FILE = os.path.join(REPO, "profiles", "frozen_scan_sizing_hbm_traffic.txt")
 

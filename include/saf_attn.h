@@ -99,7 +99,9 @@ typedef struct saf_mixed_attn_args {
   void* workspace;              /* device scratch, saf_workspace_bytes() bytes */
   int64_t workspace_bytes;
   int32_t flash_qtiles;         /* 0 = auto (1); 1 or 2 query tiles per wave (2 only up to hd 64) */
-  int32_t scan_spin_limit;      /* 0 = default bound of each look-back wait */
+  int32_t scan_spin_limit;      /* 0 = default bound of each look-back wait; < 0 = give-up
+                                   drill: every scan chunk after the first gives up at once
+                                   (tests of the error path) */
 } saf_mixed_attn_args;
 
 /* All head kinds: live flash, dense P.V, decomposed rebuild, closed-form scan. */
@@ -130,6 +132,15 @@ int64_t saf_mixed_attn_bwd_workspace_bytes(const saf_mixed_attn_args* args);
  * frozen-head values v (B, nf, T, HD); fz_idx is a host array of nf entries. */
 int saf_frozen_pv_fwd(const saf_tensor_t* patt, const saf_tensor_t* v, const int32_t* fz_idx,
                       int32_t nf, int32_t T, const saf_tensor_t* out, void* stream);
+
+/* Backward of frozen_pv (replaces _pv_bwd_kernel and _FrozenPV.backward,
+ * kernel/frozen_attn.py:91-128, :150-182): dv[b, f, j] = sum over i >= j,
+ * i < T of patt[fz_idx[f], i, j] dy[b, f, i] for j < T, with the pattern
+ * rounded to dy's dtype and fp32 accumulation.  dy is (B, nf, T, HD), dv is
+ * (B, nf, T', HD) with T' >= T: rows j >= T are not written (the caller
+ * zeroes them).  The pattern must be lower-triangular, as for the forward. */
+int saf_frozen_pv_bwd(const saf_tensor_t* patt, const saf_tensor_t* dy, const int32_t* fz_idx,
+                      int32_t nf, int32_t T, const saf_tensor_t* dv, void* stream);
 
 /* Rotary embedding of the live-head q (B, Uq, T, HD) and k (B, Uk, T, HD), in
  * place (the two may be interleaved views of one projection output): Llama
@@ -184,8 +195,10 @@ int64_t saf_workspace_bytes(int32_t B, int32_t T, int32_t head_dim, int32_t n_sc
  * reference (its Triton launch needs no workspace). */
 int64_t saf_mixed_attn_workspace_bytes(const saf_mixed_attn_args* args);
 
-/* Reads the scan's look-back error word from a workspace after the stream
- * has been synchronised: 1 if a wait hit its spin limit, else 0. */
+/* Reads the scan's look-back error word of a workspace (synchronises
+ * `stream` first): 1 if a look-back wait gave up, else 0.  A wait that gives
+ * up leaves NaN in its chunk's rows and in every later chunk of that
+ * (batch, head) sequence, never a silently incomplete sum. */
 int saf_workspace_error(const void* workspace, void* stream, int32_t* error_out);
 
 /* Kernel timing: the next main kernel this host thread launches through an

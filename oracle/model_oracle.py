@@ -110,13 +110,16 @@ def block(x, sd, l, fr, cos, sin, n_head, path):
 
 
 @torch.no_grad()
-def gpt_forward(sd, cfg, freeze, idx, path="split", all_positions=False, layers=None):
+def gpt_forward(sd, cfg, freeze, idx, path="split", all_positions=False, layers=None, positions=None):
     """Logits of the reference GPT on CPU fp32.
 
     sd: float32 state dict; cfg: dict with n_layer, n_head, n_embd,
     position_encoding, rope_base; freeze: per-layer records
     {"frozen": (H,) bool, "patterns": {...}, "decomp": {...}}; layers: run
-    only these layer indices (a bounded sample for timing)."""
+    only these layer indices (a bounded sample for timing); positions: the
+    logits of these positions only (B, len(positions), vocab), for long
+    sequences whose all-position logits would not fit; otherwise the last
+    position (the reference's prefill output) or, with all_positions, all."""
     x = sd["transformer.wte.weight"][idx]
     T = idx.size(1)
     cos = sin = None
@@ -127,6 +130,8 @@ def gpt_forward(sd, cfg, freeze, idx, path="split", all_positions=False, layers=
     for l in (range(cfg["n_layer"]) if layers is None else layers):
         x = block(x, sd, l, freeze[l], cos, sin, cfg["n_head"], path)
     x = layer_norm(x, sd["transformer.ln_f.weight"], sd.get("transformer.ln_f.bias"))
-    if not all_positions:
+    if positions is not None:
+        x = x[:, torch.as_tensor(positions), :]
+    elif not all_positions:
         x = x[:, -1:, :]
     return F.linear(x, sd["lm_head.weight"])

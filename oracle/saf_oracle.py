@@ -10,6 +10,9 @@ Each function restates the reference's algorithm from its source
   eager_mixed_attention   kernel/test_fused_attn.py:53-63 (ref) and
                           nanogpt/model.py:824-844 (_attend_dynamic), with the
                           GQA map of qwen/kernel/fused_attn.py:254-259
+  eager_rows              the same output restricted to chosen query rows
+                          (row i needs only q_i, K/V[:i+1] and P[i, :i+1]),
+                          for parity at the configs' full sizes
   decomp_logits           kernel/fused_attn.py:83-98
   decomposed_logz         kernel/fused_attn.py:101-116
   make_rho_band           kernel/fused_attn.py:65-80
@@ -219,6 +222,63 @@ def eager_mixed_attention(q, k, v, frozen, hidx=None, pidx=None, kvidx=None,
             P = dec_cache[h]
         for b in range(B):
             out[b, h] = P @ v[b, vh]
+    return out
+
+
+def sample_rows(T, n_random=128, seed=0):
+    """Query rows checked at a full-size shape: the first and last rows, both
+    sides of every 64-row boundary (the tile edges of every kernel here), and
+    `n_random` seeded random rows; sorted, unique."""
+    rng = np.random.default_rng(seed)
+    b = np.arange(64, T, 64)
+    rows = np.concatenate([[0, 1, T - 2, T - 1], b - 1, b, rng.integers(0, T, n_random)])
+    return np.unique(np.clip(rows, 0, T - 1))
+
+
+def eager_rows(q, k, v, frozen, rows, hidx=None, pidx=None, kvidx=None, patt_rows=None,
+               alpha=None, rho=None, z=None, sm_scale=None):
+    """Rows `rows` of eager_mixed_attention's output, (B, H, len(rows), HD)
+    float64, without materialising any (T, T) matrix.
+
+    Live row i: softmax(scale q_i K[:i+1]^T) V[:i+1].  Dense row i:
+    patt_rows[h][n, :i+1] V[:i+1], where patt_rows[h] holds the pattern rows
+    `rows` of head h's pattern (an (R, >= T) array: the caller reads only
+    those rows of a large pattern).  Decomposed row i:
+    exp(alpha[j] + rho[i-j] - z[i]) for j <= i, times V[:i+1].  Arrays may be
+    float32/bf16-rounded; everything is computed in float64."""
+    frozen = np.asarray(frozen)
+    rows = np.asarray(rows)
+    H = frozen.shape[0]
+    B, _, T, HD = np.shape(v)
+    if sm_scale is None:
+        sm_scale = 1.0 / math.sqrt(HD)
+    R = rows.size
+    out = np.empty((B, H, R, HD))
+    jj = np.arange(T)
+    causal = jj[None, :] <= rows[:, None]          # (R, T)
+    for h in range(H):
+        vh = h if kvidx is None else int(kvidx[h])
+        st = int(frozen[h])
+        if st == 0:
+            qs = h if hidx is None else int(hidx[h])
+            ks = qs if kvidx is None else int(kvidx[h])
+            for b in range(B):
+                s = (_f64(q[b, qs][rows]) @ _f64(k[b, ks]).T) * sm_scale
+                s = np.where(causal, s, -np.inf)
+                s = np.exp(s - s.max(-1, keepdims=True))
+                out[b, h] = (s / s.sum(-1, keepdims=True)) @ _f64(v[b, vh])
+            continue
+        if st == 1:
+            P = _f64(patt_rows[h])[:, :T]
+            P = np.where(causal, P, 0.0)
+        else:
+            a, r, zz = (_f64(np.asarray(t)[h]) for t in (alpha, rho, z))
+            dist = rows[:, None] - jj[None, :]
+            lg = a[None, :T] + r[np.clip(dist, 0, T - 1)] - zz[rows][:, None]
+            with np.errstate(invalid="ignore"):
+                P = np.where(causal, np.exp(lg), 0.0)
+        for b in range(B):
+            out[b, h] = P @ _f64(v[b, vh])
     return out
 
 

@@ -22,7 +22,10 @@
 // >= T), scans it, publishes its chunk aggregate, obtains the carry from its
 // predecessors by decoupled look-back over one tagged 64-bit status word per
 // (sequence, chunk, column), and streams Y out with non-temporal stores.
-// Every wait is bounded by spin_limit.  There is no global ticket counter: a
+// Every wait is bounded by spin_limit; a wait that gives up sets the error
+// word and makes its carry NaN, which poisons the rest of the sequence rather
+// than returning an incomplete sum (spin_limit < 0 is a host-set drill: every
+// chunk after the first gives up at once).  There is no global ticket counter: a
 // single-address device-scope atomic per workgroup serialises at about one
 // per 30 ns on this chip, which alone bounded an earlier version to 45% of
 // HBM bandwidth.
@@ -237,7 +240,11 @@ __device__ __forceinline__ void scan_body(const ScanParams& p, int chunk, int se
       }
       uint64_t* sw = sw_seq + col;
       float carry = 0.f;
-      if (chunk > 0) {
+      if (chunk > 0 && p.spin_limit < 0) {
+        // give-up drill set by the host (tests of the error path): no wait at all
+        atomicOr(p.error, 1u);
+        carry = __builtin_nanf("");
+      } else if (chunk > 0) {
         __hip_atomic_store(sw + (int64_t)chunk * HD, pack_word(1u, a_wg), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         float factor = 1.f;
         int k = chunk - 1;
@@ -264,8 +271,13 @@ __device__ __forceinline__ void scan_body(const ScanParams& p, int chunk, int se
           if (done) break;
           k -= used;
           if (used == 0) {
-            if (++spins > p.spin_limit) {  // give up: carry incomplete, kernel still drains
+            if (++spins > p.spin_limit) {
+              // give up: the kernel still drains, the error word is set, and
+              // the carry is NaN, so these rows and every later chunk of the
+              // sequence (through the published prefix) read NaN, never a
+              // silently incomplete sum
               atomicOr(p.error, 1u);
+              carry = __builtin_nanf("");
               break;
             }
             __builtin_amdgcn_s_sleep(1);

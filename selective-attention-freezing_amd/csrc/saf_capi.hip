@@ -551,7 +551,8 @@ int run_scan(const saf_mixed_attn_args* a, const Plan& pl, hipStream_t s) {
   p.n_chunks = n_scan_chunks(pl.T, pl.HD);
   p.error = reinterpret_cast<uint32_t*>(ws + 4);
   p.status = reinterpret_cast<uint64_t*>(ws + w.status_off);
-  p.spin_limit = a->scan_spin_limit > 0 ? a->scan_spin_limit : (1 << 20);
+  // 0 = the default bound; a negative value is the give-up drill (tests)
+  p.spin_limit = a->scan_spin_limit != 0 ? a->scan_spin_limit : (1 << 20);
   for (int i = 0; i < p.n_slots; ++i) {
     const int h = pl.scan[i];
     p.out_head[i] = (int16_t)h;
@@ -641,6 +642,51 @@ int saf_frozen_pv_fwd(const saf_tensor_t* patt, const saf_tensor_t* v, const int
   }
   return run_dense(*patt, *v, *out, B, T, HD, v->dtype, oh, vh, ph, nullptr, 0,
                    reinterpret_cast<hipStream_t>(stream));
+}
+
+int saf_frozen_pv_bwd(const saf_tensor_t* patt, const saf_tensor_t* dy, const int32_t* fz_idx, int32_t nf,
+                      int32_t T, const saf_tensor_t* dv, void* stream) {
+  if (patt == nullptr || dy == nullptr || dv == nullptr) return fail(SAF_EINVAL, "patt, dy and dv are required");
+  if (!present(*dy) || !present(*dv)) return fail(SAF_EINVAL, "dy and dv must be device tensors");
+  if (dy->ndim != 4 || dv->ndim != 4) return fail(SAF_EINVAL, "dy and dv must be 4-D (B, nf, T, hd)");
+  if (dy->dtype != SAF_BF16 && dy->dtype != SAF_F16)
+    return fail(SAF_EUNSUPPORTED, "frozen_pv backward supports bf16 / fp16 gradients (got %s)", dtype_name(dy->dtype));
+  const int B = (int)dv->size[0], HD = (int)dv->size[3];
+  if (nf != dv->size[1]) return fail(SAF_EINVAL, "fz_idx must have one entry per compact head (%d != %lld)", nf,
+                                    (long long)dv->size[1]);
+  if (nf > SAF_MAX_HEADS) return fail(SAF_EUNSUPPORTED, "more than %d frozen heads", SAF_MAX_HEADS);
+  if (T < 0 || T > dv->size[2]) return fail(SAF_EINVAL, "T must be within dv's sequence length");
+  if (!supported_hd(HD)) return fail(SAF_EUNSUPPORTED, "head_dim %d is not supported (32, 64, 96, 128)", HD);
+  if (dy->size[0] != B || dy->size[1] != nf || dy->size[2] != T || dy->size[3] != HD || dy->dtype != dv->dtype)
+    return fail(SAF_EINVAL, "dy must be (B, nf, T, hd) in dv's dtype");
+  if (int rc = check_act(*dy, "dy", 16)) return rc;
+  if (int rc = check_act(*dv, "dv", 8)) return rc;
+  if (nf == 0 || T == 0 || B == 0) return SAF_OK;
+  if (!present(*patt) || patt->ndim != 3 || patt->size[1] < T || patt->size[2] < T)
+    return fail(SAF_EINVAL, "patt must have shape (P, S, S) with S >= T");
+  if (patt->dtype != SAF_F32 && patt->dtype != SAF_BF16 && patt->dtype != SAF_F16)
+    return fail(SAF_EUNSUPPORTED, "unsupported patt dtype %s", dtype_name(patt->dtype));
+  if (fz_idx == nullptr) return fail(SAF_EINVAL, "fz_idx (host) is required");
+  BwdParams p{};
+  p.dout = dy->data;
+  p.dv = dv->data;
+  p.do_sb = dy->stride[0]; p.do_sh = dy->stride[1]; p.do_st = dy->stride[2];
+  p.dv_sb = dv->stride[0]; p.dv_sh = dv->stride[1]; p.dv_st = dv->stride[2];
+  p.B = B;
+  p.T = T;
+  p.n_frozen = nf;
+  for (int f = 0; f < nf; ++f) {
+    if (fz_idx[f] < 0 || fz_idx[f] >= patt->size[0])
+      return fail(SAF_EINVAL, "fz_idx[%d] = %d does not index patt", f, fz_idx[f]);
+    p.f_head[f] = (int16_t)f;  // compact head of dy and dv
+    p.pat_head[f] = (int16_t)fz_idx[f];
+    p.f_kind[f] = 1;
+  }
+  p.patt = patt->data;
+  p.patt_dtype = patt->dtype;
+  p.p_sh = patt->stride[0]; p.p_si = patt->stride[1]; p.p_sj = patt->stride[2];
+  return launched(launch_bwd_frozen_dv(p, dy->dtype, HD, reinterpret_cast<hipStream_t>(stream)),
+                  "frozen_pv backward");
 }
 
 static int rope_common(const saf_tensor_t* q, const saf_tensor_t* k, const saf_tensor_t* qw,

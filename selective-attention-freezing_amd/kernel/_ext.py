@@ -22,7 +22,7 @@ _DTYPE_CODE = {torch.float32: SAF_F32, torch.float16: SAF_F16,
 # Exported symbols, in header order (checked by the CPU test suite).
 EXPORTS = ("saf_mixed_attn_fwd", "saf_flash_fwd", "saf_frozen_dense_pv_fwd",
            "saf_frozen_decomp_fwd", "saf_frozen_scan_fwd", "saf_mixed_attn_bwd",
-           "saf_mixed_attn_bwd_workspace_bytes", "saf_frozen_pv_fwd",
+           "saf_mixed_attn_bwd_workspace_bytes", "saf_frozen_pv_fwd", "saf_frozen_pv_bwd",
            "saf_rope_qk_inplace", "saf_qk_rmsnorm_rope_inplace", "saf_add_layernorm",
            "saf_decomposed_logz", "saf_workspace_bytes", "saf_mixed_attn_workspace_bytes",
            "saf_workspace_error", "saf_time_next_kernel", "saf_last_error", "saf_version")
@@ -84,6 +84,8 @@ def lib():
                                         ctypes.c_int32, ctypes.c_int32, P(SafTensor),
                                         ctypes.c_void_p]
         L.saf_frozen_pv_fwd.restype = ctypes.c_int
+        L.saf_frozen_pv_bwd.argtypes = L.saf_frozen_pv_fwd.argtypes
+        L.saf_frozen_pv_bwd.restype = ctypes.c_int
         L.saf_rope_qk_inplace.argtypes = [P(SafTensor)] * 4 + [ctypes.c_void_p]
         L.saf_rope_qk_inplace.restype = ctypes.c_int
         L.saf_qk_rmsnorm_rope_inplace.argtypes = [P(SafTensor)] * 4 + [ctypes.c_float] + \

@@ -4,12 +4,15 @@ Drop-in for /root/reference/kernel/frozen_attn.py:185-192.  V and the output
 are COMPACT (B, nf, T, hd) tensors holding only the frozen heads; the pattern
 buffer keeps its (n_head, S, S) layout and is indexed through ``fz_idx``.  The
 product runs in libsafattn.so's dense P.V kernel (causal j-block skipping,
-pattern rounded to V's dtype before the bf16/fp16 MFMA).
+pattern rounded to V's dtype before the bf16/fp16 MFMA).  The backward,
+dV = P^T dY (/root/reference/kernel/frozen_attn.py:91-128, :174-182), runs the
+frozen-head dV kernel of the attention backward (saf_frozen_pv_bwd); rows of
+V at or past T get zero gradient.
 """
 import torch
 
 from . import _ext
-from .fused_attn import _aligned_view, _host_table
+from .fused_attn import _aligned_view, _host_table, _row_aligned
 
 HAVE_TRITON = False   # this build has no Triton; kept for import compatibility
 
@@ -20,15 +23,18 @@ def frozen_pv_usable(v):
 
 
 class _FrozenPVFn(torch.autograd.Function):
+    """v is the only differentiable input; patterns get no gradient."""
 
     @staticmethod
-    def forward(ctx, v, run):
+    def forward(ctx, v, run, bwd):
+        ctx.bwd = bwd
         return run()
 
     @staticmethod
     def backward(ctx, dy):
-        raise NotImplementedError(
-            "frozen_pv backward (dV = P^T dY) is not implemented in the MI355X build")
+        dv = ctx.bwd(dy)
+        ctx.bwd = None
+        return dv, None, None
 
 
 def frozen_pv(patt, v, fz_idx, T):
@@ -50,6 +56,18 @@ def frozen_pv(patt, v, fz_idx, T):
         _ext.check(L.saf_frozen_pv_fwd(pd, vd, fz_c, nf, int(T), od, stream))
         return out
 
+    def bwd(dy):
+        """dv (v's shape, contiguous) = P^T dy over the first T rows."""
+        dy_d = dy.to(v.dtype)
+        if not _row_aligned(dy_d, 16):
+            dy_d = dy_d.contiguous()
+        make = torch.empty if Tv == T else torch.zeros
+        dv = make((B, nf, Tv, hd), device=v.device, dtype=v.dtype)
+        stream = _ext.current_stream_ptr(v.device)
+        _ext.check(L.saf_frozen_pv_bwd(_ext.tensor_desc(patt), _ext.tensor_desc(dy_d), fz_c, nf, int(T),
+                                       _ext.tensor_desc(dv), stream))
+        return dv
+
     if torch.is_grad_enabled() and v.requires_grad:
-        return _FrozenPVFn.apply(v, run)
+        return _FrozenPVFn.apply(v, run, bwd)
     return run()

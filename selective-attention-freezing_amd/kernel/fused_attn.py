@@ -247,26 +247,32 @@ def set_kernel_timer(timer):
 class _MixedAttnFn(torch.autograd.Function):
     """Autograd node of fused_mixed_attn (kernel/fused_attn.py:621-647 of the
     reference): the forward runs the HIP forward and keeps what the backward
-    needs (out, the base-2 LSE of the live heads, the routing tables and the
-    fixed pattern buffers); the backward runs saf_mixed_attn_bwd.  Frozen
-    heads have no q/k slot, so they get no Q/K gradient; patterns and the
-    decomposed buffers are constants (no gradient, ever)."""
+    needs (the output through save_for_backward, so no reference cycle holds
+    it; the base-2 LSE of the live heads, the routing tables and the fixed
+    pattern buffers in the backward closure); the backward runs
+    saf_mixed_attn_bwd.  Frozen heads have no q/k slot, so they get no Q/K
+    gradient; patterns and the decomposed buffers are constants (no
+    gradient, ever)."""
 
     @staticmethod
     def forward(ctx, q, k, v, run, bwd):
+        out = run()
         ctx.bwd = bwd
-        return run()
+        ctx.save_for_backward(out)
+        return out
 
     @staticmethod
     def backward(ctx, dout):
-        dq, dk, dv = ctx.bwd(dout)
+        (out,) = ctx.saved_tensors
+        dq, dk, dv = ctx.bwd(dout, out)
+        ctx.bwd = None   # release the forward's buffers now
         return dq, dk, dv, None, None
 
 
 def fused_mixed_attn(q, k, v, patt, frozen, hidx=None, pidx=None,
                      sm_scale=None, alpha=None, rho=None, z=None,
                      rho_band=None, validate=True, kvidx=None,
-                     closed_form=None, lse=None, flash_qtiles=0):
+                     closed_form=None, lse=None, flash_qtiles=0, scan_spin_limit=0):
     """Causal attention over all heads, frozen heads using a fixed prior.
 
     Arguments follow /root/reference/kernel/fused_attn.py:650-680 (and
@@ -286,6 +292,10 @@ def fused_mixed_attn(q, k, v, patt, frozen, hidx=None, pidx=None,
       lse      optional (B, H, T) fp32 output for the live heads' base-2 LSE
       flash_qtiles 0 (auto: 1) / 1 / 2 query tiles per wave of the flash kernel
                (2 applies up to hd 64; larger heads use 1)
+      scan_spin_limit  0 = default bound of the scan's look-back waits; < 0
+               is the give-up drill that tests the error path (every scan
+               chunk after the first gives up: NaN rows, and with validate
+               a RuntimeError)
     Returns (B, H, T, HD) in natural head order, strided like v (like the
     reference's empty_like(v)).
     """
@@ -364,6 +374,7 @@ def fused_mixed_attn(q, k, v, patt, frozen, hidx=None, pidx=None,
     args.closed_param = keep[5]
     args.sm_scale = float(sm_scale)
     args.flash_qtiles = int(flash_qtiles)
+    args.scan_spin_limit = int(scan_spin_limit)
     # scan look-back words + partials of the causally balanced live-head kernel
     ws_bytes = int(L.saf_mixed_attn_workspace_bytes(args))
     if ws_bytes < 0:
@@ -416,13 +427,23 @@ def fused_mixed_attn(q, k, v, patt, frozen, hidx=None, pidx=None,
                     launch(kind, cur)
         else:
             _ext.check(L.saf_mixed_attn_fwd(args, cur.cuda_stream))
+        if n_scan and validate:
+            # a look-back wait that gave up leaves NaN rows (never a silently
+            # incomplete sum); with validate the call also raises
+            err = _ext.ctypes.c_int32(0)
+            _ext.check(L.saf_workspace_error(args.workspace, cur.cuda_stream, _ext.ctypes.byref(err)))
+            if err.value:
+                raise RuntimeError(
+                    "closed-form scan: a look-back wait gave up (scan_spin_limit reached); "
+                    "the affected rows of the output are NaN")
         return out
 
     # every tensor the argument block points to stays alive until the backward
-    held = (q_d, k_d, v_d, out, lse, patt, alpha if need_dec else None,
+    # (out itself is saved by the autograd node and passed back in)
+    held = (q_d, k_d, v_d, lse, patt, alpha if need_dec else None,
             rho if need_dec else None, z if need_dec else None)
 
-    def bwd(dout):
+    def bwd(dout, out_saved):
         """dq, dk (compact, contiguous; zero for slots no live head uses) and
         dv (contiguous) through saf_mixed_attn_bwd."""
         if kvidx is not None:
@@ -445,7 +466,7 @@ def fused_mixed_attn(q, k, v, patt, frozen, hidx=None, pidx=None,
         cur = torch.cuda.current_stream(v.device)
         _ext.check(L.saf_mixed_attn_bwd(bargs, _ext.tensor_desc(do), _ext.tensor_desc(dq),
                                         _ext.tensor_desc(dk), _ext.tensor_desc(dv), cur.cuda_stream))
-        _ = (keep, held)  # the host tables and tensors the argument block points to
+        _ = (keep, held, out_saved)  # what the argument block points to
         gq = dq.to(q.dtype) if dq is not None and q is not None else None
         gk = dk.to(k.dtype) if dk is not None and k is not None else None
         return gq, gk, dv

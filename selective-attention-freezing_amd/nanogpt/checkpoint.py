@@ -63,9 +63,18 @@ def build_config_from_ckpt(ckpt) -> GPTConfig:
     if "rand_mask_rate" in ma:  # renamed field of older exports
         ma["rand_proj_mask_rate"] = ma.pop("rand_mask_rate")
     cfg_dict = ckpt.get("config", {}) or {}
-    for k in ("rand_attn_pattern", "rand_attn_head_rate"):
+    # fields some exports persist only in the full config dict
+    # (eval_nanogpt_logprobs.py:66-70)
+    for k in ("rand_attn_prior_path", "rand_attn_pattern_sharing", "rand_attn_pattern",
+              "rand_attn_head_rate", "rand_attn_head_rate_per_layer"):
         if k not in ma and cfg_dict.get(k) is not None:
             ma[k] = cfg_dict[k]
+    if ma.get("rand_attn_pattern") == "":   # the reference treats "" as "none" (model.py:457)
+        ma["rand_attn_pattern"] = "none"
+    if ma.get("rand_attn_head_rate_per_layer"):
+        raise NotImplementedError(
+            f"checkpoint field rand_attn_head_rate_per_layer={ma['rand_attn_head_rate_per_layer']!r} "
+            "selects per-layer random attention heads (Method H), which this build does not implement")
     for k, want in _REQUIRED.items():
         if k in ma and ma[k] is not None and ma[k] != want:
             raise NotImplementedError(f"checkpoint field {k}={ma[k]!r} selects an architecture this build "

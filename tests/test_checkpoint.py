@@ -121,7 +121,8 @@ def test_dense_prior_export_and_defaults(tmp_path):
 
 
 @pytest.mark.parametrize("field,value", [("rand_head_rate", 0.25), ("state_size", 16),
-                                         ("rand_attn_pattern", "uniform"), ("block_type", "mamba")])
+                                         ("rand_attn_pattern", "uniform"), ("block_type", "mamba"),
+                                         ("rand_attn_head_rate_per_layer", "0.25,0.5")])
 def test_unsupported_architectures_refused(tmp_path, field, value):
     from nanogpt.checkpoint import load_model
     m0, _ = _small_model(T=64, layers=1)
@@ -129,6 +130,25 @@ def test_unsupported_architectures_refused(tmp_path, field, value):
     torch.save(ck, tmp_path / "x.pt")
     with pytest.raises(NotImplementedError, match=field):
         load_model(tmp_path / "x.pt", "cpu")
+
+
+def test_config_only_fields_and_empty_pattern(tmp_path):
+    """Fields persisted only in the full config dict are pulled in
+    (eval_nanogpt_logprobs.py:66-70): a per-layer head rate there is refused;
+    rand_attn_pattern "" means "none" (model.py:457) and loads."""
+    from nanogpt.checkpoint import load_model
+    m0, _ = _small_model(T=64, layers=1)
+    ck = {"model": _reference_layout(m0), "model_args": _model_args(m0.config),
+          "config": {"rand_attn_head_rate_per_layer": "0.1"}}
+    torch.save(ck, tmp_path / "h.pt")
+    with pytest.raises(NotImplementedError, match="rand_attn_head_rate_per_layer"):
+        load_model(tmp_path / "h.pt", "cpu")
+    ck = {"model": _reference_layout(m0), "model_args": _model_args(m0.config, rand_attn_pattern=""),
+          "config": {"rand_attn_pattern_sharing": "none", "rand_attn_prior_path": ""}}
+    torch.save(ck, tmp_path / "e.pt")
+    m1, _, _ = load_model(tmp_path / "e.pt", "cpu")
+    for k, v in m0.state_dict().items():
+        assert torch.equal(m1.state_dict()[k], v), k
 
 
 def test_packed_layout_and_pickled_objects_refused(tmp_path):

@@ -151,3 +151,33 @@ def test_backward_gqa_raises():
     y = K.fused_mixed_attn(q, k, v, patt, frozen.to(DEV), hidx.to(DEV), pidx.to(DEV), kvidx=kvidx.to(DEV))
     with pytest.raises(NotImplementedError):
         y.float().sum().backward()
+
+
+@pytest.mark.parametrize("T,Tv,S,hd,nf", [(1, 1, 64, 64, 2), (37, 40, 64, 64, 3), (700, 700, 1024, 64, 3),
+                                          (513, 600, 576, 128, 2), (1024, 1024, 1024, 96, 3)])
+def test_frozen_pv_backward(T, Tv, S, hd, nf):
+    """frozen_pv's backward dV = P^T dY (kernel/frozen_attn.py:91-128,
+    kernel/test_frozen_attn.py:57-87) with compact frozen values, a
+    non-identity fz_idx, S > T and V longer than T (rows at or past T get
+    zero gradient) against the oracle's P^T dY in float64."""
+    K = _kernel()
+    B, Hp = 2, 6
+    patt = make_pattern(Hp, S, seed=T + S + 1)
+    fz = torch.tensor([5, 0, 3][:nf], dtype=torch.int32)
+    g = torch.Generator().manual_seed(T * hd + 7)
+    v = torch.randn(B, nf, Tv, hd, generator=g).bfloat16()
+    dy = torch.randn(B, nf, T, hd, generator=g).bfloat16()
+    vd = v.to(DEV).requires_grad_(True)
+    y = K.frozen_pv(patt.to(DEV), vd, fz.to(DEV), T)
+    y.backward(dy.to(DEV))
+    torch.cuda.synchronize()
+    ref = np.zeros((B, nf, Tv, hd))
+    for f in range(nf):
+        P = patt[int(fz[f]), :T, :T].double().numpy()
+        for b in range(B):
+            ref[b, f, :T] = P.T @ f64(dy[b, f])
+    _cmp(vd.grad, ref, f"frozen_pv dV T={T} Tv={Tv} hd={hd}")
+    assert (vd.grad[:, :, T:] == 0).all()
+    # the forward of the same call is unchanged by the autograd wrapping
+    y0 = K.frozen_pv(patt.to(DEV), v.to(DEV), fz.to(DEV), T)
+    assert torch.equal(y.detach(), y0)

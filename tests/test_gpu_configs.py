@@ -1,0 +1,273 @@
+"""Parity at every BASELINE config's own workload (C0-C4), on the GPU.
+
+Op level (C1-C4): the HIP operator runs at the config's exact shape through
+the C-ABI, and the output is compared with the float64 oracle on sampled
+query rows (oracle.saf_oracle.eager_rows, pinned against the full eager
+output in tests/test_oracle.py): both sides of every 64-row boundary, the
+first and last rows and 128 seeded random rows, the same rows for every
+(batch, head), at least 256 rows each.  Bound: max-abs <= 2e-2 and
+relative-L2 <= 1e-2 (north_star), as the reference's own grid checks
+(kernel/test_fused_attn.py:162-230, oracle :53-63).
+
+  C1  B=8, H=12, T=4096, hd 64, 3 decay heads (rho ~U(0.001, 0.1)), in the
+      three forms the build can run them: closed-form scan, decomposed
+      rebuild, dense bf16 patterns (compact pidx)
+  C2  one layer of the headline: B=1, H=12, T=16384, hd 64, a mean, a decay
+      and a window head (closed-form scan), 9 live heads
+  C3  B=2, H=16, T=8192, hd 128, 4 dense bf16 heads (softmax of N(0,1)
+      logits masked causally)
+  C4  B=4, 14 query / 2 KV heads (kvidx), T=4096, hd 64, f in {0, 4, 7, 10}
+      causal-mean heads (scan), and f = 7 as dense mean patterns
+
+Model level: C0 (12 layers, T=1024) and C2 (12 layers, T=16384) built exactly
+as bench.py builds them, bf16 on the GPU, against the fp32 oracle of the
+reference's CPU split path on the host: logits cosine >= 0.9999 at every
+position (C0) or at sampled positions plus the last one (C2).
+"""
+import numpy as np
+import pytest
+import torch
+
+from oracle import model_oracle, saf_oracle as orc
+from saf_cases import compare
+from test_model import _cos, _oracle_inputs
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+SEED = 1337
+
+
+def _kernel():
+    import kernel
+    return kernel
+
+
+def _np(t):
+    return t.detach().float().cpu().numpy()
+
+
+def _routing(H, frozen_heads, state):
+    frozen = torch.zeros(H, dtype=torch.int32)
+    frozen[list(frozen_heads)] = state
+    live = [h for h in range(H) if h not in frozen_heads]
+    hidx = torch.zeros(H, dtype=torch.int32)
+    hidx[live] = torch.arange(len(live), dtype=torch.int32)
+    return frozen, hidx, live
+
+
+def _closed_buffers(H, S, kinds):
+    """(H, S) fp32 alpha / rho / z with the closed-form heads {h: (kind, p)}
+    (z from the float64 oracle; other rows zero)."""
+    alpha = np.zeros((H, S))
+    rho = np.zeros((H, S))
+    z = np.zeros((H, S))
+    for h, (kind, prm) in kinds.items():
+        alpha[h], rho[h] = orc.closed_form_params(kind, prm, S)
+        z[h] = orc.decomposed_logz(alpha[h:h + 1], rho[h:h + 1])[0]
+    f = lambda a: torch.from_numpy(a).float()
+    return f(alpha), f(rho), f(z)
+
+
+def _check_rows(y, ref, rows, what):
+    got = y[:, :, torch.as_tensor(rows, device=y.device)].float().cpu()
+    return compare(got, ref, what=what)
+
+
+def _dense_from_decomp(alpha, rho, z, heads, T):
+    """(n, T, T) bf16 patterns exp(alpha[j] + rho[i-j] - z[i]) (j <= i) built
+    on the device in fp32."""
+    i = torch.arange(T, device=DEV)
+    dist = i[:, None] - i[None, :]
+    out = torch.empty(len(heads), T, T, device=DEV, dtype=torch.bfloat16)
+    for n, h in enumerate(heads):
+        a, r, zz = (t[h].to(DEV) for t in (alpha, rho, z))
+        lg = a[None, :T] + r[dist.clamp(min=0)] - zz[:T, None]
+        out[n] = torch.exp(lg.masked_fill(dist < 0, float("-inf"))).to(torch.bfloat16)
+    return out
+
+
+# ---------------------------------------------------------------------------
+# C1: the isolated op at the 124M shape
+# ---------------------------------------------------------------------------
+
+@pytest.mark.parametrize("form", ["scan", "rebuild", "dense"])
+def test_c1_op(form):
+    K = _kernel()
+    B, H, T, hd = 8, 12, 4096, 64
+    g = torch.Generator().manual_seed(SEED)
+    fz = sorted(torch.randperm(H, generator=g)[:3].tolist())
+    rates = (0.001 + 0.099 * torch.rand(3, generator=g)).tolist()
+    frozen, hidx, live = _routing(H, fz, 2)
+    q = torch.randn(B, len(live), T, hd, generator=g).bfloat16()
+    k = torch.randn(B, len(live), T, hd, generator=g).bfloat16()
+    v = torch.randn(B, H, T, hd, generator=g).bfloat16()
+    alpha, rho, z = _closed_buffers(H, T, {h: ("decay", c) for h, c in zip(fz, rates)})
+    kw = {}
+    patt = pidx = None
+    if form == "dense":
+        patt = _dense_from_decomp(alpha, rho, z, fz, T)
+        frozen[fz] = 1
+        pidx = torch.zeros(H, dtype=torch.int32)
+        pidx[fz] = torch.arange(3, dtype=torch.int32)
+        pidx = pidx.to(DEV)
+    else:
+        kw = dict(alpha=alpha.to(DEV), rho=rho.to(DEV), z=z.to(DEV))
+        if form == "scan":
+            kw["closed_form"] = K.classify_closed_form(alpha, rho, z)
+            assert all(int(kw["closed_form"][0][h]) == K.CLOSED_DECAY for h in fz)
+    y = K.fused_mixed_attn(q.to(DEV), k.to(DEV), v.to(DEV), patt, frozen.to(DEV), hidx.to(DEV), pidx, **kw)
+    torch.cuda.synchronize()
+    rows = orc.sample_rows(T, seed=1)
+    assert rows.size >= 256
+    prow = None
+    if patt is not None:
+        ridx = torch.as_tensor(rows, device=DEV)
+        prow = {h: _np(patt[int(pidx[h])][ridx]) for h in fz}
+    ref = orc.eager_rows(_np(q), _np(k), _np(v), frozen.numpy(), rows, hidx.numpy(), patt_rows=prow,
+                         alpha=_np(alpha), rho=_np(rho), z=_np(z))
+    _check_rows(y, ref, rows, f"C1 {form}")
+
+
+# ---------------------------------------------------------------------------
+# C2: one layer of the headline shape
+# ---------------------------------------------------------------------------
+
+def test_c2_layer_op():
+    K = _kernel()
+    B, H, T, hd = 1, 12, 16384, 64
+    g = torch.Generator().manual_seed(SEED)
+    fz = torch.randperm(H, generator=g)[:3].tolist()
+    rate = 0.001 + 0.099 * float(torch.rand(1, generator=g))
+    w = int(torch.randint(64, 1025, (1,), generator=g))
+    kinds = {fz[0]: ("mean", 0.0), fz[1]: ("decay", rate), fz[2]: ("window", w)}
+    frozen, hidx, live = _routing(H, fz, 2)
+    q = torch.randn(B, len(live), T, hd, generator=g).bfloat16()
+    k = torch.randn(B, len(live), T, hd, generator=g).bfloat16()
+    v = torch.randn(B, H, T, hd, generator=g).bfloat16()
+    alpha, rho, z = _closed_buffers(H, T, kinds)
+    cf = K.classify_closed_form(alpha, rho, z)
+    assert [int(cf[0][h]) for h in fz] == [K.CLOSED_MEAN, K.CLOSED_DECAY, K.CLOSED_WINDOW]
+    # q/k as interleaved views of one (B, T, 2, U, hd) projection output, v as
+    # the transposed (B, T, H, hd) projection: the model's own layout
+    qk = torch.stack([q, k], dim=2).permute(0, 3, 2, 1, 4).contiguous().to(DEV)
+    qd, kd = qk[:, :, 0].transpose(1, 2), qk[:, :, 1].transpose(1, 2)
+    vd = v.transpose(1, 2).contiguous().to(DEV).transpose(1, 2)
+    y = K.fused_mixed_attn(qd, kd, vd, None, frozen.to(DEV), hidx.to(DEV), alpha=alpha.to(DEV),
+                           rho=rho.to(DEV), z=z.to(DEV), closed_form=cf)
+    torch.cuda.synchronize()
+    rows = orc.sample_rows(T, seed=2)
+    ref = orc.eager_rows(_np(q), _np(k), _np(v), frozen.numpy(), rows, hidx.numpy(),
+                         alpha=_np(alpha), rho=_np(rho), z=_np(z))
+    _check_rows(y, ref, rows, "C2 layer")
+
+
+# ---------------------------------------------------------------------------
+# C3: 1B-class shape, dense bf16 patterns
+# ---------------------------------------------------------------------------
+
+def test_c3_layer_op():
+    K = _kernel()
+    B, H, T, hd = 2, 16, 8192, 128
+    g = torch.Generator().manual_seed(SEED)
+    fz = sorted(torch.randperm(H, generator=g)[:4].tolist())
+    frozen, hidx, live = _routing(H, fz, 1)
+    q = torch.randn(B, len(live), T, hd, generator=g).bfloat16()
+    k = torch.randn(B, len(live), T, hd, generator=g).bfloat16()
+    v = torch.randn(B, H, T, hd, generator=g).bfloat16()
+    gd = torch.Generator(device=DEV).manual_seed(SEED)
+    patt = torch.empty(4, T, T, device=DEV, dtype=torch.bfloat16)
+    causal = torch.ones(T, T, device=DEV, dtype=torch.bool).tril_()
+    for n in range(4):
+        lg = torch.randn(T, T, device=DEV, generator=gd).masked_fill_(~causal, float("-inf"))
+        patt[n] = lg.softmax(-1).to(torch.bfloat16)
+        del lg
+    pidx = torch.zeros(H, dtype=torch.int32)
+    pidx[fz] = torch.arange(4, dtype=torch.int32)
+    y = K.fused_mixed_attn(q.to(DEV), k.to(DEV), v.to(DEV), patt, frozen.to(DEV), hidx.to(DEV), pidx.to(DEV))
+    torch.cuda.synchronize()
+    rows = orc.sample_rows(T, seed=3)
+    ridx = torch.as_tensor(rows, device=DEV)
+    prow = {h: _np(patt[int(pidx[h])][ridx]) for h in fz}
+    del patt
+    ref = orc.eager_rows(_np(q), _np(k), _np(v), frozen.numpy(), rows, hidx.numpy(), patt_rows=prow)
+    _check_rows(y, ref, rows, "C3 layer")
+
+
+# ---------------------------------------------------------------------------
+# C4: Qwen-style GQA (14 query / 2 KV heads), causal-mean heads
+# ---------------------------------------------------------------------------
+
+@pytest.mark.parametrize("f,form", [(0, "scan"), (4, "scan"), (7, "scan"), (10, "scan"), (7, "dense")])
+def test_c4_layer_op(f, form):
+    K = _kernel()
+    B, H, HKV, T, hd = 4, 14, 2, 4096, 64
+    fz = sorted(torch.randperm(H, generator=torch.Generator().manual_seed(SEED))[:f].tolist())
+    g = torch.Generator().manual_seed(SEED + f)
+    frozen, hidx, live = _routing(H, fz, 2 if form == "scan" else 1)
+    kvidx = torch.as_tensor(orc.gqa_kvidx(H, HKV))
+    q = torch.randn(B, len(live), T, hd, generator=g).bfloat16()
+    k = torch.randn(B, HKV, T, hd, generator=g).bfloat16()
+    v = torch.randn(B, HKV, T, hd, generator=g).bfloat16()
+    alpha, rho, z = _closed_buffers(H, T, {h: ("mean", 0.0) for h in fz})
+    kw, patt, pidx, prow = {}, None, None, None
+    rows = orc.sample_rows(T, seed=4)
+    if form == "scan" and f:
+        cf = K.classify_closed_form(alpha, rho, z)
+        assert all(int(cf[0][h]) == K.CLOSED_MEAN for h in fz)
+        kw = dict(alpha=alpha.to(DEV), rho=rho.to(DEV), z=z.to(DEV), closed_form=cf)
+    elif form == "dense":
+        mean = torch.from_numpy(orc.mean_pattern(T)).to(torch.bfloat16)
+        patt = mean.unsqueeze(0).to(DEV)
+        pidx = torch.zeros(H, dtype=torch.int32).to(DEV)
+        prow = {h: _np(mean[torch.as_tensor(rows)]) for h in fz}
+    y = K.fused_mixed_attn(q.to(DEV), k.to(DEV), v.to(DEV), patt, frozen.to(DEV), hidx.to(DEV), pidx,
+                           kvidx=kvidx.to(DEV), **kw)
+    torch.cuda.synchronize()
+    assert y.shape == (B, H, T, hd)
+    ref = orc.eager_rows(_np(q), _np(k), _np(v), frozen.numpy(), rows, hidx.numpy(), kvidx=kvidx.numpy(),
+                         patt_rows=prow, alpha=_np(alpha), rho=_np(rho), z=_np(z))
+    _check_rows(y, ref, rows, f"C4 f={f} {form}")
+
+
+# ---------------------------------------------------------------------------
+# C0 and C2: the whole 124M model, logits against the fp32 oracle on the host
+# ---------------------------------------------------------------------------
+
+def test_c0_model_logits():
+    import bench
+    from nanogpt import model as model_mod
+    m, x, _ = bench.build_c0_model(DEV, torch.bfloat16)
+    with torch.inference_mode():
+        n0 = model_mod.fused_dispatch_count()
+        got = m.forward_all_positions(x).float().cpu()
+        assert model_mod.fused_dispatch_count() - n0 == 12
+    sd, ocfg, freeze = _oracle_inputs(m)
+    ref = model_oracle.gpt_forward(sd, ocfg, freeze, x.cpu(), path="split", all_positions=True)
+    c = _cos(got, ref)
+    assert c >= 0.9999, f"C0 logits cosine {c:.6f}"
+
+
+@pytest.mark.timeout(600)
+def test_c2_model_logits():
+    """The headline workload itself (bench.py's C2 model, T=16384): logits at
+    sampled positions and the last-position prefill output."""
+    import bench
+    m, x, plan = bench.build_c2_model(16384, DEV, torch.bfloat16)
+    assert sum(len(v) for v in plan.values()) == 36
+    T = x.size(1)
+    pos = np.unique(np.concatenate([[0, 1, 63, 64, 4095, 4096, T - 2], np.arange(1023, T, 1024),
+                                    np.random.default_rng(5).integers(0, T, 24)]))
+    with torch.inference_mode():
+        h = m.forward_hidden(x)
+        got = m.lm_head(h[:, torch.as_tensor(pos, device=DEV)]).float().cpu()
+        last = m(x).float().cpu()
+    del h
+    sd, ocfg, freeze = _oracle_inputs(m)
+    del m
+    torch.cuda.empty_cache()
+    ref = model_oracle.gpt_forward(sd, ocfg, freeze, x.cpu(), path="split",
+                                   positions=np.concatenate([pos, [T - 1]]))
+    c = _cos(got, ref[:, :-1])
+    cl = _cos(last, ref[:, -1:])
+    assert c >= 0.9999, f"C2 sampled-position logits cosine {c:.6f}"
+    assert cl >= 0.9999, f"C2 last-position logits cosine {cl:.6f}"

@@ -119,3 +119,32 @@ def test_scan_repeat_calls_agree():
         compare(y, ref, what="repeat call")
     for y in ys[1:]:
         assert (y.float() - ys[0].float()).abs().max().item() <= 2e-2
+
+
+def test_scan_give_up_is_loud():
+    """A look-back wait that gives up must never return a silently incomplete
+    sum.  The host-set drill (scan_spin_limit < 0) makes every chunk after the
+    first give up at once; every kernel still exits normally (the stream
+    synchronises), the call raises under validate=True, the rows of the
+    first chunk are still right and every later row is NaN.  A normal call
+    on the next workspace is exact again."""
+    K = _kernel()
+    B, H, T, hd = 2, 3, 4096, 64
+    (alpha, rho, z), cf, spec = _heads(H, T, 11)
+    v_cpu = torch.randn(B, H, T, hd, generator=torch.Generator().manual_seed(11)).bfloat16()
+    v = v_cpu.to(DEV)
+    frozen = torch.full((H,), 2, dtype=torch.int32, device=DEV)
+    qk = torch.empty(B, 0, T, hd, dtype=v.dtype, device=DEV)
+    bufs = dict(alpha=alpha.to(DEV), rho=rho.to(DEV), z=z.to(DEV), closed_form=cf)
+    with pytest.raises(RuntimeError, match="gave up"):
+        K.fused_mixed_attn(qk, qk, v, None, frozen, scan_spin_limit=-1, **bufs)
+    torch.cuda.synchronize()
+    y = K.fused_mixed_attn(qk, qk, v, None, frozen, scan_spin_limit=-1, validate=False, **bufs)
+    torch.cuda.synchronize()
+    ref = _oracle(v_cpu, spec)
+    ch = 256   # scan rows per chunk at hd 64
+    compare(y[:, :, :ch], ref[:, :, :ch], what="first chunk under the give-up drill")
+    assert torch.isnan(y[:, :, ch:].float()).all()
+    y2 = K.fused_mixed_attn(qk, qk, v, None, frozen, **bufs)
+    torch.cuda.synchronize()
+    compare(y2, ref, what="normal call after the drill")

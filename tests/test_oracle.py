@@ -276,3 +276,101 @@ def test_backward_oracle_matches_finite_differences():
             a[which] = xm
             num[idx] = (fp - loss(*a)) / (2 * eps)
         assert np.abs(num - g).max() < 1e-6, f"gradient {which}"
+
+
+# ---------------------------------------------------------------------------
+# frozen_pv (kernel/frozen_attn.py:185-192; the reference's own check is
+# torch.matmul(patt[fz, :T, :T], v), kernel/test_frozen_attn.py:27-28)
+# ---------------------------------------------------------------------------
+
+def _frozen_pv_loops(patt, v, fz_idx, T):
+    B, nf, _, hd = v.shape
+    out = np.zeros((B, nf, T, hd))
+    for b in range(B):
+        for f in range(nf):
+            h = int(fz_idx[f])
+            for i in range(T):
+                for d in range(hd):
+                    out[b, f, i, d] = sum(patt[h, i, j] * v[b, f, j, d] for j in range(T))
+    return out
+
+
+def test_frozen_pv_brute_force_non_identity_index():
+    """Non-identity fz_idx, pattern buffer S > T, V longer than T: loops,
+    and torch.matmul as the reference's own definition."""
+    B, nh, S, T, hd = 2, 6, 9, 7, 3
+    rng = np.random.default_rng(31)
+    patt = np.tril(rng.random((nh, S, S)))
+    patt /= patt.sum(-1, keepdims=True)
+    fz = np.array([5, 0, 3])
+    v = rng.standard_normal((B, 3, T + 2, hd))
+    got = orc.frozen_pv(patt, v, fz, T)
+    np.testing.assert_allclose(got, _frozen_pv_loops(patt, v, fz, T), atol=1e-12)
+    tm = torch.matmul(torch.from_numpy(patt)[torch.from_numpy(fz), :T, :T].unsqueeze(0),
+                      torch.from_numpy(v[:, :, :T]))
+    np.testing.assert_allclose(got, tm.numpy(), atol=1e-12)
+
+
+def test_frozen_pv_detects_a_wrong_index():
+    """A planted mistake (the identity map in place of fz_idx, or the
+    transposed pattern) must not pass the brute-force check."""
+    B, nh, S, T, hd = 1, 6, 8, 8, 2
+    rng = np.random.default_rng(32)
+    patt = np.tril(rng.random((nh, S, S)))
+    patt /= patt.sum(-1, keepdims=True)
+    fz = np.array([5, 0, 3])
+    v = rng.standard_normal((B, 3, T, hd))
+    ref = _frozen_pv_loops(patt, v, fz, T)
+    wrong_index = orc.frozen_pv(patt, v, np.arange(3), T)
+    wrong_transpose = orc.frozen_pv(np.swapaxes(patt, 1, 2), v, fz, T)
+    assert np.abs(wrong_index - ref).max() > 1e-3
+    assert np.abs(wrong_transpose - ref).max() > 1e-3
+
+
+# ---------------------------------------------------------------------------
+# eager_rows: sampled rows of the full eager output (parity at config sizes)
+# ---------------------------------------------------------------------------
+
+def test_sample_rows_cover_tile_edges():
+    rows = orc.sample_rows(1000, n_random=16, seed=3)
+    assert rows[0] == 0 and rows[-1] == 999 and (np.diff(rows) > 0).all()
+    for b in range(64, 1000, 64):
+        assert b - 1 in rows and b in rows
+    assert orc.sample_rows(1).tolist() == [0]
+
+
+@pytest.mark.parametrize("gqa", [False, True])
+def test_eager_rows_match_full_eager(gqa):
+    """Every head kind (live, dense with compact pidx, decomposed, closed-form
+    as decomposed) and the GQA map: the sampled rows equal the full eager
+    output's rows."""
+    B, H, T, hd, S = 2, 8, 150, 8, 160
+    rng = np.random.default_rng(40)
+    frozen = np.array([0, 1, 2, 0, 2, 1, 0, 2])
+    live = np.nonzero(frozen == 0)[0]
+    hidx = np.zeros(H, dtype=np.int32)
+    hidx[live] = np.arange(live.size)
+    pidx = np.zeros(H, dtype=np.int32)
+    pidx[[1, 5]] = [1, 0]
+    patt = np.tril(rng.random((2, S, S)))
+    patt /= patt.sum(-1, keepdims=True)
+    alpha = rng.standard_normal((H, S)) * 0.8
+    rho = rng.standard_normal((H, S)) * 0.8
+    alpha[7], rho[7] = orc.closed_form_params("window", 17, S)
+    z = orc.decomposed_logz(alpha, rho)
+    kvidx = None
+    q = rng.standard_normal((B, live.size, T, hd))
+    if gqa:
+        kvidx = (np.arange(H) // 4).astype(np.int32)
+        k = rng.standard_normal((B, 2, T, hd))
+        v = rng.standard_normal((B, 2, T, hd))
+    else:
+        k = rng.standard_normal((B, live.size, T, hd))
+        v = rng.standard_normal((B, H, T, hd))
+    full = orc.eager_mixed_attention(q, k, v, frozen, hidx, pidx, kvidx, patt=patt, alpha=alpha,
+                                     rho=rho, z=z)
+    rows = orc.sample_rows(T, n_random=20, seed=1)
+    prow = {h: patt[pidx[h]][rows] for h in range(H) if frozen[h] == 1}
+    got = orc.eager_rows(q, k, v, frozen, rows, hidx, pidx, kvidx, patt_rows=prow, alpha=alpha,
+                         rho=rho, z=z)
+    np.testing.assert_allclose(got, full[:, :, rows], atol=1e-12)
