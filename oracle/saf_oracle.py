@@ -228,11 +228,13 @@ def eager_mixed_attention(q, k, v, frozen, hidx=None, pidx=None, kvidx=None,
 def sample_rows(T, n_random=128, seed=0):
     """Query rows checked at a full-size shape: the first and last rows, both
     sides of every 64-row boundary (the tile edges of every kernel here), and
-    `n_random` seeded random rows; sorted, unique."""
+    `n_random` seeded random rows distinct from those; sorted, unique."""
     rng = np.random.default_rng(seed)
     b = np.arange(64, T, 64)
-    rows = np.concatenate([[0, 1, T - 2, T - 1], b - 1, b, rng.integers(0, T, n_random)])
-    return np.unique(np.clip(rows, 0, T - 1))
+    fixed = np.unique(np.clip(np.concatenate([[0, 1, T - 2, T - 1], b - 1, b]), 0, T - 1))
+    rest = np.setdiff1d(np.arange(T), fixed)
+    extra = rng.choice(rest, size=min(n_random, rest.size), replace=False)
+    return np.unique(np.concatenate([fixed, extra]))
 
 
 def eager_rows(q, k, v, frozen, rows, hidx=None, pidx=None, kvidx=None, patt_rows=None,
