@@ -107,6 +107,24 @@ typedef struct saf_mixed_attn_args {
 /* All head kinds: live flash, dense P.V, decomposed rebuild, closed-form scan. */
 int saf_mixed_attn_fwd(const saf_mixed_attn_args* args, void* stream);
 
+/* saf_mixed_attn_fwd without a caller workspace, for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid allocation).  No counterpart in the reference (its
+ * Triton launch needs no workspace).  args->workspace and workspace_bytes are
+ * ignored: the call uses a fixed 64 MiB device array of the library instead
+ * (one per GPU, held until the process ends) and calls no allocator.
+ *   - Calls whose closed-form heads need more than 64 MiB of look-back words
+ *     return SAF_EWORKSPACE before launching anything; the partials of the
+ *     causally balanced kernels are used only when they fit as well (else
+ *     those kernels run unsplit, with the same results).
+ *   - Every call on a GPU shares that GPU's array: calls that overlap on one
+ *     GPU (concurrent streams or threads) race and must be serialised by the
+ *     caller.  What must start at zero is cleared by a fill kernel on
+ *     `stream` at each call.
+ *   - A scan look-back that gives up cannot be read back through
+ *     saf_workspace_error here; its rows are NaN, as in saf_mixed_attn_fwd. */
+int saf_mixed_attn_fwd_noalloc(const saf_mixed_attn_args* args, void* stream);
+
 /* Subsets of saf_mixed_attn_fwd: each computes only its heads' rows of out. */
 int saf_flash_fwd(const saf_mixed_attn_args* args, void* stream);
 int saf_frozen_dense_pv_fwd(const saf_mixed_attn_args* args, void* stream);

@@ -12,6 +12,7 @@
 #include <cmath>
 #include <cstdarg>
 #include <cstdio>
+#include <mutex>
 #include <string>
 #include <vector>
 
@@ -978,6 +979,66 @@ int64_t saf_mixed_attn_workspace_bytes(const saf_mixed_attn_args* args) {
                                      decomp_resident(pl.HD)).part_bytes);
   total += part;
   return total;
+}
+
+}  // extern "C"
+
+// ---- allocation-free forward ------------------------------------------------
+// The workspace of saf_mixed_attn_fwd_noalloc: one fixed array per GPU that
+// the library runs on, held until the process ends.  In host code `scratch`
+// names a host-side stand-in, never a device address: its device address is
+// read once per device (with that device current) by hipGetSymbolAddress and
+// only that address is used.
+namespace {
+
+constexpr int64_t kScratchBytes = int64_t(64) << 20;
+static __device__ __align__(256) unsigned char scratch[kScratchBytes];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+// Device address of `scratch` on the current device (looked up on the first
+// call per device).
+int scratch_address(void** out) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return fail(SAF_ELAUNCH, "hipGetDevice failed: %s", hipGetErrorString(e));
+  if (dev < 0 || dev >= kMaxDevices) return fail(SAF_EUNSUPPORTED, "device %d beyond %d devices", dev, kMaxDevices);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || p == nullptr)
+      return fail(SAF_ELAUNCH, "hipGetSymbolAddress(scratch) failed on device %d: %s", dev, hipGetErrorString(e));
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return SAF_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int saf_mixed_attn_fwd_noalloc(const saf_mixed_attn_args* args, void* stream) {
+  Plan pl;
+  if (int rc = plan_and_validate(args, kDoAll, pl, false)) return rc;
+  // the scan's look-back words must fit; the partials of the causally
+  // balanced kernels are used when they fit too (else those kernels run
+  // unsplit, with the same results)
+  const int64_t need = scan_ws_bytes(pl);
+  if (need > kScratchBytes)
+    return fail(SAF_EWORKSPACE,
+                "saf_mixed_attn_fwd_noalloc: the closed-form heads need %lld bytes of scratch, above the "
+                "%lld-byte maximum (use saf_mixed_attn_fwd with a caller workspace)",
+                (long long)need, (long long)kScratchBytes);
+  const int64_t want = saf_mixed_attn_workspace_bytes(args);
+  if (want < 0) return fail(SAF_EINVAL, "invalid arguments");
+  saf_mixed_attn_args a = *args;
+  if (int rc = scratch_address(&a.workspace)) return rc;
+  a.workspace_bytes = std::min(want, kScratchBytes);
+  return run(&a, kDoAll, stream);
 }
 
 int64_t saf_workspace_bytes(int32_t B, int32_t T, int32_t head_dim, int32_t n_scan_heads) {

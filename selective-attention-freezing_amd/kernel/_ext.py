@@ -20,7 +20,7 @@ _DTYPE_CODE = {torch.float32: SAF_F32, torch.float16: SAF_F16,
                torch.bfloat16: SAF_BF16, torch.int32: SAF_I32}
 
 # Exported symbols, in header order (checked by the CPU test suite).
-EXPORTS = ("saf_mixed_attn_fwd", "saf_flash_fwd", "saf_frozen_dense_pv_fwd",
+EXPORTS = ("saf_mixed_attn_fwd", "saf_mixed_attn_fwd_noalloc", "saf_flash_fwd", "saf_frozen_dense_pv_fwd",
            "saf_frozen_decomp_fwd", "saf_frozen_scan_fwd", "saf_mixed_attn_bwd",
            "saf_mixed_attn_bwd_workspace_bytes", "saf_frozen_pv_fwd", "saf_frozen_pv_bwd",
            "saf_rope_qk_inplace", "saf_qk_rmsnorm_rope_inplace", "saf_add_layernorm",
@@ -71,7 +71,7 @@ def lib():
                 "operators have no non-HIP fallback")
         L = ctypes.CDLL(LIB_PATH)
         P = ctypes.POINTER
-        for name in ("saf_mixed_attn_fwd", "saf_flash_fwd", "saf_frozen_dense_pv_fwd",
+        for name in ("saf_mixed_attn_fwd", "saf_mixed_attn_fwd_noalloc", "saf_flash_fwd", "saf_frozen_dense_pv_fwd",
                      "saf_frozen_decomp_fwd", "saf_frozen_scan_fwd"):
             fn = getattr(L, name)
             fn.argtypes = [P(SafMixedAttnArgs), ctypes.c_void_p]
