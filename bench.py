@@ -136,19 +136,13 @@ def live_flops(plan, n_layer, n_head, B, T, hd):
     return n_live * B * 4 * hd * T * (T + 1) // 2, n_live, n_frozen
 
 
-def cpu_baseline(model, x, plan, T, max_layers=2):
-    """Oracle restatement of the reference's CPU split path (fp32) on a bounded
-    sample: `max_layers` of the model's layers at the full C2 shape plus the
-    embedding / final norm / head, extrapolated linearly to all layers."""
-    import torch
-    from oracle import model_oracle
-
-    threads = len(os.sched_getaffinity(0))
-    torch.set_num_threads(threads)
+def _oracle_inputs(model):
+    """State dict (fp32 copy of the model's own weights) and per-layer freeze
+    records of a GPT, in the oracle's input format."""
     cfg = model.config
     sd = {k: v.detach().float().cpu() for k, v in model.state_dict().items()}
     freeze = []
-    for layer, blk in enumerate(model.transformer.h):
+    for blk in model.transformer.h:
         a = blk.attn
         rec = {"frozen": a.dyn_frozen.cpu().tolist(), "patterns": {}, "decomp": {}}
         for h in range(cfg.n_head):
@@ -157,22 +151,83 @@ def cpu_baseline(model, x, plan, T, max_layers=2):
         freeze.append(rec)
     ocfg = {"n_layer": cfg.n_layer, "n_head": cfg.n_head, "n_embd": cfg.n_embd,
             "position_encoding": "rope", "rope_base": cfg.rope_base}
-    idx = x.cpu()
-    layers = list(range(min(max_layers, cfg.n_layer)))
+    return sd, ocfg, freeze
+
+
+def cpu_model_name():
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def cpu_baseline(c2_model, c2_x, T, c2_layers=1, iters=5):
+    """The reference's CPU path (the oracle's restatement of its split
+    fallback, fp32 torch on this host's cores) at BASELINE configs[0], C0:
+    the full 12-layer 124M forward at B=1, T=1024 with 3 causal-mean heads
+    per layer, 1 warmup and `iters` timed forwards, median.  The same C0
+    model runs on the GPU in bf16 beside it (prefill tokens/s at the same
+    shape, and its last-position logits against the CPU forward's).  A
+    secondary figure extrapolates `c2_layers` layers of the C2 model at its
+    full shape to all 12 layers."""
+    import torch
+    from oracle import model_oracle
+
+    threads = len(os.sched_getaffinity(0))
+    torch.set_num_threads(threads)
+    m0, x0, _ = build_c0_model("cuda", torch.bfloat16)
+    with torch.inference_mode():
+        for _ in range(3):
+            m0(x0)
+        torch.cuda.synchronize()
+        ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(20)]
+        for a, b in ev:
+            a.record()
+            gpu_last = m0(x0)
+            b.record()
+        torch.cuda.synchronize()
+    gpu_ms = statistics.median(a.elapsed_time(b) for a, b in ev)
+    sd, ocfg, freeze = _oracle_inputs(m0)
+    idx = x0.cpu()
+    del m0
     times = []
-    for it in range(2):
+    for it in range(iters + 1):
         t0 = time.perf_counter()
-        model_oracle.gpt_forward(sd, ocfg, freeze, idx, path="split", layers=layers)
-        times.append(time.perf_counter() - t0)
-        log(f"cpu baseline sample {it}: {times[-1]:.2f} s on {threads} threads")
-    t_sample = min(times)
-    t_full = t_sample * cfg.n_layer / len(layers)
-    tok_s = idx.numel() / t_full
-    return {"value": round(tok_s, 3), "unit": "tokens/s", "cores": threads, "kind": "port",
-            "sample": (f"oracle split-path forward (fp32, torch CPU) of {len(layers)} of "
-                       f"{cfg.n_layer} C2 layers at B=1 T={T} plus embedding/head, best of 2, "
-                       f"extrapolated linearly to {cfg.n_layer} layers "
-                       f"({t_sample:.2f} s per sample)")}
+        ref = model_oracle.gpt_forward(sd, ocfg, freeze, idx, path="split")
+        dt = time.perf_counter() - t0
+        if it:
+            times.append(dt)
+        log(f"cpu baseline C0 forward {it}: {dt:.3f} s on {threads} threads" + ("" if it else " (warmup)"))
+    t_med = statistics.median(times)
+    a = gpu_last.float().cpu().double().flatten()
+    b = ref.double().flatten()
+    cos = float(a @ b / (a.norm() * b.norm()))
+    tokens = idx.numel()
+    out = {"value": round(tokens / t_med, 1), "unit": "tokens/s", "cores": threads, "kind": "port",
+           "sample": (f"C0 (BASELINE configs[0]): the full 12-layer 124M forward to last-position logits, "
+                      f"B=1, T={tokens}, 3 causal-mean heads per layer, oracle split path (the reference's "
+                      f"CPU fallback) in fp32 torch; 1 warmup + {iters} timed, median {t_med:.3f} s"),
+           "cpu_model": cpu_model_name(), "torch_threads": torch.get_num_threads(),
+           "gpu_same_shape": {"value": round(tokens / (gpu_ms / 1000.0), 1), "unit": "tokens/s",
+                              "ms_per_forward": round(gpu_ms, 3), "dtype": "bf16",
+                              "logits_cosine_vs_cpu": round(cos, 7)}}
+    if c2_layers:
+        sd2, ocfg2, freeze2 = _oracle_inputs(c2_model)
+        idx2 = c2_x.cpu()
+        layers = list(range(min(c2_layers, ocfg2["n_layer"])))
+        t0 = time.perf_counter()
+        model_oracle.gpt_forward(sd2, ocfg2, freeze2, idx2, path="split", layers=layers)
+        dt = time.perf_counter() - t0
+        t_full = dt * ocfg2["n_layer"] / len(layers)
+        out["c2_extrapolated"] = {
+            "value": round(idx2.numel() / t_full, 2), "unit": "tokens/s",
+            "sample": (f"{len(layers)} of {ocfg2['n_layer']} C2 layers at B=1 T={T} plus embedding/head "
+                       f"({dt:.2f} s), scaled linearly to all layers")}
+        log(f"cpu baseline C2 sample: {dt:.2f} s for {len(layers)} layer(s)")
+    return out
 
 
 def c4_cpu_baseline(model, sd, masks, B, T, max_layers=1):
@@ -263,6 +318,30 @@ def kernel_rooflines(summ, flash_label, traffic, steps):
     return roof, extra
 
 
+C2_FIXTURE = os.path.join(REPO, "tests", "golden", "c2_last_logits.npz")
+
+
+def c2_check(model, x):
+    """Cosine of the GPU prefill output (last-position logits) against the
+    fp32 oracle's logits for the same C2 model and tokens, computed on the
+    host and stored by tests/golden/make_c2_fixture.py; None if the fixture
+    is absent or was made for another shape."""
+    import hashlib
+    import torch
+    if not os.path.exists(C2_FIXTURE):
+        return None
+    z = np.load(C2_FIXTURE)
+    tok = hashlib.sha256(x.cpu().numpy().astype(np.int64).tobytes()).hexdigest()
+    if str(z["tokens_sha256"]) != tok:
+        return None
+    with torch.inference_mode():
+        got = model(x)[0, -1].double().cpu()
+    ref = torch.from_numpy(z["logits"]).double()
+    cos = float(got @ ref / (got.norm() * ref.norm()))
+    return {"logits_cosine_vs_fp32_oracle": round(cos, 7), "pass": cos >= 0.9999, "bound": 0.9999,
+            "reference": os.path.relpath(C2_FIXTURE, REPO)}
+
+
 def run_c2(args):
     import torch
     from nanogpt import model as model_mod
@@ -271,7 +350,7 @@ def run_c2(args):
     T = args.seq_len or 16384
     log(f"building C2 model T={T} layers={args.layers}")
     model, x, plan = build_c2_model(T, dev, torch.bfloat16, n_layer=args.layers)
-    log("model built; verifying dispatch")
+    log("model built; verifying dispatch and output")
     cfg = model.config
     hd = cfg.n_embd // cfg.n_head
     flops, n_live, n_frozen = live_flops(plan, cfg.n_layer, cfg.n_head, 1, T, hd)
@@ -283,6 +362,12 @@ def run_c2(args):
         calls = model_mod.fused_dispatch_count() - before
         if calls != cfg.n_layer:
             raise RuntimeError(f"dispatch verification failed: {calls} != {cfg.n_layer}")
+    check = c2_check(model, x) if cfg.n_layer == 12 else None
+    if check is not None:
+        log(f"C2 logits cosine vs the fp32 oracle: {check['logits_cosine_vs_fp32_oracle']:.7f}")
+        if not check["pass"]:
+            log("WARNING: the C2 prefill output fails the logits bound")
+    with torch.inference_mode():
         step_ms, wall, summ = timed_steps(lambda: model(x), args.steps, args.warmup, not args.no_timer)
 
     total_ms = sum(step_ms)
@@ -290,9 +375,23 @@ def run_c2(args):
     label = "flash_fwd_kernel<bf16,64,1>"
     roof, extra = kernel_rooflines(summ, label, pmc_traffic(label) if T == 16384 else None, args.steps)
     log(f"GPU: {tok_s:.0f} tokens/s, {total_ms / args.steps:.2f} ms/step")
+    if "frozen_scan" in extra:
+        # in the model the scan shares the GPU with the flash kernel (side
+        # stream): its event span is not an HBM fraction
+        sc = extra.pop("frozen_scan")
+        extra["frozen_scan_in_model"] = {
+            "launches": sc["launches"], "avg_span_ms": sc["avg_launch_ms"],
+            "bytes_per_launch": sc["bytes_per_launch"],
+            "note": "runs on a side stream overlapped with the live-head kernel; span, not HBM time"}
+    frozen_roof = None
+    if not args.no_sizing_scan:
+        _, frozen_roof, _, _ = sizing_scan(8, 16384, max(args.steps, 10), 3)
+        frozen_roof["workload"] = ("frozen-only sizing run B=8, H=12 closed-form heads, T=16384, hd 64 "
+                                   "(403 MB per launch), timed in this process")
+        log(f"frozen sizing scan: {frozen_roof['achieved']:.0f} GB/s = {frozen_roof['frac']:.3f} of HBM")
     cpu = None
     if not args.no_cpu_baseline:
-        cpu = cpu_baseline(model, x, plan, T, max_layers=args.cpu_layers)
+        cpu = cpu_baseline(model, x, T, c2_layers=args.cpu_layers)
 
     line = {
         "metric": METRIC, "value": round(tok_s, 1), "unit": "tokens/s", "n_gpus": 1,
@@ -306,6 +405,8 @@ def run_c2(args):
                    "median_step_ms": round(statistics.median(step_ms), 3),
                    "wall_s": round(wall, 3)},
         "roofline": roof,
+        "frozen_roofline": frozen_roof,
+        "check": check,
         "cpu_baseline": cpu,
     }
     line.update(extra)
@@ -643,18 +744,18 @@ def run_bwd(args):
     print(json.dumps(line), flush=True)
 
 
-def run_scan(args):
-    """Frozen-only sizing run of the closed-form scan (the HBM-bound frozen-head
-    kernel): every head of B=8, H=12, T=16384, hd=64 bf16 frozen to a seeded
-    mix of causal mean, exponential decay (rate ~U(0.001, 0.1)) and sliding
-    window (w ~U{64..1024}), i.e. 96 sequences of V read once and Y written
-    once (403 MB).  One step = one fused_mixed_attn call (the scan and its
-    workspace clear)."""
+def sizing_scan(B, T, steps, warmup):
+    """The frozen-only sizing run of the closed-form scan (the HBM-bound
+    frozen-head kernel): every head of (B, H=12, T, hd=64) bf16 frozen to a
+    seeded mix of causal mean, exponential decay (rate ~U(0.001, 0.1)) and
+    sliding window (w ~U{64..1024}); at B=8, T=16384 that is 96 sequences of
+    V read once and Y written once (403 MB).  One step = one
+    fused_mixed_attn call (the scan and its workspace clear).  Returns the
+    step times, the scan kernel's roofline (HIP events right around the
+    kernel) and the head kinds / parameters."""
     import torch
     import kernel
 
-    B = args.batch or 8
-    T = args.seq_len or 16384
     H, hd = 12, 64
     g = torch.Generator().manual_seed(1337)
     v = torch.randn(B, H, T, hd, generator=g).bfloat16().cuda()
@@ -672,13 +773,22 @@ def run_scan(args):
     step = lambda: kernel.fused_mixed_attn(None, None, v, None, frozen, closed_form=(kind, param),
                                            validate=False)
     with torch.inference_mode():
-        step_ms, wall, summ = timed_steps(step, args.steps, args.warmup, True)
-    _, extra = kernel_rooflines(summ, None, None, args.steps)
+        step_ms, wall, summ = timed_steps(step, steps, warmup, True)
+    _, extra = kernel_rooflines(summ, None, None, steps)
     scan = extra["frozen_scan"]
     if (B, T) == (8, 16384):
         scan["traffic"] = pmc_traffic("scan_kernel<bf16,64>", SCAN_TRAFFIC_FILE)
         scan["traffic_source"] = os.path.relpath(SCAN_TRAFFIC_FILE, REPO)
     scan["kernel"] = "scan_kernel<bf16,64>"
+    del v
+    return step_ms, scan, kind, param
+
+
+def run_scan(args):
+    """The frozen-only sizing run alone (see sizing_scan)."""
+    B = args.batch or 8
+    T = args.seq_len or 16384
+    step_ms, scan, kind, param = sizing_scan(B, T, args.steps, args.warmup)
     nbytes = scan["bytes_per_launch"]
     total_ms = sum(step_ms)
     line = {
@@ -687,8 +797,8 @@ def run_scan(args):
         "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(total_ms / args.steps, 4),
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
         "data": "synthetic (V ~ N(0, 1), seed 1337)",
-        "config": {"workload": f"frozen-only sizing run: B={B}, H={H} all frozen (mean/decay/window), T={T}, "
-                               f"hd={hd}; V read once + Y written once = {nbytes} bytes per step",
+        "config": {"workload": f"frozen-only sizing run: B={B}, H=12 all frozen (mean/decay/window), T={T}, "
+                               f"hd=64; V read once + Y written once = {nbytes} bytes per step",
                    "kinds": [int(k) for k in kind], "params": [float(x) for x in param]},
         "roofline": scan,
         "cpu_baseline": None,
@@ -779,6 +889,8 @@ def main():
     ap.add_argument("--sdpa-live", action="store_true",
                     help="c4 at rate 0: leave the model unconverted (torch SDPA) instead of the HIP flash path")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-sizing-scan", action="store_true",
+                    help="c2: skip the in-process frozen-only sizing scan (frozen_roofline)")
     ap.add_argument("--cpu-layers", type=int, default=None)
     ap.add_argument("--no-timer", action="store_true", help="skip per-kernel HIP events")
     ap.add_argument("--copy-calibration-mib", type=int, default=0,
@@ -824,7 +936,7 @@ def main():
         if args.layers is None:
             args.layers = 12
         if args.cpu_layers is None:
-            args.cpu_layers = 2
+            args.cpu_layers = 1
         run_c2(args)
 
 

@@ -114,18 +114,28 @@ struct FlashState {
     for (int dt = 0; dt < NDT; ++dt) voff[dt] = vt_read_offset<HD>(lane, dt);
   }
 
-  // S^T of sub-block ks (0/1) of the K tile: s[qt] = K_sub . Q^T
-  __device__ __forceinline__ void scores(f32x16_t (&s)[QT], const char* ktile, int ks) const {
-    uint4 ka[NKT];
+  // K A operands of sub-block ks (0/1) of a K tile
+  __device__ __forceinline__ void load_ka(uint4 (&ka)[NKT], const char* ktile, int ks) const {
 #pragma unroll
     for (int t = 0; t < NKT; ++t)
       ka[t] = *reinterpret_cast<const uint4*>(ktile + ks * 32 * KCHP * 16 + koff[t]);
+  }
+
+  // S^T of one 32-key sub-block from its K A operands: s[qt] = K_sub . Q^T
+  __device__ __forceinline__ void scores_from(f32x16_t (&s)[QT], const uint4 (&ka)[NKT]) const {
 #pragma unroll
     for (int qt = 0; qt < QT; ++qt) s[qt] = zero16();
 #pragma unroll
     for (int t = 0; t < NKT; ++t)
 #pragma unroll
       for (int qt = 0; qt < QT; ++qt) s[qt] = Elem<T>::mfma(ka[t], qf[qt][t], s[qt]);
+  }
+
+  // S^T of sub-block ks (0/1) of the K tile
+  __device__ __forceinline__ void scores(f32x16_t (&s)[QT], const char* ktile, int ks) const {
+    uint4 ka[NKT];
+    load_ka(ka, ktile, ks);
+    scores_from(s, ka);
   }
 
   // O^T += V_sub^T . P^T for sub-block ks of the V tile; P^T (packed) sits in
@@ -207,12 +217,21 @@ struct FlashState {
     exp_pack(s, bs);
   }
 
-  // One pipeline step u.  On entry `nxt` holds P_{u-1} (packed) and `cur`
-  // holds S_u.  O += P_{u-1} V (tile vP, sub-block ksP) is issued first, then
-  // S_{u+1} overwrites `nxt` (tile kS, sub-block ksS), and the softmax of
-  // S_u packs P_u into `cur` (tile kR / sub-block ksR for the rare recompute).
-  __device__ __forceinline__ void step(f32x16_t (&cur)[QT], f32x16_t (&nxt)[QT], int u, bool masked, const char* kS,
-                                       int ksS, const char* kR, int ksR, const char* vP, int ksP) {
+  // K A operands of the next step's S product are read a whole step ahead
+  // (kpre) up to hd 64; above, the 32 more VGPRs would spill, and each step
+  // reads its own
+  static constexpr bool kPrefetchK = HD <= 64;
+
+  // One pipeline step u.  On entry `nxt` holds P_{u-1} (packed), `cur`
+  // holds S_u and, with kPrefetchK, `kpre` the K A operands of S_{u+1}.
+  // O += P_{u-1} V (tile vP, sub-block ksP) is issued first, then S_{u+1}
+  // (tile kS, sub-block ksS) overwrites `nxt` (from `kpre`, whose next
+  // contents, the operands of S_{u+2} in tile kN / sub-block ksN, are read
+  // right after), and the softmax of S_u packs P_u into `cur` (tile kR /
+  // sub-block ksR for the rare recompute).
+  __device__ __forceinline__ void step(f32x16_t (&cur)[QT], f32x16_t (&nxt)[QT], uint4 (&kpre)[NKT], int u,
+                                       bool masked, const char* kS, int ksS, const char* kN, int ksN,
+                                       const char* kR, int ksR, const char* vP, int ksP) {
     // the mask touches only S_u, complete before the step: applying it first
     // keeps the MFMAs and the softmax below in one basic block.  The empty
     // volatile asm keeps the (uniform) branch a real scalar branch, so the
@@ -223,7 +242,12 @@ struct FlashState {
       mask(cur, 32 * u);
     }
     pv(nxt, vP, ksP);
-    scores(nxt, kS, ksS);
+    if constexpr (kPrefetchK) {
+      scores_from(nxt, kpre);
+      load_ka(kpre, kN, ksN);
+    } else {
+      scores(nxt, kS, ksS);
+    }
     float bs[QT];
     exp_pack(cur, bs);
     bool bad = false;
@@ -319,6 +343,8 @@ __device__ __forceinline__ void flash_unit(Params& p, const int unit, char* k0, 
 #pragma unroll
   for (int qt = 0; qt < QT; ++qt) sB[qt] = zero16();
   st.scores(sA, k0, 0);
+  uint4 kpre[NKT];  // K operands of the next S product, read one step ahead
+  if constexpr (St::kPrefetchK) st.load_ka(kpre, k0, 1);
 
   // block j in phase R (slots: K_j = R, K_{j+1} = R+1, K_{j+2} = R+2 (loading),
   // V_{j-1} = R+2, V_j = R, V_{j+1} = R+1 (loading), all mod 3); blocks at
@@ -336,10 +362,13 @@ __device__ __forceinline__ void flash_unit(Params& p, const int unit, char* k0, 
     if (j + 2 < nkb) dma.load_k(kbase, p.k_st, 64 * (j + 2), T_len, kJ2, wave);
     if (j + 1 < nkb) dma.load_v(vbase, p.v_st, 64 * (j + 1), T_len, vJ1, wave);
     const bool masked = j >= jd;
-    // u = 2j: S_{2j+1} from K_j sub 1, P_{2j-1} V_{j-1} sub 1, softmax S_{2j}
-    st.step(sA, sB, 2 * j, masked, kJ, 1, kJ, 0, vJm, 1);
-    // u = 2j+1: S_{2j+2} from K_{j+1} sub 0, P_{2j} V_j sub 0, softmax S_{2j+1}
-    st.step(sB, sA, 2 * j + 1, masked, kJ1, 0, kJ, 1, vJ, 0);
+    // u = 2j: S_{2j+1} (K_j sub 1), operands of S_{2j+2} (K_{j+1} sub 0),
+    // P_{2j-1} V_{j-1} sub 1, softmax S_{2j}
+    st.step(sA, sB, kpre, 2 * j, masked, kJ, 1, kJ1, 0, kJ, 0, vJm, 1);
+    // u = 2j+1: S_{2j+2} (K_{j+1} sub 0), operands of S_{2j+3} (K_{j+1}
+    // sub 1), P_{2j} V_j sub 0, softmax S_{2j+1}.  Past the last block these
+    // read a stale slot whose products are never used.
+    st.step(sB, sA, kpre, 2 * j + 1, masked, kJ1, 0, kJ1, 1, kJ, 1, vJ, 0);
     __syncthreads();  // waits for this block's DMA (vmcnt 0) before any wave moves on
   };
   using P0 = std::integral_constant<int, 0>;
