@@ -19,6 +19,17 @@ restates, without importing any model class:
   (:128-140, :187-194).
 Pinned by tests/golden/qwen_forward_small.npz, written by the reference's own
 adapter on CPU (tests/golden/make_golden_qwen.py).
+
+qwen35_attention restates one Qwen3.5 gated attention layer with frozen
+query heads (the reference's Qwen3.5 adapter,
+/root/reference/qwen/nanogpt/hybrid_prior_attention.py:205-470, over
+transformers' Qwen3_5Attention): q_proj emits (query, gate) per head, q/k
+RMSNorm with (1 + w) weights in fp32, RoPE on the first rotary_dim features
+only, live heads as causal softmax attention, frozen heads as P @ V of their
+KV group, every head's output times sigmoid(gate), then o_proj.  Pinned in
+tests/test_qwen.py against transformers' own module with no head frozen and
+by the invariant that a frozen head whose prior is its own softmax matrix
+changes nothing.
 """
 import math
 
@@ -108,3 +119,45 @@ def qwen_forward(sd, cfg, freeze, idx, layers=None):
         m = F.silu(F.linear(h, sd[p + "mlp.gate_proj.weight"])) * F.linear(h, sd[p + "mlp.up_proj.weight"])
         x = x + F.linear(m, sd[p + "mlp.down_proj.weight"])
     return rms_norm(x, sd["model.norm.weight"], cfg["eps"])
+
+
+def rms_norm_offset(x, w, eps):
+    """Qwen3.5 RMSNorm: x / rms(x) * (1 + w) in fp32."""
+    x = x.float()
+    return (x * torch.rsqrt(x.pow(2).mean(-1, keepdim=True) + eps)) * (1.0 + w.float())
+
+
+def apply_partial_rope(x, cos, sin):
+    """Half rotation on the first cos.shape[-1] features, the rest passed through."""
+    r = cos.shape[-1]
+    return torch.cat([apply_rope(x[..., :r], cos, sin), x[..., r:]], dim=-1)
+
+
+def qwen35_attention(x, sd, p, cfg, fr, cos, sin, return_probs=False):
+    """One Qwen3.5 gated attention layer (B, T, hidden) -> (B, T, hidden),
+    fp32.  sd: state dict with the layer's q_proj / k_proj / v_proj / o_proj
+    and q_norm / k_norm weights under prefix p; cfg: n_heads, n_kv_heads,
+    head_dim, eps; fr: None or {"mask": (H,) bool, "dense"/"alpha"+"rho"} as
+    for frozen_patterns; cos / sin: (T, rotary_dim)."""
+    B, T, _ = x.shape
+    H, HKV, hd, eps = cfg["n_heads"], cfg["n_kv_heads"], cfg["head_dim"], cfg["eps"]
+    lin = lambda name, t: F.linear(t, sd[p + name + ".weight"], sd.get(p + name + ".bias"))
+    qg = lin("q_proj", x.float()).view(B, T, H, 2 * hd)
+    q, gate = qg[..., :hd], qg[..., hd:]
+    q = rms_norm_offset(q, sd[p + "q_norm.weight"], eps).transpose(1, 2)
+    k = rms_norm_offset(lin("k_proj", x.float()).view(B, T, HKV, hd), sd[p + "k_norm.weight"], eps).transpose(1, 2)
+    v = lin("v_proj", x.float()).view(B, T, HKV, hd).transpose(1, 2)
+    q, k = apply_partial_rope(q, cos, sin), apply_partial_rope(k, cos, sin)
+    g = H // HKV
+    k = k.repeat_interleave(g, dim=1)
+    v = v.repeat_interleave(g, dim=1)
+    att = (q @ k.transpose(-2, -1)) * (1.0 / math.sqrt(hd))
+    causal = torch.tril(torch.ones(T, T, dtype=torch.bool))
+    att = att.masked_fill(~causal, float("-inf")).softmax(-1)
+    probs = att.clone()
+    if fr is not None and bool(np.any(fr["mask"])):
+        heads = [h for h in range(H) if fr["mask"][h]]
+        att[:, heads] = frozen_patterns(fr, T).unsqueeze(0).expand(B, -1, -1, -1)
+    y = (att @ v).transpose(1, 2) * torch.sigmoid(gate)
+    out = lin("o_proj", y.reshape(B, T, H * hd))
+    return (out, probs) if return_probs else out

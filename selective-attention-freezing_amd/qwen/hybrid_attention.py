@@ -1,46 +1,58 @@
-"""Hybrid (live + frozen head) attention for Hugging Face Qwen3 models.
+"""Live + frozen head attention for Hugging Face Qwen3 and Qwen3.5 models.
 
-The GQA caller of the mixed-head prefill path.  It keeps the API of
-/root/reference/qwen/nanogpt/hybrid_prior_attention.py:
-  HybridAttentionBase._hybrid_init (:74-171)   shrunken q_proj, prior buffers,
-                                               head routing tables
-  make_qwen3_hybrid_class (:477-642)           the Qwen3 forward: fused branch
-                                               (:530-584), split fallback (:586-640)
-  get_hybrid_class_for / convert_targets_to_hybrid / restore_originals (:645-729)
-and the target discovery of /root/reference/qwen/nanogpt/test_prior_pretrained.py
-(:181-240).  ``use_triton`` keeps the reference's keyword; here it selects the
-fused HIP path (libsafattn.so), which is the only fused path this build has.
+The GQA caller of the mixed-head prefill path.  Entry points keep the names
+and signatures of the reference adapter
+(/root/reference/qwen/nanogpt/hybrid_prior_attention.py): the hybrid classes
+(``make_qwen3_hybrid_class`` :477-642, ``make_qwen35_hybrid_class``
+:205-470), ``get_hybrid_class_for`` (:659-665), ``convert_targets_to_hybrid``
+(:671-722), ``restore_originals`` (:725-729), the module-global
+``fused_mixed_attn`` (the reference's bench wraps it, bench_qwen_prefill_triton.py:136-138)
+and the per-module ``hybrid_calls`` / ``triton_calls`` counters it reads
+(:169-170); plus the target discovery of
+/root/reference/qwen/nanogpt/test_prior_pretrained.py:181-240.  The layer's
+function is the reference's: query heads in ``head_mask`` skip their query
+projection and QK^T and apply a fixed causal prior to their KV group's V;
+the others are causal softmax heads; Qwen3.5's per-head sigmoid gate
+multiplies every head's output.
 
-Differences that follow from the MI355X design (fused branch, no grad):
-  * one projection GEMM for [Wq of the live heads; Wk; Wv] (weights gathered
-    once per weight version), instead of three;
-  * q_norm / k_norm and the rotary embedding of live q and raw k run as one
-    in-place HIP kernel (``qk_rmsnorm_rope_``) on the projection output;
-  * decomposed priors keep alpha, rho and z in fp32 (as the reference) and are
-    classified once at conversion: causal mean, exponential decay and sliding
-    window heads run the closed-form scan kernel; the (H, 64, S) rho band is
-    not materialised (the HIP rebuild kernel reads rho directly);
-  * the attention output is allocated T-major, so the head merge before o_proj
-    is a view.
-With gradients enabled the fused branch keeps torch's q/k norm and RoPE (the
-operators have no backward, as the reference's GQA kernel).  The Qwen3.5
-gated-attention family is not covered.
+Design of this build:
+  * ``FamilySpec`` describes a model family: where its attention class lives,
+    whether q_proj emits a (query, gate) pair per head, and whether this
+    build's fused q/k RMSNorm + RoPE kernel matches the family's prologue
+    (Qwen3: yes; Qwen3.5 with its (1 + w) norm and partial rotation: its own
+    modules run instead).
+  * ``HeadRouting`` holds one layer's routing and prior: live and frozen head
+    lists, the operator's device tables (head state, live slot, prior slot,
+    KV head) and the frozen heads' prior (compact dense rows, or fp32
+    alpha / rho / z with their closed-form classification).
+  * ``HybridAttentionBase`` is one nn.Module for every family: it adopts the
+    original's k / v / o projections and norms, keeps the live heads' query
+    rows (and every head's gate rows) as its own projection, and, on the fused
+    no-grad path, runs ONE gathered GEMM [Wq(live); Wk; Wv; Wgate] whose
+    output feeds the operator as strided views; the attention output comes
+    back T-major, so the head merge before o_proj is a view.
+  * The split path (gradients, attention masks, caches, sliding windows, CPU
+    tensors) computes the same function in torch: SDPA (or an eager softmax)
+    for the live heads over their KV group, P @ V for the frozen heads.
 """
 from __future__ import annotations
 
 import importlib
 from dataclasses import dataclass
-from typing import List, Optional, Type
+from typing import Dict, List, Optional, Type
 
 import torch
 import torch.nn as nn
 import torch.nn.functional as F
 
 import kernel as _kernel_mod
-from kernel import fused_attn_usable, classify_closed_form  # noqa: F401
-from kernel.fused_attn import decomposed_logz, decomp_logits
+from kernel import classify_closed_form, fused_attn_usable
+from kernel.fused_attn import decomp_logits, decomposed_logz
 
 _FUSED_DISPATCH_COUNT = 0
+
+# head dims the HIP operator runs (include/saf_attn.h)
+_FUSED_HEAD_DIMS = (32, 64, 96, 128)
 
 
 def fused_dispatch_count():
@@ -49,303 +61,309 @@ def fused_dispatch_count():
 
 
 def fused_mixed_attn(*args, **kwargs):
-    """Module-global hook (looked up at call time, like the reference's
-    import of ``fused_mixed_attn`` into the adapter module) so harnesses can
-    wrap or count the operator calls."""
+    """Module-global hook, looked up at call time (harnesses wrap or count it)."""
     return _kernel_mod.fused_mixed_attn(*args, **kwargs)
 
 
-class HybridAttentionBase:
-    """Shrunken q_proj, frozen-prior buffers and head routing shared by the
-    hybrid attention classes (hybrid_prior_attention.py:60-198)."""
+@dataclass(frozen=True)
+class FamilySpec:
+    class_name: str        # transformers attention class
+    module: str            # where it lives
+    gated: bool            # q_proj rows per head: query (hd), then gate (hd)
+    hip_prologue: bool     # the family's q/k norm + RoPE is saf_qk_rmsnorm_rope_inplace's
 
+
+QWEN3 = FamilySpec("Qwen3Attention", "transformers.models.qwen3.modeling_qwen3", gated=False, hip_prologue=True)
+QWEN35 = FamilySpec("Qwen3_5Attention", "transformers.models.qwen3_5.modeling_qwen3_5", gated=True,
+                    hip_prologue=False)
+FAMILIES: Dict[str, FamilySpec] = {f.class_name: f for f in (QWEN3, QWEN35)}
+
+
+class HeadRouting:
+    """One layer's split of query heads into live and frozen, the operator's
+    routing tables and the frozen heads' prior.
+
+    head_mask (H,) bool: True = frozen.  The prior is ``pattern`` ((H, T, T)
+    dense rows, those of live heads unused) or ``decomp`` = (alpha, rho),
+    (H, S) logit vectors of softmax(alpha[j] + rho[i - j])."""
+
+    def __init__(self, head_mask, n_kv_heads, device, dtype, pattern=None, decomp=None):
+        mask = torch.as_tensor(head_mask).to(torch.bool).cpu().reshape(-1)
+        H = mask.numel()
+        if H % n_kv_heads:
+            raise ValueError(f"{H} query heads do not split into {n_kv_heads} KV groups")
+        self.n_heads = H
+        self.frozen = mask.nonzero().flatten().tolist()
+        self.live = (~mask).nonzero().flatten().tolist()
+        self.decomposed = decomp is not None
+        group = H // n_kv_heads
+        kv = torch.arange(H) // group
+        live_slot = torch.zeros(H, dtype=torch.int32)
+        live_slot[self.live] = torch.arange(len(self.live), dtype=torch.int32)
+        prior_slot = torch.zeros(H, dtype=torch.int32)
+        prior_slot[self.frozen] = torch.arange(len(self.frozen), dtype=torch.int32)
+        state = mask.to(torch.int32) * (2 if self.decomposed else 1)
+        # the operator's int32 device tables (state 0 / 1 / 2, hidx, pidx, kvidx)
+        self.state = state.to(device)
+        self.live_slot = live_slot.to(device)
+        self.prior_slot = prior_slot.to(device)
+        self.kv_head = kv.to(torch.int32).to(device)
+        self.live_kv = kv[self.live].to(device)
+        self.frozen_kv = kv[self.frozen].to(device)
+        self.frozen_idx = torch.as_tensor(self.frozen, dtype=torch.long, device=device)
+        self.closed = None
+        self.patterns = self.alpha = self.rho = self.z = None
+        if self.decomposed:
+            a, r = decomp
+            self.alpha = a.detach().to(device=device, dtype=torch.float32).contiguous()
+            self.rho = r.detach().to(device=device, dtype=torch.float32).contiguous()
+            self.z = decomposed_logz(self.alpha, self.rho).contiguous()
+            if self.frozen:
+                self.closed = classify_closed_form(self.alpha, self.rho, self.z, heads=self.frozen)
+        elif self.frozen:
+            if pattern is None:
+                raise ValueError("frozen heads need a dense prior or decomp=(alpha, rho)")
+            rows = pattern[self.frozen].to(device=device, dtype=dtype).tril()
+            # causal, row-stochastic in the model dtype (the prior definition of
+            # hybrid_prior_attention.py:146-152)
+            self.patterns = (rows / rows.sum(-1, keepdim=True).clamp_min(torch.finfo(dtype).tiny)).contiguous()
+
+    def covers(self, T):
+        """True if the stored prior reaches sequence length T."""
+        if not self.frozen:
+            return True
+        ref = self.alpha if self.decomposed else self.patterns
+        return ref.size(-1) >= T
+
+    def operator_kwargs(self):
+        """The prior arguments of fused_mixed_attn for this layer."""
+        if not self.frozen:
+            return {"patt": None}
+        if self.decomposed:
+            return {"patt": None, "alpha": self.alpha, "rho": self.rho, "z": self.z,
+                    "closed_form": self.closed}
+        return {"patt": self.patterns}
+
+    def dense_priors(self, T, dtype):
+        """(n_frozen, T, T) prior matrices for the split path."""
+        if not self.decomposed:
+            return self.patterns[:, :T, :T].to(dtype)
+        idx = self.frozen_idx
+        lg = decomp_logits(self.alpha[idx, :T], self.rho[idx, :T])
+        return torch.exp(lg - self.z[idx, :T, None]).to(dtype)
+
+
+def _rows_of_heads(heads, head_dim, stride, offset=0):
+    """Row indices of `head_dim` rows per head in a weight whose head h starts
+    at row h * stride + offset."""
+    return [h * stride + offset + d for h in heads for d in range(head_dim)]
+
+
+def _sub_linear(src: nn.Linear, rows, device, dtype):
+    """nn.Linear holding rows `rows` of src (weights copied)."""
+    lin = nn.Linear(src.in_features, len(rows), bias=src.bias is not None, device=device, dtype=dtype)
+    idx = torch.as_tensor(rows, dtype=torch.long, device=src.weight.device)
+    with torch.no_grad():
+        lin.weight.copy_(src.weight.index_select(0, idx))
+        if src.bias is not None:
+            lin.bias.copy_(src.bias.index_select(0, idx))
+    return lin
+
+
+def _eager_attention(q, k, v, mask, scale, dropout, training):
+    """softmax(q k^T scale + mask) v with the weights in fp32, then cast (the
+    eager attention of the Hugging Face modules)."""
+    w = torch.matmul(q, k.transpose(-1, -2)) * scale
+    if mask is not None:
+        w = w + mask[..., :k.size(-2)]
+    else:
+        T, S = q.size(-2), k.size(-2)
+        causal = torch.ones(T, S, dtype=torch.bool, device=q.device).tril(S - T)
+        w = w.masked_fill(~causal, float("-inf"))
+    w = torch.softmax(w, dim=-1, dtype=torch.float32).to(q.dtype)
+    w = F.dropout(w, p=dropout, training=training)
+    return torch.matmul(w, v)
+
+
+class HybridAttentionBase(nn.Module):
+    """Hybrid attention layer for one model family (SPEC), built from the
+    original attention module it replaces."""
+
+    SPEC: Optional[FamilySpec] = None
     ORIGINAL_CLASS: Optional[type] = None
 
-    def _hybrid_init(self, original: nn.Module, pattern, head_mask: torch.Tensor,
-                     n_q: int, head_dim: int, device, dtype,
-                     q_per_head_dim: int = None, decomp=None):
-        """pattern: (n_q, T, T) dense priors (rows of live heads unused) or None
-        with ``decomp`` = (alpha, rho), each (n_q, S) fp32."""
-        if q_per_head_dim is None:
-            q_per_head_dim = head_dim
-        head_mask = head_mask.to(torch.bool).cpu()
-        n_pattern = int(head_mask.sum().item())
-        n_standard = n_q - n_pattern
-        self.decomposed = decomp is not None
-        self.n_q_heads = n_q
-        self.n_pattern_heads = n_pattern
-        self.n_standard_heads = n_standard
-        self.head_dim_hybrid = head_dim
-
-        if n_standard > 0:
-            row_keep = (~head_mask).repeat_interleave(q_per_head_dim)
-            q_orig = original.q_proj
-            q_small = nn.Linear(q_orig.in_features, n_standard * q_per_head_dim,
-                                bias=q_orig.bias is not None, device=device, dtype=dtype)
-            with torch.no_grad():
-                q_small.weight.copy_(q_orig.weight[row_keep.to(q_orig.weight.device)])
-                if q_orig.bias is not None:
-                    q_small.bias.copy_(q_orig.bias[row_keep.to(q_orig.bias.device)])
-            self.q_proj_std = q_small
-        else:
-            self.q_proj_std = None
-
-        pat_idx = torch.nonzero(head_mask, as_tuple=True)[0]
-        std_idx = torch.nonzero(~head_mask, as_tuple=True)[0]
-        self.register_buffer("pattern_head_idx", pat_idx.to(device))
-        self.register_buffer("standard_head_idx", std_idx.to(device))
-        self._closed = None
-        if self.decomposed:
-            alpha, rho = decomp
-            alpha = alpha.detach().to(device=device, dtype=torch.float32).contiguous()
-            rho = rho.detach().to(device=device, dtype=torch.float32).contiguous()
-            z = decomposed_logz(alpha, rho)
-            self.register_buffer("dec_alpha", alpha)
-            self.register_buffer("dec_rho", rho)
-            self.register_buffer("dec_z", z.contiguous())
-            self.register_buffer("prior_pattern", torch.empty(0, device=device, dtype=dtype))
-            if n_pattern:
-                self._closed = classify_closed_form(alpha, rho, z, heads=pat_idx.tolist())
-        elif n_pattern > 0:
-            subset = pattern[pat_idx].to(device=device, dtype=dtype)
-            # lower-triangular, row-normalised in the model dtype (:146-152)
-            subset = subset.tril()
-            subset = subset / subset.sum(dim=-1, keepdim=True).clamp_min(torch.finfo(dtype).tiny)
-            self.register_buffer("prior_pattern", subset.contiguous())
-        else:
-            self.register_buffer("prior_pattern", torch.empty(0, device=device, dtype=dtype))
-
-        # head states 0 live / 1 dense / 2 decomposed; compact Q and P slots
-        frozen_i32 = head_mask.to(device=device, dtype=torch.int32)
-        if self.decomposed:
-            frozen_i32 = frozen_i32 * 2
-        hidx_i32 = torch.zeros(n_q, device=device, dtype=torch.int32)
-        pidx_i32 = torch.zeros(n_q, device=device, dtype=torch.int32)
-        if n_standard:
-            hidx_i32[std_idx.to(device)] = torch.arange(n_standard, device=device, dtype=torch.int32)
-        if n_pattern:
-            pidx_i32[pat_idx.to(device)] = torch.arange(n_pattern, device=device, dtype=torch.int32)
-        self.register_buffer("frozen_mask_i32", frozen_i32)
-        self.register_buffer("hidx_i32", hidx_i32)
-        self.register_buffer("pidx_i32", pidx_i32)
-        self._wc_key = None
+    def __init__(self, original, pattern, head_mask, device, dtype, use_triton=True,
+                 assume_causal_prefill=False, decomp=None):
+        super().__init__()
+        spec = self.SPEC
+        cfg = original.config
+        self.config = cfg
+        self.layer_idx = original.layer_idx
+        self.layer_type = getattr(original, "layer_type", None)
+        self.num_attention_heads = cfg.num_attention_heads
+        self.num_key_value_heads = cfg.num_key_value_heads
+        self.head_dim = original.head_dim
+        self.scaling = original.scaling
+        self.attention_dropout = original.attention_dropout
+        self.is_causal = True
+        self.sliding_window = getattr(original, "sliding_window", None)
+        self.use_triton_kernel = use_triton
+        # opt-in: a square (B or 1, 1, T, T) mask passed for unpadded prefill
+        # is taken to be the causal mask the kernel applies itself
+        self.assume_causal_prefill = assume_causal_prefill
+        # run an all-live layer through the HIP flash kernel (the reference
+        # leaves such layers unconverted)
+        self.fuse_live_only = False
+        for name in ("k_proj", "v_proj", "o_proj", "q_norm", "k_norm"):
+            setattr(self, name, getattr(original, name))
+        self.routing = HeadRouting(head_mask, self.num_key_value_heads, device, dtype, pattern, decomp)
+        r, hd, H = self.routing, self.head_dim, self.num_attention_heads
+        per_head = 2 * hd if spec.gated else hd
+        # live heads' query rows; gated families: every head's gate rows
+        self.q_live = _sub_linear(original.q_proj, _rows_of_heads(r.live, hd, per_head), device, dtype) \
+            if r.live else None
+        self.gate = _sub_linear(original.q_proj, _rows_of_heads(range(H), hd, per_head, hd), device, dtype) \
+            if spec.gated else None
+        self._cache_key = None
         self.hybrid_calls = 0
-        self.triton_calls = 0  # fused-path calls (the reference's counter name)
+        self.triton_calls = 0
+        self.train(original.training)   # a new module would start in training mode
 
-    def _fused_prior_kwargs(self):
-        if self.n_pattern_heads == 0:
-            return dict(patt=None)
-        if self.decomposed:
-            return dict(patt=None, alpha=self.dec_alpha, rho=self.dec_rho, z=self.dec_z,
-                        closed_form=self._closed)
-        return dict(patt=self.prior_pattern)
-
-    def _fused_prior_ready(self, T):
-        if self.n_pattern_heads == 0:
-            return True
-        if self.decomposed:
-            return self.dec_alpha.size(-1) >= T
-        return self.prior_pattern.ndim == 3 and self.prior_pattern.size(-1) >= T
-
-    def _split_patterns(self, T, dtype):
-        """(n_pattern, T, T) dense priors for the torch split path (:187-194)."""
-        if not self.decomposed:
-            return self.prior_pattern[:, :T, :T].to(dtype)
-        idx = self.pattern_head_idx
-        lg = decomp_logits(self.dec_alpha[idx, :T], self.dec_rho[idx, :T])
-        return torch.exp(lg - self.dec_z[idx, :T][:, :, None]).to(dtype)
-
-    def _qkv_weight_cache(self):
-        """[Wq(live); Wk; Wv] (and biases), rebuilt when a weight changes."""
-        ws = [m.weight for m in (self.q_proj_std, self.k_proj, self.v_proj) if m is not None]
-        key = tuple((w._version, w.data_ptr()) for w in ws)
-        if self._wc_key != key:
+    # -- the single gathered projection of the fused path ------------------
+    def _projection_weights(self):
+        mods = [m for m in (self.q_live, self.k_proj, self.v_proj, self.gate) if m is not None]
+        key = tuple((m.weight._version, m.weight.data_ptr()) for m in mods)
+        if self._cache_key != key:
             with torch.no_grad():
-                self._wc_w = torch.cat([w.detach() for w in ws])
-                mods = [m for m in (self.q_proj_std, self.k_proj, self.v_proj) if m is not None]
-                self._wc_b = None if mods[0].bias is None else torch.cat([m.bias.detach() for m in mods])
-            self._wc_key = key
-        return self._wc_w, self._wc_b
+                self._w_cat = torch.cat([m.weight.detach() for m in mods])
+                self._b_cat = None if mods[0].bias is None else torch.cat([m.bias.detach() for m in mods])
+            self._cache_key = key
+        return self._w_cat, self._b_cat
+
+    def _rope(self):
+        return importlib.import_module(self.SPEC.module).apply_rotary_pos_emb
+
+    def _fusable(self, x, attention_mask, past_key_values, T):
+        mask_ok = attention_mask is None
+        if self.assume_causal_prefill and isinstance(attention_mask, torch.Tensor):
+            mask_ok = (attention_mask.ndim == 4 and attention_mask.shape[-2:] == (T, T)
+                       and attention_mask.shape[0] in (1, x.size(0)))
+        return (self.use_triton_kernel and (bool(self.routing.frozen) or self.fuse_live_only)
+                and not self.training and not self._builds_graph(x)
+                and fused_attn_usable(x) and mask_ok and past_key_values is None
+                and self.sliding_window is None and self.head_dim in _FUSED_HEAD_DIMS
+                and self.routing.covers(T))
+
+    def _builds_graph(self, x):
+        """True when autograd records this call: the fused path (gathered
+        weights, in-place prologue, GQA operator without a backward) is then
+        not used and the split path computes the same function."""
+        return torch.is_grad_enabled() and (x.requires_grad or any(p.requires_grad for p in self.parameters()))
+
+    def _fused_forward(self, x, cos, sin):
+        global _FUSED_DISPATCH_COUNT
+        B, T, _ = x.shape
+        r, hd, H, HKV = self.routing, self.head_dim, self.num_attention_heads, self.num_key_value_heads
+        U = len(r.live)
+        w, b = self._projection_weights()
+        y = F.linear(x, w, b).view(B, T, -1, hd)
+        q = y[:, :, :U].transpose(1, 2)
+        k = y[:, :, U:U + HKV].transpose(1, 2)
+        v = y[:, :, U + HKV:U + 2 * HKV].transpose(1, 2)
+        gate = y[:, :, U + 2 * HKV:] if self.SPEC.gated else None
+        if U:
+            if self.SPEC.hip_prologue and (cos.dim() == 2 or cos.size(0) == 1):
+                _kernel_mod.qk_rmsnorm_rope_(q, k, self.q_norm.weight, self.k_norm.weight,
+                                             self.q_norm.variance_epsilon, cos, sin)
+            else:
+                q = self.q_norm(q.transpose(1, 2)).transpose(1, 2)
+                k = self.k_norm(k.transpose(1, 2)).transpose(1, 2)
+                q, k = self._rope()(q, k, cos, sin)
+        _FUSED_DISPATCH_COUNT += 1
+        out = fused_mixed_attn(q, k, v, frozen=r.state, hidx=r.live_slot, pidx=r.prior_slot,
+                               kvidx=r.kv_head, sm_scale=self.scaling, validate=False, **r.operator_kwargs())
+        self.triton_calls += 1
+        out = out.transpose(1, 2)                     # (B, T, H, hd), a view of the T-major output
+        if gate is not None:
+            out = out * torch.sigmoid(gate)
+        return self.o_proj(out.reshape(B, T, H * hd)), None
+
+    def _split_forward(self, x, cos, sin, attention_mask):
+        B, T, _ = x.shape
+        r, hd, H, HKV = self.routing, self.head_dim, self.num_attention_heads, self.num_key_value_heads
+        k = self.k_norm(self.k_proj(x).view(B, T, HKV, hd)).transpose(1, 2)
+        v = self.v_proj(x).view(B, T, HKV, hd).transpose(1, 2)
+        out = x.new_empty(B, T, H, hd)
+        if r.live:
+            q = self.q_norm(self.q_live(x).view(B, T, len(r.live), hd)).transpose(1, 2)
+            q, k = self._rope()(q, k, cos, sin)
+            kg = k.index_select(1, r.live_kv)
+            vg = v.index_select(1, r.live_kv)
+            impl = getattr(self.config, "_attn_implementation", "eager")
+            if impl in ("sdpa", "flash_attention_2") and T > 1:
+                o = F.scaled_dot_product_attention(q, kg, vg, attn_mask=attention_mask,
+                                                   is_causal=attention_mask is None, scale=self.scaling)
+            else:
+                o = _eager_attention(q, kg, vg, attention_mask, self.scaling,
+                                     self.attention_dropout, self.training)
+            out[:, :, r.live] = o.transpose(1, 2)
+        if r.frozen:
+            vp = v.index_select(1, r.frozen_kv)
+            out[:, :, r.frozen] = torch.matmul(r.dense_priors(T, vp.dtype).unsqueeze(0), vp).transpose(1, 2)
+        if self.gate is not None:
+            out = out * torch.sigmoid(self.gate(x).view(B, T, H, hd))
+        return self.o_proj(out.reshape(B, T, H * hd)), None
+
+    def forward(self, hidden_states, position_embeddings, attention_mask=None, past_key_values=None,
+                cache_position=None, **kwargs):
+        self.hybrid_calls += 1
+        cos, sin = position_embeddings
+        T = hidden_states.size(1)
+        if self._fusable(hidden_states, attention_mask, past_key_values, T):
+            return self._fused_forward(hidden_states, cos, sin)
+        return self._split_forward(hidden_states, cos, sin, attention_mask)
+
+
+_CLASS_CACHE: Dict[str, type] = {}
+
+
+def _hybrid_class(spec: FamilySpec, name: str) -> type:
+    if spec.class_name not in _CLASS_CACHE:
+        original = getattr(importlib.import_module(spec.module), spec.class_name)
+        _CLASS_CACHE[spec.class_name] = type(name, (HybridAttentionBase,),
+                                             {"SPEC": spec, "ORIGINAL_CLASS": original})
+    return _CLASS_CACHE[spec.class_name]
 
 
 def make_qwen3_hybrid_class():
-    """Hybrid subclass of transformers' Qwen3Attention (:477-642)."""
-    qwen3 = importlib.import_module("transformers.models.qwen3.modeling_qwen3")
-    OriginalAttention = qwen3.Qwen3Attention
-    eager_attention_forward = qwen3.eager_attention_forward
-    repeat_kv = qwen3.repeat_kv
-    apply_rotary_pos_emb = qwen3.apply_rotary_pos_emb
-
-    class HybridQwen3Attention(HybridAttentionBase, OriginalAttention):
-        ORIGINAL_CLASS = OriginalAttention
-
-        def __init__(self, original, pattern, head_mask, device, dtype, use_triton=True,
-                     assume_causal_prefill=False, decomp=None):
-            nn.Module.__init__(self)
-            cfg = original.config
-            self.config = cfg
-            self.layer_idx = original.layer_idx
-            self.layer_type = getattr(original, "layer_type", None)
-            self.attention_dropout = original.attention_dropout
-            self.num_attention_heads = cfg.num_attention_heads
-            self.num_key_value_heads = cfg.num_key_value_heads
-            self._real_num_kv_groups = original.num_key_value_groups
-            # K/V are broadcast by hand on the split path
-            self.num_key_value_groups = 1
-            self.head_dim = original.head_dim
-            self.scaling = original.scaling
-            self.is_causal = original.is_causal
-            self.sliding_window = getattr(original, "sliding_window", None)
-            self.use_triton_kernel = use_triton
-            self.assume_causal_prefill = assume_causal_prefill
-            # with no frozen head the reference leaves the module unconverted;
-            # set (convert_targets_to_hybrid(fuse_live_only=True)) to run an
-            # all-live layer through the HIP flash kernel instead of SDPA
-            self.fuse_live_only = False
-            self.k_proj = original.k_proj
-            self.v_proj = original.v_proj
-            self.o_proj = original.o_proj
-            self.q_norm = original.q_norm
-            self.k_norm = original.k_norm
-            self._hybrid_init(original, pattern, head_mask, n_q=self.num_attention_heads,
-                              head_dim=self.head_dim, device=device, dtype=dtype,
-                              q_per_head_dim=self.head_dim, decomp=decomp)
-            # query head h reads KV head h // groups of the raw K/V (:526-528)
-            self.register_buffer("kvidx_i32", (
-                torch.arange(self.num_attention_heads, device=device)
-                // self._real_num_kv_groups).to(torch.int32))
-
-        def _fused_forward(self, hidden_states, cos, sin):
-            global _FUSED_DISPATCH_COUNT
-            B, T, _ = hidden_states.shape
-            n_std, hd = self.n_standard_heads, self.head_dim
-            hkv, n_q = self.num_key_value_heads, self.num_attention_heads
-            if torch.is_grad_enabled():
-                k = self.k_norm(self.k_proj(hidden_states).view(B, T, hkv, hd)).transpose(1, 2)
-                v = self.v_proj(hidden_states).view(B, T, hkv, hd).transpose(1, 2)
-                if n_std > 0:
-                    q = self.q_norm(self.q_proj_std(hidden_states).view(B, T, n_std, hd)).transpose(1, 2)
-                    q, k = apply_rotary_pos_emb(q, k, cos, sin)
-                else:
-                    q = v[:, :0]
-            else:
-                w, wb = self._qkv_weight_cache()
-                qkv = F.linear(hidden_states, w, wb).view(B, T, n_std + 2 * hkv, hd)
-                q = qkv[:, :, :n_std].transpose(1, 2)
-                k = qkv[:, :, n_std:n_std + hkv].transpose(1, 2)
-                v = qkv[:, :, n_std + hkv:].transpose(1, 2)
-                if n_std > 0:
-                    if cos.dim() == 3 and cos.size(0) != 1:
-                        # per-sequence positions: torch prologue
-                        q = self.q_norm(q.transpose(1, 2)).transpose(1, 2)
-                        k = self.k_norm(k.transpose(1, 2)).transpose(1, 2)
-                        q, k = apply_rotary_pos_emb(q, k, cos, sin)
-                    else:
-                        _kernel_mod.qk_rmsnorm_rope_(q, k, self.q_norm.weight, self.k_norm.weight,
-                                                     self.q_norm.variance_epsilon, cos, sin)
-            _FUSED_DISPATCH_COUNT += 1
-            out_heads = fused_mixed_attn(
-                q, k, v, frozen=self.frozen_mask_i32, hidx=self.hidx_i32, pidx=self.pidx_i32,
-                kvidx=self.kvidx_i32, sm_scale=self.scaling, validate=False,
-                **self._fused_prior_kwargs())
-            self.triton_calls += 1
-            out = out_heads.transpose(1, 2).reshape(B, T, n_q * hd)
-            return self.o_proj(out), None
-
-        def forward(self, hidden_states, position_embeddings, attention_mask=None,
-                    past_key_values=None, cache_position=None, **kwargs):
-            self.hybrid_calls += 1
-            B, T, _ = hidden_states.shape
-            n_std, n_pat = self.n_standard_heads, self.n_pattern_heads
-            head_dim, n_q = self.head_dim, self.num_attention_heads
-            cos, sin = position_embeddings
-
-            mask_is_supported = attention_mask is None
-            if self.assume_causal_prefill and isinstance(attention_mask, torch.Tensor):
-                mask_is_supported = (attention_mask.ndim == 4
-                                     and attention_mask.shape[-2:] == (T, T)
-                                     and attention_mask.shape[0] in (1, B))
-            can_fuse = (self.use_triton_kernel and (n_pat > 0 or self.fuse_live_only)
-                        and not self.training
-                        and fused_attn_usable(hidden_states) and mask_is_supported
-                        and past_key_values is None and self.sliding_window is None
-                        and self._fused_prior_ready(T))
-            if can_fuse:
-                return self._fused_forward(hidden_states, cos, sin)
-
-            # split path (also the correctness reference): SDPA / eager for the
-            # standard heads, dense P @ V for the pattern heads (:586-640)
-            k = self.k_norm(self.k_proj(hidden_states).view(
-                B, T, self.num_key_value_heads, head_dim)).transpose(1, 2)
-            v = self.v_proj(hidden_states).view(B, T, self.num_key_value_heads, head_dim).transpose(1, 2)
-            k_full = repeat_kv(k, self._real_num_kv_groups)
-            v_full = repeat_kv(v, self._real_num_kv_groups)
-            if n_std > 0:
-                q_std = self.q_norm(self.q_proj_std(hidden_states).view(
-                    B, T, n_std, head_dim)).transpose(1, 2)
-                k_std = k_full[:, self.standard_head_idx]
-                q_std, k_std = apply_rotary_pos_emb(q_std, k_std, cos, sin)
-                v_std = v_full[:, self.standard_head_idx]
-                impl_name = getattr(self.config, "_attn_implementation", "eager")
-                if impl_name in ("sdpa", "flash_attention_2") and T > 1:
-                    out_std = F.scaled_dot_product_attention(
-                        q_std, k_std, v_std, attn_mask=attention_mask,
-                        is_causal=attention_mask is None, scale=self.scaling).transpose(1, 2).contiguous()
-                else:
-                    out_std, _ = eager_attention_forward(
-                        self, q_std, k_std, v_std, attention_mask,
-                        dropout=0.0 if not self.training else self.attention_dropout,
-                        scaling=self.scaling)
-                out_std = out_std.view(B, T, n_std, head_dim)
-            if n_pat > 0:
-                v_pat = v_full[:, self.pattern_head_idx]
-                pat = self._split_patterns(T, v_pat.dtype)
-                out_pat = torch.matmul(pat.unsqueeze(0), v_pat).transpose(1, 2).contiguous()
-            out = hidden_states.new_empty(B, T, n_q, head_dim)
-            if n_std > 0:
-                out[:, :, self.standard_head_idx] = out_std
-            if n_pat > 0:
-                out[:, :, self.pattern_head_idx] = out_pat
-            return self.o_proj(out.reshape(B, T, n_q * head_dim)), None
-
-    return HybridQwen3Attention
+    """Hybrid class for transformers' Qwen3Attention (plain GQA + q/k norm)."""
+    return _hybrid_class(QWEN3, "HybridQwen3Attention")
 
 
-_REGISTRY_BUILDERS = {"Qwen3Attention": make_qwen3_hybrid_class}
-_BUILT_CACHE: dict = {}
+def make_qwen35_hybrid_class():
+    """Hybrid class for transformers' Qwen3_5Attention (gated attention)."""
+    return _hybrid_class(QWEN35, "HybridQwen3_5Attention")
+
+
+_MAKERS = {"Qwen3Attention": make_qwen3_hybrid_class, "Qwen3_5Attention": make_qwen35_hybrid_class}
 
 
 def get_hybrid_class_for(original_module: nn.Module) -> Optional[Type]:
-    """Hybrid class for an attention module's class name (:659-665)."""
-    name = type(original_module).__name__
-    if name not in _REGISTRY_BUILDERS:
-        return None
-    if name not in _BUILT_CACHE:
-        _BUILT_CACHE[name] = _REGISTRY_BUILDERS[name]()
-    return _BUILT_CACHE[name]
+    """The hybrid class for an attention module, or None for an unsupported family."""
+    maker = _MAKERS.get(type(original_module).__name__)
+    return None if maker is None else maker()
 
+
+# ---------------------------------------------------------------------------
+# Target discovery and conversion
+# ---------------------------------------------------------------------------
 
 @dataclass
 class SoftmaxAttentionTarget:
     layer_idx: int
     module: nn.Module
     attr_name: str
-
-
-_ATTN_ATTR_CANDIDATES = ("self_attn", "attention", "attn", "full_attn")
-
-
-def iter_blocks(model: nn.Module):
-    """The transformer blocks of a causal LM (test_prior_pretrained.py:199-212)."""
-    for path in (lambda m: m.model.layers, lambda m: m.transformer.h,
-                 lambda m: m.model.decoder.layers, lambda m: m.gpt_neox.layers):
-        try:
-            blocks = path(model)
-        except AttributeError:
-            continue
-        if blocks is not None:
-            return list(blocks)
-    raise ValueError(f"cannot find the transformer blocks of {type(model).__name__}")
+    parent: Optional[nn.Module] = None
 
 
 def _is_softmax_attention(m: nn.Module) -> bool:
@@ -353,69 +371,79 @@ def _is_softmax_attention(m: nn.Module) -> bool:
         any(hasattr(m, n) for n in ("o_proj", "c_proj"))
 
 
+def _block_lists(model: nn.Module):
+    """(path, ModuleList) of the model's stacks of transformer blocks."""
+    for path, mod in model.named_modules():
+        if isinstance(mod, nn.ModuleList) and len(mod) and \
+                any(_is_softmax_attention(c) for b in mod for c in b.children()):
+            yield path, mod
+
+
+def iter_blocks(model: nn.Module):
+    """The decoder blocks of a causal LM (the first stack holding softmax
+    attention modules)."""
+    for _, blocks in _block_lists(model):
+        return list(blocks)
+    raise ValueError(f"cannot find the transformer blocks of {type(model).__name__}")
+
+
 def discover_softmax_attention(model: nn.Module) -> List[SoftmaxAttentionTarget]:
-    """Every standard softmax-attention module, one per block (:215-240)."""
-    targets = []
-    for li, block in enumerate(iter_blocks(model)):
-        found = None
-        for name in _ATTN_ATTR_CANDIDATES:
-            m = getattr(block, name, None)
-            if m is not None and _is_softmax_attention(m):
-                found = (m, name)
-                break
-        if found is None:
-            for name, m in block.named_children():
-                if _is_softmax_attention(m):
-                    found = (m, name)
+    """Every softmax attention module that is a direct child of a decoder
+    block, in block order (blocks without one, e.g. linear-attention layers,
+    are skipped)."""
+    for _, blocks in _block_lists(model):
+        targets = []
+        for li, block in enumerate(blocks):
+            for attr, child in block.named_children():
+                if _is_softmax_attention(child):
+                    targets.append(SoftmaxAttentionTarget(li, child, attr, block))
                     break
-        if found is not None:
-            targets.append(SoftmaxAttentionTarget(li, found[0], found[1]))
-    return targets
+        return targets
+    return []
 
 
 def convert_targets_to_hybrid(model, targets, mean_attn, head_masks, device, dtype,
                               use_triton=True, assume_causal_prefill=False, decomp=None,
                               fuse_live_only=False):
-    """Swap each target's attention module for its hybrid counterpart (:671-722).
+    """Replace each target's attention module by its hybrid counterpart.
 
     mean_attn: per-target (n_heads, T, T) dense priors, or None with ``decomp``
     = per-target (alpha, rho) pairs of (n_heads, S) fp32 tensors (None entries
-    for targets with no frozen head).  Returns the list restore_originals takes.
-    fuse_live_only (an extension) also converts targets with no frozen head, so
-    their attention runs the HIP flash kernel rather than the model's SDPA.
-    """
-    if mean_attn is None:
-        if decomp is None:
-            raise ValueError("need mean_attn or decomp")
-        priors = [None] * len(targets)
-    else:
-        priors = list(mean_attn)
-    if not len(targets) == len(priors) == len(head_masks):
-        raise ValueError("targets, priors and head_masks must have one entry per target")
-    if decomp is not None and len(decomp) != len(targets):
-        raise ValueError("decomp must have one entry per target")
-    blocks = iter_blocks(model)
+    for targets with no frozen head).  Targets with no frozen head stay as
+    they are unless fuse_live_only (an extension) asks for the HIP flash path
+    there too.  Returns the list restore_originals takes."""
+    n = len(targets)
+    if mean_attn is None and decomp is None:
+        raise ValueError("need mean_attn or decomp")
+    priors = [None] * n if mean_attn is None else list(mean_attn)
+    if len(priors) != n or len(head_masks) != n or (decomp is not None and len(decomp) != n):
+        raise ValueError("targets, priors, head_masks (and decomp) must have one entry per target")
+    blocks = None
     saved = []
-    for ti, (t, prior, mask) in enumerate(zip(targets, priors, head_masks)):
-        if not bool(mask.any()) and not fuse_live_only:
-            saved.append((blocks[t.layer_idx], t.attr_name, None))
+    for i, (t, mask) in enumerate(zip(targets, head_masks)):
+        parent = t.parent
+        if parent is None:
+            blocks = blocks or iter_blocks(model)
+            parent = blocks[t.layer_idx]
+        original = getattr(parent, t.attr_name)
+        if not bool(torch.as_tensor(mask).any()) and not fuse_live_only:
+            saved.append((parent, t.attr_name, None))
             continue
-        original = getattr(blocks[t.layer_idx], t.attr_name)
         cls = get_hybrid_class_for(original)
         if cls is None:
             raise RuntimeError(f"No hybrid class registered for {type(original).__name__}")
-        hybrid = cls(original, prior, mask, device, dtype, use_triton=use_triton,
+        hybrid = cls(original, priors[i], mask, device, dtype, use_triton=use_triton,
                      assume_causal_prefill=assume_causal_prefill,
-                     decomp=None if decomp is None else decomp[ti])
+                     decomp=None if decomp is None else decomp[i])
         hybrid.fuse_live_only = bool(fuse_live_only)
         hybrid.train(original.training)
-        setattr(blocks[t.layer_idx], t.attr_name, hybrid)
-        saved.append((blocks[t.layer_idx], t.attr_name, original))
+        setattr(parent, t.attr_name, hybrid)
+        saved.append((parent, t.attr_name, original))
     return saved
 
 
 def restore_originals(saved):
-    """Undo convert_targets_to_hybrid (:725-729)."""
-    for block, attr_name, original in saved:
+    """Undo convert_targets_to_hybrid."""
+    for parent, attr_name, original in saved:
         if original is not None:
-            setattr(block, attr_name, original)
+            setattr(parent, attr_name, original)

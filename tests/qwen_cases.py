@@ -65,3 +65,33 @@ def convert_golden(model, z, repr, device, dtype):
     saved = qwen.convert_targets_to_hybrid(model, targets, mean_attn, masks, device, dtype,
                                            use_triton=True, decomp=decomp)
     return saved, fr
+
+
+def qwen35_layer(hd=64, H=8, HKV=2, hidden=256, seed=0, impl="sdpa"):
+    """A random-init transformers Qwen3_5Attention (fp32, CPU) with non-trivial
+    norm weights, its text rotary embedding (partial rotation, factor 0.25)
+    and the layer's state dict (keys relative to the module)."""
+    from transformers.models.qwen3_5 import modeling_qwen3_5 as m
+    from transformers.models.qwen3_5.configuration_qwen3_5 import Qwen3_5TextConfig
+    cfg = Qwen3_5TextConfig(hidden_size=hidden, num_attention_heads=H, num_key_value_heads=HKV, head_dim=hd,
+                            num_hidden_layers=1, layer_types=["full_attention"], intermediate_size=2 * hidden,
+                            vocab_size=128, rope_parameters={"rope_type": "default", "rope_theta": 10000.0,
+                                                             "partial_rotary_factor": 0.25})
+    cfg._attn_implementation = impl
+    torch.manual_seed(seed)
+    attn = m.Qwen3_5Attention(cfg, layer_idx=0).eval()
+    g = torch.Generator().manual_seed(seed + 1)
+    with torch.no_grad():
+        for name, p in attn.named_parameters():
+            if name.endswith("norm.weight"):
+                p.copy_(0.3 * torch.randn(p.shape, generator=g))
+            else:
+                p.copy_(torch.randn(p.shape, generator=g) * (p.shape[-1] ** -0.5))
+    rot = m.Qwen3_5TextRotaryEmbedding(cfg)
+    return attn, rot, cfg
+
+
+def qwen35_position_embeddings(rot, T, device="cpu", dtype=torch.float32, B=1):
+    x = torch.zeros(1, device=device, dtype=dtype)
+    pos = torch.arange(T, device=device)[None].expand(B, T)
+    return rot.to(device)(x, pos)

@@ -136,12 +136,57 @@ def test_c4_heads_model_vs_oracle(rate, repr):
     torch.cuda.synchronize()
     assert qwen.fused_dispatch_count() - n0 == cfg.num_hidden_layers
     if repr == "decomposed" and rate > 0:
-        assert all((blk.self_attn._closed[0][mk.numpy()] == 1).all() for blk, mk in zip(m.model.layers, masks))
+        assert all((blk.self_attn.routing.closed[0][mk.numpy()] == 1).all() for blk, mk in zip(m.model.layers, masks))
     mean = np.tril(np.ones((T, T), dtype=np.float32))
     fr = [dict(mask=mk.numpy(), dense=np.broadcast_to(mean, (14, T, T))) for mk in masks]
     ocfg = dict(n_layers=cfg.num_hidden_layers, n_heads=14, n_kv_heads=2, head_dim=64,
                 eps=cfg.rms_norm_eps, rope_theta=1e6)
     ref = qo.qwen_forward(sd, ocfg, fr, ids)
+    y = y.float().cpu()
+    assert _cos(y, ref) >= 0.9999
+    assert _rel(y, ref) <= 1e-2
+
+
+@pytest.mark.parametrize("hd", [64, 128])
+@pytest.mark.parametrize("prior", ["dense", "decomp"])
+def test_qwen35_gated_fused_path_vs_oracle(hd, prior):
+    """The Qwen3.5 gated-attention hybrid (qwen/nanogpt/hybrid_prior_attention.py:205-470)
+    on its fused path: one gathered projection [q(live); k; v; gate(all)],
+    the module's own (1 + w) q/k norms and partial RoPE, the HIP operator with
+    the GQA map, sigmoid gate, o_proj; against the fp32 oracle with the
+    module's bf16-rounded weights (cosine >= 0.9999, relative L2 <= 1e-2)."""
+    import qwen
+    attn, rot, cfg = qc.qwen35_layer(hd=hd, H=8, HKV=2, hidden=512, seed=hd)
+    attn = attn.to(DEV, torch.bfloat16)
+    T, H = 300, 8
+    sd = {k: v.detach().float().cpu() for k, v in attn.state_dict().items()}
+    mask = torch.zeros(H, dtype=torch.bool)
+    mask[[1, 2, 6]] = True
+    g = torch.Generator().manual_seed(hd + 1)
+    cls = qwen.make_qwen35_hybrid_class()
+    if prior == "dense":
+        dense = torch.rand(H, T, T, generator=g)
+        hyb = cls(attn, dense.to(DEV), mask, DEV, torch.bfloat16)
+        fr = {"mask": mask.numpy(), "dense": hyb.routing.patterns.float().cpu().numpy()}
+        full = np.zeros((H, T, T), dtype=np.float32)
+        full[[1, 2, 6]] = fr["dense"]
+        fr["dense"] = full
+    else:
+        a, r = torch.randn(H, 320, generator=g) * 0.5, torch.randn(H, 320, generator=g) * 0.5
+        a[2], r[2] = 0.0, -0.05 * torch.arange(320.0)   # a closed-form decay head
+        hyb = cls(attn, None, mask, DEV, torch.bfloat16, decomp=(a.to(DEV), r.to(DEV)))
+        assert int(hyb.routing.closed[0][2]) == 2
+        fr = {"mask": mask.numpy(), "alpha": a.numpy(), "rho": r.numpy()}
+    x = torch.randn(2, T, cfg.hidden_size, generator=torch.Generator().manual_seed(3))
+    cos, sin = qc.qwen35_position_embeddings(rot, T, device=DEV, dtype=torch.bfloat16, B=2)
+    n0 = qwen.fused_dispatch_count()
+    with torch.inference_mode():
+        y, _ = hyb(x.to(DEV, torch.bfloat16), (cos, sin))
+    torch.cuda.synchronize()
+    assert qwen.fused_dispatch_count() - n0 == 1 and hyb.triton_calls == 1
+    xr = x.to(torch.bfloat16).float()
+    ref = qo.qwen35_attention(xr, sd, "", dict(n_heads=H, n_kv_heads=2, head_dim=hd, eps=cfg.rms_norm_eps),
+                              fr, cos[0].float().cpu(), sin[0].float().cpu())
     y = y.float().cpu()
     assert _cos(y, ref) >= 0.9999
     assert _rel(y, ref) <= 1e-2

@@ -55,13 +55,14 @@ def test_adapter_tables_and_split_path_match_reference(golden, repr):
     for l, blk in enumerate(m.model.layers):
         a = blk.self_attn
         assert type(a).__name__ == "HybridQwen3Attention"
-        for name in ("frozen", "hidx", "pidx", "kvidx"):
-            got = getattr(a, f"{name}_mask_i32" if name == "frozen" else f"{name}_i32").numpy()
-            assert np.array_equal(got, golden[f"{repr}:{name}:{l}"]), (l, name)
+        tables = {"frozen": a.routing.state, "hidx": a.routing.live_slot, "pidx": a.routing.prior_slot,
+                  "kvidx": a.routing.kv_head}
+        for name, got in tables.items():
+            assert np.array_equal(got.numpy(), golden[f"{repr}:{name}:{l}"]), (l, name)
         if repr == "dense":
-            assert np.array_equal(a.prior_pattern.numpy(), golden[f"dense:prior:{l}"])
+            assert np.array_equal(a.routing.patterns.numpy(), golden[f"dense:prior:{l}"])
         else:
-            assert np.allclose(a.dec_z.numpy(), golden[f"decomp:z:{l}"], atol=1e-5, rtol=0)
+            assert np.allclose(a.routing.z.numpy(), golden[f"decomp:z:{l}"], atol=1e-5, rtol=0)
     with torch.inference_mode():
         y = qwen.backbone_forward(m.model, torch.from_numpy(golden["tokens"]))
     assert (y - torch.from_numpy(golden[f"hidden_{repr}"])).abs().max().item() < 2e-5
@@ -78,9 +79,9 @@ def test_closed_form_classification_of_mean_priors():
     m = qwen.build_model(cfg, device="cpu", dtype=torch.float32)
     saved, masks = qwen.convert_with_rate(m, 0.5, 32, repr="decomposed")
     for blk, mask in zip(m.model.layers, masks):
-        kind, param = blk.self_attn._closed
+        kind, param = blk.self_attn.routing.closed
         assert np.array_equal(kind, np.where(mask.numpy(), 1, 0))
-        assert np.array_equal(blk.self_attn.frozen_mask_i32.numpy(), 2 * mask.numpy().astype(np.int32))
+        assert np.array_equal(blk.self_attn.routing.state.numpy(), 2 * mask.numpy().astype(np.int32))
     ids = torch.randint(0, 128, (2, 32))
     with torch.inference_mode():
         yd = qwen.backbone_forward(m.model, ids)
@@ -114,3 +115,87 @@ def test_hip_prologue_refuses_cpu_tensors():
     cs = torch.zeros(8, 64)
     with pytest.raises(RuntimeError, match="HIP devices only"):
         kernel.qk_rmsnorm_rope_(q, q, w, w, 1e-6, cs, cs)
+
+
+# ---------------------------------------------------------------------------
+# Qwen3.5 gated attention (qwen/nanogpt/hybrid_prior_attention.py:205-470)
+# ---------------------------------------------------------------------------
+
+def _ocfg35(cfg):
+    return dict(n_heads=cfg.num_attention_heads, n_kv_heads=cfg.num_key_value_heads, head_dim=cfg.head_dim,
+                eps=cfg.rms_norm_eps)
+
+
+@pytest.mark.parametrize("impl", ["sdpa", "eager"])
+def test_qwen35_oracle_matches_transformers_module(impl):
+    """No head frozen: the oracle's gated layer equals transformers' own
+    Qwen3_5Attention (the library special case)."""
+    attn, rot, cfg = qc.qwen35_layer(hd=64, impl=impl)
+    x = torch.randn(2, 37, cfg.hidden_size, generator=torch.Generator().manual_seed(3))
+    cos, sin = qc.qwen35_position_embeddings(rot, 37, B=2)
+    # the models hand eager attention an explicit causal mask (SDPA: None)
+    mask = None if impl == "sdpa" else torch.full((37, 37), float("-inf")).triu(1)[None, None]
+    with torch.no_grad():
+        ref, _ = attn(x, (cos, sin), attention_mask=mask)
+    sd = {k: v.detach() for k, v in attn.state_dict().items()}
+    got = qo.qwen35_attention(x, sd, "", _ocfg35(cfg), None, cos[0], sin[0])
+    assert (got - ref).abs().max().item() < 1e-5
+
+
+def test_qwen35_oracle_frozen_self_prior_is_invariant():
+    """A frozen head whose prior is its own softmax matrix leaves the output
+    unchanged (gate, KV group and head order all exercised); a prior on the
+    wrong head does not."""
+    attn, rot, cfg = qc.qwen35_layer(hd=32, H=8, HKV=2)
+    T = 29
+    x = torch.randn(1, T, cfg.hidden_size, generator=torch.Generator().manual_seed(4))
+    cos, sin = qc.qwen35_position_embeddings(rot, T)
+    sd = {k: v.detach() for k, v in attn.state_dict().items()}
+    ocfg = _ocfg35(cfg)
+    live, probs = qo.qwen35_attention(x, sd, "", ocfg, None, cos[0], sin[0], return_probs=True)
+    mask = np.zeros(8, dtype=bool)
+    mask[[1, 6]] = True
+    dense = probs[0].numpy()
+    got = qo.qwen35_attention(x, sd, "", ocfg, {"mask": mask, "dense": dense}, cos[0], sin[0])
+    assert (got - live).abs().max().item() < 1e-5
+    wrong = dense.copy()
+    wrong[[1, 6]] = dense[[2, 5]]
+    bad = qo.qwen35_attention(x, sd, "", ocfg, {"mask": mask, "dense": wrong}, cos[0], sin[0])
+    assert (bad - live).abs().max().item() > 1e-3
+
+
+@pytest.mark.parametrize("prior", ["dense", "decomp"])
+def test_qwen35_adapter_split_path_matches_oracle(prior):
+    """The hybrid Qwen3.5 module (torch split path on the CPU) against the
+    oracle, with dense or decomposed priors; an all-live hybrid equals the
+    original module."""
+    import qwen
+    attn, rot, cfg = qc.qwen35_layer(hd=64, H=8, HKV=2, seed=5)
+    T, H = 41, 8
+    x = torch.randn(2, T, cfg.hidden_size, generator=torch.Generator().manual_seed(6))
+    cos, sin = qc.qwen35_position_embeddings(rot, T, B=2)
+    sd = {k: v.detach().clone() for k, v in attn.state_dict().items()}
+    mask = torch.zeros(H, dtype=torch.bool)
+    mask[[0, 3, 7]] = True
+    g = torch.Generator().manual_seed(8)
+    cls = qwen.make_qwen35_hybrid_class()
+    if prior == "dense":
+        dense = torch.rand(H, T, T, generator=g)
+        hyb = cls(attn, dense, mask, "cpu", torch.float32)
+        fr = {"mask": mask.numpy(), "dense": dense.numpy()}
+    else:
+        a, r = torch.randn(H, 64, generator=g) * 0.5, torch.randn(H, 64, generator=g) * 0.5
+        a[3], r[3] = 0.0, 0.0   # a closed-form (mean) head among generic ones
+        hyb = cls(attn, None, mask, "cpu", torch.float32, decomp=(a, r))
+        assert int(hyb.routing.closed[0][3]) == 1
+        fr = {"mask": mask.numpy(), "alpha": a.numpy(), "rho": r.numpy()}
+    with torch.no_grad():
+        got, _ = hyb(x, (cos, sin))
+    ref = qo.qwen35_attention(x, sd, "", _ocfg35(cfg), fr, cos[0], sin[0])
+    assert (got - ref).abs().max().item() < 1e-5
+    live = cls(attn, None, torch.zeros(H, dtype=torch.bool), "cpu", torch.float32,
+               decomp=(torch.zeros(H, 64), torch.zeros(H, 64)))
+    with torch.no_grad():
+        a_out, _ = attn(x, (cos, sin), attention_mask=None)
+        l_out, _ = live(x, (cos, sin))
+    assert (a_out - l_out).abs().max().item() < 1e-5
