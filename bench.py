@@ -869,19 +869,210 @@ def run_logz(args):
     print(json.dumps(line), flush=True)
 
 
+def build_ckpt_pair(dirpath, T, seed=1337):
+    """A synthetic checkpoint pair in the reference's export layout at the
+    124M shape (block_size T): the same random-init weights saved as a full
+    model (no frozen head) and as a frozen model with a random 25% of the
+    (layer, head) pairs frozen to learned-looking decomposed priors (alpha ~
+    N(0, 0.5^2), rho_d = -c d + N(0, 0.1^2) with c ~U(0.001, 0.05)), which are
+    no closed form and run the in-register rebuild kernel.  Written on the
+    CPU; returns (baseline path, frozen path)."""
+    import torch
+    from nanogpt.model import GPT, GPTConfig
+    from nanogpt.checkpoint import save_reference_checkpoint
+
+    torch.manual_seed(seed)
+    cfg = GPTConfig(block_size=T, vocab_size=50304, n_layer=12, n_head=12, n_embd=768, bias=False,
+                    position_encoding="rope", rand_attn_prior_repr="decomposed", rand_seed=seed)
+    model = GPT(cfg).eval()
+    base = os.path.join(dirpath, "saf124m_full.pt")
+    save_reference_checkpoint(model, base, iter_num=0)
+    g = torch.Generator().manual_seed(seed)
+    pairs = torch.randperm(144, generator=g)[:36].tolist()
+    d = torch.arange(T, dtype=torch.float32)
+    per_layer = {}
+    for idx in pairs:
+        per_layer.setdefault(idx // 12, []).append(idx % 12)
+    for layer, heads in per_layer.items():
+        n = len(heads)
+        alpha = torch.randn(n, T, generator=g) * 0.5
+        c = 0.001 + 0.049 * torch.rand(n, 1, generator=g)
+        rho = -c * d + torch.randn(n, T, generator=g) * 0.1
+        model.transformer.h[layer].attn.freeze_heads_decomposed(heads, alpha, rho)
+    frozen = os.path.join(dirpath, "saf124m_saf25.pt")
+    save_reference_checkpoint(model, frozen, iter_num=0)
+    return base, frozen
+
+
+def ckpt_leg(spec):
+    """One timing leg of a loaded export (nanogpt/bench_checkpoint_prefill.py:35-153):
+    load, verify one fused dispatch per layer, warm up, optionally capture
+    one prefill in a HIP graph, time `iters` prefills (HIP events), median."""
+    import torch
+    from nanogpt import model as model_mod
+    from nanogpt.checkpoint import load_model
+
+    model, cfg, ck = load_model(spec["ckpt"], "cuda", torch.bfloat16)
+    del ck
+    if spec["T"] > cfg.block_size:
+        raise ValueError(f"T={spec['T']} exceeds the checkpoint's block_size {cfg.block_size}")
+    frozen = sum(int(b.attn.dyn_frozen.sum()) for b in model.transformer.h)
+    x = torch.randint(0, cfg.vocab_size, (spec["B"], spec["T"]),
+                      generator=torch.Generator().manual_seed(spec["seed"] + 1)).cuda()
+    with torch.inference_mode():
+        n0 = model_mod.fused_dispatch_count()
+        model(x)
+        torch.cuda.synchronize()
+        calls = model_mod.fused_dispatch_count() - n0
+        if calls != cfg.n_layer:
+            raise RuntimeError(f"expected {cfg.n_layer} fused dispatches, observed {calls}")
+        for _ in range(spec["warmup"]):
+            model(x)
+        torch.cuda.synchronize()
+        step = lambda: model(x)
+        capture_ms = None
+        if spec["graph"]:
+            side = torch.cuda.Stream()
+            side.wait_stream(torch.cuda.current_stream())
+            with torch.cuda.stream(side):
+                for _ in range(3):
+                    model(x)
+            torch.cuda.current_stream().wait_stream(side)
+            torch.cuda.synchronize()
+            graph = torch.cuda.CUDAGraph()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            with torch.cuda.graph(graph):
+                out = model(x)
+            e1.record()
+            torch.cuda.synchronize()
+            capture_ms = e0.elapsed_time(e1)
+            eager = model(x)
+            graph.replay()
+            torch.cuda.synchronize()
+            a, b = out.double().flatten(), eager.double().flatten()
+            cos = float(a @ b / (a.norm() * b.norm()))
+            if cos < 0.9999:
+                raise RuntimeError(f"graph replay differs from the eager prefill (cosine {cos:.6f})")
+            step = graph.replay
+        ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+              for _ in range(spec["iters"])]
+        for a, b in ev:
+            a.record()
+            step()
+            b.record()
+        torch.cuda.synchronize()
+    ms = [a.elapsed_time(b) for a, b in ev]
+    med = statistics.median(ms)
+    return {"variant": spec["variant"], "ckpt": os.path.basename(spec["ckpt"]), "frozen_heads": frozen,
+            "median_ms": round(med, 4), "p10_ms": round(sorted(ms)[len(ms) // 10], 4),
+            "p90_ms": round(sorted(ms)[(9 * len(ms)) // 10], 4),
+            "tokens_per_s": round(spec["B"] * spec["T"] / (med / 1000.0), 1),
+            "execution": "hip_graph" if spec["graph"] else "eager",
+            "graph_capture_ms": None if capture_ms is None else round(capture_ms, 2)}
+
+
+def _ckpt_leg_child(spec, conn):
+    try:
+        conn.send(ckpt_leg(spec))
+    except Exception as e:  # reported by the parent
+        conn.send({"error": f"{type(e).__name__}: {e}"})
+    conn.close()
+
+
+def run_ckpt(args):
+    """Prefill of a loaded checkpoint pair (nanogpt/bench_checkpoint_prefill.py):
+    the frozen export through the fused path against its full (all-live)
+    export, B x T square causal prefill, optional HIP graph replay
+    (--graph), and with --isolate every leg in a fresh spawned process in
+    ABBA order per repeat.  Without --ckpt a synthetic pair is written
+    (build_ckpt_pair)."""
+    import multiprocessing as mp
+    import tempfile
+
+    T = args.seq_len or 4096
+    B = args.batch or 8
+    tmp = None
+    if args.ckpt:
+        base, frozen = args.ckpt_baseline, args.ckpt
+    else:
+        tmp = tempfile.mkdtemp(prefix="saf_ckpt_")
+        log(f"writing a synthetic checkpoint pair (T={T}) to {tmp}")
+        base, frozen = build_ckpt_pair(tmp, T)
+    legs = []
+    for r in range(args.repeats):
+        order = [("baseline", base), ("frozen", frozen)]
+        order = order + order[::-1] if args.isolate else order
+        for variant, path in order:
+            if path is None:
+                continue
+            legs.append({"variant": variant, "ckpt": path, "T": T, "B": B, "seed": 1337 + r,
+                         "warmup": args.warmup, "iters": args.steps, "graph": args.graph, "repeat": r})
+    results = []
+    for spec in legs:
+        if args.isolate:
+            ctx = mp.get_context("spawn")
+            parent, child = ctx.Pipe()
+            proc = ctx.Process(target=_ckpt_leg_child, args=(spec, child))
+            proc.start()
+            res = parent.recv()
+            proc.join()
+            if "error" in res:
+                raise RuntimeError(f"leg {spec['variant']} failed: {res['error']}")
+        else:
+            res = ckpt_leg(spec)
+        res["repeat"] = spec["repeat"]
+        log(f"{res['variant']}: {res['median_ms']:.3f} ms ({res['tokens_per_s']:.0f} tokens/s)")
+        results.append(res)
+    if tmp is not None:
+        for f in os.listdir(tmp):
+            os.remove(os.path.join(tmp, f))
+        os.rmdir(tmp)
+    med = lambda v: statistics.median(x["median_ms"] for x in results if x["variant"] == v)
+    f_ms = med("frozen")
+    line = {
+        "metric": "prefill tokens/sec of a loaded SAF checkpoint (1 GPU)",
+        "value": round(B * T / (f_ms / 1000.0), 1), "unit": "tokens/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(f_ms, 4),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+        "data": "synthetic tokens; " + ("checkpoint files given" if args.ckpt else
+                                        "synthetic export pair in the reference layout (seed 1337)"),
+        "config": {"workload": f"checkpoint prefill: B={B}, T={T}, "
+                               + ("isolated ABBA legs" if args.isolate else "in-process legs")
+                               + (", HIP graph replay" if args.graph else ", eager"),
+                   "frozen_ckpt": os.path.basename(frozen),
+                   "baseline_ckpt": None if base is None else os.path.basename(base)},
+        "roofline": None,
+        "cpu_baseline": None,
+        "legs": results,
+    }
+    if base is not None:
+        b_ms = med("baseline")
+        line["baseline_tokens_per_s"] = round(B * T / (b_ms / 1000.0), 1)
+        line["speedup_vs_full"] = round(b_ms / f_ms, 4)
+    print(json.dumps(line), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=10)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--workload", choices=["c1", "c2", "c3", "c4", "scan", "bwd", "logz"], default="c2",
+    ap.add_argument("--workload", choices=["c1", "c2", "c3", "c4", "scan", "bwd", "logz", "ckpt"], default="c2",
                     help="c1: the isolated op (decay heads as scan / rebuild / dense); "
                          "c2: 124M nanoGPT SAF-25%% at 16K (the headline); c3: 1B-class with dense "
                          "frozen patterns; c4: Qwen-style GQA; "
                          "scan: frozen-only sizing run of the closed-form scan (HBM roofline); "
-                         "bwd: the C1 op forward + backward; logz: freeze-time row normalisers")
+                         "bwd: the C1 op forward + backward; logz: freeze-time row normalisers; "
+                         "ckpt: prefill of a loaded checkpoint pair")
+    ap.add_argument("--ckpt", default=None, help="ckpt: frozen export (default: a synthetic pair)")
+    ap.add_argument("--ckpt-baseline", default=None, help="ckpt: the matching full export")
+    ap.add_argument("--graph", action="store_true", help="ckpt: time HIP graph replays of the prefill")
+    ap.add_argument("--isolate", action="store_true",
+                    help="ckpt: every leg in a fresh spawned process, ABBA order per repeat")
+    ap.add_argument("--repeats", type=int, default=1, help="ckpt: repeats of the leg order")
     ap.add_argument("--seq-len", type=int, default=None)
-    ap.add_argument("--batch", type=int, default=None, help="c4 only (default 4)")
+    ap.add_argument("--batch", type=int, default=None, help="c1 / c4 / scan / ckpt batch (defaults 8 / 4 / 8 / 8)")
     ap.add_argument("--layers", type=int, default=None)
     ap.add_argument("--rate", type=float, default=0.25, help="c4: frozen fraction of query heads")
     ap.add_argument("--prior-repr", choices=["decomposed", "dense"], default="decomposed",
@@ -915,6 +1106,9 @@ def main():
         return
     if args.workload == "scan":
         run_scan(args)
+        return
+    if args.workload == "ckpt":
+        run_ckpt(args)
         return
     if args.workload == "bwd":
         run_bwd(args)

@@ -149,6 +149,51 @@ def convert_state_dict(state_dict, model: GPT):
     return out
 
 
+def reference_state_dict(model: GPT, compile_prefix: bool = False):
+    """This build's GPT state in the reference's export layout, the inverse
+    of convert_state_dict: dense priors expanded to the (n_head, S, S)
+    ``dyn_pattern`` with zero rows for the other heads, the derived
+    (n_head, 64, S) ``dyn_rho_band`` added for decomposed models (rows
+    rho[r - u + S - 64], -inf outside [0, S): kernel/fused_attn.py:65-80),
+    no pattern slot table.  compile_prefix adds torch.compile's ``_orig_mod.``."""
+    from kernel.fused_attn import make_rho_band
+    out = {}
+    for k, v in model.state_dict().items():
+        if k.endswith(".attn.dyn_pattern") or k.endswith(".attn.dyn_pattern_slot"):
+            continue
+        out[k] = v.detach().cpu().clone()
+    for i, blk in enumerate(model.transformer.h):
+        a = blk.attn
+        pre = f"transformer.h.{i}.attn."
+        H, S = a.n_head, a.block_size
+        if a.dyn_pattern is not None:
+            full = torch.zeros(H, S, S, dtype=a.dyn_pattern.dtype)
+            for h in range(H):
+                slot = int(a.dyn_pattern_slot[h])
+                if slot >= 0:
+                    full[h] = a.dyn_pattern[slot].cpu()
+            out[pre + "dyn_pattern"] = full
+        if a.dyn_alpha is not None:
+            out[pre + "dyn_rho_band"] = make_rho_band(a.dyn_rho.detach().float().cpu())
+    if compile_prefix:
+        out = {_PREFIX + k: v for k, v in out.items()}
+    return out
+
+
+def save_reference_checkpoint(model: GPT, path, **extra):
+    """Write ``model`` as a checkpoint file in the reference's layout
+    (``model`` + ``model_args``, as nanogpt/train.py saves it), loadable by
+    load_model here and, for the fields the reference reads, by
+    eval_nanogpt_logprobs.py:load_model there.  ``extra`` entries (e.g.
+    iter_num) are stored beside them."""
+    cfg = model.config
+    model_args = {f.name: getattr(cfg, f.name) for f in dataclasses.fields(GPTConfig)}
+    ck = {"model": reference_state_dict(model, compile_prefix=True), "model_args": model_args}
+    ck.update(extra)
+    torch.save(ck, path)
+    return path
+
+
 def load_model(ckpt_path, device, dtype=None):
     """(model, cfg, ckpt) for a reference checkpoint file, in eval mode on
     ``device`` (and ``dtype`` if given; alpha / rho / z stay fp32)

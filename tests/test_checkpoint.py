@@ -183,3 +183,24 @@ def test_gpu_loaded_export_matches_oracle(tmp_path):
     sd, ocfg, freeze = _oracle_inputs(m0)
     ref = model_oracle.gpt_forward(sd, ocfg, freeze, x, path="eager", all_positions=True)
     assert _cos(got, ref) >= 0.9999
+
+
+def test_reference_writer_matches_layout_and_round_trips(tmp_path):
+    """save_reference_checkpoint writes the layout of _reference_layout (the
+    test's own statement of the reference export) and load_model restores
+    every weight and freeze buffer bit for bit."""
+    from nanogpt.checkpoint import load_model, reference_state_dict, save_reference_checkpoint
+    m0, _ = _small_model(T=64, layers=2)
+    want = _reference_layout(m0)
+    got = reference_state_dict(m0, compile_prefix=True)
+    assert set(got) == set(want)
+    for k, v in want.items():
+        if k.endswith("dyn_rho_band"):
+            assert got[k].shape == v.shape
+            continue
+        assert torch.equal(got[k], v), k
+    p = save_reference_checkpoint(m0, tmp_path / "w.pt", iter_num=7)
+    m1, cfg1, ck = load_model(p, "cpu")
+    assert ck["iter_num"] == 7
+    for k, v in m0.state_dict().items():
+        assert torch.equal(m1.state_dict()[k], v), k
