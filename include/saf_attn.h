@@ -25,12 +25,15 @@
  *     8-byte boundaries (status SAF_EALIGN otherwise: make the tensor
  *     contiguous and call again).
  *   - The caller allocates every buffer, including out, the optional lse and
- *     the workspace.  The library allocates no device memory.
+ *     the workspace.  The library allocates no device memory; its one device
+ *     array (the scratch of saf_mixed_attn_fwd_noalloc) exists from the
+ *     library's load on each GPU it runs on.
  *   - Head-routing tables (frozen, hidx, pidx, kvidx, closed_kind,
  *     closed_param) are HOST arrays of n_heads entries, read during the call.
  *   - Kernels are enqueued on `stream` (a hipStream_t) without any host
  *     synchronisation.  Calls are re-entrant; the only mutable global state is
- *     the thread-local error string.
+ *     the thread-local error string (and the noalloc scratch array, shared by
+ *     the calls of that one entry point).
  *   - Return value: SAF_OK (0) or a negative status; saf_last_error() then
  *     holds a message for the calling thread.
  */
@@ -146,6 +149,22 @@ int saf_mixed_attn_bwd(const saf_mixed_attn_args* args, const saf_tensor_t* dout
                        const saf_tensor_t* dk, const saf_tensor_t* dv, void* stream);
 int64_t saf_mixed_attn_bwd_workspace_bytes(const saf_mixed_attn_args* args);
 
+/* Gradients of the decomposed heads' pattern parameters (trainable alpha /
+ * rho; replaces _parameter_backward and PatternGradient.backward,
+ * supplement/trainable_pattern_kernels.py:20-80, and the dispatch of
+ * supplement/trainable_patterns.py:61-93).  args is the forward's argument
+ * block (z the normalisers of the current alpha / rho), with a workspace of
+ * saf_decomp_param_bwd_workspace_bytes() bytes; for every state-2 head
+ * (closed-form ones through their buffers), summed over the batch:
+ *   dS[i, j] = P[i, j] (dP[i, j] - delta_i), dP = dO V^T, delta_i = dO_i . out_i,
+ *   dalpha[h, j] += sum_i dS[i, j],  drho[h, d] += sum_{i-j=d} dS[i, j]
+ * into (H, S) float32 dalpha / drho that the caller zeroes (accumulated with
+ * atomic adds: the summation order, and so the last bits, vary between
+ * runs).  kvidx (GQA) is refused. */
+int saf_decomp_param_bwd(const saf_mixed_attn_args* args, const saf_tensor_t* dout, const saf_tensor_t* dalpha,
+                         const saf_tensor_t* drho, void* stream);
+int64_t saf_decomp_param_bwd_workspace_bytes(const saf_mixed_attn_args* args);
+
 /* frozen_pv: out[b, f] = patt[fz_idx[f], :T, :T] @ v[b, f] for compact
  * frozen-head values v (B, nf, T, HD); fz_idx is a host array of nf entries. */
 int saf_frozen_pv_fwd(const saf_tensor_t* patt, const saf_tensor_t* v, const int32_t* fz_idx,
@@ -197,6 +216,19 @@ int saf_add_layernorm(const saf_tensor_t* x, const saf_tensor_t* delta, const sa
  * of materialised (H, rows, S) logits at freeze time (nanogpt/model.py) and
  * per call when alpha comes without z (kernel/fused_attn.py:690-694). */
 int saf_decomposed_logz(const saf_tensor_t* alpha, const saf_tensor_t* rho, const saf_tensor_t* z, void* stream);
+
+/* Backward of saf_decomposed_logz for an upstream gradient gz = dL/dz:
+ *   dalpha[h, j] = sum_{i >= j} gz[h, i] exp(alpha[h, j] + rho[h, i - j] - z[h, i])
+ *   drho[h, d]   = sum_{i >= d} gz[h, i] exp(alpha[h, i - d] + rho[h, d] - z[h, i])
+ * with z the forward's normalisers; all six (H, S) fp32 with unit column
+ * stride; dalpha and drho are written (not accumulated).  Rows whose z is
+ * -inf contribute nothing.  Replaces the autograd of the reference's
+ * differentiable normalisers decomp_log_normalizers_fft
+ * (nanogpt/dynamic_freeze.py:330-361), which the pattern fits backpropagate
+ * through (:362-390); the sums here are exact O(S^2) sweeps, not an FFT. */
+int saf_decomposed_logz_bwd(const saf_tensor_t* alpha, const saf_tensor_t* rho, const saf_tensor_t* z,
+                            const saf_tensor_t* gz, const saf_tensor_t* dalpha, const saf_tensor_t* drho,
+                            void* stream);
 
 /* Workspace needed by saf_frozen_scan_fwd for n_scan_heads closed-form heads
  * (0 bytes when there are none). */

@@ -18,6 +18,11 @@ Each function restates the reference's algorithm from its source
   make_rho_band           kernel/fused_attn.py:65-80
   decomp_pattern          nanogpt/model.py:796-803 (exp(L - z))
   frozen_pv               kernel/frozen_attn.py:185-192 / test_frozen_attn.py:27-28
+  logz_grads              d z / d(alpha, rho) of decomposed_logz, the autograd of
+                          decomp_log_normalizers_fft (nanogpt/dynamic_freeze.py:330-361)
+  pattern_grads           dalpha / drho of decomposed heads' outputs
+                          (supplement/trainable_pattern_kernels.py:20-56,
+                          the softmax derivative of supplement/trainable_patterns.py:7-13)
   mean/decay/window       supplement/attention.py:10-25 (causal mean),
                           nanogpt/model.py:338-353 (uniform, local_window),
                           nanogpt/test_prior_flash.py:47-59 (exp(-dist/scale))
@@ -330,6 +335,50 @@ def eager_mixed_attention_grads(q, k, v, frozen, dout, hidx=None, pidx=None, pat
         for b in range(B):
             dv[b, h] += P.T @ dout[b, h]
     return dq, dk, dv
+
+
+def logz_grads(alpha, rho, gz):
+    """dalpha, drho of sum_i gz[h, i] z[h, i], z = decomposed_logz(alpha, rho):
+    dalpha_j = sum_{i>=j} gz_i P_ij, drho_d = sum_{i-j=d} gz_i P_ij with P the
+    row softmax of alpha_j + rho_{i-j} (float64)."""
+    alpha, rho, gz = _f64(alpha), _f64(rho), _f64(gz)
+    H, S = alpha.shape
+    P = decomp_pattern(alpha, rho, decomposed_logz(alpha, rho), S)
+    P = np.nan_to_num(P, nan=0.0)
+    W = gz[:, :, None] * P                       # (H, i, j)
+    da = W.sum(1)
+    dr = np.zeros((H, S))
+    for d in range(S):
+        dr[:, d] = np.trace(W, offset=-d, axis1=1, axis2=2)
+    return da, dr
+
+
+def pattern_grads(v, dout, frozen, alpha, rho, heads=None):
+    """dalpha, drho (H, S) of sum(dout * y) over the decomposed heads (state
+    2) of eager_mixed_attention, summed over the batch: with P the row
+    softmax of alpha_j + rho_{i-j}, y = P V, dP = dO V^T, delta_i = dO_i . y_i,
+    dS = P (dP - delta) and dalpha_j = sum_i dS_ij, drho_d = sum_{i-j=d} dS_ij
+    (float64, v / dout (B, H, T, HD))."""
+    v, dout = _f64(v), _f64(dout)
+    alpha, rho = _f64(alpha), _f64(rho)
+    H, S = alpha.shape
+    B, _, T, _ = v.shape
+    da = np.zeros((H, S))
+    dr = np.zeros((H, S))
+    for h in (range(H) if heads is None else heads):
+        if int(np.asarray(frozen)[h]) != 2:
+            continue
+        a, r = alpha[h:h + 1], rho[h:h + 1]
+        P = decomp_pattern(a, r, decomposed_logz(a, r), T)[0]
+        for b in range(B):
+            y = P @ v[b, h]
+            dP = dout[b, h] @ v[b, h].T
+            delta = (dout[b, h] * y).sum(-1, keepdims=True)
+            dS = P * (dP - delta)
+            da[h, :T] += dS.sum(0)
+            for d in range(T):
+                dr[h, d] += np.trace(dS, offset=-d)
+    return da, dr
 
 
 def frozen_pv(patt, v, fz_idx, T):

@@ -421,6 +421,135 @@ __global__ __launch_bounds__(256) void bwd_frozen_dv_kernel(const BwdParams p) {
   if (kv) store_out_tile<T, HD>(dvbase + (int64_t)kk * p.dv_st, dva, 1.f, g);
 }
 
+// Parameter gradients of decomposed frozen heads (trainable alpha / rho,
+// supplement/trainable_pattern_kernels.py:20-56 of the reference): with
+// P[i, j] = exp(alpha_j + rho_{i-j} - z_i) the softmax of alpha + rho over
+// j <= i, dP = dO V^T and delta_i = dO_i . O_i,
+//   dS[i, j] = P[i, j] (dP[i, j] - delta_i),
+//   dalpha[h, j] += sum_i dS[i, j],   drho[h, d] += sum_{i - j = d} dS[i, j]
+// (z's own dependence on alpha and rho is inside the softmax derivative).
+// Workgroup = 4 waves x 32 keys of one (batch, decomposed slot); query blocks
+// of 64 from the diagonal to T (dO tiles double-buffered in LDS by DMA, the
+// block's z, delta and rho window staged in LDS).  Per 32-query sub-block a
+// wave forms dP = dO V^T with the queries in the kperm row order (the lane is
+// the key, register i of lane-half g is query acc_key(i, g)), rebuilds P and
+// forms dS; dalpha accumulates per lane over every block and goes out with one
+// atomic add per key; drho goes through a ring of 256 LDS accumulators indexed
+// by distance (ds_add_f32): the distances a block can reach form a window of
+// 64 + 128 - 1 that slides by 64 per block, so after each block the 64
+// distances no later block reaches are added to drho (global atomics) and
+// their slots cleared.
+template <typename T, int HD>
+__global__ __launch_bounds__(256) void bwd_decomp_param_kernel(const BwdParams p) {
+  constexpr int BN = kBwdWaves * 32, NKT = HD / 16, VB = VRow<HD>::BYTES;
+  constexpr int RING = 256;
+  static_assert(RING >= 64 + BN - 1 + 64, "the distance ring must hold a block's window and the lag");
+  __shared__ __align__(16) char o0[VB], o1[VB];
+  __shared__ float zd0[128], zd1[128];        // z log2 e (0..63) and delta (64..127) of the block's queries
+  __shared__ float rs0[64 + BN], rs1[64 + BN];  // rho log2 e for the block's distances
+  __shared__ float ring[RING];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int n = lane & 31, g = lane >> 5;
+  const int T_len = p.T;
+  const int nbh = p.B * p.n_live;               // slots here are the decomposed heads
+  const int r = blockIdx.x % nbh;
+  const int kb = (int)(blockIdx.x / nbh);       // heaviest (most queries) first
+  const int b = r / p.n_live, slot = r % p.n_live;
+  const int h = p.out_head[slot], ph = p.pat_head[slot];
+  const T* vbase = reinterpret_cast<const T*>(p.v) + b * p.v_sb + (int64_t)h * p.v_sh;
+  const T* dobase = reinterpret_cast<const T*>(p.dout) + b * p.do_sb + (int64_t)h * p.do_sh;
+  const float* dlbase = p.delta + ((int64_t)b * p.n_live + slot) * T_len;
+
+  const int kblo = kb * BN;
+  const int k0w = kblo + wave * 32;
+  const int kk = k0w + n;
+  const bool kv = kk < T_len;
+  uint4 vf[NKT];
+#pragma unroll
+  for (int t = 0; t < NKT; ++t)
+    vf[t] = kv ? load16(vbase + (int64_t)kk * p.v_st + 16 * t + 8 * g) : make_uint4(0, 0, 0, 0);
+  const float alpha_k =
+      kv ? load_as_f32(p.alpha, (int64_t)ph * p.a_sh + (int64_t)kk * p.a_ss, p.a_dtype) * kLog2e : 0.f;
+  auto z_of = [&](int qq) {
+    return qq < T_len ? load_as_f32(p.z, (int64_t)ph * p.z_sh + (int64_t)qq * p.z_ss, p.z_dtype) * kLog2e : 0.f;
+  };
+  auto rho_of = [&](int dd) {
+    return (dd >= 0 && dd < T_len)
+               ? load_as_f32(p.rho, (int64_t)ph * p.r_sh + (int64_t)dd * p.r_ss, p.r_dtype) * kLog2e
+               : 0.f;
+  };
+  ring[tid] = 0.f;  // 256 threads, 256 slots
+
+  TileOffsets<T, HD> oo;
+  oo.init(wave, lane, p.do_st);
+  const int ib0 = kblo / 64, nqb = (T_len + 63) / 64;
+  // distances of query block i: [64 i - kblo - (BN - 1), 64 i + 63 - kblo]
+  auto dlo_of = [&](int i) { return 64 * i - kblo - (BN - 1); };
+  if (ib0 < nqb) {
+    oo.load(dobase, p.do_st, 64 * ib0, T_len, o0, wave);
+    if (tid < 64) {
+      zd0[tid] = z_of(64 * ib0 + tid);
+      zd0[64 + tid] = 64 * ib0 + tid < T_len ? dlbase[64 * ib0 + tid] : 0.f;
+    }
+    if (tid < 64 + BN - 1) rs0[tid] = rho_of(dlo_of(ib0) + tid);
+  }
+  float dacc = 0.f;
+  int flushed = 0;  // distances below this are in drho
+  for (int i = ib0; i < nqb; ++i) {
+    const char* ot = ((i - ib0) & 1) ? o1 : o0;
+    const float* zd = ((i - ib0) & 1) ? zd1 : zd0;
+    const float* rs = ((i - ib0) & 1) ? rs1 : rs0;
+    const int dmin = dlo_of(i);
+    __syncthreads();  // this block's tile and statistics are in LDS (and the ring is cleared)
+    float nz = 0.f, ndl = 0.f, nr = 0.f;
+    if (i + 1 < nqb) {
+      oo.load(dobase, p.do_st, 64 * (i + 1), T_len, ((i - ib0) & 1) ? o0 : o1, wave);
+      const int qq = 64 * (i + 1) + tid;
+      if (tid < 64) {
+        nz = z_of(qq);
+        ndl = qq < T_len ? dlbase[qq] : 0.f;
+      }
+      if (tid < 64 + BN - 1) nr = rho_of(dmin + 64 + tid);
+    }
+#pragma unroll
+    for (int qs2 = 0; qs2 < 2; ++qs2) {
+      if (64 * i + 32 * qs2 + 31 < k0w) continue;  // every query of the sub-block precedes this wave's keys
+      const int row = 32 * qs2 + kperm(n);
+      f32x16_t dp = zero16();
+#pragma unroll
+      for (int t = 0; t < NKT; ++t) dp = Elem<T>::mfma(tile_row_op<HD>(ot, row, 2 * t + g), vf[t], dp);
+#pragma unroll
+      for (int i2 = 0; i2 < 16; ++i2) {
+        const int ql = 32 * qs2 + acc_key(i2, g);
+        const int qq = 64 * i + ql;
+        const bool ok = kv && qq >= kk && qq < T_len;
+        const float pr = fast_exp2(ok ? alpha_k + rs[qq - kk - dmin] - zd[ql] : -__builtin_inff());
+        const float ds = pr * (dp[i2] - zd[64 + ql]);
+        dacc += ds;
+        if (ok) atomicAdd(&ring[(qq - kk) & (RING - 1)], ds);
+      }
+    }
+    if (tid < 64) {  // the idle slot's readers finished before the previous barrier
+      float* zn = ((i - ib0) & 1) ? zd0 : zd1;
+      zn[tid] = nz;
+      zn[64 + tid] = ndl;
+    }
+    if (tid < 64 + BN - 1) (((i - ib0) & 1) ? rs0 : rs1)[tid] = nr;
+    __syncthreads();  // every wave's ring updates of this block are in; the slot may be refilled
+    // distances below the next block's lowest are final
+    const int done = i + 1 < nqb ? min(max(dlo_of(i + 1), 0), T_len) : T_len;
+    for (int d = flushed + tid; d < done; d += 256) {
+      const float x = ring[d & (RING - 1)];
+      if (x != 0.f) atomicAdd(p.drho + (int64_t)ph * p.dr_hs + d, x);
+      ring[d & (RING - 1)] = 0.f;
+    }
+    flushed = max(flushed, done);
+  }
+  dacc = half_swap_sum(dacc);
+  if (kv && g == 0 && dacc != 0.f) atomicAdd(p.dalpha + (int64_t)ph * p.da_hs + kk, dacc);
+}
+
 // Explicit instantiations: the host pass emits a kernel's launch stub only
 // for an explicitly instantiated template here (implicit instantiation from
 // the launcher left the dK/dV and frozen-dV stubs undefined).
@@ -429,7 +558,8 @@ __global__ __launch_bounds__(256) void bwd_frozen_dv_kernel(const BwdParams p) {
   template __global__ void bwd_dq_kernel<T, HD>(const BwdParams);                       \
   template __global__ void bwd_dkdv_kernel<T, HD>(const BwdParams);                     \
   template __global__ void bwd_frozen_dv_kernel<T, HD, 1>(const BwdParams);             \
-  template __global__ void bwd_frozen_dv_kernel<T, HD, 2>(const BwdParams);
+  template __global__ void bwd_frozen_dv_kernel<T, HD, 2>(const BwdParams);             \
+  template __global__ void bwd_decomp_param_kernel<T, HD>(const BwdParams);
 #define SAF_BWD_INST_T(T) SAF_BWD_INST(T, 32) SAF_BWD_INST(T, 64) SAF_BWD_INST(T, 96) SAF_BWD_INST(T, 128)
 SAF_BWD_INST_T(__bf16)
 SAF_BWD_INST_T(_Float16)
@@ -454,12 +584,16 @@ static hipError_t bwd_launch_hd(const BwdParams& p, int which, hipStream_t s) {
     case 2:
       hipLaunchKernelGGL((bwd_dkdv_kernel<T, HD>), dim3((unsigned)(nk * p.B * p.n_live)), dim3(256), 0, s, p);
       break;
-    default: {
+    case 3: {
       const dim3 grid((unsigned)(nk * p.B * p.n_frozen));
       hipLaunchKernelGGL((bwd_frozen_dv_kernel<T, HD, 1>), grid, dim3(256), 0, s, p);
       hipLaunchKernelGGL((bwd_frozen_dv_kernel<T, HD, 2>), grid, dim3(256), 0, s, p);
       break;
     }
+    default:
+      hipLaunchKernelGGL((bwd_decomp_param_kernel<T, HD>), dim3((unsigned)(nk * p.B * p.n_live)), dim3(256), 0, s,
+                         p);
+      break;
   }
   return hipGetLastError();
 }
@@ -486,6 +620,9 @@ hipError_t launch_bwd_dq(const BwdParams& p, int dtype, int hd, hipStream_t s) {
 hipError_t launch_bwd_dkdv(const BwdParams& p, int dtype, int hd, hipStream_t s) { return bwd_dispatch(p, dtype, hd, 2, s); }
 hipError_t launch_bwd_frozen_dv(const BwdParams& p, int dtype, int hd, hipStream_t s) {
   return bwd_dispatch(p, dtype, hd, 3, s);
+}
+hipError_t launch_bwd_decomp_param(const BwdParams& p, int dtype, int hd, hipStream_t s) {
+  return bwd_dispatch(p, dtype, hd, 4, s);
 }
 
 }  // namespace saf

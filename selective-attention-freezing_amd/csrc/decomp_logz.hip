@@ -106,4 +106,87 @@ hipError_t launch_decomp_logz(const LogzParams& p, hipStream_t s) {
   return hipGetLastError();
 }
 
+
+// ---- backward of the row normalisers ------------------------------------------
+//   dalpha[h, j] = sum_{i >= j} gz[h, i] exp(alpha[h, j] + rho[h, i - j] - z[h, i])
+//   drho[h, d]   = sum_{i >= d} gz[h, i] exp(alpha[h, i - d] + rho[h, d] - z[h, i])
+// (the derivative of z = logsumexp_{j<=i}(alpha_j + rho_{i-j}); every term is
+// gz_i times a probability <= 1, so no shift is needed).  Both are one sweep
+// over the rows i >= o of an output index o: o's own logit part ("fixed":
+// alpha_j for dalpha, rho_d for drho) plus a window of the other vector at
+// i - o.  One work-group of 4 waves per (64-output block, head, which),
+// lane l owns output o = o0 + l; rows are staged in LDS chunks (gz_i and
+// -z_i log2 e, 0 / +inf-free for rows past S) with the window of the other
+// vector (-inf outside [0, S)), each wave sums a quarter of the chunk's rows,
+// and the four partial sums are added through LDS.  Rows whose z is -inf
+// (every logit -inf) contribute nothing.
+__global__ __launch_bounds__(64 * kLzWaves) void decomp_logz_bwd_kernel(const LogzBwdParams p) {
+  __shared__ float gs[kLzChunk], es[kLzChunk];
+  __shared__ float ws[kLzChunk + kLzRows];
+  __shared__ float part[kLzWaves][kLzRows];
+
+  constexpr float kLog2e = 1.4426950408889634f;
+  const float ninf = -__builtin_inff();
+  const int S = p.S;
+  const int nblk = (S + kLzRows - 1) / kLzRows;
+  const int o0 = (int)blockIdx.x * kLzRows;   // lightest blocks (late outputs) last
+  const int h = blockIdx.y;
+  const bool dr = blockIdx.z == 1;             // 0: dalpha, 1: drho
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const float* alpha = p.alpha + (int64_t)h * p.a_hs;
+  const float* rho = p.rho + (int64_t)h * p.r_hs;
+  const float* own = dr ? rho : alpha;       // logit part indexed by the output
+  const float* other = dr ? alpha : rho;     // logit part indexed by i - o
+  const int o = o0 + lane;
+  const float fixed = o < S ? own[o] * kLog2e : ninf;
+  (void)nblk;
+
+  float acc = 0.f;
+  for (int c0 = o0; c0 < S; c0 += kLzChunk) {
+    const int tlo = c0 - o0 - (kLzRows - 1);   // smallest i - o of the chunk
+    __syncthreads();
+    for (int t = tid; t < kLzChunk; t += 64 * kLzWaves) {
+      const int i = c0 + t;
+      float g = 0.f, e = ninf;
+      if (i < S) {
+        const float zi = p.z[(int64_t)h * p.z_hs + i];
+        if (zi != ninf) {
+          g = p.gz[(int64_t)h * p.g_hs + i];
+          e = -zi * kLog2e;
+        }
+      }
+      gs[t] = g;
+      es[t] = e;
+    }
+    for (int t = tid; t < kLzChunk + kLzRows - 1; t += 64 * kLzWaves) {
+      const int d = tlo + t;
+      ws[t] = (d >= 0 && d < S) ? other[d] * kLog2e : ninf;
+    }
+    __syncthreads();
+    const int tw0 = w * (kLzChunk / kLzWaves);
+    const int tw1 = min(tw0 + kLzChunk / kLzWaves, S - c0);
+    // window index of row c0 + t for this lane: (c0 + t) - o - tlo
+    const int wbase = kLzRows - 1 - lane;
+    for (int t = tw0; t < tw1; ++t) {
+      const float x = fixed + ws[wbase + t] + es[t];
+      acc = fmaf(gs[t], __builtin_amdgcn_exp2f(x), acc);
+    }
+  }
+  part[w][lane] = acc;
+  __syncthreads();
+  if (w == 0 && o < S) {
+    float tot = 0.f;
+#pragma unroll
+    for (int q = 0; q < kLzWaves; ++q) tot += part[q][lane];
+    float* out = dr ? p.drho + (int64_t)h * p.dr_hs : p.dalpha + (int64_t)h * p.da_hs;
+    out[o] = tot;
+  }
+}
+
+hipError_t launch_decomp_logz_bwd(const LogzBwdParams& p, hipStream_t s) {
+  const int nblk = (p.S + kLzRows - 1) / kLzRows;
+  hipLaunchKernelGGL(decomp_logz_bwd_kernel, dim3(nblk, p.H, 2), dim3(64 * kLzWaves), 0, s, p);
+  return hipGetLastError();
+}
+
 }  // namespace saf

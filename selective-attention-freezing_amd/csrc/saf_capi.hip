@@ -838,6 +838,38 @@ int saf_decomposed_logz(const saf_tensor_t* alpha, const saf_tensor_t* rho, cons
   return launched(launch_decomp_logz(p, reinterpret_cast<hipStream_t>(stream)), "decomposed_logz");
 }
 
+int saf_decomposed_logz_bwd(const saf_tensor_t* alpha, const saf_tensor_t* rho, const saf_tensor_t* z,
+                            const saf_tensor_t* gz, const saf_tensor_t* dalpha, const saf_tensor_t* drho,
+                            void* stream) {
+  const saf_tensor_t* ts[6] = {alpha, rho, z, gz, dalpha, drho};
+  const char* names[6] = {"alpha", "rho", "z", "gz", "dalpha", "drho"};
+  for (int i = 0; i < 6; ++i) {
+    if (ts[i] == nullptr || !present(*ts[i])) return fail(SAF_EINVAL, "%s is required", names[i]);
+    const saf_tensor_t& t = *ts[i];
+    if (t.ndim != 2 || t.size[0] != alpha->size[0] || t.size[1] != alpha->size[1])
+      return fail(SAF_EINVAL, "%s must be 2-D (H, S) like alpha", names[i]);
+    if (t.dtype != SAF_F32) return fail(SAF_EUNSUPPORTED, "%s must be fp32 (got %s)", names[i], dtype_name(t.dtype));
+    if (t.size[1] > 1 && t.stride[1] != 1) return fail(SAF_EALIGN, "%s needs a unit column stride", names[i]);
+  }
+  const int64_t H = alpha->size[0], S = alpha->size[1];
+  if (H > 65535 || S > (int64_t(1) << 30))
+    return fail(SAF_EUNSUPPORTED, "decomposed_logz backward: H = %lld, S = %lld out of range", (long long)H,
+                (long long)S);
+  if (H == 0 || S == 0) return SAF_OK;
+  LogzBwdParams p{};
+  p.alpha = static_cast<const float*>(alpha->data);
+  p.rho = static_cast<const float*>(rho->data);
+  p.z = static_cast<const float*>(z->data);
+  p.gz = static_cast<const float*>(gz->data);
+  p.dalpha = static_cast<float*>(dalpha->data);
+  p.drho = static_cast<float*>(drho->data);
+  p.a_hs = alpha->stride[0]; p.r_hs = rho->stride[0]; p.z_hs = z->stride[0]; p.g_hs = gz->stride[0];
+  p.da_hs = dalpha->stride[0]; p.dr_hs = drho->stride[0];
+  p.H = (int)H;
+  p.S = (int)S;
+  return launched(launch_decomp_logz_bwd(p, reinterpret_cast<hipStream_t>(stream)), "decomposed_logz backward");
+}
+
 // ---- backward -------------------------------------------------------------
 
 static int64_t bwd_delta_bytes(const Plan& pl) {
@@ -960,6 +992,86 @@ int saf_mixed_attn_bwd(const saf_mixed_attn_args* a, const saf_tensor_t* dout, c
     if (int rc = launched(launch_bwd_frozen_dv(p, pl.dtype, pl.HD, s), "backward frozen dv")) return rc;
   }
   return SAF_OK;
+}
+
+static std::vector<int> decomp_heads_all(const Plan& pl) {
+  std::vector<int> v = pl.decomp;
+  v.insert(v.end(), pl.scan.begin(), pl.scan.end());
+  std::sort(v.begin(), v.end());
+  return v;
+}
+
+int64_t saf_decomp_param_bwd_workspace_bytes(const saf_mixed_attn_args* args) {
+  Plan pl;
+  if (plan_and_validate(args, 0, pl, false)) return -1;
+  const int64_t n = (int64_t)pl.B * (int64_t)decomp_heads_all(pl).size() * pl.T;
+  return (n * 4 + 255) / 256 * 256;
+}
+
+int saf_decomp_param_bwd(const saf_mixed_attn_args* a, const saf_tensor_t* dout, const saf_tensor_t* dalpha,
+                         const saf_tensor_t* drho, void* stream) {
+  Plan pl;
+  if (int rc = plan_and_validate(a, 0, pl, false)) return rc;
+  if (a->kvidx != nullptr)
+    return fail(SAF_EUNSUPPORTED, "pattern gradients with kvidx (GQA) are not implemented (forward / prefill only)");
+  if (dout == nullptr || dalpha == nullptr || drho == nullptr)
+    return fail(SAF_EINVAL, "dout, dalpha and drho are required");
+  const std::vector<int> heads = decomp_heads_all(pl);
+  if (heads.empty() || pl.T == 0 || pl.B == 0) return SAF_OK;
+  const saf_tensor_t* bufs[3] = {&a->alpha, &a->rho, &a->z};
+  const char* names[3] = {"alpha", "rho", "z"};
+  for (int i = 0; i < 3; ++i) {
+    const saf_tensor_t& t = *bufs[i];
+    if (!present(t) || t.ndim != 2 || t.size[0] != pl.H || t.size[1] < pl.T)
+      return fail(SAF_EINVAL, "pattern gradients need the (H, S) decomposed buffers (%s)", names[i]);
+    if (t.dtype != SAF_F32 && t.dtype != SAF_BF16 && t.dtype != SAF_F16)
+      return fail(SAF_EUNSUPPORTED, "unsupported %s dtype %s", names[i], dtype_name(t.dtype));
+  }
+  const saf_tensor_t* gr[2] = {dalpha, drho};
+  for (int i = 0; i < 2; ++i) {
+    const saf_tensor_t& t = *gr[i];
+    if (!present(t) || t.ndim != 2 || t.size[0] != pl.H || t.size[1] < pl.T || t.dtype != SAF_F32)
+      return fail(SAF_EINVAL, "dalpha and drho must be (H, S) float32 with S >= T");
+    if (t.size[1] > 1 && t.stride[1] != 1) return fail(SAF_EALIGN, "dalpha and drho need a unit column stride");
+  }
+  if (!present(*dout) || dout->ndim != 4 || dout->dtype != a->out.dtype)
+    return fail(SAF_EINVAL, "dout must match out's shape and dtype");
+  for (int i = 0; i < 4; ++i)
+    if (dout->size[i] != a->out.size[i]) return fail(SAF_EINVAL, "dout must match out's shape and dtype");
+  if (int rc = check_act(*dout, "dout", 16)) return rc;
+  if (int rc = check_act(a->out, "out", 16)) return rc;
+  if ((int)heads.size() > kMaxHeads) return fail(SAF_EUNSUPPORTED, "too many decomposed heads");
+  const int64_t need = saf_decomp_param_bwd_workspace_bytes(a);
+  if (a->workspace == nullptr || a->workspace_bytes < need || reinterpret_cast<uintptr_t>(a->workspace) % 16 != 0)
+    return fail(SAF_EWORKSPACE, "pattern gradients need a 16-byte aligned %lld-byte workspace (got %lld)",
+                (long long)need, (long long)a->workspace_bytes);
+  BwdParams p{};
+  p.v = a->v.data;
+  p.out = a->out.data;
+  p.dout = dout->data;
+  p.v_sb = a->v.stride[0]; p.v_sh = a->v.stride[1]; p.v_st = a->v.stride[2];
+  p.o_sb = a->out.stride[0]; p.o_sh = a->out.stride[1]; p.o_st = a->out.stride[2];
+  p.do_sb = dout->stride[0]; p.do_sh = dout->stride[1]; p.do_st = dout->stride[2];
+  p.B = pl.B;
+  p.T = pl.T;
+  p.n_live = (int)heads.size();   // the decomposed heads take the live slots here
+  for (int i = 0; i < p.n_live; ++i) {
+    p.out_head[i] = (int16_t)heads[i];
+    p.pat_head[i] = (int16_t)heads[i];
+  }
+  p.delta = reinterpret_cast<float*>(a->workspace);
+  p.alpha = a->alpha.data; p.rho = a->rho.data; p.z = a->z.data;
+  p.a_dtype = a->alpha.dtype; p.r_dtype = a->rho.dtype; p.z_dtype = a->z.dtype;
+  p.a_sh = a->alpha.stride[0]; p.a_ss = a->alpha.stride[1];
+  p.r_sh = a->rho.stride[0]; p.r_ss = a->rho.stride[1];
+  p.z_sh = a->z.stride[0]; p.z_ss = a->z.stride[1];
+  p.dalpha = static_cast<float*>(dalpha->data);
+  p.drho = static_cast<float*>(drho->data);
+  p.da_hs = dalpha->stride[0];
+  p.dr_hs = drho->stride[0];
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  if (int rc = launched(launch_bwd_delta(p, pl.dtype, pl.HD, st), "pattern-gradient delta")) return rc;
+  return launched(launch_bwd_decomp_param(p, pl.dtype, pl.HD, st), "pattern gradients");
 }
 
 int64_t saf_mixed_attn_workspace_bytes(const saf_mixed_attn_args* args) {

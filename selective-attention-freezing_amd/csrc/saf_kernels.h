@@ -181,6 +181,20 @@ struct LogzParams {
 
 hipError_t launch_decomp_logz(const LogzParams& p, hipStream_t s);
 
+// Backward of the row normalisers: dalpha, drho (H, S) fp32 from gz = dL/dz.
+struct LogzBwdParams {
+  const float* alpha;
+  const float* rho;
+  const float* z;
+  const float* gz;
+  float* dalpha;
+  float* drho;
+  int64_t a_hs, r_hs, z_hs, g_hs, da_hs, dr_hs;
+  int H, S;
+};
+
+hipError_t launch_decomp_logz_bwd(const LogzBwdParams& p, hipStream_t s);
+
 // Backward of the mixed-head operator (gradients of out = attention(q, k, v)
 // with respect to q, k, v; patterns and decomposed buffers are constants).
 // Live slots index the compact q/k (q_head) and the natural head (out_head);
@@ -222,6 +236,10 @@ struct BwdParams {
   const void* z;
   int a_dtype, r_dtype, z_dtype;
   int64_t a_sh, a_ss, r_sh, r_ss, z_sh, z_ss;
+  // parameter gradients of decomposed heads (fp32 (H, S), accumulated)
+  float* dalpha;
+  float* drho;
+  int64_t da_hs, dr_hs;
 };
 static_assert(sizeof(BwdParams) <= 4096, "BwdParams must fit the kernel argument segment");
 
@@ -231,6 +249,9 @@ hipError_t launch_bwd_delta(const BwdParams& p, int dtype, int hd, hipStream_t s
 hipError_t launch_bwd_dq(const BwdParams& p, int dtype, int hd, hipStream_t s);
 hipError_t launch_bwd_dkdv(const BwdParams& p, int dtype, int hd, hipStream_t s);
 hipError_t launch_bwd_frozen_dv(const BwdParams& p, int dtype, int hd, hipStream_t s);
+// dalpha / drho of the decomposed heads: slots 0..n_live-1 are the decomposed
+// heads (out_head = head, pat_head = buffer row), delta of those rows in p.delta.
+hipError_t launch_bwd_decomp_param(const BwdParams& p, int dtype, int hd, hipStream_t s);
 
 // Queries per frozen-head workgroup (4 waves) for a query-tile count.
 inline int block_rows(int qt) { return 4 * 32 * qt; }

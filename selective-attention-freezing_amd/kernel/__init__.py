@@ -16,6 +16,7 @@ from .indexed_linear import linear_rows, linear_rows2, linear_permuted_cols
 from .rope import rope_qk_, qk_rmsnorm_rope_
 from .layernorm import add_layernorm_
 from .fused_attn import (fused_mixed_attn, fused_attn_usable, decomposed_logz,
+                         decomp_log_normalizers, decomp_log_normalizers_fft,
                          decomp_logits, make_rho_band, BAND_ROWS,
                          classify_closed_form, CLOSED_NONE, CLOSED_MEAN,
                          CLOSED_DECAY, CLOSED_WINDOW, KernelTimer, set_kernel_timer)
@@ -23,6 +24,7 @@ from .fused_attn import (fused_mixed_attn, fused_attn_usable, decomposed_logz,
 __all__ = ["frozen_pv", "frozen_pv_usable", "HAVE_TRITON",
            "linear_rows", "linear_rows2", "linear_permuted_cols",
            "fused_mixed_attn", "fused_attn_usable", "decomposed_logz",
+           "decomp_log_normalizers", "decomp_log_normalizers_fft",
            "decomp_logits", "make_rho_band", "BAND_ROWS",
            "classify_closed_form", "CLOSED_NONE", "CLOSED_MEAN",
            "CLOSED_DECAY", "CLOSED_WINDOW", "KernelTimer", "set_kernel_timer",

@@ -22,9 +22,10 @@ _DTYPE_CODE = {torch.float32: SAF_F32, torch.float16: SAF_F16,
 # Exported symbols, in header order (checked by the CPU test suite).
 EXPORTS = ("saf_mixed_attn_fwd", "saf_mixed_attn_fwd_noalloc", "saf_flash_fwd", "saf_frozen_dense_pv_fwd",
            "saf_frozen_decomp_fwd", "saf_frozen_scan_fwd", "saf_mixed_attn_bwd",
-           "saf_mixed_attn_bwd_workspace_bytes", "saf_frozen_pv_fwd", "saf_frozen_pv_bwd",
+           "saf_mixed_attn_bwd_workspace_bytes", "saf_decomp_param_bwd", "saf_decomp_param_bwd_workspace_bytes",
+           "saf_frozen_pv_fwd", "saf_frozen_pv_bwd",
            "saf_rope_qk_inplace", "saf_qk_rmsnorm_rope_inplace", "saf_add_layernorm",
-           "saf_decomposed_logz", "saf_workspace_bytes", "saf_mixed_attn_workspace_bytes",
+           "saf_decomposed_logz", "saf_decomposed_logz_bwd", "saf_workspace_bytes", "saf_mixed_attn_workspace_bytes",
            "saf_workspace_error", "saf_time_next_kernel", "saf_last_error", "saf_version")
 
 
@@ -80,6 +81,10 @@ def lib():
         L.saf_mixed_attn_bwd.restype = ctypes.c_int
         L.saf_mixed_attn_bwd_workspace_bytes.argtypes = [P(SafMixedAttnArgs)]
         L.saf_mixed_attn_bwd_workspace_bytes.restype = ctypes.c_int64
+        L.saf_decomp_param_bwd.argtypes = [P(SafMixedAttnArgs)] + [P(SafTensor)] * 3 + [ctypes.c_void_p]
+        L.saf_decomp_param_bwd.restype = ctypes.c_int
+        L.saf_decomp_param_bwd_workspace_bytes.argtypes = [P(SafMixedAttnArgs)]
+        L.saf_decomp_param_bwd_workspace_bytes.restype = ctypes.c_int64
         L.saf_frozen_pv_fwd.argtypes = [P(SafTensor), P(SafTensor), P(ctypes.c_int32),
                                         ctypes.c_int32, ctypes.c_int32, P(SafTensor),
                                         ctypes.c_void_p]
@@ -95,6 +100,8 @@ def lib():
         L.saf_add_layernorm.restype = ctypes.c_int
         L.saf_decomposed_logz.argtypes = [P(SafTensor)] * 3 + [ctypes.c_void_p]
         L.saf_decomposed_logz.restype = ctypes.c_int
+        L.saf_decomposed_logz_bwd.argtypes = [P(SafTensor)] * 6 + [ctypes.c_void_p]
+        L.saf_decomposed_logz_bwd.restype = ctypes.c_int
         L.saf_workspace_bytes.argtypes = [ctypes.c_int32] * 4
         L.saf_workspace_bytes.restype = ctypes.c_int64
         L.saf_mixed_attn_workspace_bytes.argtypes = [P(SafMixedAttnArgs)]

@@ -105,6 +105,58 @@ def decomposed_logz(alpha, rho, chunk=None):
     return z
 
 
+class _NormalisersFn(torch.autograd.Function):
+    """z = logsumexp_{j<=i}(alpha_j + rho_{i-j}) on HIP, with its exact
+    backward (saf_decomposed_logz_bwd)."""
+
+    @staticmethod
+    def forward(ctx, alpha, rho):
+        a32 = alpha.detach().float().contiguous()
+        r32 = rho.detach().float().contiguous()
+        z = decomposed_logz(a32, r32)
+        ctx.save_for_backward(a32, r32, z)
+        ctx.dtypes = (alpha.dtype, rho.dtype)
+        return z.to(alpha.dtype)
+
+    @staticmethod
+    def backward(ctx, gz):
+        a32, r32, z = ctx.saved_tensors
+        da = torch.empty_like(a32)
+        dr = torch.empty_like(r32)
+        g = gz.float().contiguous()
+        if a32.numel():
+            _ext.check(_ext.lib().saf_decomposed_logz_bwd(
+                _ext.tensor_desc(a32), _ext.tensor_desc(r32), _ext.tensor_desc(z), _ext.tensor_desc(g),
+                _ext.tensor_desc(da), _ext.tensor_desc(dr), _ext.current_stream_ptr(a32.device)))
+        return da.to(ctx.dtypes[0]), dr.to(ctx.dtypes[1])
+
+
+def decomp_log_normalizers(alpha, rho):
+    """Row log-normalisers z[h, i] = logsumexp_{j <= i}(alpha[h, j] +
+    rho[h, i - j]) of (N, T) logit vectors, differentiable in alpha and rho.
+
+    The quantity of the reference's decomp_log_normalizers_fft
+    (/root/reference/nanogpt/dynamic_freeze.py:330-361), which the pattern
+    fits backpropagate through.  Device tensors: the exact O(T^2) sums of
+    saf_decomposed_logz and saf_decomposed_logz_bwd (fp32, no FFT round-off,
+    no range shifts needed); host tensors: the row-chunked torch definition
+    under torch autograd."""
+    if alpha.shape != rho.shape or alpha.ndim != 2:
+        raise ValueError("alpha and rho must have matching (N, T) shapes")
+    if alpha.is_cuda:
+        return _NormalisersFn.apply(alpha, rho)
+    H, S = alpha.shape
+    rows = []
+    chunk = max(1, (1 << 24) // max(H * S, 1))
+    for r0 in range(0, S, chunk):
+        rows.append(decomp_logits(alpha, rho, rows=(r0, min(S, r0 + chunk))).logsumexp(-1))
+    return torch.cat(rows, dim=-1)
+
+
+# reference name (nanogpt/dynamic_freeze.py:330): same contract, exact sums
+decomp_log_normalizers_fft = decomp_log_normalizers
+
+
 # ---------------------------------------------------------------------------
 # Closed-form recognition of decomposed patterns
 # ---------------------------------------------------------------------------
@@ -251,8 +303,9 @@ class _MixedAttnFn(torch.autograd.Function):
     it; the base-2 LSE of the live heads, the routing tables and the fixed
     pattern buffers in the backward closure); the backward runs
     saf_mixed_attn_bwd.  Frozen heads have no q/k slot, so they get no Q/K
-    gradient; patterns and the decomposed buffers are constants (no
-    gradient, ever)."""
+    gradient; patterns and the decomposed buffers are constants here (no
+    gradient: trainable alpha / rho go through supplement.PatternGradient,
+    as in the reference's supplement/trainable_patterns.py:61-93)."""
 
     @staticmethod
     def forward(ctx, q, k, v, run, bwd):

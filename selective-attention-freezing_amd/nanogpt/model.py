@@ -171,14 +171,18 @@ class CausalSelfAttention(nn.Module):
 
     # -- dtype handling ---------------------------------------------------
     def _apply(self, fn, recurse=True):
-        keep = {n: getattr(self, n) for n in self._FP32_BUFFERS
+        # .data: a parameter (trainable patterns) has its data swapped in place
+        keep = {n: getattr(self, n).data for n in self._FP32_BUFFERS
                 if getattr(self, n, None) is not None}
         out = super()._apply(fn, recurse)
         for n, old in keep.items():
             new = getattr(self, n)
             if new.dtype != torch.float32:
                 # re-place the exact fp32 values on the new device
-                self._buffers[n] = old.to(device=new.device)
+                if n in self._parameters:
+                    new.data = old.to(device=new.device)
+                else:
+                    self._buffers[n] = old.to(device=new.device)
         self._fz_dirty = True
         return out
 

@@ -374,3 +374,63 @@ def test_eager_rows_match_full_eager(gqa):
     got = orc.eager_rows(q, k, v, frozen, rows, hidx, pidx, kvidx, patt_rows=prow, alpha=alpha,
                          rho=rho, z=z)
     np.testing.assert_allclose(got, full[:, :, rows], atol=1e-12)
+
+
+# ---------------------------------------------------------------------------
+# parameter gradients of decomposed patterns
+# ---------------------------------------------------------------------------
+
+def _dense_reference(v, alpha, rho):
+    """supplement/trainable_patterns.py:7-13: softmax(alpha_j + rho_{i-j})
+    (causal) applied to v, torch float64 (autograd is the library special case)."""
+    T = v.shape[-2]
+    i = torch.arange(T)
+    dist = i[:, None] - i[None, :]
+    logits = alpha[:, None, :T] + rho[:, dist.clamp_min(0)]
+    p = logits.masked_fill(dist < 0, float("-inf")).softmax(-1)
+    return p @ v
+
+
+def test_pattern_grads_match_torch_autograd():
+    rng = np.random.default_rng(50)
+    B, H, T, hd, S = 2, 4, 23, 5, 30
+    v = rng.standard_normal((B, H, T, hd))
+    dout = rng.standard_normal((B, H, T, hd))
+    alpha = rng.standard_normal((H, S)) * 0.7
+    rho = rng.standard_normal((H, S)) * 0.7
+    rho[2, 9:] = -np.inf                       # a window-like head
+    frozen = np.array([2, 0, 2, 2])
+    da, dr = orc.pattern_grads(v, dout, frozen, alpha, rho)
+    a = torch.tensor(alpha, requires_grad=True)
+    r = torch.tensor(rho, requires_grad=True)
+    y = _dense_reference(torch.from_numpy(v), a, r)
+    keep = torch.tensor([1.0, 0.0, 1.0, 1.0], dtype=torch.float64)[None, :, None, None]
+    (y * torch.from_numpy(dout) * keep).sum().backward()
+    np.testing.assert_allclose(da, a.grad.numpy(), atol=1e-10)
+    rg = np.nan_to_num(r.grad.numpy())
+    np.testing.assert_allclose(np.where(np.isfinite(rho), dr, 0.0), np.where(np.isfinite(rho), rg, 0.0), atol=1e-10)
+    assert (da[1] == 0).all() and (dr[1] == 0).all()
+
+
+def test_logz_grads_match_torch_autograd_and_fd():
+    rng = np.random.default_rng(51)
+    H, S = 3, 17
+    alpha = rng.standard_normal((H, S))
+    rho = rng.standard_normal((H, S))
+    gz = rng.standard_normal((H, S))
+    da, dr = orc.logz_grads(alpha, rho, gz)
+    a = torch.tensor(alpha, requires_grad=True)
+    r = torch.tensor(rho, requires_grad=True)
+    i = torch.arange(S)
+    dist = i[:, None] - i[None, :]
+    lg = (a[:, None, :] + r[:, dist.clamp_min(0)]).masked_fill(dist < 0, float("-inf"))
+    (lg.logsumexp(-1) * torch.from_numpy(gz)).sum().backward()
+    np.testing.assert_allclose(da, a.grad.numpy(), atol=1e-10)
+    np.testing.assert_allclose(dr, r.grad.numpy(), atol=1e-10)
+    # finite difference on one alpha and one rho entry
+    eps = 1e-6
+    f = lambda al, rh: float((orc.decomposed_logz(al, rh) * gz).sum())
+    a2 = alpha.copy(); a2[1, 4] += eps
+    assert abs((f(a2, rho) - f(alpha, rho)) / eps - da[1, 4]) < 1e-4
+    r2 = rho.copy(); r2[2, 3] += eps
+    assert abs((f(alpha, r2) - f(alpha, rho)) / eps - dr[2, 3]) < 1e-4
