@@ -34,6 +34,10 @@
  *     synchronisation.  Calls are re-entrant; the only mutable global state is
  *     the thread-local error string (and the noalloc scratch array, shared by
  *     the calls of that one entry point).
+ *   - Head dims: the forward entry points take HD in {32, 64, 96, 128, 256}
+ *     (the reference's Triton kernels take any power of two; 256 is
+ *     Qwen3.5's); the backward entry points and the fused RoPE / q-k norm
+ *     prologue take HD <= 128 and return SAF_EUNSUPPORTED above.
  *   - Return value: SAF_OK (0) or a negative status; saf_last_error() then
  *     holds a message for the calling thread.
  */

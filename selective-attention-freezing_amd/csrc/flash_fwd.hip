@@ -199,6 +199,12 @@ struct FlashState {
                                        bool masked) {
     scores(s, ktile, ks);
     if (masked) mask(s, j0);
+    rebase(s, bs);
+  }
+
+  // The recompute from raw (masked) scores s: move the reference to
+  // max(m, block max), rescale O and l, and recompute P.
+  __device__ __forceinline__ void rebase(f32x16_t (&s)[QT], float (&bs)[QT]) {
 #pragma unroll
     for (int qt = 0; qt < QT; ++qt) {
       float mx = s[qt][0];
@@ -221,6 +227,8 @@ struct FlashState {
   // (kpre) up to hd 64; above, the 32 more VGPRs would spill, and each step
   // reads its own
   static constexpr bool kPrefetchK = HD <= 64;
+  // hd 256: two LDS slots per operand (four 32 KB tiles); see flash_unit
+  static constexpr bool kTwoSlot = HD > 128;
 
   // One pipeline step u.  On entry `nxt` holds P_{u-1} (packed), `cur`
   // holds S_u and, with kPrefetchK, `kpre` the K A operands of S_{u+1}.
@@ -257,15 +265,44 @@ struct FlashState {
 #pragma unroll
     for (int qt = 0; qt < QT; ++qt) l_run[qt] += bs[qt];
   }
+
+  // The step of the two-slot schedule: as step() without the K prefetch,
+  // and the rare recompute starts from a register copy of the masked raw
+  // scores, so no K tile has to outlive the step that reads it.
+  __device__ __forceinline__ void step_raw(f32x16_t (&cur)[QT], f32x16_t (&nxt)[QT], int u, bool masked,
+                                           const char* kS, int ksS, const char* vP, int ksP) {
+    if (masked) {
+      asm volatile("" ::: "memory");
+      mask(cur, 32 * u);
+    }
+    pv(nxt, vP, ksP);
+    scores(nxt, kS, ksS);
+    f32x16_t raw[QT];
+#pragma unroll
+    for (int qt = 0; qt < QT; ++qt) raw[qt] = cur[qt];
+    float bs[QT];
+    exp_pack(cur, bs);
+    bool bad = false;
+#pragma unroll
+    for (int qt = 0; qt < QT; ++qt) bad |= bs[qt] > kRedoSum;
+    if (__builtin_amdgcn_ballot_w64(bad)) {
+#pragma unroll
+      for (int qt = 0; qt < QT; ++qt) cur[qt] = raw[qt];
+      rebase(cur, bs);
+    }
+#pragma unroll
+    for (int qt = 0; qt < QT; ++qt) l_run[qt] += bs[qt];
+  }
 };
 
 // hd <= 64: three waves per SIMD (three resident 4-wave workgroups of 128
 // queries, within 170 registers) or two of 256 queries (within 256
-// registers).  Larger heads: one workgroup's three K and V slots fill most of
+// registers).  hd 96 / 128: one workgroup's three K and V slots fill most of
 // the CU's LDS, so the workgroup has 8 waves (two per SIMD) sharing them.
-// The host's flash_resident() and flash_block_rows() mirror this.
+// hd 256: 4 waves, one per SIMD (512 registers each), over two slots per
+// operand.  The host's flash_resident() and flash_block_rows() mirror this.
 template <int HD, int QT>
-constexpr int flash_waves_per_eu() { return HD <= 64 ? (QT == 1 ? 3 : 2) : (QT == 1 ? 2 : 1); }
+constexpr int flash_waves_per_eu() { return HD <= 64 ? (QT == 1 ? 3 : 2) : (HD <= 128 && QT == 1 ? 2 : 1); }
 
 // One work unit of the live-head kernel: unit = item * (B * n_slots) + r,
 // item = a query block (and key segment), r = (batch, live slot).
@@ -315,13 +352,14 @@ __device__ __forceinline__ void flash_unit(Params& p, const int unit, char* k0, 
   TileDma<T, HD> dma;
   dma.init(wave, lane, p.k_st, p.v_st);
 
-  // prologue DMA: K_kb0, K_kb0+1, V_kb0 into slot 0 / 1 / 0; slot 2 of V
-  // (the "V_{kb0-1}" of the first step, multiplied by P = 0) gets finite
-  // data too, since 0 * NaN from stale LDS would poison O
+  // prologue DMA: K_kb0, K_kb0+1, V_kb0 into slot 0 / 1 / 0; the V slot of
+  // "V_{kb0-1}" (slot 2, or slot 1 of the two-slot schedule), multiplied by
+  // P = 0 in the first step, gets finite data too, since 0 * NaN from stale
+  // LDS would poison O
   dma.load_k(kbase, p.k_st, 64 * kb0, T_len, k0, wave);
   if (kb0 + 1 < nkb) dma.load_k(kbase, p.k_st, 64 * (kb0 + 1), T_len, k1, wave);
   dma.load_v(vbase, p.v_st, 64 * kb0, T_len, v0, wave);
-  dma.load_v(vbase, p.v_st, 64 * kb0, T_len, v2, wave);
+  dma.load_v(vbase, p.v_st, 64 * kb0, T_len, St::kTwoSlot ? v1 : v2, wave);
 
 #pragma unroll
   for (int qt = 0; qt < QT; ++qt) {
@@ -343,50 +381,86 @@ __device__ __forceinline__ void flash_unit(Params& p, const int unit, char* k0, 
 #pragma unroll
   for (int qt = 0; qt < QT; ++qt) sB[qt] = zero16();
   st.scores(sA, k0, 0);
-  uint4 kpre[NKT];  // K operands of the next S product, read one step ahead
-  if constexpr (St::kPrefetchK) st.load_ka(kpre, k0, 1);
+  if constexpr (St::kTwoSlot) {
+    // hd 256: four 32 KB tiles fit the LDS, not six.  Block j (phase R =
+    // (j - kb0) & 1): K_j in k_R, K_{j+1} in k_{1-R}, V_j in v_R, V_{j-1} in
+    // v_{1-R}.  After the first step K_j and V_{j-1} are dead (the rare
+    // recompute keeps raw scores in registers), so one barrier mid-block
+    // frees their slots for K_{j+2} and V_{j+1}, each with two steps to
+    // land before the next block's barrier waits for them.
+    auto block2 = [&](const int j, auto phase) {
+      constexpr int R = decltype(phase)::value;
+      char* const kJ = R ? k1 : k0;
+      char* const kJ1 = R ? k0 : k1;
+      char* const vJ = R ? v1 : v0;
+      char* const vJm = R ? v0 : v1;
+      const bool masked = j >= jd;
+      // u = 2j: S_{2j+1} (K_j sub 1), P_{2j-1} V_{j-1} sub 1, softmax S_{2j}
+      st.step_raw(sA, sB, 2 * j, masked, kJ, 1, vJm, 1);
+      __syncthreads();  // K_j and V_{j-1} read by every wave; K_{j+1} and V_j landed (vmcnt 0)
+      if (j + 2 < nkb) dma.load_k(kbase, p.k_st, 64 * (j + 2), T_len, kJ, wave);
+      if (j + 1 < nkb) dma.load_v(vbase, p.v_st, 64 * (j + 1), T_len, vJm, wave);
+      // u = 2j+1: S_{2j+2} (K_{j+1} sub 0; past the last block a stale slot
+      // whose scores are never used), P_{2j} V_j sub 0, softmax S_{2j+1}
+      st.step_raw(sB, sA, 2 * j + 1, masked, kJ1, 0, vJ, 0);
+    };
+    using P0 = std::integral_constant<int, 0>;
+    using P1 = std::integral_constant<int, 1>;
+    int j = kb0, ph;
+    for (;;) {
+      if (j >= nkb) { ph = 0; break; }
+      block2(j++, P0());
+      if (j >= nkb) { ph = 1; break; }
+      block2(j++, P1());
+    }
+    // P_{2 nkb - 1} . V_{nkb-1} sub 1 (V_{nkb-1} is in v0 when the last block had phase 0)
+    st.pv(sB, ph == 1 ? v0 : v1, 1);
+  } else {
+    uint4 kpre[NKT];  // K operands of the next S product, read one step ahead
+    if constexpr (St::kPrefetchK) st.load_ka(kpre, k0, 1);
 
-  // block j in phase R (slots: K_j = R, K_{j+1} = R+1, K_{j+2} = R+2 (loading),
-  // V_{j-1} = R+2, V_j = R, V_{j+1} = R+1 (loading), all mod 3); blocks at
-  // or past jd hold the diagonal and run the masked steps
-  auto block = [&](const int j, auto phase) {
-    constexpr int R = decltype(phase)::value;
-    char* const ks[3] = {k0, k1, k2};
-    char* const vs[3] = {v0, v1, v2};
-    char* const kJ = ks[R];
-    char* const kJ1 = ks[(R + 1) % 3];
-    char* const kJ2 = ks[(R + 2) % 3];
-    char* const vJm = vs[(R + 2) % 3];
-    char* const vJ = vs[R];
-    char* const vJ1 = vs[(R + 1) % 3];
-    if (j + 2 < nkb) dma.load_k(kbase, p.k_st, 64 * (j + 2), T_len, kJ2, wave);
-    if (j + 1 < nkb) dma.load_v(vbase, p.v_st, 64 * (j + 1), T_len, vJ1, wave);
-    const bool masked = j >= jd;
-    // u = 2j: S_{2j+1} (K_j sub 1), operands of S_{2j+2} (K_{j+1} sub 0),
-    // P_{2j-1} V_{j-1} sub 1, softmax S_{2j}
-    st.step(sA, sB, kpre, 2 * j, masked, kJ, 1, kJ1, 0, kJ, 0, vJm, 1);
-    // u = 2j+1: S_{2j+2} (K_{j+1} sub 0), operands of S_{2j+3} (K_{j+1}
-    // sub 1), P_{2j} V_j sub 0, softmax S_{2j+1}.  Past the last block these
-    // read a stale slot whose products are never used.
-    st.step(sB, sA, kpre, 2 * j + 1, masked, kJ1, 0, kJ1, 1, kJ, 1, vJ, 0);
-    __syncthreads();  // waits for this block's DMA (vmcnt 0) before any wave moves on
-  };
-  using P0 = std::integral_constant<int, 0>;
-  using P1 = std::integral_constant<int, 1>;
-  using P2 = std::integral_constant<int, 2>;
-  // blocks run as a chain of phases 0 -> 1 -> 2 -> 0, so every DMA target and
-  // every read names a static LDS slot
-  int j = kb0, ph;
-  for (;;) {
-    if (j >= nkb) { ph = 0; break; }
-    block(j++, P0());
-    if (j >= nkb) { ph = 1; break; }
-    block(j++, P1());
-    if (j >= nkb) { ph = 2; break; }
-    block(j++, P2());
+    // block j in phase R (slots: K_j = R, K_{j+1} = R+1, K_{j+2} = R+2 (loading),
+    // V_{j-1} = R+2, V_j = R, V_{j+1} = R+1 (loading), all mod 3); blocks at
+    // or past jd hold the diagonal and run the masked steps
+    auto block = [&](const int j, auto phase) {
+      constexpr int R = decltype(phase)::value;
+      char* const ks[3] = {k0, k1, k2};
+      char* const vs[3] = {v0, v1, v2};
+      char* const kJ = ks[R];
+      char* const kJ1 = ks[(R + 1) % 3];
+      char* const kJ2 = ks[(R + 2) % 3];
+      char* const vJm = vs[(R + 2) % 3];
+      char* const vJ = vs[R];
+      char* const vJ1 = vs[(R + 1) % 3];
+      if (j + 2 < nkb) dma.load_k(kbase, p.k_st, 64 * (j + 2), T_len, kJ2, wave);
+      if (j + 1 < nkb) dma.load_v(vbase, p.v_st, 64 * (j + 1), T_len, vJ1, wave);
+      const bool masked = j >= jd;
+      // u = 2j: S_{2j+1} (K_j sub 1), operands of S_{2j+2} (K_{j+1} sub 0),
+      // P_{2j-1} V_{j-1} sub 1, softmax S_{2j}
+      st.step(sA, sB, kpre, 2 * j, masked, kJ, 1, kJ1, 0, kJ, 0, vJm, 1);
+      // u = 2j+1: S_{2j+2} (K_{j+1} sub 0), operands of S_{2j+3} (K_{j+1}
+      // sub 1), P_{2j} V_j sub 0, softmax S_{2j+1}.  Past the last block these
+      // read a stale slot whose products are never used.
+      st.step(sB, sA, kpre, 2 * j + 1, masked, kJ1, 0, kJ1, 1, kJ, 1, vJ, 0);
+      __syncthreads();  // waits for this block's DMA (vmcnt 0) before any wave moves on
+    };
+    using P0 = std::integral_constant<int, 0>;
+    using P1 = std::integral_constant<int, 1>;
+    using P2 = std::integral_constant<int, 2>;
+    // blocks run as a chain of phases 0 -> 1 -> 2 -> 0, so every DMA target and
+    // every read names a static LDS slot
+    int j = kb0, ph;
+    for (;;) {
+      if (j >= nkb) { ph = 0; break; }
+      block(j++, P0());
+      if (j >= nkb) { ph = 1; break; }
+      block(j++, P1());
+      if (j >= nkb) { ph = 2; break; }
+      block(j++, P2());
+    }
+    // P_{2 nkb - 1} . V_{nkb-1} sub 1 (V_{nkb-1} sits in the slot of phase ph - 1)
+    st.pv(sB, ph == 1 ? v0 : (ph == 2 ? v1 : v2), 1);
   }
-  // P_{2 nkb - 1} . V_{nkb-1} sub 1 (V_{nkb-1} sits in the slot of phase ph - 1)
-  st.pv(sB, ph == 1 ? v0 : (ph == 2 ? v1 : v2), 1);
 
 #pragma unroll
   for (int qt = 0; qt < QT; ++qt) {
@@ -431,8 +505,11 @@ __global__ __launch_bounds__(64 * flash_waves(HD))
 __attribute__((amdgpu_waves_per_eu(flash_waves_per_eu<HD, QT>(), flash_waves_per_eu<HD, QT>())))
 void flash_fwd_kernel(const FlashParams p) {
   constexpr int KB = KLayout<HD>::BYTES, VB = VRow<HD>::BYTES;
-  __shared__ __align__(16) char k0[KB], k1[KB], k2[KB];
-  __shared__ __align__(16) char v0[VB], v1[VB], v2[VB];
+  // hd 256 uses two slots per operand (k2 / v2 are never touched there and
+  // take one byte)
+  constexpr int KB3 = HD > 128 ? 1 : KB, VB3 = HD > 128 ? 1 : VB;
+  __shared__ __align__(16) char k0[KB], k1[KB], k2[KB3];
+  __shared__ __align__(16) char v0[VB], v1[VB], v2[VB3];
   if constexpr (!PERSIST) {
     flash_unit<T, HD, QT>(p, blockIdx.x, k0, k1, k2, v0, v1, v2);
   } else {
@@ -533,7 +610,7 @@ __global__ __launch_bounds__(256) void flash_combine_kernel(const CombineParams 
   template __global__ void flash_fwd_kernel<T, HD, QT, true>(const FlashParams);
 #define SAF_FLASH_INST_HD(T) \
   SAF_FLASH_INST(T, 32, 1) SAF_FLASH_INST(T, 32, 2) SAF_FLASH_INST(T, 64, 1) SAF_FLASH_INST(T, 64, 2) \
-  SAF_FLASH_INST(T, 96, 1) SAF_FLASH_INST(T, 128, 1)
+  SAF_FLASH_INST(T, 96, 1) SAF_FLASH_INST(T, 128, 1) SAF_FLASH_INST(T, 256, 1)
 SAF_FLASH_INST_HD(__bf16)
 SAF_FLASH_INST_HD(_Float16)
 #undef SAF_FLASH_INST_HD
@@ -561,6 +638,7 @@ static hipError_t launch_flash_hd(const FlashParams& p, int hd, int qt, hipStrea
     case 64 * 4 + 2: return launch_flash_t<T, 64, 2>(p, s);
     case 96 * 4 + 1: return launch_flash_t<T, 96, 1>(p, s);
     case 128 * 4 + 1: return launch_flash_t<T, 128, 1>(p, s);
+    case 256 * 4 + 1: return launch_flash_t<T, 256, 1>(p, s);
     default: return hipErrorInvalidValue;
   }
 }
@@ -579,6 +657,7 @@ static hipError_t launch_combine_t(const CombineParams& p, int hd, hipStream_t s
     case 64: hipLaunchKernelGGL((flash_combine_kernel<T, 64>), grid, dim3(256), 0, s, p); break;
     case 96: hipLaunchKernelGGL((flash_combine_kernel<T, 96>), grid, dim3(256), 0, s, p); break;
     case 128: hipLaunchKernelGGL((flash_combine_kernel<T, 128>), grid, dim3(256), 0, s, p); break;
+    case 256: hipLaunchKernelGGL((flash_combine_kernel<T, 256>), grid, dim3(256), 0, s, p); break;
     default: return hipErrorInvalidValue;
   }
   return hipGetLastError();

@@ -24,8 +24,10 @@
 
 namespace saf {
 
-// Resident rebuild workgroups per CU (decomp_resident() on the host).
-constexpr int decomp_waves_per_eu(int) { return 3; }
+// Resident rebuild workgroups per CU (decomp_resident() on the host): two
+// at hd 256, whose 128 accumulator registers per wave need the 256-register
+// budget of two waves per SIMD.
+constexpr int decomp_waves_per_eu(int hd) { return hd > 128 ? 2 : 3; }
 
 // Decomposed frozen heads: P^T rebuilt in registers, one 16-key operand at a
 // time and consumed by its MFMAs right away (building a whole 64-key block of
@@ -542,10 +544,13 @@ static void launch_dense_t(const FrozenParams& p, hipStream_t s) {
 
 template <typename T, typename PT, int HD>
 static void launch_dense_nb(const FrozenParams& p, hipStream_t s) {
-  if (dense_batch_group(p.B) == 2)
-    launch_dense_t<T, PT, HD, 2>(p, s);
-  else
-    launch_dense_t<T, PT, HD, 1>(p, s);
+  if constexpr (HD <= 128) {
+    if (dense_batch_group(p.B, HD) == 2) {
+      launch_dense_t<T, PT, HD, 2>(p, s);
+      return;
+    }
+  }
+  launch_dense_t<T, PT, HD, 1>(p, s);
 }
 
 template <typename T, int HD, int QT>
@@ -571,6 +576,7 @@ static hipError_t launch_frozen_hd(const FrozenParams& p, int hd, int mode, hipS
     case 64: return launch_frozen_t<T, 64, 2>(p, mode, s);
     case 96: return launch_frozen_t<T, 96, 1>(p, mode, s);
     case 128: return launch_frozen_t<T, 128, 1>(p, mode, s);
+    case 256: return launch_frozen_t<T, 256, 1>(p, mode, s);
     default: return hipErrorInvalidValue;
   }
 }

@@ -58,7 +58,7 @@ template <int HD> struct ScanShape {
   static constexpr int CH = NRL * R;
 };
 static_assert(ScanShape<32>::CH == 512 && ScanShape<64>::CH == 256 && ScanShape<96>::CH == 128 &&
-                  ScanShape<128>::CH == 128,
+                  ScanShape<128>::CH == 128 && ScanShape<256>::CH == 128,
               "scan_chunk_rows() must match ScanShape");
 
 // Predecessor status words read per look-back round trip.
@@ -366,6 +366,7 @@ static hipError_t launch_scan_hd(const ScanParams& p, int hd, hipStream_t s) {
     case 64: return launch_scan_t<T, 64>(p, s);
     case 96: return launch_scan_t<T, 96>(p, s);
     case 128: return launch_scan_t<T, 128>(p, s);
+    case 256: return launch_scan_t<T, 256>(p, s);
     default: return hipErrorInvalidValue;
   }
 }

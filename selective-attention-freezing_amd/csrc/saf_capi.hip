@@ -66,7 +66,10 @@ int check_act(const saf_tensor_t& t, const char* name, int align) {
   return SAF_OK;
 }
 
-bool supported_hd(int64_t hd) { return hd == 32 || hd == 64 || hd == 96 || hd == 128; }
+// Head dims of the forward kernels; the backward kernels and the fused
+// RoPE / q-k norm prologue stop at 128.
+bool supported_hd(int64_t hd) { return hd == 32 || hd == 64 || hd == 96 || hd == 128 || hd == 256; }
+bool supported_bwd_hd(int64_t hd) { return hd == 32 || hd == 64 || hd == 96 || hd == 128; }
 
 int n_scan_chunks(int T, int hd) { return (T + scan_chunk_rows(hd) - 1) / scan_chunk_rows(hd); }
 
@@ -111,7 +114,8 @@ int plan_and_validate(const saf_mixed_attn_args* a, unsigned which, Plan& pl, bo
   pl.HD = (int)v.size[3];
   pl.dtype = v.dtype;
   pl.H = a->n_heads;
-  if (!supported_hd(pl.HD)) return fail(SAF_EUNSUPPORTED, "head_dim %d is not supported (32, 64, 96, 128)", pl.HD);
+  if (!supported_hd(pl.HD))
+    return fail(SAF_EUNSUPPORTED, "head_dim %d is not supported (32, 64, 96, 128, 256)", pl.HD);
   if (pl.H <= 0 || pl.H > SAF_MAX_HEADS)
     return fail(SAF_EUNSUPPORTED, "n_heads %d outside 1..%d", pl.H, SAF_MAX_HEADS);
   if (a->frozen == nullptr) return fail(SAF_EINVAL, "frozen (host head-state table) is required");
@@ -241,7 +245,8 @@ int cu_count() {
 
 // Resident live-head workgroups per CU (flash_waves_per_eu in the kernel:
 // three 128-query workgroups at hd <= 64, two of 256 queries; one 8-wave
-// workgroup at larger head dims, where its LDS slots fill most of the CU).
+// workgroup at hd 96 / 128, where its LDS slots fill most of the CU; one
+// 4-wave workgroup of 128 queries at hd 256, one wave per SIMD).
 int flash_resident(int HD, int qt) { return HD <= 64 ? (qt == 1 ? 3 : 2) : 1; }
 
 struct FlashPlan {
@@ -428,12 +433,12 @@ void fill_frozen_common(FrozenParams& p, const saf_tensor_t& v, const saf_tensor
 
 int frozen_qtiles(int hd) { return hd <= 64 ? 2 : 1; }
 // Resident rebuild workgroups per CU (decomp_waves_per_eu in the kernel).
-int decomp_resident(int) { return 3; }
+int decomp_resident(int hd) { return hd > 128 ? 2 : 3; }
 
 // Dense P.V work plan: query blocks of the kernel's shape, balanced over the
 // batch groups that share a pattern (dense_batch_group).
 FlashPlan plan_dense(int B, int n_slots, int T, int HD) {
-  const int nb = dense_batch_group(B);
+  const int nb = dense_batch_group(B, HD);
   return plan_flash(B / nb, n_slots, T, HD, dense_block_rows(B, HD), kDenseResident, nb);
 }
 
@@ -622,7 +627,7 @@ int saf_frozen_pv_fwd(const saf_tensor_t* patt, const saf_tensor_t* v, const int
                                     (long long)v->size[1]);
   if (nf > SAF_MAX_HEADS) return fail(SAF_EUNSUPPORTED, "more than %d frozen heads", SAF_MAX_HEADS);
   if (T < 0 || T > v->size[2]) return fail(SAF_EINVAL, "T must be within v's sequence length");
-  if (!supported_hd(HD)) return fail(SAF_EUNSUPPORTED, "head_dim %d is not supported (32, 64, 96, 128)", HD);
+  if (!supported_hd(HD)) return fail(SAF_EUNSUPPORTED, "head_dim %d is not supported (32, 64, 96, 128, 256)", HD);
   if (out->size[0] != B || out->size[1] != nf || out->size[2] != T || out->size[3] != HD || out->dtype != v->dtype)
     return fail(SAF_EINVAL, "out must be (B, nf, T, hd) in v's dtype");
   if (int rc = check_act(*v, "v", 16)) return rc;
@@ -657,7 +662,8 @@ int saf_frozen_pv_bwd(const saf_tensor_t* patt, const saf_tensor_t* dy, const in
                                     (long long)dv->size[1]);
   if (nf > SAF_MAX_HEADS) return fail(SAF_EUNSUPPORTED, "more than %d frozen heads", SAF_MAX_HEADS);
   if (T < 0 || T > dv->size[2]) return fail(SAF_EINVAL, "T must be within dv's sequence length");
-  if (!supported_hd(HD)) return fail(SAF_EUNSUPPORTED, "head_dim %d is not supported (32, 64, 96, 128)", HD);
+  if (!supported_bwd_hd(HD))
+    return fail(SAF_EUNSUPPORTED, "frozen_pv backward: head_dim %d is not supported (32, 64, 96, 128)", HD);
   if (dy->size[0] != B || dy->size[1] != nf || dy->size[2] != T || dy->size[3] != HD || dy->dtype != dv->dtype)
     return fail(SAF_EINVAL, "dy must be (B, nf, T, hd) in dv's dtype");
   if (int rc = check_act(*dy, "dy", 16)) return rc;
@@ -704,7 +710,8 @@ static int rope_common(const saf_tensor_t* q, const saf_tensor_t* k, const saf_t
   const int64_t B = q->size[0], T = q->size[2], hd = q->size[3];
   if (k->size[0] != B || k->size[2] != T || k->size[3] != hd)
     return fail(SAF_EINVAL, "q and k batch, sequence and head dimensions must match");
-  if (!supported_hd(hd)) return fail(SAF_EUNSUPPORTED, "head_dim %lld is not supported (32, 64, 96, 128)", (long long)hd);
+  if (!supported_bwd_hd(hd))
+    return fail(SAF_EUNSUPPORTED, "rope: head_dim %lld is not supported (32, 64, 96, 128)", (long long)hd);
   const saf_tensor_t* cs[2] = {cos, sin};
   for (int i = 0; i < 2; ++i) {
     const saf_tensor_t& t = *cs[i];
@@ -888,6 +895,8 @@ int saf_mixed_attn_bwd(const saf_mixed_attn_args* a, const saf_tensor_t* dout, c
   if (int rc = plan_and_validate(a, kDoFlash | kDoDense | kDoDecomp, pl, false)) return rc;
   if (a->kvidx != nullptr)
     return fail(SAF_EUNSUPPORTED, "backward with kvidx (GQA) is not implemented (forward / prefill only)");
+  if (!supported_bwd_hd(pl.HD))
+    return fail(SAF_EUNSUPPORTED, "backward: head_dim %d is not supported (32, 64, 96, 128)", pl.HD);
   if (dout == nullptr || dv == nullptr) return fail(SAF_EINVAL, "dout and dv are required");
   auto same4 = [](const saf_tensor_t& t, const saf_tensor_t& ref) {
     for (int i = 0; i < 4; ++i)
@@ -1014,6 +1023,8 @@ int saf_decomp_param_bwd(const saf_mixed_attn_args* a, const saf_tensor_t* dout,
   if (int rc = plan_and_validate(a, 0, pl, false)) return rc;
   if (a->kvidx != nullptr)
     return fail(SAF_EUNSUPPORTED, "pattern gradients with kvidx (GQA) are not implemented (forward / prefill only)");
+  if (!supported_bwd_hd(pl.HD))
+    return fail(SAF_EUNSUPPORTED, "pattern gradients: head_dim %d is not supported (32, 64, 96, 128)", pl.HD);
   if (dout == nullptr || dalpha == nullptr || drho == nullptr)
     return fail(SAF_EINVAL, "dout, dalpha and drho are required");
   const std::vector<int> heads = decomp_heads_all(pl);

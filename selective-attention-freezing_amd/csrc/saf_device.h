@@ -140,7 +140,7 @@ __device__ inline int acc_key(int i, int g) { return 16 * (i >> 3) + 8 * g + (i 
 // A-lanes of an MFMA (32 different keys, same chunk) hit distinct banks.
 template <int HD> struct KLayout {
   static constexpr int KCH = HD / 8;
-  static constexpr int KCHP = KCH <= 4 ? 4 : (KCH <= 8 ? 8 : 16);
+  static constexpr int KCHP = KCH <= 4 ? 4 : (KCH <= 8 ? 8 : (KCH <= 16 ? 16 : 32));
   static constexpr int BYTES = 64 * KCHP * 16;
   __device__ static inline int chunk(int key, int c) {
     const int f = (key & 3) | ((key >> 1) & 4);
@@ -165,7 +165,7 @@ template <int HD> struct VLayout {
 // four rows a 16-lane group of ds_read_b64_tr_b16 touches fall in four
 // different bank quarters.
 template <int HD> struct VRow {
-  static constexpr int VSEG = HD / 16 <= 4 ? 4 : 8;
+  static constexpr int VSEG = HD / 16 <= 4 ? 4 : (HD / 16 <= 8 ? 8 : 16);
   static constexpr int PITCH = VSEG * 32;
   static constexpr int CHP = 2 * VSEG;  // 16-byte chunks per row
   static constexpr int BYTES = 64 * PITCH;

@@ -258,17 +258,20 @@ inline int block_rows(int qt) { return 4 * 32 * qt; }
 
 // Dense P.V shape: a workgroup of kDenseWaves waves (two per SIMD, one
 // query tile of 32 rows each) serves a group of NB batch elements (2 when
-// the batch is even, else 1) that share every pattern operand; one workgroup
-// per CU (its three V slots fill most of the LDS at hd 128).
+// the batch is even and hd <= 128, else 1: the accumulators of two hd-256
+// sequences would not fit two waves per SIMD) that share every pattern
+// operand; one workgroup per CU (its three V slots fill most of the LDS at
+// hd 128).
 constexpr int kDenseWaves = 8;
-constexpr int dense_batch_group(int B) { return B % 2 == 0 ? 2 : 1; }
+constexpr int dense_batch_group(int B, int hd) { return B % 2 == 0 && hd <= 128 ? 2 : 1; }
 constexpr int dense_qtiles(int, int) { return 1; }
 constexpr int dense_block_rows(int, int) { return kDenseWaves * 32; }
 constexpr int kDenseResident = 1;
 
-// Waves of a live-head workgroup: 8 above hd 64 (two per SIMD sharing one
-// set of LDS tiles), else 4.
-constexpr int flash_waves(int hd) { return hd > 64 ? 8 : 4; }
+// Waves of a live-head workgroup: 8 for hd 96 / 128 (two per SIMD sharing
+// one set of LDS tiles), else 4 (hd 256: one wave per SIMD, whose 512
+// registers hold the 32 x 256 O^T accumulators and the Q operands).
+constexpr int flash_waves(int hd) { return hd > 64 && hd <= 128 ? 8 : 4; }
 // Queries per live-head workgroup.
 inline int flash_block_rows(int hd, int qt) { return flash_waves(hd) * 32 * qt; }
 

@@ -52,7 +52,9 @@ from kernel.fused_attn import decomp_logits, decomposed_logz
 _FUSED_DISPATCH_COUNT = 0
 
 # head dims the HIP operator runs (include/saf_attn.h)
-_FUSED_HEAD_DIMS = (32, 64, 96, 128)
+_FUSED_HEAD_DIMS = (32, 64, 96, 128, 256)
+# head dims of the fused q/k RMSNorm + RoPE kernel (larger heads use torch's)
+_PROLOGUE_HEAD_DIMS = (32, 64, 96, 128)
 
 
 def fused_dispatch_count():
@@ -272,7 +274,8 @@ class HybridAttentionBase(nn.Module):
         v = y[:, :, U + HKV:U + 2 * HKV].transpose(1, 2)
         gate = y[:, :, U + 2 * HKV:] if self.SPEC.gated else None
         if U:
-            if self.SPEC.hip_prologue and (cos.dim() == 2 or cos.size(0) == 1):
+            if (self.SPEC.hip_prologue and hd in _PROLOGUE_HEAD_DIMS
+                    and (cos.dim() == 2 or cos.size(0) == 1)):
                 _kernel_mod.qk_rmsnorm_rope_(q, k, self.q_norm.weight, self.k_norm.weight,
                                              self.q_norm.variance_epsilon, cos, sin)
             else:

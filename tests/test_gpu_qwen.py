@@ -147,7 +147,7 @@ def test_c4_heads_model_vs_oracle(rate, repr):
     assert _rel(y, ref) <= 1e-2
 
 
-@pytest.mark.parametrize("hd", [64, 128])
+@pytest.mark.parametrize("hd", [64, 128, 256])
 @pytest.mark.parametrize("prior", ["dense", "decomp"])
 def test_qwen35_gated_fused_path_vs_oracle(hd, prior):
     """The Qwen3.5 gated-attention hybrid (qwen/nanogpt/hybrid_prior_attention.py:205-470)
