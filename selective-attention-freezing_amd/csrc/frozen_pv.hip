@@ -29,11 +29,32 @@ namespace saf {
 // budget of two waves per SIMD.
 constexpr int decomp_waves_per_eu(int hd) { return hd > 128 ? 2 : 3; }
 
-// Decomposed frozen heads: P^T rebuilt in registers, one 16-key operand at a
-// time and consumed by its MFMAs right away (building a whole 64-key block of
+// Decomposed frozen heads, P = exp(alpha_j + rho_{i-j} - z_i), in one of
+// two forms chosen per workgroup from the parameters it reads.
+//
+// Factored form (bf16): P = diag(2^(A + R - z)) . E . diag(2^(a - A)) with
+// E_ij = 2^(r_{i-j} - R), everything in log2 units (a = alpha log2 e, r, z
+// likewise) and A, R the maxima of a and r over the keys and distances the
+// workgroup reaches.  So Y = 2^(A + R - z_i) (E V'), V'_j = 2^(a_j - A) v_j:
+// the key factors are applied once per V row while it is staged in LDS, E is
+// a Toeplitz matrix whose 2^(r_d - R) values are computed once per distance
+// and block (not per cell), and the row factor is applied to the fp32
+// accumulators at the end.  Each lane's E^T operand (8 consecutive
+// distances, reversed) is one aligned ds_read_b128 from one of 8 copies of
+// the block's distance window shifted by 0..7 elements.  Every factor is
+// <= 1 before the row factor, and the form is used only when every row's z
+// is within kFactorRange of A + R, so every cell that matters (P > 2^-24)
+// has both bf16 factors far above the normal range limit and the products
+// stay normal in fp32; otherwise (and for fp16, whose exponent range is too
+// short) the workgroup rebuilds P cell by cell.
+//
+// Rebuild form: P^T rebuilt in registers, one 16-key operand at a time and
+// consumed by its MFMAs right away (building a whole 64-key block of
 // operands first pushed the accumulators into AGPR copies at one wave per
 // SIMD).  alpha, rho and z are staged pre-multiplied by log2(e), so a cell
 // costs one add, one subtract and one exp2.
+constexpr float kFactorRange = 80.f;
+
 template <typename T, int HD, int QT>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(decomp_waves_per_eu(HD), decomp_waves_per_eu(HD))))
 void frozen_decomp_kernel(const FrozenParams p) {
@@ -42,9 +63,14 @@ void frozen_decomp_kernel(const FrozenParams p) {
   constexpr int BM = NW * 32 * QT;
   constexpr int NDT = HD / 32;
   constexpr int RW = BM + 64;  // rho window staged per key block
+  constexpr int RWL = RW + 8;  // length of one shifted copy of the factored window (bf16)
+  constexpr int ERN = (RW + NTHR - 1) / NTHR;
+  constexpr bool kFactorable = std::is_same<T, __bf16>::value;
   __shared__ __align__(16) uint4 v_lds[2][VLayout<HD>::BYTES / 16];
   __shared__ float a_lds[2][MODE == 1 ? 64 : 1];
   __shared__ float r_lds[2][MODE == 1 ? RW : 1];
+  __shared__ __align__(16) uint16_t er_lds[kFactorable ? 2 : 1][8][kFactorable ? RWL : 8];
+  __shared__ float red_lds[3][NW];
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (SGPR)
@@ -80,6 +106,9 @@ void frozen_decomp_kernel(const FrozenParams p) {
   const int kend_w = min(q0w + 32 * QT, T_len);
   const int nkb_w = min(nkb, kend_w > 0 ? (kend_w + 63) / 64 : 0);  // blocks this wave's rows reach
 
+  auto alpha_at = [&](int j) { return load_as_f32(p.alpha, (int64_t)ph * p.a_sh + (int64_t)j * p.a_ss, p.a_dtype); };
+  auto rho_at = [&](int d) { return load_as_f32(p.rho, (int64_t)ph * p.r_sh + (int64_t)d * p.r_ss, p.r_dtype); };
+
   // per-lane row normaliser (decomposed); rows >= T get +inf -> exact zeros
   float zq[QT];
 #pragma unroll
@@ -90,94 +119,216 @@ void frozen_decomp_kernel(const FrozenParams p) {
       zq[qt] = load_as_f32(p.z, (int64_t)ph * p.z_sh + (int64_t)i * p.z_ss, p.z_dtype) * kLog2e;
   }
 
+  // factored form: A = max a over keys < kend_wg, R = max r over distances
+  // < kend_wg (supersets of what any key segment of this block reaches), and
+  // the smallest z of the block's rows decide it for the whole workgroup
+  bool factored = false;
+  float aoff = 0.f, roff = 0.f;
+  if constexpr (kFactorable) {
+    float am = -INFINITY, rm = -INFINITY, zm = INFINITY;
+    for (int j = tid; j < kend_wg; j += NTHR) {
+      am = fmaxf(am, alpha_at(j));
+      rm = fmaxf(rm, rho_at(j));
+    }
+    for (int i = q0 + tid; i < kend_wg; i += NTHR)
+      zm = fminf(zm, load_as_f32(p.z, (int64_t)ph * p.z_sh + (int64_t)i * p.z_ss, p.z_dtype));
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) {
+      am = fmaxf(am, __shfl_xor(am, off));
+      rm = fmaxf(rm, __shfl_xor(rm, off));
+      zm = fminf(zm, __shfl_xor(zm, off));
+    }
+    if (lane == 0) {
+      red_lds[0][wave] = am;
+      red_lds[1][wave] = rm;
+      red_lds[2][wave] = zm;
+    }
+    __syncthreads();
+    am = fmaxf(fmaxf(red_lds[0][0], red_lds[0][1]), fmaxf(red_lds[0][2], red_lds[0][3])) * kLog2e;
+    rm = fmaxf(fmaxf(red_lds[1][0], red_lds[1][1]), fmaxf(red_lds[1][2], red_lds[1][3])) * kLog2e;
+    zm = fminf(fminf(red_lds[2][0], red_lds[2][1]), fminf(red_lds[2][2], red_lds[2][3])) * kLog2e;
+    factored = __builtin_isfinite(am) && __builtin_isfinite(rm) && __builtin_isfinite(zm) &&
+               zm >= am + rm - kFactorRange;
+    aoff = am;
+    roff = rm;
+  }
+
   f32x16_t o[QT][NDT];
 #pragma unroll
   for (int qt = 0; qt < QT; ++qt)
 #pragma unroll
     for (int dt = 0; dt < NDT; ++dt) o[qt][dt] = zero16();
 
-  // decomposed: alpha[j0 + t] for t < 64 and rho[d] for d = dmin + t, t < RW,
-  // dmin = q0 - j0 - 63.  Out-of-range distances are -inf (exact zero cells).
-  float a_reg = 0.f, r_reg[(RW + NTHR - 1) / NTHR];
-  auto stage_params = [&](int j0) {
-    if (MODE != 1) return;
-    if (tid < 64) {
-      const int j = j0 + tid;
-      a_reg = j < T_len ? load_as_f32(p.alpha, (int64_t)ph * p.a_sh + (int64_t)j * p.a_ss, p.a_dtype) * kLog2e : 0.f;
-    }
-    const int dmin = q0 - j0 - 63;
-#pragma unroll
-    for (int u = 0; u < (RW + NTHR - 1) / NTHR; ++u) {
-      const int t = tid + u * NTHR;
-      const int d = dmin + t;
-      r_reg[u] = (t < RW && d >= 0 && d < T_len)
-                     ? load_as_f32(p.rho, (int64_t)ph * p.r_sh + (int64_t)d * p.r_ss, p.r_dtype) * kLog2e
-                     : -INFINITY;
-    }
-  };
-  auto store_params = [&](int buf) {
-    if (MODE != 1) return;
-    if (tid < 64) a_lds[buf][tid] = a_reg;
-#pragma unroll
-    for (int u = 0; u < (RW + NTHR - 1) / NTHR; ++u) {
-      const int t = tid + u * NTHR;
-      if (t < RW) r_lds[buf][t] = r_reg[u];
-    }
-  };
-
   VStager<T, HD, NTHR> vst;
-  vst.load(vbase, p.v_st, 64 * kb0, T_len, tid);
-  stage_params(64 * kb0);
-  vst.store(reinterpret_cast<uint32_t*>(v_lds[0]), tid);
-  store_params(0);
-  __syncthreads();
+  float rowscale[QT];
 
-  for (int j = kb0; j < nkb; ++j) {
-    const int buf = (j - kb0) & 1;
-    const bool more = j + 1 < nkb;
-    if (more) {
-      vst.load(vbase, p.v_st, 64 * (j + 1), T_len, tid);
-      stage_params(64 * (j + 1));
-    }
-    if (j < nkb_w) {
-      const int j0 = 64 * j;
-      const uint4* vt = v_lds[buf];
+  if (factored) {
+    // V' rows: the key factor 2^(a_j - A) applied while staging
+    auto scale_v = [&](int j0) {
 #pragma unroll
-      for (int ks = 0; ks < 2; ++ks)
+      for (int pp = 0; pp < VStager<T, HD, NTHR>::PER_THR; ++pp) {
+        const int key = j0 + vst.item_key(pp, tid);
+        const float f0 = key < T_len ? fast_exp2(fmaf(alpha_at(key), kLog2e, -aoff)) : 0.f;
+        const float f1 = key + 1 < T_len ? fast_exp2(fmaf(alpha_at(key + 1), kLog2e, -aoff)) : 0.f;
+        vst.scale_rows(pp, f0, f1);
+      }
+    };
+    // distance window of block j0: m in [0, RW) holds E(d), d = q0 - j0 + BM - m
+    // (the window reversed); copy c holds window element c + k at k
+    float er[ERN];
+    auto stage_er = [&](int j0) {
 #pragma unroll
-        for (int sh = 0; sh < 2; ++sh) {
-          const int jb = j0 + 32 * ks + 16 * sh + 8 * g;
-          uint4 pb[QT];
+      for (int u = 0; u < ERN; ++u) {
+        const int m = tid + u * NTHR;
+        const int d = q0 - j0 + BM - m;
+        er[u] = (m < RW && d >= 0 && d < T_len) ? fast_exp2(fmaf(rho_at(d), kLog2e, -roff)) : 0.f;
+      }
+    };
+    auto store_er = [&](int buf) {
 #pragma unroll
-          for (int qt = 0; qt < QT; ++qt) {
-            const int i = q0w + 32 * qt + n;
-            const int dbase = i - jb - (q0 - j0 - 63);  // index of d = i - jb in r_lds
-            float e[8];
+      for (int u = 0; u < ERN; ++u) {
+        const int m = tid + u * NTHR;
+        if (m < RW) {
+          const uint16_t bits = (uint16_t)(Elem<T>::pack2(er[u], 0.f) & 0xffffu);
 #pragma unroll
-            for (int u = 0; u < 8; ++u)
-              e[u] = fast_exp2(a_lds[buf][jb - j0 + u] + r_lds[buf][dbase - u] - zq[qt]);
-            pb[qt] = make_uint4(Elem<T>::pack2(e[0], e[1]), Elem<T>::pack2(e[2], e[3]),
-                                Elem<T>::pack2(e[4], e[5]), Elem<T>::pack2(e[6], e[7]));
-          }
-#pragma unroll
-          for (int dt = 0; dt < NDT; ++dt) {
-            const uint4 a = vt[VLayout<HD>::chunk(32 * dt + n, 4 * ks + 2 * sh + g)];
-#pragma unroll
-            for (int qt = 0; qt < QT; ++qt) o[qt][dt] = Elem<T>::mfma(a, pb[qt], o[qt][dt]);
-          }
+          for (int c = 0; c < 8; ++c)
+            if (m >= c) er_lds[buf][c][m - c] = bits;
         }
+      }
+    };
+    // lane (n, g), query tile qt reads keys jb + 0..7 (jb = j0 + 16 st + 8g)
+    // of row i: window elements s .. s+7, s = BM - (i - q0) + 16 st + 8g, from
+    // copy (s & 7) = (-(i - q0)) & 7 at element s - (s & 7)
+    int ec[QT], ek[QT];
+#pragma unroll
+    for (int qt = 0; qt < QT; ++qt) {
+      const int il = q0w + 32 * qt + n - q0;
+      ec[qt] = (-il) & 7;
+      ek[qt] = BM - il - ec[qt] + 8 * g;
     }
-    if (more) {
-      vst.store(reinterpret_cast<uint32_t*>(v_lds[buf ^ 1]), tid);
-      store_params(buf ^ 1);
-    }
+
+    vst.load(vbase, p.v_st, 64 * kb0, T_len, tid);
+    scale_v(64 * kb0);
+    stage_er(64 * kb0);
+    vst.store(reinterpret_cast<uint32_t*>(v_lds[0]), tid);
+    store_er(0);
     __syncthreads();
+    for (int j = kb0; j < nkb; ++j) {
+      const int buf = (j - kb0) & 1;
+      const bool more = j + 1 < nkb;
+      if (more) {
+        vst.load(vbase, p.v_st, 64 * (j + 1), T_len, tid);
+        scale_v(64 * (j + 1));
+        stage_er(64 * (j + 1));
+      }
+      if (j < nkb_w) {
+        const uint4* vt = v_lds[buf];
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+          for (int sh = 0; sh < 2; ++sh) {
+            uint4 pb[QT];
+#pragma unroll
+            for (int qt = 0; qt < QT; ++qt)
+              pb[qt] = *reinterpret_cast<const uint4*>(&er_lds[buf][ec[qt]][ek[qt] + 32 * ks + 16 * sh]);
+#pragma unroll
+            for (int dt = 0; dt < NDT; ++dt) {
+              const uint4 a = vt[VLayout<HD>::chunk(32 * dt + n, 4 * ks + 2 * sh + g)];
+#pragma unroll
+              for (int qt = 0; qt < QT; ++qt) o[qt][dt] = Elem<T>::mfma(a, pb[qt], o[qt][dt]);
+            }
+          }
+      }
+      if (more) {
+        vst.store(reinterpret_cast<uint32_t*>(v_lds[buf ^ 1]), tid);
+        store_er(buf ^ 1);
+      }
+      __syncthreads();
+    }
+#pragma unroll
+    for (int qt = 0; qt < QT; ++qt) rowscale[qt] = fast_exp2(aoff + roff - zq[qt]);
+  } else {
+    // decomposed: alpha[j0 + t] for t < 64 and rho[d] for d = dmin + t, t < RW,
+    // dmin = q0 - j0 - 63.  Out-of-range distances are -inf (exact zero cells).
+    float a_reg = 0.f, r_reg[(RW + NTHR - 1) / NTHR];
+    auto stage_params = [&](int j0) {
+      if (tid < 64) {
+        const int j = j0 + tid;
+        a_reg = j < T_len ? alpha_at(j) * kLog2e : 0.f;
+      }
+      const int dmin = q0 - j0 - 63;
+#pragma unroll
+      for (int u = 0; u < (RW + NTHR - 1) / NTHR; ++u) {
+        const int t = tid + u * NTHR;
+        const int d = dmin + t;
+        r_reg[u] = (t < RW && d >= 0 && d < T_len) ? rho_at(d) * kLog2e : -INFINITY;
+      }
+    };
+    auto store_params = [&](int buf) {
+      if (tid < 64) a_lds[buf][tid] = a_reg;
+#pragma unroll
+      for (int u = 0; u < (RW + NTHR - 1) / NTHR; ++u) {
+        const int t = tid + u * NTHR;
+        if (t < RW) r_lds[buf][t] = r_reg[u];
+      }
+    };
+
+    vst.load(vbase, p.v_st, 64 * kb0, T_len, tid);
+    stage_params(64 * kb0);
+    vst.store(reinterpret_cast<uint32_t*>(v_lds[0]), tid);
+    store_params(0);
+    __syncthreads();
+
+    for (int j = kb0; j < nkb; ++j) {
+      const int buf = (j - kb0) & 1;
+      const bool more = j + 1 < nkb;
+      if (more) {
+        vst.load(vbase, p.v_st, 64 * (j + 1), T_len, tid);
+        stage_params(64 * (j + 1));
+      }
+      if (j < nkb_w) {
+        const int j0 = 64 * j;
+        const uint4* vt = v_lds[buf];
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+          for (int sh = 0; sh < 2; ++sh) {
+            const int jb = j0 + 32 * ks + 16 * sh + 8 * g;
+            uint4 pb[QT];
+#pragma unroll
+            for (int qt = 0; qt < QT; ++qt) {
+              const int i = q0w + 32 * qt + n;
+              const int dbase = i - jb - (q0 - j0 - 63);  // index of d = i - jb in r_lds
+              float e[8];
+#pragma unroll
+              for (int u = 0; u < 8; ++u)
+                e[u] = fast_exp2(a_lds[buf][jb - j0 + u] + r_lds[buf][dbase - u] - zq[qt]);
+              pb[qt] = make_uint4(Elem<T>::pack2(e[0], e[1]), Elem<T>::pack2(e[2], e[3]),
+                                  Elem<T>::pack2(e[4], e[5]), Elem<T>::pack2(e[6], e[7]));
+            }
+#pragma unroll
+            for (int dt = 0; dt < NDT; ++dt) {
+              const uint4 a = vt[VLayout<HD>::chunk(32 * dt + n, 4 * ks + 2 * sh + g)];
+#pragma unroll
+              for (int qt = 0; qt < QT; ++qt) o[qt][dt] = Elem<T>::mfma(a, pb[qt], o[qt][dt]);
+            }
+          }
+      }
+      if (more) {
+        vst.store(reinterpret_cast<uint32_t*>(v_lds[buf ^ 1]), tid);
+        store_params(buf ^ 1);
+      }
+      __syncthreads();
+    }
+#pragma unroll
+    for (int qt = 0; qt < QT; ++qt) rowscale[qt] = 1.f;
   }
 
 #pragma unroll
   for (int qt = 0; qt < QT; ++qt) {
     const int i = q0w + 32 * qt + n;
     if (i >= T_len) continue;
+    const float sc = rowscale[qt];
     if (split) {  // plain-sum partial of this key segment, added up by the combine kernel
       const int64_t pidx = (int64_t)r * p.n_part_per_head + p.part_base[qb] + seg;
       float* po = p.part_o + (pidx * BM + (i - q0)) * HD;
@@ -186,9 +337,10 @@ void frozen_decomp_kernel(const FrozenParams p) {
 #pragma unroll
         for (int r4 = 0; r4 < 4; ++r4)
           *reinterpret_cast<float4*>(po + 32 * dt + 8 * r4 + 4 * g) =
-              make_float4(o[qt][dt][4 * r4], o[qt][dt][4 * r4 + 1], o[qt][dt][4 * r4 + 2], o[qt][dt][4 * r4 + 3]);
+              make_float4(o[qt][dt][4 * r4] * sc, o[qt][dt][4 * r4 + 1] * sc, o[qt][dt][4 * r4 + 2] * sc,
+                          o[qt][dt][4 * r4 + 3] * sc);
     } else {
-      store_out_tile<T, HD>(obase + (int64_t)i * p.o_st, o[qt], 1.f, g);
+      store_out_tile<T, HD>(obase + (int64_t)i * p.o_st, o[qt], sc, g);
     }
   }
 }

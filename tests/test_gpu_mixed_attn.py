@@ -155,6 +155,37 @@ def test_decomposed_extreme_logits(case):
     run_case(B, H, T, hd, S, fz, dec, no_patt=np_, dec_scale=40.0)
 
 
+def test_decomposed_factored_and_rebuilt_workgroups():
+    """The decomposed kernel picks, per workgroup, the factored form (key and
+    row factors around a Toeplitz operand) when every row's z lies within
+    kFactorRange of max(a) + max(r), else the cell-by-cell rebuild.  Head 0:
+    moderate parameters (factored everywhere); head 1: an alpha spike of +150
+    at key 1500 (workgroups past it rebuild, those before stay factored); head
+    2: rho with -inf entries (a window) and a lane of -inf alpha; head 3: a
+    slow ramp of alpha over 200 log units (factored only where the ramp's
+    span allows).  Both forms against the float64 oracle, bf16 and fp16
+    (fp16 always rebuilds)."""
+    import kernel
+    B, H, T, hd, S = 2, 4, 2500, 64, 2560
+    g = torch.Generator().manual_seed(77)
+    alpha = torch.randn(H, S, generator=g) * 0.7
+    rho = torch.randn(H, S, generator=g) * 0.7
+    alpha[1, 1500] = 150.0
+    rho[2, 300:] = float("-inf")
+    alpha[2, 40:48] = float("-inf")
+    alpha[3] = torch.linspace(-100.0, 100.0, S)
+    z = torch.from_numpy(orc.decomposed_logz(alpha.double().numpy(), rho.double().numpy())).float()
+    frozen = torch.full((H,), 2, dtype=torch.int32)
+    for dtype in (torch.bfloat16, torch.float16):
+        q, k, v = qkv(B, H, T, hd, seed=5, dtype=dtype)
+        y = kernel.fused_mixed_attn(q[:, :0].to(DEV), k[:, :0].to(DEV), v.to(DEV), None, frozen.to(DEV),
+                                    alpha=alpha.to(DEV), rho=rho.to(DEV), z=z.to(DEV))
+        torch.cuda.synchronize()
+        ref = orc.eager_mixed_attention(None, None, f64(v), frozen.numpy(), alpha=f64(alpha), rho=f64(rho),
+                                        z=f64(z))
+        compare(y, ref, what=f"decomposed factored/rebuilt {dtype}")
+
+
 def test_compact_pidx_with_decomposed():
     run_case(2, 12, 700, 64, 1024, [3, 9], [0, 7], strided=True, compact_patt=True)
 
