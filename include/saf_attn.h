@@ -36,8 +36,15 @@
  *     the calls of that one entry point).
  *   - Head dims: the forward entry points take HD in {32, 64, 96, 128, 256}
  *     (the reference's Triton kernels take any power of two; 256 is
- *     Qwen3.5's); the backward entry points and the fused RoPE / q-k norm
- *     prologue take HD <= 128 and return SAF_EUNSUPPORTED above.
+ *     Qwen3.5's); the bf16 / fp16 backward entry points and the fused RoPE /
+ *     q-k norm prologue take HD <= 128 and return SAF_EUNSUPPORTED above.
+ *   - Activation dtypes: bf16 and fp16 run the MFMA kernels; float32 q/k/v
+ *     (the reference's IEEE-dot contract, kernel/fused_attn.py:36-37) run
+ *     fp32 vector-ALU kernels in saf_mixed_attn_fwd / _bwd, the per-kind
+ *     entry points and saf_frozen_pv_fwd / _bwd, every HD above, with no
+ *     workspace (closed-form heads go through their alpha / rho / z in the
+ *     decomposed pass, so saf_frozen_scan_fwd has nothing to do for them).
+ *     saf_decomp_param_bwd takes bf16 / fp16 only.
  *   - Return value: SAF_OK (0) or a negative status; saf_last_error() then
  *     holds a message for the calling thread.
  */

@@ -610,6 +610,7 @@ static hipError_t bwd_launch(const BwdParams& p, int hd, int which, hipStream_t 
 }
 
 static hipError_t bwd_dispatch(const BwdParams& p, int dtype, int hd, int which, hipStream_t s) {
+  if (dtype == kF32) return which <= 3 ? launch_f32_bwd(p, hd, which, s) : hipErrorInvalidValue;
   if (dtype == kBF16) return bwd_launch<__bf16>(p, hd, which, s);
   if (dtype == kF16) return bwd_launch<_Float16>(p, hd, which, s);
   return hipErrorInvalidValue;

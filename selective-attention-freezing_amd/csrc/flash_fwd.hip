@@ -644,6 +644,7 @@ static hipError_t launch_flash_hd(const FlashParams& p, int hd, int qt, hipStrea
 }
 
 hipError_t launch_flash(const FlashParams& p, int dtype, int hd, int qt, hipStream_t s) {
+  if (dtype == kF32) return launch_f32_live(p, hd, s);
   if (dtype == kBF16) return launch_flash_hd<__bf16>(p, hd, qt, s);
   if (dtype == kF16) return launch_flash_hd<_Float16>(p, hd, qt, s);
   return hipErrorInvalidValue;

@@ -735,6 +735,7 @@ static hipError_t launch_frozen_hd(const FrozenParams& p, int hd, int mode, hipS
 
 
 hipError_t launch_frozen_pv(const FrozenParams& p, int dtype, int hd, int mode, hipStream_t s) {
+  if (dtype == kF32) return launch_f32_frozen(p, hd, mode, s);
   if (dtype == kBF16) return launch_frozen_hd<__bf16>(p, hd, mode, s);
   if (dtype == kF16) return launch_frozen_hd<_Float16>(p, hd, mode, s);
   return hipErrorInvalidValue;

@@ -104,9 +104,7 @@ int plan_and_validate(const saf_mixed_attn_args* a, unsigned which, Plan& pl, bo
   const saf_tensor_t& v = a->v;
   if (!present(v)) return fail(SAF_EINVAL, "v is required");
   if (v.ndim != 4) return fail(SAF_EINVAL, "q, k, v must be 4-D");
-  if (v.dtype == SAF_F32)
-    return fail(SAF_EUNSUPPORTED, "float32 attention inputs are not supported by the MFMA path (use bf16 or fp16)");
-  if (v.dtype != SAF_BF16 && v.dtype != SAF_F16)
+  if (v.dtype != SAF_BF16 && v.dtype != SAF_F16 && v.dtype != SAF_F32)
     return fail(SAF_EUNSUPPORTED, "unsupported v dtype %s", dtype_name(v.dtype));
   pl.B = (int)v.size[0];
   pl.HV = (int)v.size[1];
@@ -150,7 +148,12 @@ int plan_and_validate(const saf_mixed_attn_args* a, unsigned which, Plan& pl, bo
           return fail(SAF_EINVAL, "decay rate of head %d must be finite and > 0 (got %g)", h, prm);
         if (ck == SAF_CLOSED_WINDOW && !(prm >= 1.f && prm < 2.1e9f && prm == std::floor(prm)))
           return fail(SAF_EINVAL, "window length of head %d must be an integer >= 1 (got %g)", h, prm);
-        pl.scan.push_back(h);
+        // float32 inputs have no scan kernel: closed forms run through their
+        // decomposed buffers with the other state-2 heads
+        if (v.dtype == SAF_F32)
+          pl.decomp.push_back(h);
+        else
+          pl.scan.push_back(h);
       } else {
         pl.decomp.push_back(h);
       }
@@ -378,11 +381,12 @@ int run_flash(const saf_mixed_attn_args* a, const Plan& pl, hipStream_t s) {
   // the work queue pays off for the one-workgroup-per-CU kernel above hd 64
   // (C3 flash 458 -> 426 us); at hd <= 64 the three resident workgroups per
   // CU keep the CUs fed and the queue measured 4% slower
-  if (pl.HD > 64 && have_ws && a->workspace_bytes >= part_off) {
+  const bool f32 = pl.dtype == SAF_F32;  // the float32 kernel neither splits nor queues
+  if (!f32 && pl.HD > 64 && have_ws && a->workspace_bytes >= part_off) {
     p.queue = reinterpret_cast<unsigned*>(reinterpret_cast<char*>(a->workspace) + queue_off);
     p.max_grid = cu_count() * flash_resident(pl.HD, qt);
   }
-  if (fp.n_items && have_ws && a->workspace_bytes >= part_off + fp.part_bytes) {
+  if (!f32 && fp.n_items && have_ws && a->workspace_bytes >= part_off + fp.part_bytes) {
     char* ws = reinterpret_cast<char*>(a->workspace) + part_off;
     const int64_t nbh = (int64_t)pl.B * p.n_slots;
     p.n_items = fp.n_items;
@@ -469,7 +473,8 @@ int run_dense(const saf_tensor_t& patt, const saf_tensor_t& v, const saf_tensor_
     p.pat_head[i] = (int16_t)pat_head[i];
   }
   FlashPlan fp = plan_dense(B, p.n_slots, T, HD);
-  if (fp.n_items && ws != nullptr && ws_bytes >= fp.part_bytes && reinterpret_cast<uintptr_t>(ws) % 16 == 0) {
+  if (dtype != SAF_F32 && fp.n_items && ws != nullptr && ws_bytes >= fp.part_bytes &&
+      reinterpret_cast<uintptr_t>(ws) % 16 == 0) {
     p.n_items = fp.n_items;
     p.seg_len = fp.seg_len;
     p.n_part_per_head = fp.n_part_per_head;
@@ -515,7 +520,7 @@ int run_decomp(const saf_mixed_attn_args* a, const Plan& pl, hipStream_t s) {
   const int BM = block_rows(frozen_qtiles(pl.HD));
   FlashPlan fp = plan_flash(pl.B, p.n_slots, pl.T, pl.HD, BM, decomp_resident(pl.HD));
   const int64_t part_off = scan_ws_bytes(pl);
-  if (fp.n_items && a->workspace != nullptr && a->workspace_bytes >= part_off + fp.part_bytes &&
+  if (pl.dtype != SAF_F32 && fp.n_items && a->workspace != nullptr && a->workspace_bytes >= part_off + fp.part_bytes &&
       reinterpret_cast<uintptr_t>(a->workspace) % 16 == 0) {
     p.n_items = fp.n_items;
     p.seg_len = fp.seg_len;
@@ -618,9 +623,7 @@ int saf_frozen_pv_fwd(const saf_tensor_t* patt, const saf_tensor_t* v, const int
   if (patt == nullptr || v == nullptr || out == nullptr) return fail(SAF_EINVAL, "patt, v and out are required");
   if (!present(*v) || !present(*out)) return fail(SAF_EINVAL, "v and out must be device tensors");
   if (v->ndim != 4 || out->ndim != 4) return fail(SAF_EINVAL, "v and out must be 4-D (B, nf, T, hd)");
-  if (v->dtype == SAF_F32)
-    return fail(SAF_EUNSUPPORTED, "float32 values are not supported by the MFMA path (use bf16 or fp16)");
-  if (v->dtype != SAF_BF16 && v->dtype != SAF_F16)
+  if (v->dtype != SAF_BF16 && v->dtype != SAF_F16 && v->dtype != SAF_F32)
     return fail(SAF_EUNSUPPORTED, "unsupported v dtype %s", dtype_name(v->dtype));
   const int B = (int)v->size[0], HD = (int)v->size[3];
   if (nf != v->size[1]) return fail(SAF_EINVAL, "fz_idx must have one entry per compact head (%d != %lld)", nf,
@@ -655,14 +658,14 @@ int saf_frozen_pv_bwd(const saf_tensor_t* patt, const saf_tensor_t* dy, const in
   if (patt == nullptr || dy == nullptr || dv == nullptr) return fail(SAF_EINVAL, "patt, dy and dv are required");
   if (!present(*dy) || !present(*dv)) return fail(SAF_EINVAL, "dy and dv must be device tensors");
   if (dy->ndim != 4 || dv->ndim != 4) return fail(SAF_EINVAL, "dy and dv must be 4-D (B, nf, T, hd)");
-  if (dy->dtype != SAF_BF16 && dy->dtype != SAF_F16)
-    return fail(SAF_EUNSUPPORTED, "frozen_pv backward supports bf16 / fp16 gradients (got %s)", dtype_name(dy->dtype));
+  if (dy->dtype != SAF_BF16 && dy->dtype != SAF_F16 && dy->dtype != SAF_F32)
+    return fail(SAF_EUNSUPPORTED, "frozen_pv backward: unsupported gradient dtype %s", dtype_name(dy->dtype));
   const int B = (int)dv->size[0], HD = (int)dv->size[3];
   if (nf != dv->size[1]) return fail(SAF_EINVAL, "fz_idx must have one entry per compact head (%d != %lld)", nf,
                                     (long long)dv->size[1]);
   if (nf > SAF_MAX_HEADS) return fail(SAF_EUNSUPPORTED, "more than %d frozen heads", SAF_MAX_HEADS);
   if (T < 0 || T > dv->size[2]) return fail(SAF_EINVAL, "T must be within dv's sequence length");
-  if (!supported_bwd_hd(HD))
+  if (!supported_bwd_hd(HD) && !(HD == 256 && dy->dtype == SAF_F32))
     return fail(SAF_EUNSUPPORTED, "frozen_pv backward: head_dim %d is not supported (32, 64, 96, 128)", HD);
   if (dy->size[0] != B || dy->size[1] != nf || dy->size[2] != T || dy->size[3] != HD || dy->dtype != dv->dtype)
     return fail(SAF_EINVAL, "dy must be (B, nf, T, hd) in dv's dtype");
@@ -895,7 +898,7 @@ int saf_mixed_attn_bwd(const saf_mixed_attn_args* a, const saf_tensor_t* dout, c
   if (int rc = plan_and_validate(a, kDoFlash | kDoDense | kDoDecomp, pl, false)) return rc;
   if (a->kvidx != nullptr)
     return fail(SAF_EUNSUPPORTED, "backward with kvidx (GQA) is not implemented (forward / prefill only)");
-  if (!supported_bwd_hd(pl.HD))
+  if (!supported_bwd_hd(pl.HD) && pl.dtype != SAF_F32)  // the float32 kernels take hd 256 too
     return fail(SAF_EUNSUPPORTED, "backward: head_dim %d is not supported (32, 64, 96, 128)", pl.HD);
   if (dout == nullptr || dv == nullptr) return fail(SAF_EINVAL, "dout and dv are required");
   auto same4 = [](const saf_tensor_t& t, const saf_tensor_t& ref) {
@@ -1023,6 +1026,8 @@ int saf_decomp_param_bwd(const saf_mixed_attn_args* a, const saf_tensor_t* dout,
   if (int rc = plan_and_validate(a, 0, pl, false)) return rc;
   if (a->kvidx != nullptr)
     return fail(SAF_EUNSUPPORTED, "pattern gradients with kvidx (GQA) are not implemented (forward / prefill only)");
+  if (pl.dtype == SAF_F32)
+    return fail(SAF_EUNSUPPORTED, "pattern gradients take bf16 / fp16 attention inputs (float32 is not implemented)");
   if (!supported_bwd_hd(pl.HD))
     return fail(SAF_EUNSUPPORTED, "pattern gradients: head_dim %d is not supported (32, 64, 96, 128)", pl.HD);
   if (dout == nullptr || dalpha == nullptr || drho == nullptr)
@@ -1088,6 +1093,7 @@ int saf_decomp_param_bwd(const saf_mixed_attn_args* a, const saf_tensor_t* dout,
 int64_t saf_mixed_attn_workspace_bytes(const saf_mixed_attn_args* args) {
   Plan pl;
   if (plan_and_validate(args, kDoFlash | kDoScan, pl, false)) return -1;
+  if (pl.dtype == SAF_F32) return 0;  // no scan, no split
   int64_t total = scan_ws_bytes(pl), part = 0;
   if (!pl.live.empty()) {
     const int qt = flash_qtiles_for(args, pl.HD);

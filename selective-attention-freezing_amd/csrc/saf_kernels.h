@@ -253,6 +253,12 @@ hipError_t launch_bwd_frozen_dv(const BwdParams& p, int dtype, int hd, hipStream
 // heads (out_head = head, pat_head = buffer row), delta of those rows in p.delta.
 hipError_t launch_bwd_decomp_param(const BwdParams& p, int dtype, int hd, hipStream_t s);
 
+// float32 inputs (attn_f32.hip): the same parameter blocks, no causal split
+// (n_items 0), no work queue; which: 0 delta, 1 dQ, 2 dK / dV, 3 frozen dV.
+hipError_t launch_f32_live(const FlashParams& p, int hd, hipStream_t s);
+hipError_t launch_f32_frozen(const FrozenParams& p, int hd, int mode, hipStream_t s);
+hipError_t launch_f32_bwd(const BwdParams& p, int hd, int which, hipStream_t s);
+
 // Queries per frozen-head workgroup (4 waves) for a query-tile count.
 inline int block_rows(int qt) { return 4 * 32 * qt; }
 

@@ -358,6 +358,10 @@ def fused_mixed_attn(q, k, v, patt, frozen, hidx=None, pidx=None,
     kv_identity = kvidx is None
     if alpha is not None and z is None:
         z = decomposed_logz(alpha.float(), rho.float()).to(alpha.dtype)
+    if v.dtype == torch.float32:
+        # the float32 kernels have no scan: closed forms run through their
+        # decomposed buffers like the other state-2 heads
+        closed_form = None
     if validate:
         _validate(q, k, v, patt, frozen, hidx, pidx, alpha, rho, z, rho_band, kvidx)
     if not v.is_cuda:

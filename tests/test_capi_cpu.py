@@ -66,7 +66,8 @@ def _args(H=4, T=64, hd=64, dtype=_ext.SAF_BF16, frozen=None, ptr=0x100000):
 
 @pytest.mark.parametrize("mutate,code,msg", [
     (lambda a: setattr(a, "n_heads", 0), _ext.SAF_EUNSUPPORTED, "n_heads"),
-    (lambda a: setattr(a.v, "dtype", _ext.SAF_F32), _ext.SAF_EUNSUPPORTED, "float32"),
+    (lambda a: setattr(a.v, "dtype", _ext.SAF_I32), _ext.SAF_EUNSUPPORTED, "int32"),
+    (lambda a: setattr(a.v, "dtype", _ext.SAF_F32), _ext.SAF_EINVAL, "dtype must match"),
     (lambda a: a.v.size.__setitem__(3, 80), _ext.SAF_EUNSUPPORTED, "head_dim"),
     (lambda a: a.out.size.__setitem__(2, 63), _ext.SAF_EINVAL, "out must have shape"),
     (lambda a: a.v.stride.__setitem__(3, 2), _ext.SAF_EALIGN, "contiguous last"),
