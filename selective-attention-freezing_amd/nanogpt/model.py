@@ -339,7 +339,10 @@ class CausalSelfAttention(nn.Module):
                 if self.position_encoding == "rope":
                     if rope is None:
                         raise ValueError("RoPE Q/K requested without a rotary cache")
-                    _kernel_mod.rope_qk_(qu, ku, *rope)
+                    if qu.dtype in (torch.bfloat16, torch.float16):
+                        _kernel_mod.rope_qk_(qu, ku, *rope)
+                    else:  # the in-place kernel is bf16 / fp16; fp32 keeps torch's rotation
+                        qu, ku = apply_rotary_pos_emb(qu, ku, *rope)
         _FUSED_DISPATCH_COUNT += 1
         dec = self._dec_any
         y = fused_mixed_attn(qu, ku, v, self.dyn_pattern, self._fz_mask_i32, hidx,

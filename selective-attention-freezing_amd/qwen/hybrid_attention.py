@@ -274,7 +274,7 @@ class HybridAttentionBase(nn.Module):
         v = y[:, :, U + HKV:U + 2 * HKV].transpose(1, 2)
         gate = y[:, :, U + 2 * HKV:] if self.SPEC.gated else None
         if U:
-            if (self.SPEC.hip_prologue and hd in _PROLOGUE_HEAD_DIMS
+            if (self.SPEC.hip_prologue and hd in _PROLOGUE_HEAD_DIMS and q.dtype != torch.float32
                     and (cos.dim() == 2 or cos.size(0) == 1)):
                 _kernel_mod.qk_rmsnorm_rope_(q, k, self.q_norm.weight, self.k_norm.weight,
                                              self.q_norm.variance_epsilon, cos, sin)

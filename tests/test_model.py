@@ -83,6 +83,20 @@ def test_gpu_model_logits_match_oracle():
 
 
 @pytest.mark.gpu
+def test_gpu_model_fp32_logits_match_oracle():
+    """The fp32 model (the fp32 kernels, torch's RoPE) against the fp32 oracle:
+    max-abs 2e-4 on every logit (the reference's fp32 contract at the op
+    level is 2e-5 on attention outputs)."""
+    m, x = _small_model(T=256, layers=2, device="cuda", dtype=torch.float32)
+    with torch.inference_mode():
+        logits = m.forward_all_positions(x).float().cpu()
+    sd, ocfg, freeze = _oracle_inputs(m)
+    ref = model_oracle.gpt_forward(sd, ocfg, freeze, x.cpu(), path="eager", all_positions=True)
+    err = (logits - ref).abs().max().item()
+    assert err <= 2e-4, f"fp32 logits max_abs {err:.3e}"
+
+
+@pytest.mark.gpu
 def test_gpu_model_nothing_frozen_and_all_frozen():
     from nanogpt.model import GPT, GPTConfig
     torch.manual_seed(0)
