@@ -353,13 +353,16 @@ def logz_grads(alpha, rho, gz):
     return da, dr
 
 
-def pattern_grads(v, dout, frozen, alpha, rho, heads=None):
+def pattern_grads(v, dout, frozen, alpha, rho, heads=None, out=None):
     """dalpha, drho (H, S) of sum(dout * y) over the decomposed heads (state
     2) of eager_mixed_attention, summed over the batch: with P the row
     softmax of alpha_j + rho_{i-j}, y = P V, dP = dO V^T, delta_i = dO_i . y_i,
     dS = P (dP - delta) and dalpha_j = sum_i dS_ij, drho_d = sum_{i-j=d} dS_ij
-    (float64, v / dout (B, H, T, HD))."""
+    (float64, v / dout (B, H, T, HD)).  With `out` (B, H, T, HD) delta is
+    taken from it instead of the exact y, as the reference's kernel takes it
+    from the saved forward output (supplement/trainable_pattern_kernels.py:44)."""
     v, dout = _f64(v), _f64(dout)
+    out = None if out is None else _f64(out)
     alpha, rho = _f64(alpha), _f64(rho)
     H, S = alpha.shape
     B, _, T, _ = v.shape
@@ -373,7 +376,7 @@ def pattern_grads(v, dout, frozen, alpha, rho, heads=None):
         for b in range(B):
             y = P @ v[b, h]
             dP = dout[b, h] @ v[b, h].T
-            delta = (dout[b, h] * y).sum(-1, keepdims=True)
+            delta = (dout[b, h] * (y if out is None else out[b, h])).sum(-1, keepdims=True)
             dS = P * (dP - delta)
             da[h, :T] += dS.sum(0)
             for d in range(T):

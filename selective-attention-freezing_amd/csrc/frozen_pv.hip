@@ -29,24 +29,38 @@ namespace saf {
 // budget of two waves per SIMD.
 constexpr int decomp_waves_per_eu(int hd) { return hd > 128 ? 2 : 3; }
 
+// s_waitcnt immediates (gfx9 encoding: vmcnt bits 3:0 and 15:14, expcnt
+// 6:4, lgkmcnt 11:8): vmcnt <= n alone, and vmcnt <= n with lgkmcnt 0.
+constexpr int waitcnt_vm(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8); }
+constexpr int waitcnt_vm_lgkm0(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4); }
+
 // Decomposed frozen heads, P = exp(alpha_j + rho_{i-j} - z_i), in one of
-// two forms chosen per workgroup from the parameters it reads.
+// two forms chosen per workgroup.
 //
-// Factored form (bf16): P = diag(2^(A + R - z)) . E . diag(2^(a - A)) with
-// E_ij = 2^(r_{i-j} - R), everything in log2 units (a = alpha log2 e, r, z
-// likewise) and A, R the maxima of a and r over the keys and distances the
-// workgroup reaches.  So Y = 2^(A + R - z_i) (E V'), V'_j = 2^(a_j - A) v_j:
-// the key factors are applied once per V row while it is staged in LDS, E is
-// a Toeplitz matrix whose 2^(r_d - R) values are computed once per distance
-// and block (not per cell), and the row factor is applied to the fp32
-// accumulators at the end.  Each lane's E^T operand (8 consecutive
-// distances, reversed) is one aligned ds_read_b128 from one of 8 copies of
-// the block's distance window shifted by 0..7 elements.  Every factor is
-// <= 1 before the row factor, and the form is used only when every row's z
-// is within kFactorRange of A + R, so every cell that matters (P > 2^-24)
-// has both bf16 factors far above the normal range limit and the products
-// stay normal in fp32; otherwise (and for fp16, whose exponent range is too
-// short) the workgroup rebuilds P cell by cell.
+// Factored form (bf16, hd <= 128, with the workspace's key-scaled values):
+// in log2 units (a = alpha log2 e, r, z likewise), with A_k the maximum of a
+// over 64-key block k, A the maximum of A_k over the blocks the workgroup
+// reads and R the maximum of r over the distances it reaches,
+//   P_ij = 2^(A + R - z_i) . E_ij . 2^(a_j - A_k),  E_ij = 2^(r_{i-j} - R + A_k - A)
+// for key j in block k.  So Y = 2^(A + R - z_i) (E V'), V'_j = 2^(a_j - A_k) v_j:
+//   - V' is written once per (batch, head) by decomp_prescale_kernel and
+//     arrives here by buffer_load ... lds DMA into the live-head kernel's VRow
+//     tiles, two blocks ahead in three static slots; its V'^T operands come
+//     from ds_read_b64_tr_b16 pairs;
+//   - E costs one exp per distance per 64-key block, not one per cell: the
+//     block's distance window (with its block shift A_k - A) goes to LDS in 8
+//     copies shifted by 0..7 elements (two slots, staged one block ahead),
+//     so each lane's E^T operand (8 consecutive distances, reversed) is one
+//     aligned ds_read_b128 whose copy and offset are per-lane constants;
+//     E is held as a bf16 pair hi + lo and costs two MFMAs per operand, so
+//     the form rounds only V' (once, like the rebuild form's P);
+//   - the row factor multiplies the fp32 accumulators at the end.
+// Every factor is <= 1 before the row factor, and the form is used only when
+// every row's z is within kFactorRange of A + R, so every cell that matters
+// (P > 2^-24) has both bf16 factors far above the normal range limit and the
+// products stay normal in fp32; otherwise (and for fp16, whose exponent range
+// is too short, or without the workspace) the workgroup rebuilds P cell by
+// cell.
 //
 // Rebuild form: P^T rebuilt in registers, one 16-key operand at a time and
 // consumed by its MFMAs right away (building a whole 64-key block of
@@ -55,21 +69,33 @@ constexpr int decomp_waves_per_eu(int hd) { return hd > 128 ? 2 : 3; }
 // costs one add, one subtract and one exp2.
 constexpr float kFactorRange = 80.f;
 
+// (The body is a device function: the kernel template's host stub is then
+// emitted for every launch site.)
 template <typename T, int HD, int QT>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(decomp_waves_per_eu(HD), decomp_waves_per_eu(HD))))
-void frozen_decomp_kernel(const FrozenParams p) {
-  constexpr int MODE = 1;
+__device__ __forceinline__ void decomp_body(const FrozenParams& p) {
   constexpr int NW = 4, NTHR = 256;
   constexpr int BM = NW * 32 * QT;
   constexpr int NDT = HD / 32;
-  constexpr int RW = BM + 64;  // rho window staged per key block
-  constexpr int RWL = RW + 8;  // length of one shifted copy of the factored window (bf16)
+  constexpr int RW = BM + 64;  // rho / distance window per key block
+  constexpr int RWL = RW + 8;  // one shifted copy of the factored window (bf16 elements)
   constexpr int ERN = (RW + NTHR - 1) / NTHR;
-  constexpr bool kFactorable = std::is_same<T, __bf16>::value;
-  __shared__ __align__(16) uint4 v_lds[2][VLayout<HD>::BYTES / 16];
-  __shared__ float a_lds[2][MODE == 1 ? 64 : 1];
-  __shared__ float r_lds[2][MODE == 1 ? RW : 1];
-  __shared__ __align__(16) uint16_t er_lds[kFactorable ? 2 : 1][8][kFactorable ? RWL : 8];
+  constexpr bool kFactorable = std::is_same<T, __bf16>::value && HD <= 128;
+  // LDS: the factored form's three V' tiles (vs0..vs2) and two distance
+  // windows of hi and lo copies (eb0, eb1), or the rebuild form's two V^T
+  // tiles (vs0, vs1) and alpha / rho windows (eb0).  Separate objects, so the
+  // compiler sees that reading one slot cannot alias the DMA into another
+  // and puts no vmcnt wait before the block's LDS reads.
+  constexpr int VB = VRow<HD>::BYTES, PITCH = VRow<HD>::PITCH;
+  constexpr int VN = VRow<HD>::CHP / NW;  // V' DMA chunks per thread per tile
+  constexpr int kEBytes = 2 * 8 * RWL * 2;  // one E slot: hi and lo, 8 shifted copies each
+  constexpr int kVtBytes = VLayout<HD>::BYTES;
+  constexpr int kPrmBytes = 2 * 64 * 4 + 2 * RW * 4;  // rebuild: alpha and rho windows, two buffers
+  constexpr int kVSlot = kFactorable && VB > kVtBytes ? VB : kVtBytes;
+  constexpr int kE0 = kFactorable && kEBytes > kPrmBytes ? kEBytes : kPrmBytes;
+  __shared__ __align__(16) char vs0[kVSlot], vs1[kVSlot];
+  __shared__ __align__(16) char vs2[kFactorable ? VB : 16];
+  __shared__ __align__(16) char eb0[kE0];
+  __shared__ __align__(16) char eb1[kFactorable ? kEBytes : 16];
   __shared__ float red_lds[3][NW];
 
   const int tid = threadIdx.x, lane = tid & 63;
@@ -109,48 +135,13 @@ void frozen_decomp_kernel(const FrozenParams p) {
   auto alpha_at = [&](int j) { return load_as_f32(p.alpha, (int64_t)ph * p.a_sh + (int64_t)j * p.a_ss, p.a_dtype); };
   auto rho_at = [&](int d) { return load_as_f32(p.rho, (int64_t)ph * p.r_sh + (int64_t)d * p.r_ss, p.r_dtype); };
 
-  // per-lane row normaliser (decomposed); rows >= T get +inf -> exact zeros
+  // per-lane row normaliser; rows >= T get +inf -> exact zeros
   float zq[QT];
 #pragma unroll
   for (int qt = 0; qt < QT; ++qt) {
     const int i = q0w + 32 * qt + n;
-    zq[qt] = INFINITY;
-    if (MODE == 1 && i < T_len)
-      zq[qt] = load_as_f32(p.z, (int64_t)ph * p.z_sh + (int64_t)i * p.z_ss, p.z_dtype) * kLog2e;
-  }
-
-  // factored form: A = max a over keys < kend_wg, R = max r over distances
-  // < kend_wg (supersets of what any key segment of this block reaches), and
-  // the smallest z of the block's rows decide it for the whole workgroup
-  bool factored = false;
-  float aoff = 0.f, roff = 0.f;
-  if constexpr (kFactorable) {
-    float am = -INFINITY, rm = -INFINITY, zm = INFINITY;
-    for (int j = tid; j < kend_wg; j += NTHR) {
-      am = fmaxf(am, alpha_at(j));
-      rm = fmaxf(rm, rho_at(j));
-    }
-    for (int i = q0 + tid; i < kend_wg; i += NTHR)
-      zm = fminf(zm, load_as_f32(p.z, (int64_t)ph * p.z_sh + (int64_t)i * p.z_ss, p.z_dtype));
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) {
-      am = fmaxf(am, __shfl_xor(am, off));
-      rm = fmaxf(rm, __shfl_xor(rm, off));
-      zm = fminf(zm, __shfl_xor(zm, off));
-    }
-    if (lane == 0) {
-      red_lds[0][wave] = am;
-      red_lds[1][wave] = rm;
-      red_lds[2][wave] = zm;
-    }
-    __syncthreads();
-    am = fmaxf(fmaxf(red_lds[0][0], red_lds[0][1]), fmaxf(red_lds[0][2], red_lds[0][3])) * kLog2e;
-    rm = fmaxf(fmaxf(red_lds[1][0], red_lds[1][1]), fmaxf(red_lds[1][2], red_lds[1][3])) * kLog2e;
-    zm = fminf(fminf(red_lds[2][0], red_lds[2][1]), fminf(red_lds[2][2], red_lds[2][3])) * kLog2e;
-    factored = __builtin_isfinite(am) && __builtin_isfinite(rm) && __builtin_isfinite(zm) &&
-               zm >= am + rm - kFactorRange;
-    aoff = am;
-    roff = rm;
+    zq[qt] = i < T_len ? load_as_f32(p.z, (int64_t)ph * p.z_sh + (int64_t)i * p.z_ss, p.z_dtype) * kLog2e
+                       : INFINITY;
   }
 
   f32x16_t o[QT][NDT];
@@ -158,99 +149,216 @@ void frozen_decomp_kernel(const FrozenParams p) {
   for (int qt = 0; qt < QT; ++qt)
 #pragma unroll
     for (int dt = 0; dt < NDT; ++dt) o[qt][dt] = zero16();
-
-  VStager<T, HD, NTHR> vst;
   float rowscale[QT];
 
-  if (factored) {
-    // V' rows: the key factor 2^(a_j - A) applied while staging
-    auto scale_v = [&](int j0) {
+  // factored form: A = max A_k over this segment's key blocks, R = max r
+  // over distances < kend_wg (a superset of what any key segment of this
+  // block reaches) and the smallest z of the block's rows decide it for the
+  // whole workgroup
+  bool factored = false;
+  float aoff = 0.f, roff = 0.f;
+  const float* const ablk = p.a_off + (int64_t)slot * ((T_len + 63) / 64);
+  if constexpr (kFactorable) {
+    if (p.vp != nullptr) {
+      float am = -INFINITY, rm = -INFINITY, zm = INFINITY;
+      for (int k = kb0 + tid; k < nkb; k += NTHR) am = fmaxf(am, ablk[k]);
+      for (int j = tid; j < kend_wg; j += NTHR) rm = fmaxf(rm, rho_at(j));
+      for (int i = q0 + tid; i < kend_wg; i += NTHR)
+        zm = fminf(zm, load_as_f32(p.z, (int64_t)ph * p.z_sh + (int64_t)i * p.z_ss, p.z_dtype));
 #pragma unroll
-      for (int pp = 0; pp < VStager<T, HD, NTHR>::PER_THR; ++pp) {
-        const int key = j0 + vst.item_key(pp, tid);
-        const float f0 = key < T_len ? fast_exp2(fmaf(alpha_at(key), kLog2e, -aoff)) : 0.f;
-        const float f1 = key + 1 < T_len ? fast_exp2(fmaf(alpha_at(key + 1), kLog2e, -aoff)) : 0.f;
-        vst.scale_rows(pp, f0, f1);
+      for (int off = 32; off >= 1; off >>= 1) {
+        am = fmaxf(am, __shfl_xor(am, off));
+        rm = fmaxf(rm, __shfl_xor(rm, off));
+        zm = fminf(zm, __shfl_xor(zm, off));
       }
-    };
-    // distance window of block j0: m in [0, RW) holds E(d), d = q0 - j0 + BM - m
-    // (the window reversed); copy c holds window element c + k at k
-    float er[ERN];
-    auto stage_er = [&](int j0) {
-#pragma unroll
-      for (int u = 0; u < ERN; ++u) {
-        const int m = tid + u * NTHR;
-        const int d = q0 - j0 + BM - m;
-        er[u] = (m < RW && d >= 0 && d < T_len) ? fast_exp2(fmaf(rho_at(d), kLog2e, -roff)) : 0.f;
-      }
-    };
-    auto store_er = [&](int buf) {
-#pragma unroll
-      for (int u = 0; u < ERN; ++u) {
-        const int m = tid + u * NTHR;
-        if (m < RW) {
-          const uint16_t bits = (uint16_t)(Elem<T>::pack2(er[u], 0.f) & 0xffffu);
-#pragma unroll
-          for (int c = 0; c < 8; ++c)
-            if (m >= c) er_lds[buf][c][m - c] = bits;
-        }
-      }
-    };
-    // lane (n, g), query tile qt reads keys jb + 0..7 (jb = j0 + 16 st + 8g)
-    // of row i: window elements s .. s+7, s = BM - (i - q0) + 16 st + 8g, from
-    // copy (s & 7) = (-(i - q0)) & 7 at element s - (s & 7)
-    int ec[QT], ek[QT];
-#pragma unroll
-    for (int qt = 0; qt < QT; ++qt) {
-      const int il = q0w + 32 * qt + n - q0;
-      ec[qt] = (-il) & 7;
-      ek[qt] = BM - il - ec[qt] + 8 * g;
-    }
-
-    vst.load(vbase, p.v_st, 64 * kb0, T_len, tid);
-    scale_v(64 * kb0);
-    stage_er(64 * kb0);
-    vst.store(reinterpret_cast<uint32_t*>(v_lds[0]), tid);
-    store_er(0);
-    __syncthreads();
-    for (int j = kb0; j < nkb; ++j) {
-      const int buf = (j - kb0) & 1;
-      const bool more = j + 1 < nkb;
-      if (more) {
-        vst.load(vbase, p.v_st, 64 * (j + 1), T_len, tid);
-        scale_v(64 * (j + 1));
-        stage_er(64 * (j + 1));
-      }
-      if (j < nkb_w) {
-        const uint4* vt = v_lds[buf];
-#pragma unroll
-        for (int ks = 0; ks < 2; ++ks)
-#pragma unroll
-          for (int sh = 0; sh < 2; ++sh) {
-            uint4 pb[QT];
-#pragma unroll
-            for (int qt = 0; qt < QT; ++qt)
-              pb[qt] = *reinterpret_cast<const uint4*>(&er_lds[buf][ec[qt]][ek[qt] + 32 * ks + 16 * sh]);
-#pragma unroll
-            for (int dt = 0; dt < NDT; ++dt) {
-              const uint4 a = vt[VLayout<HD>::chunk(32 * dt + n, 4 * ks + 2 * sh + g)];
-#pragma unroll
-              for (int qt = 0; qt < QT; ++qt) o[qt][dt] = Elem<T>::mfma(a, pb[qt], o[qt][dt]);
-            }
-          }
-      }
-      if (more) {
-        vst.store(reinterpret_cast<uint32_t*>(v_lds[buf ^ 1]), tid);
-        store_er(buf ^ 1);
+      if (lane == 0) {
+        red_lds[0][wave] = am;
+        red_lds[1][wave] = rm;
+        red_lds[2][wave] = zm;
       }
       __syncthreads();
+      am = fmaxf(fmaxf(red_lds[0][0], red_lds[0][1]), fmaxf(red_lds[0][2], red_lds[0][3]));
+      rm = fmaxf(fmaxf(red_lds[1][0], red_lds[1][1]), fmaxf(red_lds[1][2], red_lds[1][3])) * kLog2e;
+      zm = fminf(fminf(red_lds[2][0], red_lds[2][1]), fminf(red_lds[2][2], red_lds[2][3])) * kLog2e;
+      factored = __builtin_isfinite(am) && __builtin_isfinite(rm) && __builtin_isfinite(zm) &&
+                 zm >= am + rm - kFactorRange;
+      aoff = am;
+      roff = rm;
     }
+  }
+
+  if constexpr (kFactorable) {
+    if (factored) {
+      const T* vpbase = reinterpret_cast<const T*>(p.vp) + ((int64_t)b * p.n_slots + slot) * T_len * HD;
+      uint32_t voff[VN];
 #pragma unroll
-    for (int qt = 0; qt < QT; ++qt) rowscale[qt] = fast_exp2(aoff + roff - zq[qt]);
-  } else {
-    // decomposed: alpha[j0 + t] for t < 64 and rho[d] for d = dmin + t, t < RW,
+      for (int pp = 0; pp < VN; ++pp) voff[pp] = vrow_dma_offset<T, HD>((NW * pp + wave) * 64 + lane, HD);
+      int vro[NDT];
+#pragma unroll
+      for (int dt = 0; dt < NDT; ++dt) vro[dt] = vt_read_offset<HD>(lane, dt);
+      using S0 = std::integral_constant<int, 0>;
+      using S1 = std::integral_constant<int, 1>;
+      // V'_j into V slot `slot`; a block past this segment gets an empty
+      // descriptor (no memory read, the slot is filled with zeros), so every
+      // block issues the same loads and the vmcnt counts below are static
+      auto load_v = [&](int j, auto slot) {
+        constexpr int V = decltype(slot)::value;
+        char* const tile = V == 0 ? vs0 : (V == 1 ? vs1 : vs2);
+        const __amdgpu_buffer_rsrc_t rs = rows_rsrc(vpbase, (int64_t)HD, 64 * j, j < nkb ? T_len : 0);
+#pragma unroll
+        for (int pp = 0; pp < VN; ++pp)
+          __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, SAF_LDS_PTR(tile + (NW * pp + wave) * 1024), 16, voff[pp], 0,
+                                                   0, 0);
+      };
+      // distance window of block j0: m in [0, RW) holds E(d), d = q0 - j0 + BM - m
+      // (the window reversed), as a bf16 pair hi + lo (E - hi rounded), so E
+      // costs no rounding beyond V''s; copy c holds window element c + k at k.
+      // The fp32 rho log2 e values (r2) are loaded (branch-free, clamped index)
+      // one block ahead, their exps written after the block's MFMAs into the
+      // other slot.
+      float er[ERN], ab = 0.f;
+      int ej0 = 0;
+      const float* const r2 = p.r2 + (int64_t)slot * T_len;
+      const int nblk = (T_len + 63) / 64;
+      auto load_er = [&](int jb) {  // unconditional: indices clamped past the end
+        const int j0 = 64 * jb;
+#pragma unroll
+        for (int u = 0; u < ERN; ++u) er[u] = r2[min(max(q0 - j0 + BM - (tid + u * NTHR), 0), T_len - 1)];
+        ab = ablk[min(jb, nblk - 1)];
+        ej0 = j0;
+      };
+      auto e_slot = [&](auto slot) {
+        return reinterpret_cast<uint16_t(*)[8][RWL]>(decltype(slot)::value ? eb1 : eb0);
+      };
+      auto store_er = [&](auto slot) {
+        uint16_t(*const ew)[8][RWL] = e_slot(slot);
+#pragma unroll
+        for (int u = 0; u < ERN; ++u) {
+          const int m = tid + u * NTHR;
+          const int d = q0 - ej0 + BM - m;
+          if (m < RW) {
+            // A_k - A - R; -inf for a block whose keys all have alpha -inf
+            const float x = d >= 0 && d < T_len ? fast_exp2(er[u] + (ab - aoff - roff)) : 0.f;
+            const uint32_t hl = Elem<T>::pack2(x, 0.f) & 0xffffu;
+            const uint32_t lo = Elem<T>::pack2(x - Elem<T>::lo(hl), 0.f) & 0xffffu;
+#pragma unroll
+            for (int c = 0; c < 8; ++c)
+              if (m >= c) {
+                ew[0][c][m - c] = (uint16_t)hl;
+                ew[1][c][m - c] = (uint16_t)lo;
+              }
+          }
+        }
+      };
+      // lane (n, g), query tile qt reads keys jb + 0..7 (jb = j0 + 16 st + 8g)
+      // of row i: window elements s .. s+7, s = BM - (i - q0) + 16 st + 8g, from
+      // copy (s & 7) = (-(i - q0)) & 7 at element s - (s & 7)
+      int ec[QT], ek[QT];
+#pragma unroll
+      for (int qt = 0; qt < QT; ++qt) {
+        const int il = q0w + 32 * qt + n - q0;
+        ec[qt] = (-il) & 7;
+        ek[qt] = BM - il - ec[qt] + 8 * g;
+      }
+
+      // prologue: E of block kb0 in E slot 0, V' of kb0 and kb0+1 in V slots 0, 1
+      load_er(kb0);
+      load_v(kb0, S0());
+      load_v(kb0 + 1, S1());
+      store_er(S0());
+      asm volatile("" ::: "memory");
+      __builtin_amdgcn_s_waitcnt(waitcnt_vm_lgkm0(VN));
+      __builtin_amdgcn_s_barrier();
+      asm volatile("" ::: "memory");
+      // block j in phase P: V'_j in V slot P % 3, E_j in E slot P % 2 (both
+      // compile-time, so every LDS access names one array and none waits on
+      // another slot's DMA).  E_{j+1} goes to the other E slot and V'_{j+2}
+      // to V slot (P + 2) % 3, both last read in block j-1.  The rho loads are
+      // issued before the DMA, so the wait for them leaves the DMA in flight;
+      // the closing barrier waits for V'_{j+1} alone (vmcnt VN, the DMA of
+      // V'_{j+2} stays in flight; a __syncthreads would drain it) and for this
+      // block's LDS writes (lgkmcnt 0).
+      auto block = [&](const int j, auto phase) {
+        constexpr int PH = decltype(phase)::value;
+        constexpr int R = PH % 3;
+        using ESlot = std::integral_constant<int, PH % 2>;
+        using ENext = std::integral_constant<int, 1 - PH % 2>;
+        using VAhead = std::integral_constant<int, (R + 2) % 3>;
+        const char* const vt = R == 0 ? vs0 : (R == 1 ? vs1 : vs2);
+        uint16_t(*const ew)[8][RWL] = e_slot(ESlot());
+        load_er(j + 1);
+        load_v(j + 2, VAhead());
+        if (j < nkb_w) {
+#pragma unroll
+          for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+            for (int sh = 0; sh < 2; ++sh) {
+              uint4 pb[QT], pl[QT];
+#pragma unroll
+              for (int qt = 0; qt < QT; ++qt) {
+                pb[qt] = *reinterpret_cast<const uint4*>(&ew[0][ec[qt]][ek[qt] + 32 * ks + 16 * sh]);
+                pl[qt] = *reinterpret_cast<const uint4*>(&ew[1][ec[qt]][ek[qt] + 32 * ks + 16 * sh]);
+              }
+              uint4 a[NDT];
+#pragma unroll
+              for (int dt = 0; dt < NDT; ++dt) {
+                const char* src = vt + (32 * ks + 16 * sh) * PITCH + vro[dt];
+                const uint2 lo = ds_read_tr16(src);
+                const uint2 hi = ds_read_tr16(src + 4 * PITCH);
+                a[dt] = make_uint4(lo.x, lo.y, hi.x, hi.y);
+              }
+              // the hi products of every accumulator, then the lo ones: no
+              // MFMA waits on the one before it
+#pragma unroll
+              for (int dt = 0; dt < NDT; ++dt)
+#pragma unroll
+                for (int qt = 0; qt < QT; ++qt) o[qt][dt] = Elem<T>::mfma(a[dt], pb[qt], o[qt][dt]);
+#pragma unroll
+              for (int dt = 0; dt < NDT; ++dt)
+#pragma unroll
+                for (int qt = 0; qt < QT; ++qt) o[qt][dt] = Elem<T>::mfma(a[dt], pl[qt], o[qt][dt]);
+            }
+        }
+        if (j + 1 < nkb) store_er(ENext());
+        asm volatile("" ::: "memory");
+        __builtin_amdgcn_s_waitcnt(waitcnt_vm_lgkm0(VN));
+        __builtin_amdgcn_s_barrier();
+        asm volatile("" ::: "memory");
+      };
+      using Q0 = std::integral_constant<int, 0>;
+      using Q1 = std::integral_constant<int, 1>;
+      using Q2 = std::integral_constant<int, 2>;
+      using Q3 = std::integral_constant<int, 3>;
+      using Q4 = std::integral_constant<int, 4>;
+      using Q5 = std::integral_constant<int, 5>;
+      for (int j = kb0;;) {
+        if (j >= nkb) break;
+        block(j++, Q0());
+        if (j >= nkb) break;
+        block(j++, Q1());
+        if (j >= nkb) break;
+        block(j++, Q2());
+        if (j >= nkb) break;
+        block(j++, Q3());
+        if (j >= nkb) break;
+        block(j++, Q4());
+        if (j >= nkb) break;
+        block(j++, Q5());
+      }
+      // the last (empty) DMAs land before the workgroup's LDS is released
+      asm volatile("" ::: "memory");
+      __builtin_amdgcn_s_waitcnt(waitcnt_vm_lgkm0(0));
+#pragma unroll
+      for (int qt = 0; qt < QT; ++qt) rowscale[qt] = fast_exp2(aoff + roff - zq[qt]);
+    }
+  }
+  if (!factored) {
+    // alpha[j0 + t] for t < 64 and rho[d] for d = dmin + t, t < RW,
     // dmin = q0 - j0 - 63.  Out-of-range distances are -inf (exact zero cells).
-    float a_reg = 0.f, r_reg[(RW + NTHR - 1) / NTHR];
+    auto v_lds = [&](int buf) { return reinterpret_cast<uint4*>(buf ? vs1 : vs0); };
+    float(*const a_lds)[64] = reinterpret_cast<float(*)[64]>(eb0);
+    float(*const r_lds)[RW] = reinterpret_cast<float(*)[RW]>(eb0 + 2 * 64 * 4);
+    float a_reg = 0.f, r_reg[ERN];
     auto stage_params = [&](int j0) {
       if (tid < 64) {
         const int j = j0 + tid;
@@ -258,7 +366,7 @@ void frozen_decomp_kernel(const FrozenParams p) {
       }
       const int dmin = q0 - j0 - 63;
 #pragma unroll
-      for (int u = 0; u < (RW + NTHR - 1) / NTHR; ++u) {
+      for (int u = 0; u < ERN; ++u) {
         const int t = tid + u * NTHR;
         const int d = dmin + t;
         r_reg[u] = (t < RW && d >= 0 && d < T_len) ? rho_at(d) * kLog2e : -INFINITY;
@@ -267,15 +375,16 @@ void frozen_decomp_kernel(const FrozenParams p) {
     auto store_params = [&](int buf) {
       if (tid < 64) a_lds[buf][tid] = a_reg;
 #pragma unroll
-      for (int u = 0; u < (RW + NTHR - 1) / NTHR; ++u) {
+      for (int u = 0; u < ERN; ++u) {
         const int t = tid + u * NTHR;
         if (t < RW) r_lds[buf][t] = r_reg[u];
       }
     };
 
+    VStager<T, HD, NTHR> vst;
     vst.load(vbase, p.v_st, 64 * kb0, T_len, tid);
     stage_params(64 * kb0);
-    vst.store(reinterpret_cast<uint32_t*>(v_lds[0]), tid);
+    vst.store(reinterpret_cast<uint32_t*>(v_lds(0)), tid);
     store_params(0);
     __syncthreads();
 
@@ -288,7 +397,7 @@ void frozen_decomp_kernel(const FrozenParams p) {
       }
       if (j < nkb_w) {
         const int j0 = 64 * j;
-        const uint4* vt = v_lds[buf];
+        const uint4* vt = v_lds(buf);
 #pragma unroll
         for (int ks = 0; ks < 2; ++ks)
 #pragma unroll
@@ -315,7 +424,7 @@ void frozen_decomp_kernel(const FrozenParams p) {
           }
       }
       if (more) {
-        vst.store(reinterpret_cast<uint32_t*>(v_lds[buf ^ 1]), tid);
+        vst.store(reinterpret_cast<uint32_t*>(v_lds(buf ^ 1)), tid);
         store_params(buf ^ 1);
       }
       __syncthreads();
@@ -341,6 +450,63 @@ void frozen_decomp_kernel(const FrozenParams p) {
                           o[qt][dt][4 * r4 + 3] * sc);
     } else {
       store_out_tile<T, HD>(obase + (int64_t)i * p.o_st, o[qt], sc, g);
+    }
+  }
+}
+
+template <typename T, int HD, int QT>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(decomp_waves_per_eu(HD), decomp_waves_per_eu(HD))))
+void frozen_decomp_kernel(const FrozenParams p) {
+  decomp_body<T, HD, QT>(p);
+}
+
+// vp[b, slot, j] = 2^(alpha_j log2 e - A_k) v[b, v_head, j] in T, with
+// A_k = max alpha log2 e over the 64-key block k = j / 64 of the slot's head
+// (a_off[slot * nblk + k], nblk = ceil(T / 64), written by batch 0's
+// workgroup, which also writes r2[slot, d] = rho_d log2 e for the block's
+// distances, so the main kernel reads rho as plain fp32).  One workgroup per (key block, slot, batch); every wave reduces
+// the block's alpha itself, so nothing orders workgroups.  vp holds T rows
+// per (batch, slot); the main kernel's buffer-resource bound reads rows past
+// T as zero.
+template <typename T, int HD>
+__global__ __launch_bounds__(256) void decomp_prescale_kernel(const FrozenParams p) {
+  constexpr int CH = HD / 8;          // 16-byte chunks per row
+  constexpr int PER = 64 * CH / 256;  // chunks per thread
+  static_assert(64 * CH % 256 == 0, "a key block's chunks split evenly over the threads");
+  const int kb = blockIdx.x, slot = blockIdx.y, b = blockIdx.z, j0 = 64 * kb;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int ph = p.pat_head[slot];
+  const T* vbase = reinterpret_cast<const T*>(p.v) + b * p.v_sb + (int64_t)p.v_head[slot] * p.v_sh;
+  uint4 w[PER];
+#pragma unroll
+  for (int u = 0; u < PER; ++u) {
+    const int idx = tid + 256 * u, row = j0 + idx / CH, c = idx % CH;
+    w[u] = row < p.T ? *reinterpret_cast<const uint4*>(vbase + (int64_t)row * p.v_st + 8 * c) : make_uint4(0, 0, 0, 0);
+  }
+  const float al =
+      j0 + lane < p.T ? load_as_f32(p.alpha, (int64_t)ph * p.a_sh + (int64_t)(j0 + lane) * p.a_ss, p.a_dtype) * kLog2e
+                      : -INFINITY;
+  float am = al;
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) am = fmaxf(am, __shfl_xor(am, off));
+  if (b == 0) {
+    if (tid == 0) p.a_off[(int64_t)slot * ((p.T + 63) / 64) + kb] = am;
+    if (tid >= 64 && tid < 128 && j0 + lane < p.T)
+      p.r2[(int64_t)slot * p.T + j0 + lane] =
+          load_as_f32(p.rho, (int64_t)ph * p.r_sh + (int64_t)(j0 + lane) * p.r_ss, p.r_dtype) * kLog2e;
+  }
+  T* vp = reinterpret_cast<T*>(p.vp) + ((int64_t)b * p.n_slots + slot) * p.T * HD;
+#pragma unroll
+  for (int u = 0; u < PER; ++u) {
+    const int idx = tid + 256 * u, rl = idx / CH, c = idx % CH;
+    const float ar = __shfl(al, rl);
+    const float f = ar == -INFINITY ? 0.f : fast_exp2(ar - am);  // am is finite when ar is
+    if (j0 + rl < p.T) {
+      const uint32_t in[4] = {w[u].x, w[u].y, w[u].z, w[u].w};
+      uint32_t out[4];
+#pragma unroll
+      for (int m = 0; m < 4; ++m) out[m] = Elem<T>::pack2(Elem<T>::lo(in[m]) * f, Elem<T>::hi(in[m]) * f);
+      *reinterpret_cast<uint4*>(vp + (int64_t)(j0 + rl) * HD + 8 * c) = make_uint4(out[0], out[1], out[2], out[3]);
     }
   }
 }
@@ -407,10 +573,6 @@ __device__ inline uint4 p_chunk(const FrozenParams& p, const PT* prow, int kstar
   return make_uint4(Elem<T>::pack2(e[0], e[1]), Elem<T>::pack2(e[2], e[3]), Elem<T>::pack2(e[4], e[5]),
                     Elem<T>::pack2(e[6], e[7]));
 }
-
-// s_waitcnt immediate that waits for vmcnt <= n alone (expcnt and lgkmcnt
-// left at their maxima; gfx9 encoding: vmcnt bits 3:0 and 15:14).
-constexpr int waitcnt_vm(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8); }
 
 // Per-wave state of the dense P.V kernel (below): the lane's pattern rows,
 // the V DMA and V^T read offsets, and the O^T accumulators of NB sequences.
@@ -733,6 +895,24 @@ static hipError_t launch_frozen_hd(const FrozenParams& p, int hd, int mode, hipS
   }
 }
 
+
+template <int HD>
+static hipError_t launch_prescale_hd(const FrozenParams& p, hipStream_t s) {
+  const dim3 grid((unsigned)((p.T + 63) / 64), (unsigned)p.n_slots, (unsigned)p.B);
+  hipLaunchKernelGGL((decomp_prescale_kernel<__bf16, HD>), grid, dim3(256), 0, s, p);
+  return hipGetLastError();
+}
+
+hipError_t launch_decomp_prescale(const FrozenParams& p, int dtype, int hd, hipStream_t s) {
+  if (dtype != kBF16) return hipErrorInvalidValue;
+  switch (hd) {
+    case 32: return launch_prescale_hd<32>(p, s);
+    case 64: return launch_prescale_hd<64>(p, s);
+    case 96: return launch_prescale_hd<96>(p, s);
+    case 128: return launch_prescale_hd<128>(p, s);
+    default: return hipErrorInvalidValue;
+  }
+}
 
 hipError_t launch_frozen_pv(const FrozenParams& p, int dtype, int hd, int mode, hipStream_t s) {
   if (dtype == kF32) return launch_f32_frozen(p, hd, mode, s);

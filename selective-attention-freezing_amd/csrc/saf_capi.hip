@@ -499,6 +499,43 @@ int run_dense(const saf_tensor_t& patt, const saf_tensor_t& v, const saf_tensor_
   return launched(launch_flash_combine(c, dtype, HD, s), "dense P.V combine");
 }
 
+// Workspace regions after the scan's: the fp32 partials of split query
+// blocks (flash, dense and decomposed kernels run one after the other and
+// share them), then the factored decomposed form's per-key-block alpha
+// maxima a_off (n_dec x ceil(T / 64) floats), rho log2 e r2 (n_dec x T
+// floats) and key-scaled values vp (B, n_dec, T, HD) bf16 (bf16, hd <= 128
+// only).
+int64_t round256(int64_t n) { return (n + 255) / 256 * 256; }
+
+int64_t part_region_bytes(const saf_mixed_attn_args* args, const Plan& pl) {
+  int64_t part = 0;
+  if (!pl.live.empty()) {
+    const int qt = flash_qtiles_for(args, pl.HD);
+    const FlashPlan fp = plan_flash(pl.B, (int)pl.live.size(), pl.T, pl.HD, flash_block_rows(pl.HD, qt),
+                                    flash_resident(pl.HD, qt));
+    part = kQueueBytes + fp.part_bytes;
+  }
+  if (!pl.dense.empty())
+    part = std::max(part, plan_dense(pl.B, (int)pl.dense.size(), pl.T, pl.HD).part_bytes);
+  if (!pl.decomp.empty())
+    part = std::max(part, plan_flash(pl.B, (int)pl.decomp.size(), pl.T, pl.HD, block_rows(frozen_qtiles(pl.HD)),
+                                     decomp_resident(pl.HD)).part_bytes);
+  return round256(part);
+}
+
+// Per-key-block alpha maxima (n_dec x ceil(T / 64) floats), rho log2 e in
+// fp32 (n_dec x T), then the key-scaled values.
+int64_t decomp_aoff_bytes(const Plan& pl) {
+  return round256((int64_t)pl.decomp.size() * ((pl.T + 63) / 64) * 4);
+}
+int64_t decomp_r2_bytes(const Plan& pl) { return round256((int64_t)pl.decomp.size() * pl.T * 4); }
+
+int64_t decomp_vp_bytes(const Plan& pl) {
+  if (pl.dtype != SAF_BF16 || pl.HD > 128 || pl.decomp.empty()) return 0;
+  const int64_t nd = (int64_t)pl.decomp.size();
+  return decomp_aoff_bytes(pl) + decomp_r2_bytes(pl) + round256((int64_t)pl.B * nd * pl.T * pl.HD * 2);
+}
+
 // Decomposed P.V (rebuilt in registers), causally balanced like run_dense
 // when the workspace holds the plan's partials (same region as the flash and
 // dense partials: the kernels run one after the other on the stream).
@@ -531,7 +568,24 @@ int run_decomp(const saf_mixed_attn_args* a, const Plan& pl, hipStream_t s) {
   } else {
     fp = FlashPlan();
   }
-  if (int rc = launched(timed([&] { return launch_frozen_pv(p, pl.dtype, pl.HD, 1, s); }, s), "decomposed P.V"))
+  // the factored form needs the key-scaled values in the workspace
+  const int64_t vp_off = part_off + part_region_bytes(a, pl), vp_bytes = decomp_vp_bytes(pl);
+  const bool factored = vp_bytes > 0 && a->workspace != nullptr && a->workspace_bytes >= vp_off + vp_bytes &&
+                        reinterpret_cast<uintptr_t>(a->workspace) % 256 == 0;
+  if (factored) {
+    char* w = reinterpret_cast<char*>(a->workspace) + vp_off;
+    p.a_off = reinterpret_cast<float*>(w);
+    p.r2 = reinterpret_cast<float*>(w + decomp_aoff_bytes(pl));
+    p.vp = w + decomp_aoff_bytes(pl) + decomp_r2_bytes(pl);
+  }
+  if (int rc = launched(timed([&] {
+                          if (factored) {
+                            const hipError_t e = launch_decomp_prescale(p, pl.dtype, pl.HD, s);
+                            if (e != hipSuccess) return e;
+                          }
+                          return launch_frozen_pv(p, pl.dtype, pl.HD, 1, s);
+                        }, s),
+                        "decomposed P.V"))
     return rc;
   if (fp.n_split == 0) return SAF_OK;
   CombineParams c{};
@@ -1094,20 +1148,7 @@ int64_t saf_mixed_attn_workspace_bytes(const saf_mixed_attn_args* args) {
   Plan pl;
   if (plan_and_validate(args, kDoFlash | kDoScan, pl, false)) return -1;
   if (pl.dtype == SAF_F32) return 0;  // no scan, no split
-  int64_t total = scan_ws_bytes(pl), part = 0;
-  if (!pl.live.empty()) {
-    const int qt = flash_qtiles_for(args, pl.HD);
-    const FlashPlan fp = plan_flash(pl.B, (int)pl.live.size(), pl.T, pl.HD, flash_block_rows(pl.HD, qt),
-                                    flash_resident(pl.HD, qt));
-    part = kQueueBytes + fp.part_bytes;
-  }
-  if (!pl.dense.empty())
-    part = std::max(part, plan_dense(pl.B, (int)pl.dense.size(), pl.T, pl.HD).part_bytes);
-  if (!pl.decomp.empty())
-    part = std::max(part, plan_flash(pl.B, (int)pl.decomp.size(), pl.T, pl.HD, block_rows(frozen_qtiles(pl.HD)),
-                                     decomp_resident(pl.HD)).part_bytes);
-  total += part;
-  return total;
+  return scan_ws_bytes(pl) + part_region_bytes(args, pl) + decomp_vp_bytes(pl);
 }
 
 }  // extern "C"

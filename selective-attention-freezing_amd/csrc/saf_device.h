@@ -245,19 +245,6 @@ template <typename T, int HD, int NTHR> struct VStager {
     }
   }
 
-  // Key rows of item p (keys j0 + 2kp and j0 + 2kp + 1) and the factor
-  // hook: multiply row 2kp by f0 and row 2kp+1 by f1 (rounded back to T).
-  __device__ inline int item_key(int p, int tid) const { return 2 * ((tid + p * NTHR) / KCH); }
-  __device__ inline void scale_rows(int p, float f0, float f1) {
-    uint32_t* a = reinterpret_cast<uint32_t*>(&r0[p]);
-    uint32_t* b = reinterpret_cast<uint32_t*>(&r1[p]);
-#pragma unroll
-    for (int m = 0; m < 4; ++m) {
-      a[m] = Elem<T>::pack2(Elem<T>::lo(a[m]) * f0, Elem<T>::hi(a[m]) * f0);
-      b[m] = Elem<T>::pack2(Elem<T>::lo(b[m]) * f1, Elem<T>::hi(b[m]) * f1);
-    }
-  }
-
   // Transposed store: dword (key 2kp, key 2kp+1) of column d = 8c + e.
   __device__ inline void store(uint32_t* vt, int tid) const {
 #pragma unroll

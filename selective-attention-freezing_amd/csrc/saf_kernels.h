@@ -88,6 +88,15 @@ struct FrozenParams {
   int a_dtype, r_dtype, z_dtype;
   int64_t a_sh, a_ss, r_sh, r_ss, z_sh, z_ss;
   int B, T, n_slots, n_qblk;
+  // decomposed heads, factored form (null: cell-by-cell rebuild only):
+  // a_off[slot][k] = max alpha log2 e over 64-key block k of the slot's head
+  // (n_slots x ceil(T / 64)), vp = the key-scaled values
+  // 2^(alpha_j log2 e - a_off[slot][j / 64]) v_j, (B, n_slots, T, HD) in the
+  // input dtype, r2[slot][d] = rho_d log2 e (n_slots x T) (workspace, all
+  // written by launch_decomp_prescale)
+  float* a_off;
+  void* vp;
+  float* r2;
   int16_t out_head[kMaxHeads];
   int16_t v_head[kMaxHeads];
   int16_t pat_head[kMaxHeads];  // dense: pattern row; decomposed: buffer row
@@ -164,6 +173,9 @@ inline int scan_chunk_rows(int hd) { return hd == 32 ? 512 : (hd == 64 ? 256 : 1
 hipError_t launch_flash(const FlashParams& p, int dtype, int hd, int qt, hipStream_t s);
 hipError_t launch_flash_combine(const CombineParams& p, int dtype, int hd, hipStream_t s);
 hipError_t launch_frozen_pv(const FrozenParams& p, int dtype, int hd, int mode, hipStream_t s);
+// Factored decomposed heads: a_off and the key-scaled values vp in one launch
+// (bf16, hd <= 128).
+hipError_t launch_decomp_prescale(const FrozenParams& p, int dtype, int hd, hipStream_t s);
 hipError_t launch_scan(const ScanParams& p, int dtype, int hd, hipStream_t s);
 hipError_t launch_zero_u32(uint32_t* ptr, int64_t n, hipStream_t s);
 hipError_t launch_rope(const RopeParams& p, int dtype, hipStream_t s);

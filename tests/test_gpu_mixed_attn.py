@@ -383,7 +383,7 @@ def test_invalid_args_raise():
     frozen = torch.zeros(4, dtype=torch.int32, device=DEV)
     with pytest.raises(NotImplementedError):
         K.fused_mixed_attn(q.to(DEV), k.to(DEV), v.to(DEV), None, frozen)
-    q, k, v = qkv(1, 4, 64, 64, seed=1, dtype=torch.float32)
+    q, k, v = qkv(1, 4, 64, 64, seed=1, dtype=torch.float64)
     with pytest.raises(NotImplementedError):
         K.fused_mixed_attn(q.to(DEV), k.to(DEV), v.to(DEV), None, frozen)
     q, k, v = qkv(1, 4, 64, 64, seed=1, dtype=torch.bfloat16)

@@ -410,6 +410,21 @@ def test_pattern_grads_match_torch_autograd():
     rg = np.nan_to_num(r.grad.numpy())
     np.testing.assert_allclose(np.where(np.isfinite(rho), dr, 0.0), np.where(np.isfinite(rho), rg, 0.0), atol=1e-10)
     assert (da[1] == 0).all() and (dr[1] == 0).all()
+    # delta from a given output: the exact output reproduces the default; a
+    # perturbation e of one row i0 shifts sum_j dalpha_j by -sum_b dO_i0 . e
+    # (P's rows sum to 1) and drho by the same amount over d <= i0
+    y_np = y.detach().numpy()
+    da_y, dr_y = orc.pattern_grads(v, dout, frozen, alpha, rho, out=y_np)
+    np.testing.assert_allclose(da_y, da, atol=1e-10)
+    np.testing.assert_allclose(dr_y, dr, atol=1e-10)
+    i0, e = 11, rng.standard_normal((B, hd))
+    y_p = y_np.copy()
+    y_p[:, 0, i0] += e
+    da_p, dr_p = orc.pattern_grads(v, dout, frozen, alpha, rho, out=y_p)
+    shift = -float((dout[:, 0, i0] * e).sum())
+    assert abs((da_p[0] - da[0]).sum() - shift) < 1e-9
+    assert abs((dr_p[0] - dr[0]).sum() - shift) < 1e-9
+    np.testing.assert_allclose(da_p[2:], da[2:], atol=1e-12)
 
 
 def test_logz_grads_match_torch_autograd_and_fd():
