@@ -289,6 +289,9 @@ __device__ __forceinline__ void decomp_body(const FrozenParams& p) {
         load_er(j + 1);
         load_v(j + 2, VAhead());
         if (j < nkb_w) {
+          // Toeplitz reuse: query tile 1 sits 32 rows below tile 0, so its
+          // operand of key step (1, sh) is tile 0's of step (0, sh)
+          uint4 keep_b[2], keep_l[2];
 #pragma unroll
           for (int ks = 0; ks < 2; ++ks)
 #pragma unroll
@@ -296,8 +299,17 @@ __device__ __forceinline__ void decomp_body(const FrozenParams& p) {
               uint4 pb[QT], pl[QT];
 #pragma unroll
               for (int qt = 0; qt < QT; ++qt) {
-                pb[qt] = *reinterpret_cast<const uint4*>(&ew[0][ec[qt]][ek[qt] + 32 * ks + 16 * sh]);
-                pl[qt] = *reinterpret_cast<const uint4*>(&ew[1][ec[qt]][ek[qt] + 32 * ks + 16 * sh]);
+                if (QT == 2 && qt == 1 && ks == 1) {
+                  pb[qt] = keep_b[sh];
+                  pl[qt] = keep_l[sh];
+                } else {
+                  pb[qt] = *reinterpret_cast<const uint4*>(&ew[0][ec[qt]][ek[qt] + 32 * ks + 16 * sh]);
+                  pl[qt] = *reinterpret_cast<const uint4*>(&ew[1][ec[qt]][ek[qt] + 32 * ks + 16 * sh]);
+                }
+              }
+              if (ks == 0) {
+                keep_b[sh] = pb[0];
+                keep_l[sh] = pl[0];
               }
               uint4 a[NDT];
 #pragma unroll
