@@ -28,17 +28,16 @@ constexpr int kBwdWaves = 4;
 // 16-byte operand of a VRow tile: elements 8c .. 8c+7 of row r.
 template <int HD>
 __device__ __forceinline__ uint4 tile_row_op(const char* tile, int r, int c) {
-  const int seg = ((c >> 1) ^ (r & 3)) << 1 | (c & 1);
-  return *reinterpret_cast<const uint4*>(tile + r * VRow<HD>::PITCH + seg * 16);
+  return *reinterpret_cast<const uint4*>(tile + r * VRow<HD>::PITCH + 16 * (c ^ VRow<HD>::swz(r)));
 }
 
 // Transposed operand of a VRow tile: lane (n, g) receives rows
 // 16 ks + 8 g + 0..7 of column 32 dt + n.
 template <int HD>
 __device__ __forceinline__ uint4 tile_col_op(const char* tile, int ks, int dt, int lane) {
-  const char* src = tile + 16 * ks * VRow<HD>::PITCH + vt_read_offset<HD>(lane, dt);
-  const uint2 lo = ds_read_tr16(src);
-  const uint2 hi = ds_read_tr16(src + 4 * VRow<HD>::PITCH);
+  const char* base = tile + 16 * ks * VRow<HD>::PITCH;
+  const uint2 lo = ds_read_tr16(base + vt_read_offset<HD>(lane, dt, 0));
+  const uint2 hi = ds_read_tr16(base + vt_read_offset<HD>(lane, dt, 1));
   return make_uint4(lo.x, lo.y, hi.x, hi.y);
 }
 

@@ -69,8 +69,7 @@ template <typename T, int HD> struct TileDma {
     for (int p = 0; p < KN; ++p) {
       const int X = (NW * p + wave) * 64 + lane;
       const int key = X / KCHP, slot = X % KCHP;
-      const int f = (key & 3) | ((key >> 1) & 4);
-      const int c = slot ^ (f & (KCHP - 1));
+      const int c = slot ^ KLayout<HD>::swz(key);
       koff[p] = (uint32_t)(key * k_st * (int64_t)sizeof(T)) + 16u * (c < KCH ? c : 0);
     }
 #pragma unroll
@@ -100,7 +99,7 @@ struct FlashState {
   f32x16_t o[QT][NDT];        // O^T accumulators
   float m_run[QT], l_run[QT];
   int koff[NKT];              // byte offset of this lane's K A operand of step t in a sub-block
-  int voff[NDT];              // byte offset of this lane's V^T tr-read source for d tile dt
+  int voff[NDT], voffh[NDT];  // byte offsets of this lane's V^T tr-read pair for d tile dt
   float c;                    // sm_scale * log2(e)
   int n, g, q0w;
 
@@ -111,7 +110,10 @@ struct FlashState {
 #pragma unroll
     for (int t = 0; t < NKT; ++t) koff[t] = 16 * KLayout<HD>::chunk(key, 2 * t + g);
 #pragma unroll
-    for (int dt = 0; dt < NDT; ++dt) voff[dt] = vt_read_offset<HD>(lane, dt);
+    for (int dt = 0; dt < NDT; ++dt) {
+      voff[dt] = vt_read_offset<HD>(lane, dt, 0);
+      voffh[dt] = vt_read_offset<HD>(lane, dt, 1);
+    }
   }
 
   // K A operands of sub-block ks (0/1) of a K tile
@@ -146,9 +148,9 @@ struct FlashState {
     for (int s2 = 0; s2 < 2; ++s2)
 #pragma unroll
       for (int dt = 0; dt < NDT; ++dt) {
-        const char* src = vtile + (32 * ks + 16 * s2) * VRow<HD>::PITCH + voff[dt];
-        const uint2 lo = ds_read_tr16(src);
-        const uint2 hi = ds_read_tr16(src + 4 * VRow<HD>::PITCH);
+        const char* base = vtile + (32 * ks + 16 * s2) * VRow<HD>::PITCH;
+        const uint2 lo = ds_read_tr16(base + voff[dt]);
+        const uint2 hi = ds_read_tr16(base + (VRow<HD>::M2 ? voffh[dt] : voff[dt] + 4 * VRow<HD>::PITCH));
         const uint4 a = make_uint4(lo.x, lo.y, hi.x, hi.y);
 #pragma unroll
         for (int qt = 0; qt < QT; ++qt) {

@@ -77,7 +77,10 @@ __device__ __forceinline__ void decomp_body(const FrozenParams& p) {
   constexpr int BM = NW * 32 * QT;
   constexpr int NDT = HD / 32;
   constexpr int RW = BM + 64;  // rho / distance window per key block
-  constexpr int RWL = RW + 8;  // one shifted copy of the factored window (bf16 elements)
+  // the factored window's 8 shifted copies (bf16 elements): copy c starts at
+  // element c RWL + (c ? 8 : 0), which (searched over copy pitches and
+  // shifts) keeps every 16-lane group of one E^T read on distinct banks
+  constexpr int RWL = RW + 16;
   constexpr int ERN = (RW + NTHR - 1) / NTHR;
   constexpr bool kFactorable = std::is_same<T, __bf16>::value && HD <= 128;
   // LDS: the factored form's three V' tiles (vs0..vs2) and two distance
@@ -193,9 +196,12 @@ __device__ __forceinline__ void decomp_body(const FrozenParams& p) {
       uint32_t voff[VN];
 #pragma unroll
       for (int pp = 0; pp < VN; ++pp) voff[pp] = vrow_dma_offset<T, HD>((NW * pp + wave) * 64 + lane, HD);
-      int vro[NDT];
+      int vro[NDT], vroh[NDT];
 #pragma unroll
-      for (int dt = 0; dt < NDT; ++dt) vro[dt] = vt_read_offset<HD>(lane, dt);
+      for (int dt = 0; dt < NDT; ++dt) {
+        vro[dt] = vt_read_offset<HD>(lane, dt, 0);
+        vroh[dt] = vt_read_offset<HD>(lane, dt, 1);
+      }
       using S0 = std::integral_constant<int, 0>;
       using S1 = std::integral_constant<int, 1>;
       // V'_j into V slot `slot`; a block past this segment gets an empty
@@ -228,10 +234,11 @@ __device__ __forceinline__ void decomp_body(const FrozenParams& p) {
         ej0 = j0;
       };
       auto e_slot = [&](auto slot) {
-        return reinterpret_cast<uint16_t(*)[8][RWL]>(decltype(slot)::value ? eb1 : eb0);
+        return reinterpret_cast<uint16_t(*)[8 * RWL]>(decltype(slot)::value ? eb1 : eb0);
       };
+      auto ecopy = [](int c) { return c * RWL + (c ? 8 : 0); };
       auto store_er = [&](auto slot) {
-        uint16_t(*const ew)[8][RWL] = e_slot(slot);
+        uint16_t(*const ew)[8 * RWL] = e_slot(slot);
 #pragma unroll
         for (int u = 0; u < ERN; ++u) {
           const int m = tid + u * NTHR;
@@ -244,21 +251,22 @@ __device__ __forceinline__ void decomp_body(const FrozenParams& p) {
 #pragma unroll
             for (int c = 0; c < 8; ++c)
               if (m >= c) {
-                ew[0][c][m - c] = (uint16_t)hl;
-                ew[1][c][m - c] = (uint16_t)lo;
+                ew[0][ecopy(c) + m - c] = (uint16_t)hl;
+                ew[1][ecopy(c) + m - c] = (uint16_t)lo;
               }
           }
         }
       };
       // lane (n, g), query tile qt reads keys jb + 0..7 (jb = j0 + 16 st + 8g)
       // of row i: window elements s .. s+7, s = BM - (i - q0) + 16 st + 8g, from
-      // copy (s & 7) = (-(i - q0)) & 7 at element s - (s & 7)
-      int ec[QT], ek[QT];
+      // copy (s & 7) = (-(i - q0)) & 7 at element s - (s & 7): eo = the element
+      // offset of the lane's first read in the slot
+      int eo[QT];
 #pragma unroll
       for (int qt = 0; qt < QT; ++qt) {
         const int il = q0w + 32 * qt + n - q0;
-        ec[qt] = (-il) & 7;
-        ek[qt] = BM - il - ec[qt] + 8 * g;
+        const int ec = (-il) & 7;
+        eo[qt] = ecopy(ec) + BM - il - ec + 8 * g;
       }
 
       // prologue: E of block kb0 in E slot 0, V' of kb0 and kb0+1 in V slots 0, 1
@@ -285,7 +293,7 @@ __device__ __forceinline__ void decomp_body(const FrozenParams& p) {
         using ENext = std::integral_constant<int, 1 - PH % 2>;
         using VAhead = std::integral_constant<int, (R + 2) % 3>;
         const char* const vt = R == 0 ? vs0 : (R == 1 ? vs1 : vs2);
-        uint16_t(*const ew)[8][RWL] = e_slot(ESlot());
+        uint16_t(*const ew)[8 * RWL] = e_slot(ESlot());
         load_er(j + 1);
         load_v(j + 2, VAhead());
         if (j < nkb_w) {
@@ -303,8 +311,8 @@ __device__ __forceinline__ void decomp_body(const FrozenParams& p) {
                   pb[qt] = keep_b[sh];
                   pl[qt] = keep_l[sh];
                 } else {
-                  pb[qt] = *reinterpret_cast<const uint4*>(&ew[0][ec[qt]][ek[qt] + 32 * ks + 16 * sh]);
-                  pl[qt] = *reinterpret_cast<const uint4*>(&ew[1][ec[qt]][ek[qt] + 32 * ks + 16 * sh]);
+                  pb[qt] = *reinterpret_cast<const uint4*>(&ew[0][eo[qt] + 32 * ks + 16 * sh]);
+                  pl[qt] = *reinterpret_cast<const uint4*>(&ew[1][eo[qt] + 32 * ks + 16 * sh]);
                 }
               }
               if (ks == 0) {
@@ -314,9 +322,9 @@ __device__ __forceinline__ void decomp_body(const FrozenParams& p) {
               uint4 a[NDT];
 #pragma unroll
               for (int dt = 0; dt < NDT; ++dt) {
-                const char* src = vt + (32 * ks + 16 * sh) * PITCH + vro[dt];
-                const uint2 lo = ds_read_tr16(src);
-                const uint2 hi = ds_read_tr16(src + 4 * PITCH);
+                const char* base = vt + (32 * ks + 16 * sh) * PITCH;
+                const uint2 lo = ds_read_tr16(base + vro[dt]);
+                const uint2 hi = ds_read_tr16(base + (VRow<HD>::M2 ? vroh[dt] : vro[dt] + 4 * PITCH));
                 a[dt] = make_uint4(lo.x, lo.y, hi.x, hi.y);
               }
               // the hi products of every accumulator, then the lo ones: no
@@ -606,7 +614,7 @@ struct DenseState {
   uint32_t poff[QT];     // fast path: byte offset of key 8g of the row in the descriptor
   __amdgpu_buffer_rsrc_t prs;
   uint32_t voff[VN];
-  int vro[NDT];
+  int vro[NDT], vroh[NDT];  // V^T tr-read pair offsets of d tile dt
   f32x16_t o[NB][QT][NDT];
 
   // DMA of the 64-key V tiles of block j of the NB sequences into `tile`:
@@ -668,9 +676,9 @@ struct DenseState {
         for (int nb = 0; nb < NB; ++nb)
 #pragma unroll
           for (int dt = 0; dt < NDT; ++dt) {
-            const char* src = cur + nb * VB + (32 * ks + 16 * sh) * PITCH + vro[dt];
-            const uint2 lo = ds_read_tr16(src);
-            const uint2 hi = ds_read_tr16(src + 4 * PITCH);
+            const char* base = cur + nb * VB + (32 * ks + 16 * sh) * PITCH;
+            const uint2 lo = ds_read_tr16(base + vro[dt]);
+            const uint2 hi = ds_read_tr16(base + (VRow<HD>::M2 ? vroh[dt] : vro[dt] + 4 * PITCH));
             const uint4 a = make_uint4(lo.x, lo.y, hi.x, hi.y);
 #pragma unroll
             for (int qt = 0; qt < QT; ++qt) o[nb][qt][dt] = Elem<T>::mfma(a, pb[ks][sh][qt], o[nb][qt][dt]);
@@ -786,7 +794,10 @@ void frozen_dense_kernel(const FrozenParams p) {
 #pragma unroll
   for (int pp = 0; pp < St::VN; ++pp) st.voff[pp] = vrow_dma_offset<T, HD>((NW * pp + wave) * 64 + lane, p.v_st);
 #pragma unroll
-  for (int dt = 0; dt < NDT; ++dt) st.vro[dt] = vt_read_offset<HD>(lane, dt);
+  for (int dt = 0; dt < NDT; ++dt) {
+    st.vro[dt] = vt_read_offset<HD>(lane, dt, 0);
+    st.vroh[dt] = vt_read_offset<HD>(lane, dt, 1);
+  }
   // pattern rows of this lane (rows past T read row T-1 and are masked); the
   // descriptor runs from the workgroup's first pattern row to the end of the
   // buffer

@@ -136,16 +136,22 @@ __device__ inline int acc_key(int i, int g) { return 16 * (i >> 3) + 8 * g + (i 
 
 // ---- LDS layouts -------------------------------------------------------------
 // K tile: 64 keys x HD, row pitch KCHP 16-byte chunks (KCHP = next pow2 of
-// HD/8).  Chunks are XOR-swizzled by a function of the key so that the 32
-// A-lanes of an MFMA (32 different keys, same chunk) hit distinct banks.
+// HD/8).  Chunk c of key row `key` is stored at slot c ^ swz(key), swz an
+// XOR-linear function of the key's low four bits, chosen (by exhaustive
+// search over such functions) so that the ds_read_b128 of one K operand
+// (lane (n, g): key kperm(n), chunk 2t + g) is free of bank conflicts both
+// in 8-lane groups over 32 banks and in 16-lane groups over 64 banks.
 template <int HD> struct KLayout {
   static constexpr int KCH = HD / 8;
   static constexpr int KCHP = KCH <= 4 ? 4 : (KCH <= 8 ? 8 : (KCH <= 16 ? 16 : 32));
   static constexpr int BYTES = 64 * KCHP * 16;
-  __device__ static inline int chunk(int key, int c) {
-    const int f = (key & 3) | ((key >> 1) & 4);
-    return key * KCHP + (c ^ (f & (KCHP - 1)));
+  // XOR masks contributed by key bits 0..3
+  static constexpr int M0 = KCHP == 4 ? 0 : 1, M1 = KCHP == 4 ? 1 : 2, M2 = KCHP == 4 ? 1 : (KCHP == 8 ? 1 : 4),
+                       M3 = KCHP == 4 ? 2 : (KCHP == 8 ? 4 : 12);
+  __device__ static inline int swz(int key) {
+    return ((key & 1) ? M0 : 0) ^ ((key & 2) ? M1 : 0) ^ ((key & 4) ? M2 : 0) ^ ((key & 8) ? M3 : 0);
   }
+  __device__ static inline int chunk(int key, int c) { return key * KCHP + (c ^ swz(key)); }
 };
 
 // V^T tile: HD rows (d) x 64 keys = 8 chunks of 8 keys per row, swizzled so
@@ -160,15 +166,27 @@ template <int HD> struct VLayout {
 
 #define SAF_LDS_PTR(p) ((__attribute__((address_space(3))) void*)(p))
 
-// V tile: 64 key rows of HD values; row pitch VSEG 32-byte segments; the
-// logical segment s of key row r is stored at segment s ^ (r & 3), so the
-// four rows a 16-lane group of ds_read_b64_tr_b16 touches fall in four
-// different bank quarters.
+// V tile: 64 key rows of HD values, row pitch VSEG 32-byte segments.  The
+// logical 16-byte chunk c of row r is stored at chunk c ^ swz(r), swz an
+// XOR-linear function of the row's low four bits chosen (by exhaustive
+// search over such functions) so that both reads of a tile are free of
+// bank conflicts, in 8-lane groups over 32 banks and in 16-lane groups over
+// 64 banks (32 lanes for the 8-byte reads): ds_read_b64_tr_b16 (the V^T
+// operand: rows 8g + 0..3 (+4), two chunks of one column block) and
+// ds_read_b128 (a row operand: rows kperm(0..31), one chunk).  hd 256 tiles
+// (no row operands: the backward stops at hd 128) take M2 = 0, so a lane's
+// second transposing read is its first plus 4 rows and needs no register.
 template <int HD> struct VRow {
   static constexpr int VSEG = HD / 16 <= 4 ? 4 : (HD / 16 <= 8 ? 8 : 16);
   static constexpr int PITCH = VSEG * 32;
   static constexpr int CHP = 2 * VSEG;  // 16-byte chunks per row
   static constexpr int BYTES = 64 * PITCH;
+  // XOR masks contributed by row bits 0..3
+  static constexpr int M0 = CHP == 8 ? 2 : 4, M1 = CHP == 8 ? 4 : 10, M2 = CHP == 32 ? 0 : 1,
+                       M3 = CHP == 32 ? 0 : 3;
+  __device__ static inline int swz(int r) {
+    return ((r & 1) ? M0 : 0) ^ ((r & 2) ? M1 : 0) ^ ((r & 4) ? M2 : 0) ^ ((r & 8) ? M3 : 0);
+  }
 };
 
 typedef short short4_t __attribute__((ext_vector_type(4)));
@@ -183,13 +201,15 @@ __device__ __forceinline__ uint2 ds_read_tr16(const char* p) {
 // Lane offset (within a V tile in the VRow layout) of the ds_read_tr16 pair
 // that builds the V^T A operand of rows d = 32 dt + (lane % 32) for keys
 // 8 (lane / 32) + 0..7 of a 16-key step: the operand is
-// (tr16(base + off), tr16(base + off + 4 PITCH)) with base at the step's
-// first key row.
+// (tr16(base + off(0)), tr16(base + off(1))) with base at the step's first
+// key row (a multiple of 16, which leaves the swizzle unchanged); `hi` = 1
+// reads keys 4..7 of the lane's eight.
 template <int HD>
-__device__ inline int vt_read_offset(int lane, int dt) {
+__device__ inline int vt_read_offset(int lane, int dt, int hi) {
   const int i = lane & 15, gh = (lane >> 4) & 1, g = lane >> 5;
-  const int vkey = 8 * g + (i >> 2);
-  return vkey * VRow<HD>::PITCH + (((2 * dt + gh) ^ (i >> 2)) << 5) + 8 * (i & 3);
+  const int vkey = 8 * g + (i >> 2) + 4 * hi;
+  const int c = 4 * dt + 2 * gh + ((i >> 1) & 1);
+  return vkey * VRow<HD>::PITCH + 16 * (c ^ VRow<HD>::swz(vkey)) + 8 * (i & 1);
 }
 
 // Source offset of DMA chunk X of a 64-key V tile in the VRow layout:
@@ -200,7 +220,7 @@ template <typename T, int HD>
 __device__ inline uint32_t vrow_dma_offset(int X, int64_t v_st) {
   constexpr int KCH = HD / 8;
   const int key = X / VRow<HD>::CHP, pc = X % VRow<HD>::CHP;
-  const int c = 2 * ((pc >> 1) ^ (key & 3)) + (pc & 1);
+  const int c = pc ^ VRow<HD>::swz(key);
   return (uint32_t)(key * v_st * (int64_t)sizeof(T)) + 16u * (c < KCH ? c : 0);
 }
 
