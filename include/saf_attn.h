@@ -248,11 +248,14 @@ int64_t saf_workspace_bytes(int32_t B, int32_t T, int32_t head_dim, int32_t n_sc
 /* Workspace that lets one saf_mixed_attn_fwd (or per-kind) call with these
  * arguments (workspace fields ignored) use every optimisation: the closed-form
  * scan's look-back words, then one region of fp32 partials shared by the
- * live-head and the dense P.V kernels' causal load balancing (long query
- * blocks split into key segments and merged by a combine kernel; the two run
- * one after the other on the stream).  A smaller workspace still works if it
- * covers the scan: those kernels then run unsplit.  Partials need a 16-byte
- * aligned workspace.  Returns -1 on invalid arguments.  No counterpart in the
+ * live-head, dense P.V and decomposed kernels' causal load balancing (long
+ * query blocks split into key segments and merged by a combine kernel; the
+ * kernels run one after the other on the stream), then the decomposed heads'
+ * key-scaled values for their factored form (bf16, hd <= 128).  A smaller
+ * workspace still works if it covers the scan: those kernels then run
+ * unsplit, and decomposed heads rebuild P cell by cell (equal to rounding).
+ * Partials need a 16-byte aligned workspace, the factored form a 256-byte
+ * aligned one.  Returns -1 on invalid arguments.  No counterpart in the
  * reference (its Triton launch needs no workspace). */
 int64_t saf_mixed_attn_workspace_bytes(const saf_mixed_attn_args* args);
 
