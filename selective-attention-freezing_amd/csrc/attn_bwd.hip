@@ -17,6 +17,8 @@
 // Each wave owns 32 rows of the output (queries for dQ, keys for dK / dV);
 // a lane owns one of them, so the per-row softmax statistics are per lane
 // (dQ) or, with the row-permuted (kperm) products, per register (dK / dV).
+#include <type_traits>
+
 #include "saf_kernels.h"
 
 namespace saf {
@@ -158,19 +160,30 @@ __global__ __launch_bounds__(256) void bwd_dq_kernel(const BwdParams p) {
 #pragma unroll
         for (int t = 0; t < NKT; ++t) dp = Elem<T>::mfma(tile_row_op<HD>(vt, row, 2 * t + g), dof[t], dp);
         uint32_t w[8];
+        // dS = P (dP - delta); a sub-block with every key at or below every
+        // query of the wave (and every query < T) skips the per-element mask
+        // through a uniform branch; masked scores go through exp2(-inf) = 0
+        auto ds_pack = [&](auto masked) {
 #pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          float ds2[2];
+          for (int e = 0; e < 8; ++e) {
+            float ds2[2];
 #pragma unroll
-          for (int u = 0; u < 2; ++u) {
-            const int i = 2 * e + u;
-            const int key = 64 * j + 32 * ks + acc_key(i, g);
-            // masked scores go through exp2(-inf) = 0: no branch per element
-            const float pr = fast_exp2((qv && key <= q) ? s[i] * c - lse2 : -__builtin_inff());
-            ds2[u] = pr * (dp[i] - dl);
+            for (int u = 0; u < 2; ++u) {
+              const int i = 2 * e + u;
+              float x = s[i] * c - lse2;
+              if constexpr (decltype(masked)::value) {
+                const int key = 64 * j + 32 * ks + acc_key(i, g);
+                x = (qv && key <= q) ? x : -__builtin_inff();
+              }
+              ds2[u] = fast_exp2(x) * (dp[i] - dl);
+            }
+            w[e] = Elem<T>::pack2(ds2[0], ds2[1]);
           }
-          w[e] = Elem<T>::pack2(ds2[0], ds2[1]);
-        }
+        };
+        if (64 * j + 32 * ks + 31 <= q0w && q0w + 31 < T_len)
+          ds_pack(std::false_type());
+        else
+          ds_pack(std::true_type());
 #pragma unroll
         for (int s2 = 0; s2 < 2; ++s2) {
           const uint4 bop = make_uint4(w[4 * s2], w[4 * s2 + 1], w[4 * s2 + 2], w[4 * s2 + 3]);
@@ -276,21 +289,33 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void b
 #pragma unroll
       for (int t = 0; t < NKT; ++t) dp = Elem<T>::mfma(tile_row_op<HD>(ot, row, 2 * t + g), vf[t], dp);
       uint32_t pw[8], dw[8];
+      // a sub-block with every query at or past every key of the wave (all
+      // valid) skips the per-element mask through a uniform branch
+      auto p_ds_pack = [&](auto masked) {
 #pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        float pr2[2], ds2[2];
+        for (int e = 0; e < 8; ++e) {
+          float pr2[2], ds2[2];
 #pragma unroll
-        for (int u = 0; u < 2; ++u) {
-          const int i2 = 2 * e + u;
-          const int ql = 32 * qs2 + acc_key(i2, g);  // query within the tile
-          const int qq = 64 * i + ql;
-          const float pr = fast_exp2((kv && qq >= kk && qq < T_len) ? s[i2] * c - ls[ql] : -__builtin_inff());
-          pr2[u] = pr;
-          ds2[u] = pr * (dp[i2] - ls[64 + ql]);
+          for (int u = 0; u < 2; ++u) {
+            const int i2 = 2 * e + u;
+            const int ql = 32 * qs2 + acc_key(i2, g);  // query within the tile
+            float x = s[i2] * c - ls[ql];
+            if constexpr (decltype(masked)::value) {
+              const int qq = 64 * i + ql;
+              x = (kv && qq >= kk && qq < T_len) ? x : -__builtin_inff();
+            }
+            const float pr = fast_exp2(x);
+            pr2[u] = pr;
+            ds2[u] = pr * (dp[i2] - ls[64 + ql]);
+          }
+          pw[e] = Elem<T>::pack2(pr2[0], pr2[1]);
+          dw[e] = Elem<T>::pack2(ds2[0], ds2[1]);
         }
-        pw[e] = Elem<T>::pack2(pr2[0], pr2[1]);
-        dw[e] = Elem<T>::pack2(ds2[0], ds2[1]);
-      }
+      };
+      if (qbase_row >= k0w + 31 && k0w + 31 < T_len && qbase_row + 31 < T_len)
+        p_ds_pack(std::false_type());
+      else
+        p_ds_pack(std::true_type());
 #pragma unroll
       for (int s2 = 0; s2 < 2; ++s2) {
         const uint4 bp = make_uint4(pw[4 * s2], pw[4 * s2 + 1], pw[4 * s2 + 2], pw[4 * s2 + 3]);
