@@ -413,23 +413,34 @@ __global__ __launch_bounds__(256) void bwd_frozen_dv_kernel(const BwdParams p) {
     for (int ks = 0; ks < 4; ++ks) {
       const int q0 = 64 * i + 16 * ks;
       if (q0 + 15 < k0w) continue;  // every query of the step precedes this wave's keys
-      // B operand: P[q0 + 8g + e, kk] for e = 0..7, in the activation dtype
+      // B operand: P[q0 + 8g + e, kk] for e = 0..7, in the activation dtype;
+      // a step with every query at or past every key of the wave (all
+      // valid) skips the per-element mask through a uniform branch
       float e8[8];
+      auto p_col = [&](auto masked) {
 #pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const int qq = q0 + 8 * g + e;
-        const bool ok = kv && qq >= kk && qq < T_len;
-        float v = 0.f;
-        if (KIND == 1) {
-          if (ok) v = load_as_f32(p.patt, (int64_t)ph * p.p_sh + (int64_t)qq * p.p_si + (int64_t)kk * p.p_sj, p.patt_dtype);
-        } else {
-          // every (query, key) pair of the block indexes inside the staged
-          // rho window and z row, so the reads need no guard; masked pairs
-          // take exp2(-inf) = 0
-          v = fast_exp2(ok ? alpha_k + rs[qq - kk - dmin] - zs[qq - 64 * i] : -__builtin_inff());
+        for (int e = 0; e < 8; ++e) {
+          const int qq = q0 + 8 * g + e;
+          const bool ok = !decltype(masked)::value || (kv && qq >= kk && qq < T_len);
+          float v = 0.f;
+          if (KIND == 1) {
+            if (ok)
+              v = load_as_f32(p.patt, (int64_t)ph * p.p_sh + (int64_t)qq * p.p_si + (int64_t)kk * p.p_sj,
+                              p.patt_dtype);
+          } else {
+            // every (query, key) pair of the block indexes inside the staged
+            // rho window and z row, so the reads need no guard; masked pairs
+            // take exp2(-inf) = 0
+            const float x = alpha_k + rs[qq - kk - dmin] - zs[qq - 64 * i];
+            v = fast_exp2(ok ? x : -__builtin_inff());
+          }
+          e8[e] = v;
         }
-        e8[e] = v;
-      }
+      };
+      if (q0 >= k0w + 31 && k0w + 31 < T_len && q0 + 15 < T_len)
+        p_col(std::false_type());
+      else
+        p_col(std::true_type());
       const uint4 bop = make_uint4(Elem<T>::pack2(e8[0], e8[1]), Elem<T>::pack2(e8[2], e8[3]),
                                    Elem<T>::pack2(e8[4], e8[5]), Elem<T>::pack2(e8[6], e8[7]));
 #pragma unroll
