@@ -92,15 +92,21 @@ __global__ __launch_bounds__(256) void bwd_delta_kernel(const BwdParams p) {
 }
 
 // dQ of the live heads.  Workgroup = 4 waves x 32 queries of one (batch,
-// live slot); key blocks of 64 (K and V tiles double-buffered in LDS) up to
-// the diagonal.  Per 32-key sub-block a wave forms S^T = K Q^T and
-// dP^T = V dO^T (keys in the kperm row order, so register i of lane-half g is
-// key acc_key(i, g)), P^T = 2^(S^T c - lse), dS^T = P^T (dP^T - delta), and
-// accumulates dQ^T += K^T dS^T (K^T from transposing tile reads).
+// live slot); key blocks of 64 up to the diagonal.  Per 32-key sub-block a
+// wave forms S^T = K Q^T and dP^T = V dO^T (keys in the kperm row order, so
+// register i of lane-half g is key acc_key(i, g)), P^T = 2^(S^T c - lse),
+// dS^T = P^T (dP^T - delta), and accumulates dQ^T += K^T dS^T (K^T from
+// transposing tile reads).  K and V tiles arrive by DMA into static slots with
+// counted waits and a bare barrier per block, as in the dK/dV kernel below:
+// up to hd 64 two blocks ahead in three slots; above, one block ahead in two
+// (three 32 KB slot pairs would leave one workgroup per CU: hd 128 dQ 610 ->
+// 840 us).
 template <typename T, int HD>
 __global__ __launch_bounds__(256) void bwd_dq_kernel(const BwdParams p) {
   constexpr int BM = kBwdWaves * 32, NKT = HD / 16, NDT = HD / 32, VB = VRow<HD>::BYTES;
-  __shared__ __align__(16) char k0[VB], k1[VB], v0[VB], v1[VB];
+  constexpr int NS = HD <= 64 ? 3 : 2, AHEAD = NS - 1;
+  constexpr int kOps = 2 * TileOffsets<T, HD>::VN;  // loads per wave per block
+  __shared__ __align__(16) char k0[VB], k1[VB], k2[NS == 3 ? VB : 16], v0[VB], v1[VB], v2[NS == 3 ? VB : 16];
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int n = lane & 31, g = lane >> 5;
@@ -138,18 +144,23 @@ __global__ __launch_bounds__(256) void bwd_dq_kernel(const BwdParams p) {
   vo.init(wave, lane, p.v_st);
   const int nkb = (min(qb * BM + BM, T_len) + 63) / 64;
 
-  for (int j = 0; j < nkb; ++j) {
-    const char* kt = (j & 1) ? k1 : k0;
-    const char* vt = (j & 1) ? v1 : v0;
-    if (j == 0) {
-      ko.load(kbase, p.k_st, 0, T_len, k0, wave);
-      vo.load(vbase, p.v_st, 0, T_len, v0, wave);
-    }
-    __syncthreads();  // this block's K and V tiles are in LDS
-    if (j + 1 < nkb) {
-      ko.load(kbase, p.k_st, 64 * (j + 1), T_len, (j & 1) ? k0 : k1, wave);
-      vo.load(vbase, p.v_st, 64 * (j + 1), T_len, (j & 1) ? v0 : v1, wave);
-    }
+  auto load_block = [&](int j, auto slotc) {
+    constexpr int S = decltype(slotc)::value;
+    const int lim = j < nkb ? T_len : 0;  // past the last block: an empty descriptor
+    ko.load(kbase, p.k_st, 64 * j, lim, S == 0 ? k0 : (S == 1 ? k1 : k2), wave);
+    vo.load(vbase, p.v_st, 64 * j, lim, S == 0 ? v0 : (S == 1 ? v1 : v2), wave);
+  };
+  auto meet = [&]() {  // the next block has landed (with three slots the one after stays in flight)
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_waitcnt(waitcnt_vm((AHEAD - 1) * kOps));
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+  };
+  auto block = [&](const int j, auto phase) {
+    constexpr int R = decltype(phase)::value;
+    const char* const kt = R == 0 ? k0 : (R == 1 ? k1 : k2);
+    const char* const vt = R == 0 ? v0 : (R == 1 ? v1 : v2);
+    load_block(j + AHEAD, std::integral_constant<int, (R + AHEAD) % NS>());
     if (64 * j <= q0w + 31) {  // else every key of the block is past this wave's queries
 #pragma unroll
       for (int ks = 0; ks < 2; ++ks) {
@@ -193,23 +204,45 @@ __global__ __launch_bounds__(256) void bwd_dq_kernel(const BwdParams p) {
         }
       }
     }
-    __syncthreads();  // every wave is done with this slot before it is refilled
+    meet();  // block j+1 has landed and slot R is read
+  };
+
+  using S0 = std::integral_constant<int, 0>;
+  using S1 = std::integral_constant<int, 1>;
+  load_block(0, S0());
+  if constexpr (NS == 3) load_block(1, S1());
+  meet();
+  using P0 = std::integral_constant<int, 0>;
+  using P1 = std::integral_constant<int, 1>;
+  using P2 = std::integral_constant<int, 2 % NS>;
+  for (int j = 0;;) {
+    if (j >= nkb) break;
+    block(j++, P0());
+    if (j >= nkb) break;
+    block(j++, P1());
+    if constexpr (NS == 3) {
+      if (j >= nkb) break;
+      block(j++, P2());
+    }
   }
+  // the last (empty) DMAs land before the workgroup's LDS is released
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
   if (qv) store_out_tile<T, HD>(dqbase + (int64_t)q * p.dq_st, dqa, p.sm_scale, g);
 }
 
-// dK and dV of the live heads.  Workgroup = 4 waves x 32 keys of one (batch,
-// live slot); query blocks of 64 from the diagonal to T (Q, dO tiles and the
-// blocks' lse / delta double-buffered in LDS).  Per 32-query sub-block a
-// wave forms S = Q K^T and dP = dO V^T with the queries in the kperm row
-// order (register i of lane-half g is query acc_key(i, g); the lane is the
-// key), P = 2^(S c - lse_q), dS = P (dP - delta_q), and accumulates
-// dV^T += dO^T P and dK^T += Q^T dS (dO^T, Q^T from transposing tile reads).
+// Waves per SIMD of the dK/dV kernel: its accumulators, K / V rows and three
+// pipeline slots fit three waves only up to hd 32 (at hd 64 three waves spilled
+// 59 registers and ran 1.8x slower than two).
+constexpr int dkdv_waves_per_eu(int hd) { return hd <= 32 ? 3 : (hd <= 64 ? 2 : 1); }
+
 template <typename T, int HD>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void bwd_dkdv_kernel(const BwdParams p) {
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(dkdv_waves_per_eu(HD), dkdv_waves_per_eu(HD))))
+void bwd_dkdv_kernel(const BwdParams p) {
   constexpr int BN = kBwdWaves * 32, NKT = HD / 16, NDT = HD / 32, VB = VRow<HD>::BYTES;
-  __shared__ __align__(16) char q0[VB], q1[VB], o0[VB], o1[VB];
-  __shared__ float ls0[128], ls1[128];  // lse (0..63) and delta (64..127) of the tile's queries
+  constexpr int kOps = 2 * TileOffsets<T, HD>::VN + 1;  // loads per wave per block
+  __shared__ __align__(16) char q0[VB], q1[VB], q2[VB], o0[VB], o1[VB], o2[VB];
+  __shared__ __align__(16) float ls0[4][64], ls1[4][64], ls2[4][64];
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int n = lane & 31, g = lane >> 5;
@@ -249,35 +282,37 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void b
   qo.init(wave, lane, p.q_st);
   oo.init(wave, lane, p.do_st);
   const int ib0 = (kb * BN) / 64, nqb = (T_len + 63) / 64;
+  const bool lse_wave = wave < 2;
+  const uint32_t ls_off =
+      lane < 32 ? (uint32_t)((int64_t)(32 * (wave & 1) + lane) * (lse_wave ? p.l_st : 1) * 4) : 0x80000000u;
 
-  // query block i lives in slot i & 1: Q tile, dO tile, and lse / delta.
-  // The next block's tiles go out by DMA and its lse / delta into registers
-  // right after the barrier; the registers land in the idle slot after the
-  // block's products, so no load latency sits in front of a barrier.
-  if (ib0 < nqb) {
-    qo.load(qbase, p.q_st, 64 * ib0, T_len, q0, wave);
-    oo.load(dobase, p.do_st, 64 * ib0, T_len, o0, wave);
-    if (tid < 64) {
-      const int qq = 64 * ib0 + tid;
-      ls0[tid] = qq < T_len ? lsebase[(int64_t)qq * p.l_st] : 0.f;
-      ls0[64 + tid] = qq < T_len ? dlbase[qq] : 0.f;
-    }
-  }
-  for (int i = ib0; i < nqb; ++i) {
-    const char* qt = ((i - ib0) & 1) ? q1 : q0;
-    const char* ot = ((i - ib0) & 1) ? o1 : o0;
-    const float* ls = ((i - ib0) & 1) ? ls1 : ls0;
-    __syncthreads();  // this block's tiles and statistics are in LDS
-    float nlse = 0.f, ndel = 0.f;
-    if (i + 1 < nqb) {
-      qo.load(qbase, p.q_st, 64 * (i + 1), T_len, ((i - ib0) & 1) ? q0 : q1, wave);
-      oo.load(dobase, p.do_st, 64 * (i + 1), T_len, ((i - ib0) & 1) ? o0 : o1, wave);
-      const int qq = 64 * (i + 1) + tid;
-      if (tid < 64 && qq < T_len) {
-        nlse = lsebase[(int64_t)qq * p.l_st];
-        ndel = dlbase[qq];
-      }
-    }
+  using S0 = std::integral_constant<int, 0>;
+  using S1 = std::integral_constant<int, 1>;
+  auto load_block = [&](int i, auto slotc) {
+    constexpr int S = decltype(slotc)::value;
+    char* const qt = S == 0 ? q0 : (S == 1 ? q1 : q2);
+    char* const ot = S == 0 ? o0 : (S == 1 ? o1 : o2);
+    float(*const lt)[64] = S == 0 ? ls0 : (S == 1 ? ls1 : ls2);
+    const int lim = i < nqb ? T_len : 0;  // past the last block: an empty descriptor
+    qo.load(qbase, p.q_st, 64 * i, lim, qt, wave);
+    oo.load(dobase, p.do_st, 64 * i, lim, ot, wave);
+    const __amdgpu_buffer_rsrc_t lr =
+        lse_wave ? rows_rsrc(lsebase, p.l_st, 64 * i, lim) : rows_rsrc(dlbase, (int64_t)1, 64 * i, lim);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(lr, SAF_LDS_PTR(&lt[wave][0]), 4, ls_off, 0, 0, 0);
+  };
+  auto meet = [&]() {
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_waitcnt(waitcnt_vm(kOps));
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+  };
+
+  auto block = [&](const int i, auto phase) {
+    constexpr int R = decltype(phase)::value;
+    const char* const qt = R == 0 ? q0 : (R == 1 ? q1 : q2);
+    const char* const ot = R == 0 ? o0 : (R == 1 ? o1 : o2);
+    float(*const ls)[64] = R == 0 ? ls0 : (R == 1 ? ls1 : ls2);
+    load_block(i + 2, std::integral_constant<int, (R + 2) % 3>());
 #pragma unroll
     for (int qs2 = 0; qs2 < 2; ++qs2) {
       const int qbase_row = 64 * i + 32 * qs2;
@@ -290,7 +325,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void b
       for (int t = 0; t < NKT; ++t) dp = Elem<T>::mfma(tile_row_op<HD>(ot, row, 2 * t + g), vf[t], dp);
       uint32_t pw[8], dw[8];
       // a sub-block with every query at or past every key of the wave (all
-      // valid) skips the per-element mask through a uniform branch
+      // valid) skips the per-element mask through a uniform branch; query
+      // acc_key(i2, g) of sub-block qs2 has its lse in row qs2 of the slot's
+      // statistics and its delta in row 2 + qs2
       auto p_ds_pack = [&](auto masked) {
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
@@ -298,15 +335,15 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void b
 #pragma unroll
           for (int u = 0; u < 2; ++u) {
             const int i2 = 2 * e + u;
-            const int ql = 32 * qs2 + acc_key(i2, g);  // query within the tile
-            float x = s[i2] * c - ls[ql];
+            const int ql = acc_key(i2, g);  // query within the sub-block
+            float x = s[i2] * c - ls[qs2][ql];
             if constexpr (decltype(masked)::value) {
-              const int qq = 64 * i + ql;
+              const int qq = qbase_row + ql;
               x = (kv && qq >= kk && qq < T_len) ? x : -__builtin_inff();
             }
             const float pr = fast_exp2(x);
             pr2[u] = pr;
-            ds2[u] = pr * (dp[i2] - ls[64 + ql]);
+            ds2[u] = pr * (dp[i2] - ls[2 + qs2][ql]);
           }
           pw[e] = Elem<T>::pack2(pr2[0], pr2[1]);
           dw[e] = Elem<T>::pack2(ds2[0], ds2[1]);
@@ -327,12 +364,27 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void b
         }
       }
     }
-    if (tid < 64) {  // the idle slot's readers finished before the previous barrier
-      float* ln = ((i - ib0) & 1) ? ls0 : ls1;
-      ln[tid] = nlse;
-      ln[64 + tid] = ndel;
+    meet();  // block i+1 has landed (block i+2 stays in flight) and slot R is read
+  };
+
+  if (ib0 < nqb) {
+    load_block(ib0, S0());
+    load_block(ib0 + 1, S1());
+    meet();
+    using P0 = std::integral_constant<int, 0>;
+    using P1 = std::integral_constant<int, 1>;
+    using P2 = std::integral_constant<int, 2>;
+    for (int i = ib0;;) {
+      if (i >= nqb) break;
+      block(i++, P0());
+      if (i >= nqb) break;
+      block(i++, P1());
+      if (i >= nqb) break;
+      block(i++, P2());
     }
-    __syncthreads();  // every wave is done with this slot before it is refilled
+    // the last (empty) DMAs land before the workgroup's LDS is released
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
   }
   if (kv) {
     store_out_tile<T, HD>(dkbase + (int64_t)kk * p.dk_st, dka, p.sm_scale, g);

@@ -29,11 +29,6 @@ namespace saf {
 // budget of two waves per SIMD.
 constexpr int decomp_waves_per_eu(int hd) { return hd > 128 ? 2 : 3; }
 
-// s_waitcnt immediates (gfx9 encoding: vmcnt bits 3:0 and 15:14, expcnt
-// 6:4, lgkmcnt 11:8): vmcnt <= n alone, and vmcnt <= n with lgkmcnt 0.
-constexpr int waitcnt_vm(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8); }
-constexpr int waitcnt_vm_lgkm0(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4); }
-
 // Decomposed frozen heads, P = exp(alpha_j + rho_{i-j} - z_i), in one of
 // two forms chosen per workgroup.
 //

@@ -166,6 +166,11 @@ template <int HD> struct VLayout {
 
 #define SAF_LDS_PTR(p) ((__attribute__((address_space(3))) void*)(p))
 
+// s_waitcnt immediates (gfx9 encoding: vmcnt bits 3:0 and 15:14, expcnt
+// 6:4, lgkmcnt 11:8): vmcnt <= n alone, and vmcnt <= n with lgkmcnt 0.
+constexpr int waitcnt_vm(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8); }
+constexpr int waitcnt_vm_lgkm0(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4); }
+
 // V tile: 64 key rows of HD values, row pitch VSEG 32-byte segments.  The
 // logical 16-byte chunk c of row r is stored at chunk c ^ swz(r), swz an
 // XOR-linear function of the row's low four bits chosen (by exhaustive
