@@ -150,17 +150,19 @@ __device__ __forceinline__ void decomp_body(const FrozenParams& p) {
   float rowscale[QT];
 
   // factored form: A = max A_k over this segment's key blocks, R = max r
-  // over distances < kend_wg (a superset of what any key segment of this
-  // block reaches) and the smallest z of the block's rows decide it for the
-  // whole workgroup
+  // over the 64-distance blocks below kend_wg (a superset of what any key
+  // segment of this block reaches; both maxima come from the pre-pass) and
+  // the smallest z of the block's rows decide it for the whole workgroup
   bool factored = false;
   float aoff = 0.f, roff = 0.f;
-  const float* const ablk = p.a_off + (int64_t)slot * ((T_len + 63) / 64);
+  const int nblk = (T_len + 63) / 64;
+  const float* const ablk = p.a_off + (int64_t)slot * nblk;
   if constexpr (kFactorable) {
     if (p.vp != nullptr) {
+      const float* const rblk = p.a_off + (int64_t)(p.n_slots + slot) * nblk;
       float am = -INFINITY, rm = -INFINITY, zm = INFINITY;
       for (int k = kb0 + tid; k < nkb; k += NTHR) am = fmaxf(am, ablk[k]);
-      for (int j = tid; j < kend_wg; j += NTHR) rm = fmaxf(rm, rho_at(j));
+      for (int k = tid; k < nkb_qb; k += NTHR) rm = fmaxf(rm, rblk[k]);
       for (int i = q0 + tid; i < kend_wg; i += NTHR)
         zm = fminf(zm, load_as_f32(p.z, (int64_t)ph * p.z_sh + (int64_t)i * p.z_ss, p.z_dtype));
 #pragma unroll
@@ -176,7 +178,7 @@ __device__ __forceinline__ void decomp_body(const FrozenParams& p) {
       }
       __syncthreads();
       am = fmaxf(fmaxf(red_lds[0][0], red_lds[0][1]), fmaxf(red_lds[0][2], red_lds[0][3]));
-      rm = fmaxf(fmaxf(red_lds[1][0], red_lds[1][1]), fmaxf(red_lds[1][2], red_lds[1][3])) * kLog2e;
+      rm = fmaxf(fmaxf(red_lds[1][0], red_lds[1][1]), fmaxf(red_lds[1][2], red_lds[1][3]));
       zm = fminf(fminf(red_lds[2][0], red_lds[2][1]), fminf(red_lds[2][2], red_lds[2][3])) * kLog2e;
       factored = __builtin_isfinite(am) && __builtin_isfinite(rm) && __builtin_isfinite(zm) &&
                  zm >= am + rm - kFactorRange;
@@ -220,7 +222,6 @@ __device__ __forceinline__ void decomp_body(const FrozenParams& p) {
       float er[ERN], ab = 0.f;
       int ej0 = 0;
       const float* const r2 = p.r2 + (int64_t)slot * T_len;
-      const int nblk = (T_len + 63) / 64;
       auto load_er = [&](int jb) {  // unconditional: indices clamped past the end
         const int j0 = 64 * jb;
 #pragma unroll
@@ -477,12 +478,14 @@ void frozen_decomp_kernel(const FrozenParams p) {
 
 // vp[b, slot, j] = 2^(alpha_j log2 e - A_k) v[b, v_head, j] in T, with
 // A_k = max alpha log2 e over the 64-key block k = j / 64 of the slot's head
-// (a_off[slot * nblk + k], nblk = ceil(T / 64), written by batch 0's
-// workgroup, which also writes r2[slot, d] = rho_d log2 e for the block's
-// distances, so the main kernel reads rho as plain fp32).  One workgroup per (key block, slot, batch); every wave reduces
-// the block's alpha itself, so nothing orders workgroups.  vp holds T rows
-// per (batch, slot); the main kernel's buffer-resource bound reads rows past
-// T as zero.
+// (a_off[slot * nblk + k], nblk = ceil(T / 64)).  Batch 0's workgroup also
+// writes r2[slot, d] = rho_d log2 e for the block's 64 distances (the main
+// kernel then reads rho as plain fp32) and their maximum
+// a_off[(n_slots + slot) * nblk + k] (so a workgroup's R is a maximum over
+// at most nblk values).  One workgroup per (key block, slot, batch); every
+// wave reduces the block's alpha itself, so nothing orders workgroups.  vp
+// holds T rows per (batch, slot); the main kernel's buffer-resource bound
+// reads rows past T as zero.
 template <typename T, int HD>
 __global__ __launch_bounds__(256) void decomp_prescale_kernel(const FrozenParams p) {
   constexpr int CH = HD / 8;          // 16-byte chunks per row
@@ -505,10 +508,18 @@ __global__ __launch_bounds__(256) void decomp_prescale_kernel(const FrozenParams
 #pragma unroll
   for (int off = 32; off >= 1; off >>= 1) am = fmaxf(am, __shfl_xor(am, off));
   if (b == 0) {
-    if (tid == 0) p.a_off[(int64_t)slot * ((p.T + 63) / 64) + kb] = am;
-    if (tid >= 64 && tid < 128 && j0 + lane < p.T)
-      p.r2[(int64_t)slot * p.T + j0 + lane] =
-          load_as_f32(p.rho, (int64_t)ph * p.r_sh + (int64_t)(j0 + lane) * p.r_ss, p.r_dtype) * kLog2e;
+    const int nblk = (p.T + 63) / 64;
+    if (tid == 0) p.a_off[(int64_t)slot * nblk + kb] = am;
+    if (tid >= 64 && tid < 128) {  // wave 1: the block's distances
+      const float rv = j0 + lane < p.T
+                           ? load_as_f32(p.rho, (int64_t)ph * p.r_sh + (int64_t)(j0 + lane) * p.r_ss, p.r_dtype) * kLog2e
+                           : -INFINITY;
+      if (j0 + lane < p.T) p.r2[(int64_t)slot * p.T + j0 + lane] = rv;
+      float rmx = rv;
+#pragma unroll
+      for (int off = 32; off >= 1; off >>= 1) rmx = fmaxf(rmx, __shfl_xor(rmx, off));
+      if (lane == 0) p.a_off[(int64_t)(p.n_slots + slot) * nblk + kb] = rmx;
+    }
   }
   T* vp = reinterpret_cast<T*>(p.vp) + ((int64_t)b * p.n_slots + slot) * p.T * HD;
 #pragma unroll

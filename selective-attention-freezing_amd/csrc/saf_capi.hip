@@ -501,10 +501,10 @@ int run_dense(const saf_tensor_t& patt, const saf_tensor_t& v, const saf_tensor_
 
 // Workspace regions after the scan's: the fp32 partials of split query
 // blocks (flash, dense and decomposed kernels run one after the other and
-// share them), then the factored decomposed form's per-key-block alpha
-// maxima a_off (n_dec x ceil(T / 64) floats), rho log2 e r2 (n_dec x T
-// floats) and key-scaled values vp (B, n_dec, T, HD) bf16 (bf16, hd <= 128
-// only).
+// share them), then the factored decomposed form's per-64-block maxima of
+// alpha and of rho a_off (2 x n_dec x ceil(T / 64) floats), rho log2 e r2
+// (n_dec x T floats) and key-scaled values vp (B, n_dec, T, HD) bf16 (bf16,
+// hd <= 128 only).
 int64_t round256(int64_t n) { return (n + 255) / 256 * 256; }
 
 int64_t part_region_bytes(const saf_mixed_attn_args* args, const Plan& pl) {
@@ -523,10 +523,10 @@ int64_t part_region_bytes(const saf_mixed_attn_args* args, const Plan& pl) {
   return round256(part);
 }
 
-// Per-key-block alpha maxima (n_dec x ceil(T / 64) floats), rho log2 e in
-// fp32 (n_dec x T), then the key-scaled values.
+// Per-64-block maxima of alpha and of rho (2 x n_dec x ceil(T / 64) floats),
+// rho log2 e in fp32 (n_dec x T), then the key-scaled values.
 int64_t decomp_aoff_bytes(const Plan& pl) {
-  return round256((int64_t)pl.decomp.size() * ((pl.T + 63) / 64) * 4);
+  return round256(2 * (int64_t)pl.decomp.size() * ((pl.T + 63) / 64) * 4);
 }
 int64_t decomp_r2_bytes(const Plan& pl) { return round256((int64_t)pl.decomp.size() * pl.T * 4); }
 

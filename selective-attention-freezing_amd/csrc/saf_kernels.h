@@ -90,7 +90,8 @@ struct FrozenParams {
   int B, T, n_slots, n_qblk;
   // decomposed heads, factored form (null: cell-by-cell rebuild only):
   // a_off[slot][k] = max alpha log2 e over 64-key block k of the slot's head
-  // (n_slots x ceil(T / 64)), vp = the key-scaled values
+  // (n_slots x ceil(T / 64)), followed by the same layout of maxima of
+  // rho log2 e over 64-distance blocks, vp = the key-scaled values
   // 2^(alpha_j log2 e - a_off[slot][j / 64]) v_j, (B, n_slots, T, HD) in the
   // input dtype, r2[slot][d] = rho_d log2 e (n_slots x T) (workspace, all
   // written by launch_decomp_prescale)
