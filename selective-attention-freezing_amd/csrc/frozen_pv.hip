@@ -24,10 +24,12 @@
 
 namespace saf {
 
-// Resident rebuild workgroups per CU (decomp_resident() on the host): two
-// at hd 256, whose 128 accumulator registers per wave need the 256-register
+// Resident decomposed workgroups per CU (decomp_resident() on the host):
+// three up to hd 64; two above, where the factored form's three V' slots and
+// two distance windows take 62.5 KB of LDS (three workgroups need <= 53 KB)
+// and hd 256's 128 accumulator registers per wave need the 256-register
 // budget of two waves per SIMD.
-constexpr int decomp_waves_per_eu(int hd) { return hd > 128 ? 2 : 3; }
+constexpr int decomp_waves_per_eu(int hd) { return hd > 64 ? 2 : 3; }
 
 // Decomposed frozen heads, P = exp(alpha_j + rho_{i-j} - z_i), in one of
 // two forms chosen per workgroup.

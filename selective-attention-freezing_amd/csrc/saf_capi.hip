@@ -437,7 +437,7 @@ void fill_frozen_common(FrozenParams& p, const saf_tensor_t& v, const saf_tensor
 
 int frozen_qtiles(int hd) { return hd <= 64 ? 2 : 1; }
 // Resident rebuild workgroups per CU (decomp_waves_per_eu in the kernel).
-int decomp_resident(int hd) { return hd > 128 ? 2 : 3; }
+int decomp_resident(int hd) { return hd > 64 ? 2 : 3; }
 
 // Dense P.V work plan: query blocks of the kernel's shape, balanced over the
 // batch groups that share a pattern (dense_batch_group).
