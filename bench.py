@@ -329,7 +329,10 @@ def kernel_rooflines(summ, flash_label, traffic, steps):
         n, ms, work = summ["dense"]
         extra["frozen_dense_pv"] = {"launches": n, "avg_launch_ms": round(ms / n, 4),
                                     "flop_per_launch": work // n}
-    extra["attention_ms_per_step"] = round(sum(v[1] for v in summ.values()) / steps, 3)
+    # kernels on the launch stream only: the scan runs on a side stream
+    # beside them, so its span would count time twice
+    extra["attention_kernels_ms_per_step"] = round(
+        sum(v[1] for k, v in summ.items() if k != "scan") / steps, 3)
     return roof, extra
 
 

@@ -674,23 +674,41 @@ struct DenseState {
         }
   }
 
-  // O^T += V^T P^T for one 64-key block (V tiles at `cur`)
+  // V^T operands of every d tile for 16-key step k (keys 16k..16k+15 of the
+  // block) of sequence nb
+  __device__ __forceinline__ void read_vt(const char* cur, int k, int nb, uint4 (&a)[NDT]) const {
+    const char* base = cur + nb * VB + 16 * k * PITCH;
+#pragma unroll
+    for (int dt = 0; dt < NDT; ++dt) {
+      const uint2 lo = ds_read_tr16(base + vro[dt]);
+      const uint2 hi = ds_read_tr16(base + (VRow<HD>::M2 ? vroh[dt] : vro[dt] + 4 * PITCH));
+      a[dt] = make_uint4(lo.x, lo.y, hi.x, hi.y);
+    }
+  }
+
+  // O^T += V^T P^T for one 64-key block (V tiles at `cur`), in 4 NB steps
+  // (16 keys, one sequence): the V^T operands of step t + 1 are read while
+  // the MFMAs of step t run, in two register sets, so each group of NDT QT
+  // MFMAs waits for reads issued one group earlier (read next to its MFMA,
+  // every MFMA waited for a full LDS round trip)
   __device__ __forceinline__ void mma_block(const char* cur, const uint4 (&pb)[2][2][QT]) {
+    constexpr int NS = 4 * NB;
+    uint4 a[2][NDT];
+    read_vt(cur, 0, 0, a[0]);
 #pragma unroll
-    for (int ks = 0; ks < 2; ++ks)
+    for (int t = 0; t < NS; ++t) {
+      if (t + 1 < NS) read_vt(cur, (t + 1) / NB, (t + 1) % NB, a[(t + 1) & 1]);
+      // keep the order: the scheduler otherwise sinks each read next to its
+      // MFMA again to save registers
+      __builtin_amdgcn_sched_barrier(0);
+      const int k = t / NB, nb = t % NB;
 #pragma unroll
-      for (int sh = 0; sh < 2; ++sh)
+      for (int dt = 0; dt < NDT; ++dt)
 #pragma unroll
-        for (int nb = 0; nb < NB; ++nb)
-#pragma unroll
-          for (int dt = 0; dt < NDT; ++dt) {
-            const char* base = cur + nb * VB + (32 * ks + 16 * sh) * PITCH;
-            const uint2 lo = ds_read_tr16(base + vro[dt]);
-            const uint2 hi = ds_read_tr16(base + (VRow<HD>::M2 ? vroh[dt] : vro[dt] + 4 * PITCH));
-            const uint4 a = make_uint4(lo.x, lo.y, hi.x, hi.y);
-#pragma unroll
-            for (int qt = 0; qt < QT; ++qt) o[nb][qt][dt] = Elem<T>::mfma(a, pb[ks][sh][qt], o[nb][qt][dt]);
-          }
+        for (int qt = 0; qt < QT; ++qt)
+          o[nb][qt][dt] = Elem<T>::mfma(a[t & 1][dt], pb[k >> 1][k & 1][qt], o[nb][qt][dt]);
+      __builtin_amdgcn_sched_barrier(0);
+    }
   }
 
   // Block j of the key range [kb0, kb1) (this wave's rows reach blocks
