@@ -241,6 +241,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(dkdv_waves_
 void bwd_dkdv_kernel(const BwdParams p) {
   constexpr int BN = kBwdWaves * 32, NKT = HD / 16, NDT = HD / 32, VB = VRow<HD>::BYTES;
   constexpr int kOps = 2 * TileOffsets<T, HD>::VN + 1;  // loads per wave per block
+  constexpr bool kBatch = dkdv_waves_per_eu(HD) == 1;
   __shared__ __align__(16) char q0[VB], q1[VB], q2[VB], o0[VB], o1[VB], o2[VB];
   __shared__ __align__(16) float ls0[4][64], ls1[4][64], ls2[4][64];
   const int tid = threadIdx.x, lane = tid & 63;
@@ -319,10 +320,38 @@ void bwd_dkdv_kernel(const BwdParams p) {
       if (qbase_row + 31 < k0w) continue;  // every query of the sub-block precedes this wave's keys
       const int row = 32 * qs2 + kperm(n);
       f32x16_t s = zero16(), dp = zero16();
+      uint4 co[2][NDT], cq[2][NDT];  // column operands of the dV / dK products (kBatch)
+      if constexpr (kBatch) {
+        // one wave per SIMD: no other wave covers the LDS latency, so the
+        // row operands are read in one batch before the S / dP MFMAs and the
+        // column operands before the softmax VALU work (the scheduler keeps
+        // each read next to its MFMA otherwise)
+        uint4 qa[NKT], oa[NKT];
 #pragma unroll
-      for (int t = 0; t < NKT; ++t) s = Elem<T>::mfma(tile_row_op<HD>(qt, row, 2 * t + g), kf[t], s);
+        for (int t = 0; t < NKT; ++t) {
+          qa[t] = tile_row_op<HD>(qt, row, 2 * t + g);
+          oa[t] = tile_row_op<HD>(ot, row, 2 * t + g);
+        }
+        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-      for (int t = 0; t < NKT; ++t) dp = Elem<T>::mfma(tile_row_op<HD>(ot, row, 2 * t + g), vf[t], dp);
+        for (int t = 0; t < NKT; ++t) {
+          s = Elem<T>::mfma(qa[t], kf[t], s);
+          dp = Elem<T>::mfma(oa[t], vf[t], dp);
+        }
+#pragma unroll
+        for (int s2 = 0; s2 < 2; ++s2)
+#pragma unroll
+          for (int dt = 0; dt < NDT; ++dt) {
+            co[s2][dt] = tile_col_op<HD>(ot, 2 * qs2 + s2, dt, lane);
+            cq[s2][dt] = tile_col_op<HD>(qt, 2 * qs2 + s2, dt, lane);
+          }
+        __builtin_amdgcn_sched_barrier(0);
+      } else {
+#pragma unroll
+        for (int t = 0; t < NKT; ++t) s = Elem<T>::mfma(tile_row_op<HD>(qt, row, 2 * t + g), kf[t], s);
+#pragma unroll
+        for (int t = 0; t < NKT; ++t) dp = Elem<T>::mfma(tile_row_op<HD>(ot, row, 2 * t + g), vf[t], dp);
+      }
       uint32_t pw[8], dw[8];
       // a sub-block with every query at or past every key of the wave (all
       // valid) skips the per-element mask through a uniform branch; query
@@ -359,8 +388,8 @@ void bwd_dkdv_kernel(const BwdParams p) {
         const uint4 bd = make_uint4(dw[4 * s2], dw[4 * s2 + 1], dw[4 * s2 + 2], dw[4 * s2 + 3]);
 #pragma unroll
         for (int dt = 0; dt < NDT; ++dt) {
-          dva[dt] = Elem<T>::mfma(tile_col_op<HD>(ot, 2 * qs2 + s2, dt, lane), bp, dva[dt]);
-          dka[dt] = Elem<T>::mfma(tile_col_op<HD>(qt, 2 * qs2 + s2, dt, lane), bd, dka[dt]);
+          dva[dt] = Elem<T>::mfma(kBatch ? co[s2][dt] : tile_col_op<HD>(ot, 2 * qs2 + s2, dt, lane), bp, dva[dt]);
+          dka[dt] = Elem<T>::mfma(kBatch ? cq[s2][dt] : tile_col_op<HD>(qt, 2 * qs2 + s2, dt, lane), bd, dka[dt]);
         }
       }
     }
