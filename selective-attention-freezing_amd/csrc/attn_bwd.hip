@@ -64,6 +64,11 @@ struct TileOffsets {
 
 __device__ __forceinline__ uint4 load16(const void* p) { return *reinterpret_cast<const uint4*>(p); }
 
+// The eight 16-bit elements of w (bf16 or fp16) with their signs flipped.
+__device__ __forceinline__ uint4 neg_halves(uint4 w) {
+  return make_uint4(w.x ^ 0x80008000u, w.y ^ 0x80008000u, w.z ^ 0x80008000u, w.w ^ 0x80008000u);
+}
+
 }  // namespace
 
 // delta[b, slot, i] = sum_d out[b, h, i, d] * dout[b, h, i, d] over the live
@@ -269,7 +274,8 @@ void bwd_dkdv_kernel(const BwdParams p) {
 #pragma unroll
   for (int t = 0; t < NKT; ++t) {
     kf[t] = kv ? load16(kbase + (int64_t)kk * p.k_st + 16 * t + 8 * g) : make_uint4(0, 0, 0, 0);
-    vf[t] = kv ? load16(vbase + (int64_t)kk * p.v_st + 16 * t + 8 * g) : make_uint4(0, 0, 0, 0);
+    // -V: the dP chain starts from delta, so it ends at delta - dP
+    vf[t] = kv ? neg_halves(load16(vbase + (int64_t)kk * p.v_st + 16 * t + 8 * g)) : make_uint4(0, 0, 0, 0);
   }
   const float c = p.scale_log2;
   f32x16_t dka[NDT], dva[NDT];
@@ -319,7 +325,10 @@ void bwd_dkdv_kernel(const BwdParams p) {
       const int qbase_row = 64 * i + 32 * qs2;
       if (qbase_row + 31 < k0w) continue;  // every query of the sub-block precedes this wave's keys
       const int row = 32 * qs2 + kperm(n);
-      f32x16_t s = zero16(), dp = zero16();
+      // dp starts from the delta of each element's query and ends at delta - dP
+      f32x16_t s = zero16(), dp;
+#pragma unroll
+      for (int i2 = 0; i2 < 16; ++i2) dp[i2] = ls[2 + qs2][acc_key(i2, g)];
       uint4 co[2][NDT], cq[2][NDT];  // column operands of the dV / dK products (kBatch)
       if constexpr (kBatch) {
         // one wave per SIMD: no other wave covers the LDS latency, so the
@@ -372,7 +381,7 @@ void bwd_dkdv_kernel(const BwdParams p) {
             }
             const float pr = fast_exp2(x);
             pr2[u] = pr;
-            ds2[u] = pr * (dp[i2] - ls[2 + qs2][ql]);
+            ds2[u] = pr * -dp[i2];
           }
           pw[e] = Elem<T>::pack2(pr2[0], pr2[1]);
           dw[e] = Elem<T>::pack2(ds2[0], ds2[1]);
