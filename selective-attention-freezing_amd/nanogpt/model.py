@@ -305,6 +305,10 @@ class CausalSelfAttention(nn.Module):
         return self._wc_qkv, self._wc_qkvb
 
     def forward(self, x, rope=None):
+        return self.c_proj(self.attend(x, rope))
+
+    def attend(self, x, rope=None):
+        """The block's attention before the output projection: (B, T, C) head outputs."""
         global _FUSED_DISPATCH_COUNT
         if self._fz_dirty:
             self._refresh_freeze_cache()
@@ -351,8 +355,7 @@ class CausalSelfAttention(nn.Module):
                              rho=self.dyn_rho if dec else None,
                              z=self.dyn_z if dec else None,
                              validate=False, closed_form=self._closed)
-        y = y.transpose(1, 2).reshape(B, T, nh * hd)
-        return self.c_proj(y)
+        return y.transpose(1, 2).reshape(B, T, nh * hd)
 
 
 class MLP(nn.Module):
@@ -437,15 +440,28 @@ class GPT(nn.Module):
             # prefill: each residual add of Block.forward runs fused with the
             # LayerNorm after it (ln_2, then the next block's ln_1 or ln_f);
             # x is the embedding output, updated in place
+            # without projection biases the residual add runs inside the
+            # projection GEMM (x += y W^T, one rounding) and the LayerNorm
+            # after it reads x alone
             x = x.contiguous()
+            x2 = x.view(-1, x.size(-1))
             ln = blocks[0].ln_1
             h = _kernel_mod.add_layernorm_(x, None, ln.weight, ln.bias)
             for i, block in enumerate(blocks):
-                a = block.attn(h, rope=rope)
-                h = _kernel_mod.add_layernorm_(x, a, block.ln_2.weight, block.ln_2.bias)
-                m = block.mlp(h)
+                attn, mlp = block.attn, block.mlp
+                if attn.c_proj.bias is None:
+                    y = attn.attend(h, rope=rope)
+                    x2.addmm_(y.reshape(x2.size(0), -1), attn.c_proj.weight.t())
+                    h = _kernel_mod.add_layernorm_(x, None, block.ln_2.weight, block.ln_2.bias)
+                else:
+                    h = _kernel_mod.add_layernorm_(x, attn(h, rope=rope), block.ln_2.weight, block.ln_2.bias)
                 ln = blocks[i + 1].ln_1 if i + 1 < len(blocks) else self.transformer.ln_f
-                h = _kernel_mod.add_layernorm_(x, m, ln.weight, ln.bias)
+                if mlp.c_proj.bias is None:
+                    u = mlp.gelu(mlp.c_fc(h))
+                    x2.addmm_(u.reshape(x2.size(0), -1), mlp.c_proj.weight.t())
+                    h = _kernel_mod.add_layernorm_(x, None, ln.weight, ln.bias)
+                else:
+                    h = _kernel_mod.add_layernorm_(x, mlp(h), ln.weight, ln.bias)
             return h
         for block in blocks:
             x = block(x, rope=rope)
