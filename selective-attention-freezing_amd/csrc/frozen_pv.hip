@@ -79,6 +79,7 @@ __device__ __forceinline__ void decomp_body(const FrozenParams& p) {
   // shifts) keeps every 16-lane group of one E^T read on distinct banks
   constexpr int RWL = RW + 16;
   constexpr int ERN = (RW + NTHR - 1) / NTHR;
+  static_assert(RW % 2 == 0 && RW / 2 <= NTHR, "one thread per pair of factored-window elements");
   constexpr bool kFactorable = std::is_same<T, __bf16>::value && HD <= 128;
   // LDS: the factored form's three V' tiles (vs0..vs2) and two distance
   // windows of hi and lo copies (eb0, eb1), or the rebuild form's two V^T
@@ -221,13 +222,18 @@ __device__ __forceinline__ void decomp_body(const FrozenParams& p) {
       // The fp32 rho log2 e values (r2) are loaded (branch-free, clamped index)
       // one block ahead, their exps written after the block's MFMAs into the
       // other slot.
-      float er[ERN], ab = 0.f;
+      // Thread t < RW / 2 owns window elements 2t and 2t + 1 and also computes
+      // 2t + 2, so that every copy is written in aligned 32-bit words: an even
+      // copy c stores (2t, 2t + 1) at its position 2t - c, an odd one
+      // (2t + 1, 2t + 2) at 2t + 1 - c (16-bit stores put two lanes on one
+      // bank word).
+      float er[3], ab = 0.f;
       int ej0 = 0;
       const float* const r2 = p.r2 + (int64_t)slot * T_len;
       auto load_er = [&](int jb) {  // unconditional: indices clamped past the end
         const int j0 = 64 * jb;
 #pragma unroll
-        for (int u = 0; u < ERN; ++u) er[u] = r2[min(max(q0 - j0 + BM - (tid + u * NTHR), 0), T_len - 1)];
+        for (int u = 0; u < 3; ++u) er[u] = r2[min(max(q0 - j0 + BM - (2 * tid + u), 0), T_len - 1)];
         ab = ablk[min(jb, nblk - 1)];
         ej0 = j0;
       };
@@ -237,21 +243,25 @@ __device__ __forceinline__ void decomp_body(const FrozenParams& p) {
       auto ecopy = [](int c) { return c * RWL + (c ? 8 : 0); };
       auto store_er = [&](auto slot) {
         uint16_t(*const ew)[8 * RWL] = e_slot(slot);
+        if (tid < RW / 2) {
+          uint32_t hv[3], lv[3];  // hi and lo bits of window elements 2t, 2t + 1, 2t + 2
 #pragma unroll
-        for (int u = 0; u < ERN; ++u) {
-          const int m = tid + u * NTHR;
-          const int d = q0 - ej0 + BM - m;
-          if (m < RW) {
+          for (int u = 0; u < 3; ++u) {
+            const int m = 2 * tid + u;
+            const int d = q0 - ej0 + BM - m;
             // A_k - A - R; -inf for a block whose keys all have alpha -inf
-            const float x = d >= 0 && d < T_len ? fast_exp2(er[u] + (ab - aoff - roff)) : 0.f;
-            const uint32_t hl = Elem<T>::pack2(x, 0.f) & 0xffffu;
-            const uint32_t lo = Elem<T>::pack2(x - Elem<T>::lo(hl), 0.f) & 0xffffu;
+            const float x = m < RW && d >= 0 && d < T_len ? fast_exp2(er[u] + (ab - aoff - roff)) : 0.f;
+            hv[u] = Elem<T>::pack2(x, 0.f) & 0xffffu;
+            lv[u] = Elem<T>::pack2(x - Elem<T>::lo(hv[u]), 0.f) & 0xffffu;
+          }
 #pragma unroll
-            for (int c = 0; c < 8; ++c)
-              if (m >= c) {
-                ew[0][ecopy(c) + m - c] = (uint16_t)hl;
-                ew[1][ecopy(c) + m - c] = (uint16_t)lo;
-              }
+          for (int c = 0; c < 8; ++c) {
+            const int e0 = c & 1;             // the word's first element: 2t + e0
+            const int pos = 2 * tid + e0 - c;  // even: its position in copy c
+            if (pos >= 0) {
+              *reinterpret_cast<uint32_t*>(&ew[0][ecopy(c) + pos]) = hv[e0] | (hv[e0 + 1] << 16);
+              *reinterpret_cast<uint32_t*>(&ew[1][ecopy(c) + pos]) = lv[e0] | (lv[e0 + 1] << 16);
+            }
           }
         }
       };
