@@ -204,6 +204,21 @@ struct FlashState {
     rebase(s, bs);
   }
 
+  // Before any accumulation: the reference maximum from the item's first
+  // sub-block of raw (masked) scores, so its softmax stays on the common path
+  // (from kMinit every item's first step took the recompute).  O and l are
+  // still zero; a row with no finite score keeps kMinit.
+  __device__ __forceinline__ void seed_max(const f32x16_t (&s)[QT]) {
+#pragma unroll
+    for (int qt = 0; qt < QT; ++qt) {
+      float mx = s[qt][0];
+#pragma unroll
+      for (int i = 1; i < 16; ++i) mx = fmaxf(mx, s[qt][i]);
+      mx = half_swap_max(mx);
+      m_run[qt] = fmaxf(m_run[qt], mx * c);
+    }
+  }
+
   // The recompute from raw (masked) scores s: move the reference to
   // max(m, block max), rescale O and l, and recompute P.
   __device__ __forceinline__ void rebase(f32x16_t (&s)[QT], float (&bs)[QT]) {
@@ -383,6 +398,8 @@ __device__ __forceinline__ void flash_unit(Params& p, const int unit, char* k0, 
 #pragma unroll
   for (int qt = 0; qt < QT; ++qt) sB[qt] = zero16();
   st.scores(sA, k0, 0);
+  if (kb0 >= jd) st.mask(sA, 64 * kb0);  // as the first step will
+  st.seed_max(sA);
   if constexpr (St::kTwoSlot) {
     // hd 256: four 32 KB tiles fit the LDS, not six.  Block j (phase R =
     // (j - kb0) & 1): K_j in k_R, K_{j+1} in k_{1-R}, V_j in v_R, V_{j-1} in
