@@ -34,12 +34,26 @@ __device__ __forceinline__ uint4 tile_row_op(const char* tile, int r, int c) {
 }
 
 // Transposed operand of a VRow tile: lane (n, g) receives rows
-// 16 ks + 8 g + 0..7 of column 32 dt + n.
+// 16 ks + 8 g + 0..7 of column 32 dt + n.  The lane's read offsets are
+// computed once (ColOffsets): computed next to each read, their XOR-swizzled
+// column was unbounded to the compiler, which then let a read reach the
+// neighbouring LDS slots and waited for the DMA in flight into them.
+template <int HD> struct ColOffsets {
+  int lo[HD / 32], hi[HD / 32];
+  __device__ __forceinline__ void init(int lane) {
+#pragma unroll
+    for (int dt = 0; dt < HD / 32; ++dt) {
+      lo[dt] = vt_read_offset<HD>(lane, dt, 0);
+      hi[dt] = vt_read_offset<HD>(lane, dt, 1);
+    }
+  }
+};
+
 template <int HD>
-__device__ __forceinline__ uint4 tile_col_op(const char* tile, int ks, int dt, int lane) {
+__device__ __forceinline__ uint4 tile_col_op(const char* tile, int ks, int dt, const ColOffsets<HD>& cof) {
   const char* base = tile + 16 * ks * VRow<HD>::PITCH;
-  const uint2 lo = ds_read_tr16(base + vt_read_offset<HD>(lane, dt, 0));
-  const uint2 hi = ds_read_tr16(base + vt_read_offset<HD>(lane, dt, 1));
+  const uint2 lo = ds_read_tr16(base + cof.lo[dt]);
+  const uint2 hi = ds_read_tr16(base + cof.hi[dt]);
   return make_uint4(lo.x, lo.y, hi.x, hi.y);
 }
 
@@ -145,6 +159,8 @@ __global__ __launch_bounds__(256) void bwd_dq_kernel(const BwdParams p) {
   for (int dt = 0; dt < NDT; ++dt) dqa[dt] = zero16();
 
   TileOffsets<T, HD> ko, vo;
+  ColOffsets<HD> cof;
+  cof.init(lane);
   ko.init(wave, lane, p.k_st);
   vo.init(wave, lane, p.v_st);
   const int nkb = (min(qb * BM + BM, T_len) + 63) / 64;
@@ -205,7 +221,7 @@ __global__ __launch_bounds__(256) void bwd_dq_kernel(const BwdParams p) {
           const uint4 bop = make_uint4(w[4 * s2], w[4 * s2 + 1], w[4 * s2 + 2], w[4 * s2 + 3]);
 #pragma unroll
           for (int dt = 0; dt < NDT; ++dt)
-            dqa[dt] = Elem<T>::mfma(tile_col_op<HD>(kt, 2 * ks + s2, dt, lane), bop, dqa[dt]);
+            dqa[dt] = Elem<T>::mfma(tile_col_op<HD>(kt, 2 * ks + s2, dt, cof), bop, dqa[dt]);
         }
       }
     }
@@ -286,6 +302,8 @@ void bwd_dkdv_kernel(const BwdParams p) {
   }
 
   TileOffsets<T, HD> qo, oo;
+  ColOffsets<HD> cof;
+  cof.init(lane);
   qo.init(wave, lane, p.q_st);
   oo.init(wave, lane, p.do_st);
   const int ib0 = (kb * BN) / 64, nqb = (T_len + 63) / 64;
@@ -351,8 +369,8 @@ void bwd_dkdv_kernel(const BwdParams p) {
         for (int s2 = 0; s2 < 2; ++s2)
 #pragma unroll
           for (int dt = 0; dt < NDT; ++dt) {
-            co[s2][dt] = tile_col_op<HD>(ot, 2 * qs2 + s2, dt, lane);
-            cq[s2][dt] = tile_col_op<HD>(qt, 2 * qs2 + s2, dt, lane);
+            co[s2][dt] = tile_col_op<HD>(ot, 2 * qs2 + s2, dt, cof);
+            cq[s2][dt] = tile_col_op<HD>(qt, 2 * qs2 + s2, dt, cof);
           }
         __builtin_amdgcn_sched_barrier(0);
       } else {
@@ -397,8 +415,8 @@ void bwd_dkdv_kernel(const BwdParams p) {
         const uint4 bd = make_uint4(dw[4 * s2], dw[4 * s2 + 1], dw[4 * s2 + 2], dw[4 * s2 + 3]);
 #pragma unroll
         for (int dt = 0; dt < NDT; ++dt) {
-          dva[dt] = Elem<T>::mfma(kBatch ? co[s2][dt] : tile_col_op<HD>(ot, 2 * qs2 + s2, dt, lane), bp, dva[dt]);
-          dka[dt] = Elem<T>::mfma(kBatch ? cq[s2][dt] : tile_col_op<HD>(qt, 2 * qs2 + s2, dt, lane), bd, dka[dt]);
+          dva[dt] = Elem<T>::mfma(kBatch ? co[s2][dt] : tile_col_op<HD>(ot, 2 * qs2 + s2, dt, cof), bp, dva[dt]);
+          dka[dt] = Elem<T>::mfma(kBatch ? cq[s2][dt] : tile_col_op<HD>(qt, 2 * qs2 + s2, dt, cof), bd, dka[dt]);
         }
       }
     }
@@ -432,18 +450,26 @@ void bwd_dkdv_kernel(const BwdParams p) {
 
 // dV of the frozen heads: dV[j] = sum_{i >= j} P[i, j] dO[i].  Workgroup =
 // 4 waves x 32 keys of one (batch, frozen slot); query blocks of 64 from the
-// diagonal (dO tiles double-buffered in LDS).  The B operand of
-// dV^T += dO^T P is a column of P for 8 consecutive queries: gathered from
-// the dense pattern (rounded to the activation dtype) or rebuilt as
-// P[i, j] = 2^((alpha_j + rho_{i-j} - z_i) log2 e) for decomposed heads
-// (closed-form heads included); cells with i < j or i >= T are zero.
+// diagonal.  The B operand of dV^T += dO^T P is a column of P for 8
+// consecutive queries: gathered from the dense pattern (rounded to the
+// activation dtype) or rebuilt as P[i, j] = 2^((alpha_j + rho_{i-j} - z_i)
+// log2 e) for decomposed heads (closed-form heads included); cells with
+// i < j or i >= T are zero.
+//
+// dO tiles arrive by DMA two blocks ahead in three static LDS slots (an
+// empty descriptor past the last block, so every block issues the same
+// loads); a decomposed block's z and rho window is loaded into registers one
+// block ahead, before that DMA, and written into the next block's slot.  The
+// block ends with a counted wait (the DMA two ahead stays in flight) and a
+// bare barrier: one barrier per block instead of two draining ones.
 template <typename T, int HD, int KIND>
 __global__ __launch_bounds__(256) void bwd_frozen_dv_kernel(const BwdParams p) {
   constexpr int BN = kBwdWaves * 32, NDT = HD / 32, VB = VRow<HD>::BYTES;
-  __shared__ __align__(16) char o0[VB], o1[VB];
+  constexpr int VN = TileOffsets<T, HD>::VN;  // DMA loads per wave per dO tile
+  __shared__ __align__(16) char o0[VB], o1[VB], o2[VB];
   // decomposed heads: z_q log2 e of the block's 64 queries and rho_d log2 e
   // for every distance d = q - key the block meets (64 + 128 - 1 values)
-  __shared__ float zs2[2][64], rs2[2][64 + BN];
+  __shared__ float zs3[3][64], rs3[3][64 + BN];
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int n = lane & 31, g = lane >> 5;
@@ -467,9 +493,9 @@ __global__ __launch_bounds__(256) void bwd_frozen_dv_kernel(const BwdParams p) {
 
   TileOffsets<T, HD> oo;
   oo.init(wave, lane, p.do_st);
+  ColOffsets<HD> cof;
+  cof.init(lane);
   const int ib0 = (kb * BN) / 64, nqb = (T_len + 63) / 64;
-  // z (per query) and the rho window of query block i, pre-scaled by log2 e;
-  // the next block's are loaded into registers while this one is computed
   auto z_of = [&](int qq) {
     return qq < T_len ? load_as_f32(p.z, (int64_t)ph * p.z_sh + (int64_t)qq * p.z_ss, p.z_dtype) * kLog2e : 0.f;
   };
@@ -478,27 +504,46 @@ __global__ __launch_bounds__(256) void bwd_frozen_dv_kernel(const BwdParams p) {
                ? load_as_f32(p.rho, (int64_t)ph * p.r_sh + (int64_t)dd * p.r_ss, p.r_dtype) * kLog2e
                : 0.f;
   };
-  if (ib0 < nqb) {
-    oo.load(dobase, p.do_st, 64 * ib0, T_len, o0, wave);
+  // the next block's values as raw bits: converted where they are written,
+  // so the wait for them falls there too
+  // Every thread loads (from a clamped index) so that every wave issues the
+  // same loads and the counted waits hold; values out of range are dropped.
+  auto z_bits = [&](int qq) {
+    const uint32_t w = load_bits(p.z, (int64_t)ph * p.z_sh + (int64_t)min(max(qq, 0), T_len - 1) * p.z_ss, p.z_dtype);
+    return qq < T_len ? w : 0u;
+  };
+  auto rho_bits = [&](int dd) {
+    const uint32_t w = load_bits(p.rho, (int64_t)ph * p.r_sh + (int64_t)min(max(dd, 0), T_len - 1) * p.r_ss, p.r_dtype);
+    return (dd >= 0 && dd < T_len) ? w : 0u;
+  };
+  auto dmin_of = [&](int i) { return 64 * i - kb * BN - (BN - 1); };  // smallest q - key of block i
+  auto load_do = [&](int i, auto slotc) {
+    constexpr int S = decltype(slotc)::value;
+    oo.load(dobase, p.do_st, 64 * i, i < nqb ? T_len : 0, S == 0 ? o0 : (S == 1 ? o1 : o2), wave);
+  };
+  auto meet = [&]() {  // the next block's dO tile has landed (the one after stays in flight)
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_waitcnt(waitcnt_vm_lgkm0(VN));
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+  };
+
+  auto block = [&](const int i, auto phase) {
+    constexpr int R = decltype(phase)::value;
+    const char* const ot = R == 0 ? o0 : (R == 1 ? o1 : o2);
+    const float* const zs = zs3[R];
+    const float* const rs = rs3[R];
+    const int dmin = dmin_of(i);
+    // the next block's z / rho, then the dO tile two blocks ahead: waiting
+    // for the register loads leaves that DMA in flight
+    uint32_t nz = 0u, nr = 0u;
     if (KIND == 2) {
-      if (tid < 64) zs2[0][tid] = z_of(64 * ib0 + tid);
-      if (tid < 64 + BN - 1) rs2[0][tid] = rho_of(64 * ib0 - kb * BN - (BN - 1) + tid);
+      nz = z_bits(64 * (i + 1) + min(tid, 63));
+      nr = rho_bits(dmin + 64 + min(tid, 64 + BN - 2));
     }
-  }
-  for (int i = ib0; i < nqb; ++i) {
-    const char* ot = ((i - ib0) & 1) ? o1 : o0;
-    const int dmin = 64 * i - kb * BN - (BN - 1);  // smallest q - key of the block
-    const float* zs = zs2[(i - ib0) & 1];
-    const float* rs = rs2[(i - ib0) & 1];
-    __syncthreads();  // this block's dO tile (and z / rho window) is in LDS
-    float nz = 0.f, nr = 0.f;
-    if (i + 1 < nqb) {
-      oo.load(dobase, p.do_st, 64 * (i + 1), T_len, ((i - ib0) & 1) ? o0 : o1, wave);
-      if (KIND == 2) {
-        if (tid < 64) nz = z_of(64 * (i + 1) + tid);
-        if (tid < 64 + BN - 1) nr = rho_of(dmin + 64 + tid);
-      }
-    }
+    asm volatile("" ::: "memory");
+    load_do(i + 2, std::integral_constant<int, (R + 2) % 3>());
+    asm volatile("" ::: "memory");
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks) {
       const int q0 = 64 * i + 16 * ks;
@@ -534,14 +579,39 @@ __global__ __launch_bounds__(256) void bwd_frozen_dv_kernel(const BwdParams p) {
       const uint4 bop = make_uint4(Elem<T>::pack2(e8[0], e8[1]), Elem<T>::pack2(e8[2], e8[3]),
                                    Elem<T>::pack2(e8[4], e8[5]), Elem<T>::pack2(e8[6], e8[7]));
 #pragma unroll
-      for (int dt = 0; dt < NDT; ++dt) dva[dt] = Elem<T>::mfma(tile_col_op<HD>(ot, ks, dt, lane), bop, dva[dt]);
+      for (int dt = 0; dt < NDT; ++dt) dva[dt] = Elem<T>::mfma(tile_col_op<HD>(ot, ks, dt, cof), bop, dva[dt]);
     }
-    if (KIND == 2) {  // the idle slot's readers finished before the previous barrier
-      const int nx = ((i - ib0) & 1) ^ 1;
-      if (tid < 64) zs2[nx][tid] = nz;
-      if (tid < 64 + BN - 1) rs2[nx][tid] = nr;
+    if (KIND == 2) {  // the next block's slot was last read two blocks ago
+      constexpr int RN = (R + 1) % 3;
+      if (tid < 64) zs3[RN][tid] = bits_to_f32(nz, p.z_dtype) * kLog2e;
+      if (tid < 64 + BN - 1) rs3[RN][tid] = bits_to_f32(nr, p.r_dtype) * kLog2e;
     }
-    __syncthreads();  // every wave is done with this slot before it is refilled
+    meet();
+  };
+
+  if (ib0 < nqb) {
+    if (KIND == 2) {
+      if (tid < 64) zs3[0][tid] = z_of(64 * ib0 + tid);
+      if (tid < 64 + BN - 1) rs3[0][tid] = rho_of(dmin_of(ib0) + tid);
+    }
+    asm volatile("" ::: "memory");
+    load_do(ib0, std::integral_constant<int, 0>());
+    load_do(ib0 + 1, std::integral_constant<int, 1>());
+    meet();
+    using P0 = std::integral_constant<int, 0>;
+    using P1 = std::integral_constant<int, 1>;
+    using P2 = std::integral_constant<int, 2>;
+    for (int i = ib0;;) {
+      if (i >= nqb) break;
+      block(i++, P0());
+      if (i >= nqb) break;
+      block(i++, P1());
+      if (i >= nqb) break;
+      block(i++, P2());
+    }
+    // the last (empty) DMAs land before the workgroup's LDS is released
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
   }
   if (kv) store_out_tile<T, HD>(dvbase + (int64_t)kk * p.dv_st, dva, 1.f, g);
 }

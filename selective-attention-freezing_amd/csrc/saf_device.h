@@ -103,6 +103,18 @@ __device__ inline float load_as_f32(const void* p, int64_t idx, int dtype) {
   return (float)__builtin_bit_cast(_Float16, bits);
 }
 
+// load_as_f32 in two halves, so that a caller can place the wait for the
+// load at the value's use: the element's raw bits (fp32, or a 16-bit element
+// zero-extended), then their value as fp32.
+__device__ inline uint32_t load_bits(const void* p, int64_t idx, int dtype) {
+  return dtype == 0 ? reinterpret_cast<const uint32_t*>(p)[idx] : (uint32_t)reinterpret_cast<const uint16_t*>(p)[idx];
+}
+__device__ inline float bits_to_f32(uint32_t bits, int dtype) {
+  if (dtype == 0) return __uint_as_float(bits);
+  if (dtype == 2) return __uint_as_float(bits << 16);
+  return (float)__builtin_bit_cast(_Float16, (uint16_t)bits);
+}
+
 __device__ inline f32x16_t zero16() {
   f32x16_t z;
 #pragma unroll
