@@ -106,3 +106,21 @@ def test_cpu_tensors_fail_loudly():
         kernel.fused_mixed_attn(q, q, q, None, torch.zeros(1, dtype=torch.int32))
     with pytest.raises(RuntimeError, match="HIP devices only"):
         kernel.frozen_pv(torch.zeros(1, 4, 4), q, torch.zeros(1, dtype=torch.int32), 4)
+
+
+def test_host_table_cached_per_tensor_and_version():
+    """The routing tables are planned on the host: the copy is made once per
+    tensor and refreshed only when the tensor changes in place, so callers
+    that keep their tables (as the reference's models keep buffers) pay no
+    device-to-host copy per call."""
+    from kernel import fused_attn as F
+    t = torch.tensor([0, 2, 1, 0], dtype=torch.int32)
+    a = F._host_table(t)
+    assert a.tolist() == [0, 2, 1, 0]
+    assert F._host_table(t) is a                      # cached on the tensor
+    t[1] = 1                                          # in-place change: version moves
+    b = F._host_table(t)
+    assert b.tolist() == [0, 1, 1, 0]
+    assert F._host_table(t.clone()) is not b          # another tensor: its own copy
+    assert F._host_table(None) is None
+    assert F._host_table([1, 2]).tolist() == [1, 2]
