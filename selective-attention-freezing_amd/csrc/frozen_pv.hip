@@ -917,6 +917,12 @@ static void launch_dense_t(const FrozenParams& p, hipStream_t s) {
 
 template <typename T, typename PT, int HD>
 static void launch_dense_nb(const FrozenParams& p, hipStream_t s) {
+  if constexpr (HD <= 64) {
+    if (dense_batch_group(p.B, HD) == 4) {
+      launch_dense_t<T, PT, HD, 4>(p, s);
+      return;
+    }
+  }
   if constexpr (HD <= 128) {
     if (dense_batch_group(p.B, HD) == 2) {
       launch_dense_t<T, PT, HD, 2>(p, s);

@@ -276,13 +276,15 @@ hipError_t launch_f32_bwd(const BwdParams& p, int hd, int which, hipStream_t s);
 inline int block_rows(int qt) { return 4 * 32 * qt; }
 
 // Dense P.V shape: a workgroup of kDenseWaves waves (two per SIMD, one
-// query tile of 32 rows each) serves a group of NB batch elements (2 when
-// the batch is even and hd <= 128, else 1: the accumulators of two hd-256
-// sequences would not fit two waves per SIMD) that share every pattern
-// operand; one workgroup per CU (its three V slots fill most of the LDS at
+// query tile of 32 rows each) serves a group of NB batch elements that share
+// every pattern operand, as many as 128 accumulator registers per wave
+// allow: 4 at hd <= 64 (batch a multiple of 4), 2 at hd <= 128 (even batch),
+// else 1; one workgroup per CU (its three V slots fill most of the LDS at
 // hd 128).
 constexpr int kDenseWaves = 8;
-constexpr int dense_batch_group(int B, int hd) { return B % 2 == 0 && hd <= 128 ? 2 : 1; }
+constexpr int dense_batch_group(int B, int hd) {
+  return B % 4 == 0 && hd <= 64 ? 4 : (B % 2 == 0 && hd <= 128 ? 2 : 1);
+}
 constexpr int dense_qtiles(int, int) { return 1; }
 constexpr int dense_block_rows(int, int) { return kDenseWaves * 32; }
 constexpr int kDenseResident = 1;

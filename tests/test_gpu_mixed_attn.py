@@ -267,7 +267,8 @@ def test_dense_causal_split(T, hd, pdtype):
 
 @pytest.mark.parametrize("B,T,hd,dtype", [(1, 8, 64, torch.bfloat16), (2, 72, 32, torch.bfloat16),
                                           (3, 1000, 128, torch.bfloat16), (2, 1544, 64, torch.float16),
-                                          (4, 520, 96, torch.bfloat16), (1, 2048, 128, torch.float16)])
+                                          (4, 520, 96, torch.bfloat16), (1, 2048, 128, torch.float16),
+                                          (4, 777, 32, torch.bfloat16), (8, 600, 64, torch.float16)])
 def test_dense_pattern_in_activation_dtype(B, T, hd, dtype):
     """Dense patterns stored in the activation dtype with 16-byte rows (the
     kernel's unconditional buffer-load path) and S = T, so the last rows'
