@@ -10,14 +10,15 @@
 //     buffers, as in /root/reference/kernel/fused_attn.py:145-180; cells with
 //     j > i are exactly zero.
 //
-// The P.V half is the same as the live-head kernel: one workgroup = 4 waves
-// x 32*QT query rows; V^T tiles double-buffered in LDS; P^T lives in the
-// B-operand lane layout (lane (n, g) owns query n and keys 8g + 0..7 of each
-// 16-key step).  Dense: each lane reads its P^T operands directly from the
-// pattern rows (16 bytes per operand, rounded to the input dtype once unless
-// already in it), 64 rows per wave, causally balanced work items; workgroups
-// that share P (the batch siblings) are placed on the same XCD so the second
-// one reads it from that XCD's L2.  Decomposed: P^T is rebuilt in registers.
+// The P.V half is the live-head kernel's: O^T += V^T P^T on MFMA, V^T
+// operands from VRow tiles in LDS (transposing reads), P^T in the B-operand
+// lane layout (lane (n, g) owns query n and keys 8g + 0..7 of each 16-key
+// step).  Dense (frozen_dense_kernel): 8 waves x 32 rows, each lane reading
+// its P^T operands straight from the pattern rows (16 bytes per operand,
+// rounded to the input dtype once unless already in it) for the 2 or 4 batch
+// elements that share them, causally balanced work items.  Decomposed
+// (frozen_decomp_kernel): 4 waves x 32 QT rows, P^T from a Toeplitz window in
+// LDS (factored form) or rebuilt in registers.
 #include <type_traits>
 
 #include "saf_kernels.h"
