@@ -86,28 +86,35 @@ __device__ __forceinline__ uint4 neg_halves(uint4 w) {
 }  // namespace
 
 // delta[b, slot, i] = sum_d out[b, h, i, d] * dout[b, h, i, d] over the live
-// rows (one thread per row, fp32).
+// rows, fp32.  A row is read by delta_lanes(HD) lanes, 16 bytes each, so one
+// load instruction covers whole rows (one lane per row touched 64 rows per
+// instruction), and the lanes' sums meet by shuffles.
+constexpr int delta_lanes(int hd) { return hd <= 32 ? 4 : (hd <= 64 ? 8 : (hd <= 128 ? 16 : 32)); }
+
 template <typename T, int HD>
 __global__ __launch_bounds__(256) void bwd_delta_kernel(const BwdParams p) {
-  const int64_t row = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  constexpr int NC = HD / 8, LANES = delta_lanes(HD);
+  const int c = (int)(threadIdx.x & (LANES - 1));
+  const int64_t row = (int64_t)blockIdx.x * (256 / LANES) + threadIdx.x / LANES;
   const int64_t n_rows = (int64_t)p.B * p.n_live * p.T;
-  if (row >= n_rows) return;
-  const int i = (int)(row % p.T);
-  const int bs = (int)(row / p.T);
-  const int b = bs / p.n_live, slot = bs % p.n_live;
-  const int h = p.out_head[slot];
-  const T* o = reinterpret_cast<const T*>(p.out) + b * p.o_sb + (int64_t)h * p.o_sh + (int64_t)i * p.o_st;
-  const T* d = reinterpret_cast<const T*>(p.dout) + b * p.do_sb + (int64_t)h * p.do_sh + (int64_t)i * p.do_st;
   float acc = 0.f;
-#pragma unroll
-  for (int c = 0; c < HD / 8; ++c) {
+  if (row < n_rows && c < NC) {
+    const int i = (int)(row % p.T);
+    const int bs = (int)(row / p.T);
+    const int b = bs / p.n_live, slot = bs % p.n_live;
+    const int h = p.out_head[slot];
+    const T* o = reinterpret_cast<const T*>(p.out) + b * p.o_sb + (int64_t)h * p.o_sh + (int64_t)i * p.o_st;
+    const T* d = reinterpret_cast<const T*>(p.dout) + b * p.do_sb + (int64_t)h * p.do_sh + (int64_t)i * p.do_st;
     const uint4 a = load16(o + 8 * c), e = load16(d + 8 * c);
     const uint32_t wa[4] = {a.x, a.y, a.z, a.w}, we[4] = {e.x, e.y, e.z, e.w};
 #pragma unroll
     for (int m = 0; m < 4; ++m)
       acc += Elem<T>::lo(wa[m]) * Elem<T>::lo(we[m]) + Elem<T>::hi(wa[m]) * Elem<T>::hi(we[m]);
   }
-  p.delta[row] = acc;
+  // the lanes of a row are an aligned group of the wave (all in or all out of range)
+#pragma unroll
+  for (int m = LANES / 2; m >= 1; m >>= 1) acc += __shfl_xor(acc, m, LANES);
+  if (row < n_rows && c == 0) p.delta[row] = acc;
 }
 
 // dQ of the live heads.  Workgroup = 4 waves x 32 queries of one (batch,
@@ -770,7 +777,8 @@ static hipError_t bwd_launch_hd(const BwdParams& p, int which, hipStream_t s) {
   switch (which) {
     case 0: {
       const int64_t rows = (int64_t)p.B * p.n_live * T_len;
-      hipLaunchKernelGGL((bwd_delta_kernel<T, HD>), dim3((unsigned)((rows + 255) / 256)), dim3(256), 0, s, p);
+      const int64_t per_wg = 256 / delta_lanes(HD);
+      hipLaunchKernelGGL((bwd_delta_kernel<T, HD>), dim3((unsigned)((rows + per_wg - 1) / per_wg)), dim3(256), 0, s, p);
       break;
     }
     case 1:
