@@ -208,7 +208,13 @@ class CausalSelfAttention(nn.Module):
             old = self.dyn_pattern
             n_old = 0 if old is None else old.size(0)
             S = self.block_size
-            new = torch.zeros(n_old + len(need), S, S, device=dev, dtype=self._pattern_dtype)
+            # Rows S elements apart at a multiple of 4 KB all start on the same
+            # HBM channels, and the dense P.V kernel reads one 32-byte piece
+            # of each of many rows at once: 256 bytes of padding per row
+            # spread those reads.  The buffer stays an (n, S, S) view.
+            elem = torch.empty((), dtype=self._pattern_dtype).element_size()
+            pad = 256 // elem if (S * elem) % 4096 == 0 else 0
+            new = torch.zeros(n_old + len(need), S, S + pad, device=dev, dtype=self._pattern_dtype)[:, :, :S]
             if old is not None:
                 new[:n_old] = old
             for i, h in enumerate(need):

@@ -148,6 +148,49 @@ def test_fp32_pattern_buffers_survive_bf16_cast():
     assert m.rotary.cos_f32.dtype == torch.float32
 
 
+def test_dense_pattern_rows_padded_off_4k_pitch():
+    """A pattern row pitch at a multiple of 4 KB gets 256 bytes of padding per
+    row; the buffer is still an (n, S, S) view holding freeze_heads' values
+    (nanogpt/model.py freeze_heads normalisation) with zeros past T."""
+    from nanogpt.model import GPT, GPTConfig
+    for S, pad in ((1024, 64), (1088, 0)):  # fp32 rows: 4096 bytes -> padded; 4352 bytes -> as is
+        cfg = GPTConfig(block_size=S, vocab_size=1000, n_layer=1, n_head=4, n_embd=256, bias=False)
+        a = GPT(cfg).eval().transformer.h[0].attn
+        p = torch.rand(2, 900, 900, generator=torch.Generator().manual_seed(S))
+        a.freeze_heads([1, 3], p)
+        assert a.dyn_pattern.shape == (2, S, S) and a.dyn_pattern.stride(1) == S + pad
+        ref = p.tril()
+        ref = ref / ref.sum(-1, keepdim=True).clamp_min(1e-12)
+        for j, h in enumerate([1, 3]):
+            s = int(a.dyn_pattern_slot[h])
+            assert torch.equal(a.dyn_pattern[s, :900, :900], ref[j])
+            assert not a.dyn_pattern[s, 900:].any() and not a.dyn_pattern[s, :, 900:].any()
+
+
+@pytest.mark.gpu
+def test_gpu_padded_pattern_rows_give_identical_logits():
+    """bf16 patterns of 2048-row pitch (padded by freeze_heads) against the same
+    patterns made contiguous: the dense kernel's results are bit-identical."""
+    from nanogpt.model import GPT, GPTConfig
+    torch.manual_seed(0)
+    S = 2048
+    cfg = GPTConfig(block_size=S, vocab_size=1000, n_layer=2, n_head=4, n_embd=256, bias=False,
+                    freeze_pattern_dtype="bfloat16")
+    m = GPT(cfg).to("cuda", torch.bfloat16).eval()
+    g = torch.Generator().manual_seed(1)
+    for blk in m.transformer.h:
+        blk.attn.freeze_heads([0, 2], torch.rand(2, S, S, generator=g).cuda())
+    assert m.transformer.h[0].attn.dyn_pattern.stride(1) == S + 128
+    x = torch.randint(0, 1000, (2, S), generator=g).cuda()
+    with torch.inference_mode():
+        got = m.forward_all_positions(x).float().cpu()
+    for blk in m.transformer.h:
+        blk.attn.dyn_pattern = blk.attn.dyn_pattern.contiguous()
+    with torch.inference_mode():
+        ref = m.forward_all_positions(x).float().cpu()
+    assert torch.isfinite(got).all() and torch.equal(got, ref)
+
+
 def test_product_model_has_no_cpu_path():
     m, x = _small_model(T=64, layers=1)
     with pytest.raises(RuntimeError, match="HIP devices only"):
