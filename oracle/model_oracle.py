@@ -87,10 +87,11 @@ def attention(x, sd, p, fr, cos, sin, n_head, path):
     parts = []
     if uf:
         cols = torch.tensor([h * hd + d for h in uf for d in range(hd)])
-        q = F.linear(x, sd[p + "q_proj.weight"][cols]).view(B, T, len(uf), hd).transpose(1, 2)
-        k = F.linear(x, sd[p + "k_proj.weight"][cols]).view(B, T, len(uf), hd).transpose(1, 2)
-        if sd.get(p + "q_proj.bias") is not None:
-            raise NotImplementedError("bias=True projections are not restated")
+        # linear_rows2: the live heads' rows of Wq / Wk and of their biases
+        # (kernel/indexed_linear.py:131-135)
+        rows = lambda n: None if sd.get(p + n) is None else sd[p + n][cols]
+        q = F.linear(x, sd[p + "q_proj.weight"][cols], rows("q_proj.bias")).view(B, T, len(uf), hd).transpose(1, 2)
+        k = F.linear(x, sd[p + "k_proj.weight"][cols], rows("k_proj.bias")).view(B, T, len(uf), hd).transpose(1, 2)
         if cos is not None:
             q, k = apply_rope(q, k, cos, sin)
         parts.append(F.scaled_dot_product_attention(q, k, v[:, uf], is_causal=True).transpose(1, 2))

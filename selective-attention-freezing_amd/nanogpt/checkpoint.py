@@ -3,7 +3,7 @@ this build's GPT.
 
 Follows /root/reference/nanogpt/eval_nanogpt_logprobs.py:51-104
 (``build_config_from_ckpt``, ``load_model``) and the lazy-buffer handling of
-/root/reference/nanogpt/model.py:900-911, with three differences that follow
+/root/reference/nanogpt/model.py:900-911, with four differences that follow
 from this build:
 
 * the file is read with ``torch.load(weights_only=True)``: tensors, dicts,
@@ -16,7 +16,11 @@ from this build:
   so the loader moves each dense-frozen head's matrix, bit for bit, into its
   slot, in head order;
 * ``dyn_rho_band`` (the reference's (n_head, 64, S) derived band) is dropped:
-  the HIP kernels read rho directly.
+  the HIP kernels read rho directly;
+* the reference's Block names its attention ``main_block``
+  (/root/reference/nanogpt/model.py:1219), so its export keys are
+  ``transformer.h.{i}.main_block.*``; this build's Block calls the module
+  ``attn``, and the loader renames the keys.
 
 Only the architecture this build implements loads: standard softmax heads
 with dynamic per-head freezing (any fraction frozen, dense or decomposed
@@ -51,6 +55,9 @@ _REQUIRED = {
 }
 
 _PREFIX = "_orig_mod."
+# The reference's Block holds its attention as ``main_block``
+# (/root/reference/nanogpt/model.py:1219); this build's Block calls it ``attn``.
+_REF_ATTN, _ATTN = ".main_block.", ".attn."
 
 
 def build_config_from_ckpt(ckpt) -> GPTConfig:
@@ -101,11 +108,28 @@ def _layout_check(ckpt):
         raise NotImplementedError(f"attention layout {layout.get('mode')!r} (packed heads) is not supported")
 
 
+def _attn_key(name):
+    """This build's key for a reference state-dict key: the compile prefix
+    stripped and the block's ``main_block.`` renamed ``attn.``."""
+    if name.startswith(_PREFIX):
+        name = name[len(_PREFIX):]
+    if name.startswith("transformer.h.") and _REF_ATTN in name:
+        name = name.replace(_REF_ATTN, _ATTN, 1)
+    return name
+
+
 @torch.no_grad()
 def convert_state_dict(state_dict, model: GPT):
-    """Reference state dict -> this build's, in place on ``model``'s pattern
-    slots.  Returns the dict to pass to ``model.load_state_dict``."""
-    sd = {(k[len(_PREFIX):] if k.startswith(_PREFIX) else k): v for k, v in state_dict.items()}
+    """Reference state dict (keys ``transformer.h.{i}.main_block.*``, with or
+    without torch.compile's ``_orig_mod.``) -> this build's, in place on
+    ``model``'s pattern slots.  Returns the dict to pass to
+    ``model.load_state_dict(..., strict=True)``."""
+    sd = {}
+    for k, v in state_dict.items():
+        name = _attn_key(k)
+        if name.startswith("transformer.h.") and ".attn.dyn_pattern_slot" in name:
+            raise ValueError(f"{k}: not a reference export (this build's own pattern-slot table)")
+        sd[name] = v
     out = {}
     for name, v in sd.items():
         if name.endswith(".attn.dyn_rho_band") or name.endswith(".attn.bias"):
@@ -124,7 +148,9 @@ def convert_state_dict(state_dict, model: GPT):
                 for n in ("dyn_alpha", "dyn_rho", "dyn_z"):
                     out[pre + n] = torch.zeros(H, S)
             out[pre + "dyn_pattern_slot"] = torch.full((H,), -1, dtype=torch.int32)
+            a.dyn_pattern = None
             continue
+        # the dense representation registers no dyn_decomp (model.py:659-672)
         decomp = sd.get(pre + "dyn_decomp", torch.zeros(H, dtype=torch.bool))
         out[pre + "dyn_decomp"] = decomp
         if a.dyn_alpha is not None and pre + "dyn_alpha" not in sd:
@@ -136,11 +162,13 @@ def convert_state_dict(state_dict, model: GPT):
             full = sd.get(pre + "dyn_pattern")
             if full is None or full.dim() != 3 or full.size(0) != H:
                 raise ValueError(f"layer {i}: dense-frozen heads {dense} need a (n_head, S, S) dyn_pattern")
+            # padded slots on the model's device; load_state_dict copies the
+            # compact matrices into them, so the layout survives the load
+            a.dyn_pattern = a._alloc_patterns(len(dense), a._pattern_dtype, a.dyn_frozen.device)
             compact = torch.empty(len(dense), S, S, dtype=a._pattern_dtype)
             for s, h in enumerate(dense):
                 compact[s] = full[h]
                 slot[h] = s
-            a.dyn_pattern = compact.to(a.dyn_frozen.device)
             out[pre + "dyn_pattern"] = compact
         else:
             a.dyn_pattern = None
@@ -151,30 +179,53 @@ def convert_state_dict(state_dict, model: GPT):
 
 def reference_state_dict(model: GPT, compile_prefix: bool = False):
     """This build's GPT state in the reference's export layout, the inverse
-    of convert_state_dict: dense priors expanded to the (n_head, S, S)
-    ``dyn_pattern`` with zero rows for the other heads, the derived
-    (n_head, 64, S) ``dyn_rho_band`` added for decomposed models (rows
-    rho[r - u + S - 64], -inf outside [0, S): kernel/fused_attn.py:65-80),
-    no pattern slot table.  compile_prefix adds torch.compile's ``_orig_mod.``."""
+    of convert_state_dict.  Attention keys are ``transformer.h.{i}.main_block.*``
+    and each layer carries exactly the buffers the reference's dynamic
+    CausalSelfAttention saves (nanogpt/model.py:647-672, :735-764):
+      * ``dyn_frozen``;
+      * dense representation: ``dyn_pattern`` (n_head, S, S), always, with
+        zero rows for heads that are not dense-frozen;
+      * decomposed representation: ``dyn_decomp``, ``dyn_alpha``, ``dyn_rho``,
+        ``dyn_z``; the lazily created ``dyn_rho_band`` (n_head, 64, S) (rows
+        rho[r - u + S - 64], -inf outside [0, S): kernel/fused_attn.py:65-80)
+        when a decomposed head is frozen, and ``dyn_pattern`` when a dense one
+        is.
+    No pattern-slot table.  compile_prefix adds torch.compile's ``_orig_mod.``."""
     from kernel.fused_attn import make_rho_band
+    decomposed = model.config.rand_attn_prior_repr == "decomposed"
+    own = {"dyn_pattern", "dyn_pattern_slot", "dyn_decomp", "dyn_alpha", "dyn_rho", "dyn_z"}
     out = {}
     for k, v in model.state_dict().items():
-        if k.endswith(".attn.dyn_pattern") or k.endswith(".attn.dyn_pattern_slot"):
-            continue
+        if k.startswith("transformer.h.") and _ATTN in k:
+            if k.rsplit(".", 1)[1] in own:
+                continue
+            k = k.replace(_ATTN, _REF_ATTN, 1)
         out[k] = v.detach().cpu().clone()
     for i, blk in enumerate(model.transformer.h):
         a = blk.attn
-        pre = f"transformer.h.{i}.attn."
+        pre = f"transformer.h.{i}.main_block."
         H, S = a.n_head, a.block_size
-        if a.dyn_pattern is not None:
-            full = torch.zeros(H, S, S, dtype=a.dyn_pattern.dtype)
+        frozen = a.dyn_frozen.cpu()
+        dec = a.dyn_decomp.cpu() & frozen
+        if decomposed:
+            out[pre + "dyn_decomp"] = a.dyn_decomp.detach().cpu().clone()
+            for n in ("dyn_alpha", "dyn_rho", "dyn_z"):
+                out[pre + n] = getattr(a, n).detach().cpu().clone()
+            if bool(dec.any()):
+                # zero rows except the decomposed-frozen heads' (model.py:757-763)
+                band = torch.zeros(H, 64, S, dtype=a.dyn_rho.dtype)
+                idx = dec.nonzero(as_tuple=True)[0]
+                band[idx] = make_rho_band(a.dyn_rho.detach().cpu()[idx])
+                out[pre + "dyn_rho_band"] = band
+        dense = frozen & ~dec
+        if not decomposed or bool(dense.any()):
+            dtype = a._pattern_dtype if a.dyn_pattern is None else a.dyn_pattern.dtype
+            full = torch.zeros(H, S, S, dtype=dtype)
             for h in range(H):
                 slot = int(a.dyn_pattern_slot[h])
-                if slot >= 0:
+                if slot >= 0 and bool(dense[h]):
                     full[h] = a.dyn_pattern[slot].cpu()
             out[pre + "dyn_pattern"] = full
-        if a.dyn_alpha is not None:
-            out[pre + "dyn_rho_band"] = make_rho_band(a.dyn_rho.detach().float().cpu())
     if compile_prefix:
         out = {_PREFIX + k: v for k, v in out.items()}
     return out

@@ -183,8 +183,33 @@ class CausalSelfAttention(nn.Module):
                     new.data = old.to(device=new.device)
                 else:
                     self._buffers[n] = old.to(device=new.device)
+        # a move or cast returns the patterns contiguous: back into padded rows
+        if self.dyn_pattern is not None and self.dyn_pattern.stride() != self._pattern_strides(
+                self.dyn_pattern.size(0), self.dyn_pattern.dtype):
+            p = self.dyn_pattern
+            self.dyn_pattern = self._alloc_patterns(p.size(0), p.dtype, p.device)
+            self.dyn_pattern.copy_(p)
         self._fz_dirty = True
         return out
+
+    # -- compact dense pattern storage --------------------------------------
+    def _pattern_pad(self, dtype):
+        """Row padding (elements) of the compact patterns: rows S elements
+        apart at a multiple of 4 KB all start on the same HBM channels, and
+        the dense P.V kernel reads one 32-byte piece of each of many rows at
+        once, so such pitches get 256 bytes more."""
+        elem = torch.empty((), dtype=dtype).element_size()
+        return 256 // elem if (self.block_size * elem) % 4096 == 0 else 0
+
+    def _pattern_strides(self, n, dtype):
+        S = self.block_size
+        pitch = S + self._pattern_pad(dtype)
+        return (S * pitch, pitch, 1)
+
+    def _alloc_patterns(self, n, dtype, device):
+        """Zeroed (n, S, S) pattern slots: a view of (n, S, S + pad) storage."""
+        S = self.block_size
+        return torch.zeros(n, S, S + self._pattern_pad(dtype), device=device, dtype=dtype)[:, :, :S]
 
     # -- freeze installers (nanogpt/model.py:705-772) -----------------------
     @torch.no_grad()
@@ -207,14 +232,7 @@ class CausalSelfAttention(nn.Module):
         if need:
             old = self.dyn_pattern
             n_old = 0 if old is None else old.size(0)
-            S = self.block_size
-            # Rows S elements apart at a multiple of 4 KB all start on the same
-            # HBM channels, and the dense P.V kernel reads one 32-byte piece
-            # of each of many rows at once: 256 bytes of padding per row
-            # spread those reads.  The buffer stays an (n, S, S) view.
-            elem = torch.empty((), dtype=self._pattern_dtype).element_size()
-            pad = 256 // elem if (S * elem) % 4096 == 0 else 0
-            new = torch.zeros(n_old + len(need), S, S + pad, device=dev, dtype=self._pattern_dtype)[:, :, :S]
+            new = self._alloc_patterns(n_old + len(need), self._pattern_dtype if old is None else old.dtype, dev)
             if old is not None:
                 new[:n_old] = old
             for i, h in enumerate(need):

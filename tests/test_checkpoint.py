@@ -1,49 +1,112 @@
 """Loader of the reference's nanoGPT checkpoints (nanogpt/checkpoint.py).
 
-The released exports are not available offline, so the checkpoints here are
-synthetic files in the reference's layout, built from a model of this repo:
-``model_args`` + ``model`` (state dict with the ``_orig_mod.`` compile
-prefix), the dense prior as the reference's (n_head, S, S) ``dyn_pattern``
-with zero rows for other heads, the derived (n_head, 64, S) ``dyn_rho_band``
-(/root/reference/nanogpt/model.py:647-672, :900-911), and the reference's
-GPTConfig defaults for absent fields (:1248-1285).
+The released exports are not available offline.  The loader is pinned on
+tests/golden/gpt_export_small.npz, which the reference's own GPT wrote
+(tests/golden/make_golden.py): its state dicts under their own key names
+(``transformer.h.{i}.main_block.*``, every buffer the reference saves:
+dyn_frozen, dyn_decomp / dyn_alpha / dyn_rho / dyn_z, the lazily created
+dyn_rho_band and dyn_pattern, the dense representation's (n_head, S, S)
+dyn_pattern), its GPTConfig as model_args and its split-path logits.  A
+checkpoint file is assembled from them as nanogpt/train.py saves one
+(``model`` with torch.compile's ``_orig_mod.`` prefix, ``model_args``,
+optimizer state, ``config``, RNG state) and read back with
+``weights_only=True``.
 
-CPU: bit-exact round trip of every weight and freeze buffer, non-dynamic and
-learned-absolute exports, refusals.  GPU: logits of a loaded export with
-learned (non-closed-form) decomposed heads against the fp32 oracle.
+CPU: the loaded model reproduces the reference's logits through the oracle;
+reference_state_dict writes back exactly the reference's keys and values;
+synthetic exports (written by the now-pinned reference_state_dict) round-trip
+bit for bit; refusals.  GPU: the bf16 HIP model of a loaded export against the
+reference's logits, and an export with learned alpha / rho heads against the
+fp32 oracle.
 """
+import json
+import os
 import pickle
 
+import numpy as np
 import pytest
 import torch
 
 from oracle import model_oracle
 from test_model import _cos, _oracle_inputs, _small_model
 
+FIX = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "gpt_export_small.npz")
 
-def _reference_layout(m, compile_prefix=True):
-    """State dict of model m as the reference's GPT would save it."""
+
+def _fixture(tag):
+    """(reference state dict, model_args, tokens, logits_split) of one model
+    of the export fixture; every floating tensor of the reference model is
+    fp32 (float16-stored entries are exact)."""
+    d = np.load(FIX, allow_pickle=False)
+    f16 = set(json.loads(str(d[f"{tag}/f16keys"])))
+    pre = f"{tag}/sd/"
     sd = {}
-    for k, v in m.state_dict().items():
-        if k.endswith(".attn.dyn_pattern") or k.endswith(".attn.dyn_pattern_slot"):
-            continue
-        sd[k] = v.clone()
-    for i, blk in enumerate(m.transformer.h):
-        a = blk.attn
-        H, S = a.n_head, a.block_size
-        pre = f"transformer.h.{i}.attn."
-        if a.dyn_pattern is not None:
-            full = torch.zeros(H, S, S, dtype=a.dyn_pattern.dtype)
-            for h in range(H):
-                s = int(a.dyn_pattern_slot[h])
-                if s >= 0:
-                    full[h] = a.dyn_pattern[s]
-            sd[pre + "dyn_pattern"] = full
-        if a.dyn_alpha is not None:
-            sd[pre + "dyn_rho_band"] = torch.zeros(H, 64, S)
-    if compile_prefix:
-        sd = {"_orig_mod." + k: v for k, v in sd.items()}
-    return sd
+    for k in d.files:
+        if k.startswith(pre):
+            name = k[len(pre):]
+            t = torch.from_numpy(d[k].copy())
+            sd[name] = t.float() if name in f16 else t
+    return (sd, json.loads(str(d[f"{tag}/model_args"])), torch.from_numpy(d[f"{tag}/tokens"]),
+            torch.from_numpy(d[f"{tag}/logits_split"]))
+
+
+def _train_py_checkpoint(path, sd, model_args):
+    """A checkpoint file laid out as nanogpt/train.py:688-700 writes it."""
+    ck = {"model": {"_orig_mod." + k: v for k, v in sd.items()},
+          "optimizer": {"state": {0: {"step": torch.tensor(5.0), "exp_avg": torch.zeros(3)}},
+                        "param_groups": [{"lr": 6e-4, "params": [0]}]},
+          "model_args": model_args, "attention_layout": None, "iter_num": 5000, "best_val_loss": 3.02,
+          "config": {"dataset": "openwebtext", "batch_size": 12},
+          "cpu_rng_state": torch.random.get_rng_state(), "cuda_rng_states": None}
+    torch.save(ck, path)
+    return path
+
+
+@pytest.mark.parametrize("tag", ["decomposed", "dense"])
+def test_reference_export_loads_and_reproduces_logits(tmp_path, tag):
+    """The reference's own export loads strictly and the loaded weights and
+    freeze state give the reference's split-path logits (oracle, fp32)."""
+    from nanogpt.checkpoint import load_model
+    sd, ma, x, want = _fixture(tag)
+    assert any(".main_block." in k for k in sd) and not any(".attn." in k for k in sd)
+    m, cfg, ck = load_model(_train_py_checkpoint(tmp_path / "ref.pt", sd, ma), "cpu")
+    assert cfg.rand_attn_prior_repr == tag and ck["iter_num"] == 5000
+    got_sd, ocfg, freeze = _oracle_inputs(m)
+    for k, v in sd.items():
+        mine = k.replace(".main_block.", ".attn.")
+        if mine in got_sd and not k.endswith("dyn_pattern"):
+            assert torch.equal(got_sd[mine], v.float()), k
+    got = model_oracle.gpt_forward(got_sd, ocfg, freeze, x, path="split", all_positions=True)
+    np.testing.assert_allclose(got.numpy(), want.numpy(), atol=2e-5, rtol=1e-5)
+
+
+@pytest.mark.parametrize("tag", ["decomposed", "dense"])
+def test_reference_state_dict_is_the_reference_layout(tag):
+    """Written back, a loaded export has exactly the reference's key set,
+    dtypes and values (dense patterns expanded to (n_head, S, S), the rho
+    band rebuilt from rho)."""
+    from nanogpt.checkpoint import convert_state_dict, reference_state_dict, build_config_from_ckpt
+    from nanogpt.model import GPT
+    sd, ma, _, _ = _fixture(tag)
+    m = GPT(build_config_from_ckpt({"model_args": ma}))
+    m.load_state_dict(convert_state_dict(sd, m), strict=True)
+    got = reference_state_dict(m)
+    assert set(got) == set(sd), (set(got) ^ set(sd))
+    for k, v in sd.items():
+        assert got[k].dtype == v.dtype and got[k].shape == v.shape, k
+        assert torch.equal(got[k], v), k
+    pref = reference_state_dict(m, compile_prefix=True)
+    assert set(pref) == {"_orig_mod." + k for k in sd}
+
+
+def _save(tmp_path, m, name="ckpt.pt", **extra):
+    from nanogpt.checkpoint import reference_state_dict
+    ck = {"model": reference_state_dict(m, compile_prefix=True), "model_args": _model_args(m.config),
+          "iter_num": 1000, "best_val_loss": 3.1, "config": {"dataset": "openwebtext"}}
+    ck.update(extra)
+    p = tmp_path / name
+    torch.save(ck, p)
+    return p
 
 
 def _model_args(cfg, **over):
@@ -54,15 +117,6 @@ def _model_args(cfg, **over):
           "state_size": 0, "rand_head_rate": 0.0, "rand_mask_rate": 1.0, "rand_components": "none"}
     ma.update(over)
     return ma
-
-
-def _save(tmp_path, m, name="ckpt.pt", **extra):
-    ck = {"model": _reference_layout(m), "model_args": _model_args(m.config), "iter_num": 1000,
-          "best_val_loss": 3.1, "config": {"dataset": "openwebtext"}}
-    ck.update(extra)
-    p = tmp_path / name
-    torch.save(ck, p)
-    return p
 
 
 def test_round_trip_is_bit_exact(tmp_path):
@@ -93,7 +147,7 @@ def test_dense_prior_export_and_defaults(tmp_path):
     """A dense-prior export (rand_attn_prior_repr='dense', no decomposed
     buffers) and a non-dynamic learned-absolute export with fields absent
     (reference defaults apply)."""
-    from nanogpt.checkpoint import load_model
+    from nanogpt.checkpoint import load_model, reference_state_dict
     from nanogpt.model import GPT, GPTConfig
     torch.manual_seed(0)
     cfg = GPTConfig(block_size=64, vocab_size=500, n_layer=2, n_head=4, n_embd=128, bias=True,
@@ -110,7 +164,8 @@ def test_dense_prior_export_and_defaults(tmp_path):
     cfg2 = GPTConfig(block_size=64, vocab_size=500, n_layer=1, n_head=4, n_embd=128,
                      position_encoding="learned_absolute")
     m2 = GPT(cfg2).eval()
-    sd = {k: v for k, v in m2.state_dict().items() if ".attn.dyn_" not in k}
+    # a non-dynamic reference model saves no dyn_* buffer at all
+    sd = {k: v for k, v in reference_state_dict(m2).items() if ".main_block.dyn_" not in k}
     ck = {"model": sd, "model_args": {"block_size": 64, "vocab_size": 500, "n_layer": 1, "n_head": 4,
                                       "n_embd": 128}}
     torch.save(ck, tmp_path / "plain.pt")
@@ -124,9 +179,10 @@ def test_dense_prior_export_and_defaults(tmp_path):
                                          ("rand_attn_pattern", "uniform"), ("block_type", "mamba"),
                                          ("rand_attn_head_rate_per_layer", "0.25,0.5")])
 def test_unsupported_architectures_refused(tmp_path, field, value):
-    from nanogpt.checkpoint import load_model
+    from nanogpt.checkpoint import load_model, reference_state_dict
     m0, _ = _small_model(T=64, layers=1)
-    ck = {"model": _reference_layout(m0), "model_args": _model_args(m0.config, **{field: value})}
+    ck = {"model": reference_state_dict(m0, compile_prefix=True),
+          "model_args": _model_args(m0.config, **{field: value})}
     torch.save(ck, tmp_path / "x.pt")
     with pytest.raises(NotImplementedError, match=field):
         load_model(tmp_path / "x.pt", "cpu")
@@ -136,14 +192,15 @@ def test_config_only_fields_and_empty_pattern(tmp_path):
     """Fields persisted only in the full config dict are pulled in
     (eval_nanogpt_logprobs.py:66-70): a per-layer head rate there is refused;
     rand_attn_pattern "" means "none" (model.py:457) and loads."""
-    from nanogpt.checkpoint import load_model
+    from nanogpt.checkpoint import load_model, reference_state_dict
     m0, _ = _small_model(T=64, layers=1)
-    ck = {"model": _reference_layout(m0), "model_args": _model_args(m0.config),
+    ck = {"model": reference_state_dict(m0, compile_prefix=True), "model_args": _model_args(m0.config),
           "config": {"rand_attn_head_rate_per_layer": "0.1"}}
     torch.save(ck, tmp_path / "h.pt")
     with pytest.raises(NotImplementedError, match="rand_attn_head_rate_per_layer"):
         load_model(tmp_path / "h.pt", "cpu")
-    ck = {"model": _reference_layout(m0), "model_args": _model_args(m0.config, rand_attn_pattern=""),
+    ck = {"model": reference_state_dict(m0, compile_prefix=True),
+          "model_args": _model_args(m0.config, rand_attn_pattern=""),
           "config": {"rand_attn_pattern_sharing": "none", "rand_attn_prior_path": ""}}
     torch.save(ck, tmp_path / "e.pt")
     m1, _, _ = load_model(tmp_path / "e.pt", "cpu")
@@ -185,22 +242,54 @@ def test_gpu_loaded_export_matches_oracle(tmp_path):
     assert _cos(got, ref) >= 0.9999
 
 
-def test_reference_writer_matches_layout_and_round_trips(tmp_path):
-    """save_reference_checkpoint writes the layout of _reference_layout (the
-    test's own statement of the reference export) and load_model restores
-    every weight and freeze buffer bit for bit."""
-    from nanogpt.checkpoint import load_model, reference_state_dict, save_reference_checkpoint
+def test_reference_writer_round_trips(tmp_path):
+    """save_reference_checkpoint (reference_state_dict, pinned above on the
+    reference's own export) writes a file load_model restores bit for bit."""
+    from nanogpt.checkpoint import load_model, save_reference_checkpoint
     m0, _ = _small_model(T=64, layers=2)
-    want = _reference_layout(m0)
-    got = reference_state_dict(m0, compile_prefix=True)
-    assert set(got) == set(want)
-    for k, v in want.items():
-        if k.endswith("dyn_rho_band"):
-            assert got[k].shape == v.shape
-            continue
-        assert torch.equal(got[k], v), k
     p = save_reference_checkpoint(m0, tmp_path / "w.pt", iter_num=7)
+    ck = torch.load(p, weights_only=True)
+    assert all(k.startswith("_orig_mod.") for k in ck["model"])
+    assert not any(".attn." in k for k in ck["model"])
     m1, cfg1, ck = load_model(p, "cpu")
     assert ck["iter_num"] == 7
     for k, v in m0.state_dict().items():
         assert torch.equal(m1.state_dict()[k], v), k
+
+
+def test_loaded_dense_patterns_keep_padded_rows(tmp_path):
+    """Dense patterns of a loaded export sit in the padded slots freeze_heads
+    allocates (rows at a 4 KB-multiple pitch get 256 bytes more), and a later
+    dtype cast keeps that layout."""
+    from nanogpt.checkpoint import load_model
+    from nanogpt.model import GPT, GPTConfig
+    torch.manual_seed(1)
+    cfg = GPTConfig(block_size=1024, vocab_size=64, n_layer=1, n_head=2, n_embd=64, bias=False,
+                    rand_attn_prior_repr="decomposed")
+    m0 = GPT(cfg).eval()
+    pat = torch.rand(1, 1024, 1024)
+    m0.transformer.h[0].attn.freeze_heads([1], pat)
+    m1, _, _ = load_model(_save(tmp_path, m0), "cpu")
+    a = m1.transformer.h[0].attn
+    assert a.dyn_pattern.shape == (1, 1024, 1024) and a.dyn_pattern.stride() == (1024 * 1088, 1088, 1)
+    assert torch.equal(a.dyn_pattern, m0.transformer.h[0].attn.dyn_pattern)
+    m1.to(dtype=torch.float64)   # 8 KB rows: padded again (a cast returns contiguous tensors)
+    assert a.dyn_pattern.dtype == torch.float64 and a.dyn_pattern.stride(1) == 1024 + 32
+    assert torch.equal(a.dyn_pattern, m0.transformer.h[0].attn.dyn_pattern.double())
+    m1.to(dtype=torch.bfloat16)  # 2 KB rows: no padding
+    assert a.dyn_pattern.dtype == torch.bfloat16 and a.dyn_pattern.stride(1) == 1024
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("tag", ["decomposed", "dense"])
+def test_gpu_reference_export_matches_reference_logits(tmp_path, tag):
+    """The reference's own export, loaded onto the GPU in bf16 and run through
+    the HIP path: all-position logits against the reference's fp32 split-path
+    logits, cosine >= 0.9999."""
+    from nanogpt.checkpoint import load_model
+    sd, ma, x, want = _fixture(tag)
+    m, _, _ = load_model(_train_py_checkpoint(tmp_path / "ref.pt", sd, ma), "cuda", dtype=torch.bfloat16)
+    with torch.inference_mode():
+        got = m.forward_all_positions(x.cuda()).float().cpu()
+    c = _cos(got, want)
+    assert c >= 0.9999, f"logits cosine {c:.6f}"
