@@ -530,7 +530,17 @@ void flash_fwd_kernel(const FlashParams p) {
   __shared__ __align__(16) char k0[KB], k1[KB], k2[KB3];
   __shared__ __align__(16) char v0[VB], v1[VB], v2[VB3];
   if constexpr (!PERSIST) {
-    flash_unit<T, HD, QT>(p, blockIdx.x, k0, k1, k2, v0, v1, v2);
+    // XCD-aware head order.  Workgroup i runs on XCD i % 8, and unit
+    // item * nbh + r takes (batch, live slot) r of an item.  Within each
+    // aligned group of 8 slots, slot r is swapped for the slot of the same
+    // group whose index is i mod 8: slot s < 8 * (nbh / 8) then always runs
+    // on XCD s % 8, so each XCD's L2 holds the K / V of its own heads (the
+    // nbh % 8 remaining slots spread over the XCDs).  A permutation of the
+    // slots within each item; the identity when nbh is a multiple of 8.
+    int unit = blockIdx.x;
+    const int nbh = p.B * p.n_slots, r = unit % nbh;
+    if (r < (nbh & ~7)) unit += ((r & ~7) | (unit & 7)) - r;
+    flash_unit<T, HD, QT>(p, unit, k0, k1, k2, v0, v1, v2);
   } else {
     __shared__ int next_unit;
     const int n_units = (p.n_items ? p.n_items : p.n_qblk) * p.B * p.n_slots;
