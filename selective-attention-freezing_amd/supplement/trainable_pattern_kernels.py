@@ -19,7 +19,7 @@ import numpy as np
 import torch
 
 import kernel._ext as _ext
-from kernel.fused_attn import decomposed_logz
+from kernel.fused_attn import _host_table, decomposed_logz
 
 
 @torch.no_grad()
@@ -45,8 +45,7 @@ def pattern_gradients(out, value, alpha, rho, z, states, grad):
     alpha, rho, z: (H, S) with S >= T."""
     if not value.is_cuda:
         raise RuntimeError("pattern_gradients runs on HIP devices only (got a CPU tensor)")
-    st = states.detach().to("cpu", torch.int32).numpy() if torch.is_tensor(states) \
-        else np.asarray(states, dtype=np.int32)
+    st = _host_table(states) if torch.is_tensor(states) else np.asarray(states, dtype=np.int32)
     da = torch.zeros(alpha.shape, device=value.device, dtype=torch.float32)
     dr = torch.zeros(rho.shape, device=value.device, dtype=torch.float32)
     if not (st == 2).any():
@@ -82,8 +81,9 @@ class PatternGradient(torch.autograd.Function):
     @staticmethod
     def forward(ctx, out, value, alpha, rho, z, states):
         ctx.save_for_backward(out, value, alpha, rho, z)
-        ctx.states = states.detach().to("cpu", torch.int32) if torch.is_tensor(states) \
-            else torch.as_tensor(states, dtype=torch.int32)
+        # host copy of the head states: cached per table version, so no
+        # device-to-host copy drains the stream per call
+        ctx.states = _host_table(states) if torch.is_tensor(states) else np.asarray(states, dtype=np.int32)
         return out
 
     @staticmethod

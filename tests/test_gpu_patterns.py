@@ -139,6 +139,30 @@ def restore_dispatch():
         module.fused_mixed_attn = fn._original
 
 
+def test_patched_dispatch_adds_pattern_gradients(restore_dispatch):
+    """A direct caller handing trainable alpha / rho to the patched
+    nanogpt.model.fused_mixed_attn gets z derived and the pattern gradients
+    added: the same dalpha / drho as the explicit PatternGradient route."""
+    import supplement
+    from nanogpt import model as module
+    supplement.patch_fused_dispatch()
+    B, H, T, hd, S, dec = 2, 6, 300, 64, 512, [1, 4]
+    frozen, hidx, live = routing(H, {h: 2 for h in dec})
+    alpha, rho, _ = make_decomp(H, S, seed=5, scale=0.8)
+    q, k, v = qkv(B, H, T, hd, seed=17, dtype=torch.bfloat16)
+    a_p = alpha.to(DEV).requires_grad_(True)
+    r_p = rho.to(DEV).requires_grad_(True)
+    y = module.fused_mixed_attn(q[:, live].contiguous().to(DEV), k[:, live].contiguous().to(DEV), v.to(DEV),
+                                None, frozen.to(DEV), hidx.to(DEV), alpha=a_p, rho=r_p)
+    w = torch.randn(y.shape, generator=torch.Generator().manual_seed(23)).to(DEV)
+    (y.float() * w).sum().backward()
+    torch.cuda.synchronize()
+    da, dr = orc.pattern_grads(f64(v), f64(w.bfloat16()), frozen.numpy(), alpha.double().numpy(),
+                               rho.double().numpy(), out=f64(y))
+    _rel_ok(a_p.grad, da, "dalpha via dispatch")
+    _rel_ok(r_p.grad, dr, "drho via dispatch")
+
+
 def _freeze_records(m, req):
     """Model-oracle freeze records whose decomposed rows are the trainable
     (alpha, rho) of `req` and z their differentiable logsumexp."""

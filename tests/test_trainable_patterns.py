@@ -46,7 +46,7 @@ def test_enable_turns_fitted_buffers_into_parameters(restore_dispatch):
     assert "dyn_alpha" in dict(m.transformer.h[1].attn.named_buffers())
     assert opt.param_groups[-1]["weight_decay"] == 0.0 and len(opt.param_groups[-1]["params"]) == 2
     assert getattr(module.fused_mixed_attn, "_trainable_patterns", False)
-    assert getattr(a0.dyn_alpha, "_pattern_cache_enabled", False)
+    assert a0._patterns is m._saf_patterns and m.transformer.h[1].attn._patterns is None
     with pytest.raises(RuntimeError, match="already enabled"):
         supplement.enable(m)
     # patching twice keeps one wrapper
@@ -103,3 +103,46 @@ def test_host_normalisers_gradient_matches_oracle():
     np.testing.assert_allclose(a.grad.numpy(), da, atol=1e-10)
     np.testing.assert_allclose(r.grad.numpy(), dr, atol=1e-10)
     assert kernel.decomp_log_normalizers_fft is kernel.decomp_log_normalizers
+
+
+def test_normaliser_cache_follows_parameters_and_optimizer_steps(restore_dispatch, monkeypatch):
+    """z is computed once per (layer, length) while the parameters stay put;
+    an in-place edit (version counter), another length, the optimizer's step
+    (generation) or clear_pattern_cache recompute it.  The HIP normalisers are
+    replaced by a counting host stand-in (the cache logic is host code)."""
+    import supplement
+    import supplement.trainable_patterns as tp
+    from kernel.fused_attn import decomposed_logz
+    from nanogpt import model as module
+    calls = []
+
+    def fake(alpha, rho, length):
+        calls.append(int(length))
+        z = torch.zeros(alpha.shape)
+        z[:, :length] = decomposed_logz(alpha[:, :length].detach().float(), rho[:, :length].detach().float())
+        return z
+    monkeypatch.setattr(tp, "normalisers", fake)
+    m = _model()
+    opt = torch.optim.SGD(m.parameters(), lr=0.0)
+    supplement.enable(m, opt)
+    pats, a0 = m._saf_patterns, m.transformer.h[0].attn
+    z1 = pats.z_for(a0, 48)
+    assert pats.z_for(a0, 48) is z1 and calls == [48]
+    np.testing.assert_allclose(z1[:, :48].numpy(), orc.decomposed_logz(
+        a0.dyn_alpha.detach()[:, :48].double().numpy(), a0.dyn_rho.detach()[:, :48].double().numpy()),
+        rtol=1e-5, atol=1e-5)
+    pats.z_for(a0, 64)
+    assert calls == [48, 64]
+    with torch.no_grad():
+        a0.dyn_rho[0, 3] += 1.0
+    pats.z_for(a0, 64)
+    assert calls == [48, 64, 64]
+    pats.z_for(a0, 64)
+    opt.step()
+    pats.z_for(a0, 64)
+    assert calls == [48, 64, 64, 64]
+    module.fused_mixed_attn.clear_pattern_cache()
+    pats.z_for(a0, 64)
+    assert calls == [48, 64, 64, 64, 64]
+    kw = pats.kernel_inputs(a0, 64)
+    assert kw["closed_form"] is None and not kw["alpha"].requires_grad and kw["z"] is pats.z_for(a0, 64)
