@@ -9,9 +9,14 @@ _attend_cheap :946-1015), MLP (:1193-1207), Block (:1214-1240) and GPT
 (:1312-1417, weight tying and GPT-2 init).
 
 Differences that follow from the MI355X design:
-  * every attention call goes through ``fused_mixed_attn`` (looked up as a
-    module global at call time, so harnesses can count dispatches); with no
-    head frozen it runs the same HIP flash kernel for every head;
+  * every attention call of the default (fused) route goes through
+    ``fused_mixed_attn`` (looked up as a module global at call time, so
+    harnesses can count dispatches); with no head frozen it runs the same HIP
+    flash kernel for every head.  The split route (FROZEN_ATTN_FUSED=0,
+    :29-32, :1017-1061) runs the live heads through the same operator with
+    no head frozen and the frozen ones through frozen_pv (dense heads) or the
+    frozen-only operator (when decomposed heads are frozen, where the
+    reference materialises their patterns);
   * decomposed pattern parameters (alpha, rho, z) stay fp32 whatever the model
     dtype, the convention of the reference's Qwen adapter
     (qwen/nanogpt/hybrid_prior_attention.py:128-140): z of a slow decay rounded
@@ -27,6 +32,7 @@ randomisation ablations, stateful blocks, checkpoint loading and training
 utilities of the reference model are outside this path.
 """
 import math
+import os
 from dataclasses import dataclass
 
 import torch
@@ -37,6 +43,13 @@ from kernel import (fused_mixed_attn, decomposed_logz, classify_closed_form,  # 
                     BAND_ROWS)
 import kernel as _kernel_mod
 
+# One mixed-head operator call for live and frozen heads (the default).
+# FROZEN_ATTN_FUSED=0 selects the split route instead (nanogpt/model.py:29-32,
+# :1017-1061): V projected for all heads in [live..., frozen...] order, the
+# live heads through the flash kernel, the frozen ones through frozen_pv (or
+# the frozen-only mixed operator when decomposed heads are frozen),
+# concatenated, and c_proj applied to the matching column permutation.
+_FUSED = os.environ.get("FROZEN_ATTN_FUSED", "1") != "0"
 _FUSED_DISPATCH_COUNT = 0
 
 
@@ -168,6 +181,9 @@ class CausalSelfAttention(nn.Module):
         self.register_buffer("dyn_pattern_slot", torch.full((H,), -1, dtype=torch.int32))
         self._fz_dirty = True
         self._wc_key = None
+        self._ws_key = None
+        # trainable-pattern owner (supplement.enable), consulted per forward
+        self._patterns = None
 
     # -- dtype handling ---------------------------------------------------
     def _apply(self, fn, recurse=True):
@@ -301,12 +317,109 @@ class CausalSelfAttention(nn.Module):
                                                 heads=dec_heads)
         else:
             self._closed = None
+        # split route: [live..., frozen...] column order and the frozen group's
+        # own tables (states, pattern slots, closed forms in that order)
+        fz = self._fz_idx
+        self._cperm_cols = (torch.cat([self._uf_idx, fz])[:, None] * hd + ar).reshape(-1)
+        self._fz_states_i32 = self._fz_mask_i32.index_select(0, fz)
+        self._fz_slots_i32 = self.dyn_pattern_slot.index_select(0, fz).clamp(min=0).to(torch.int32)
+        self._fz_hidx_i32 = torch.zeros(self._n_frozen, dtype=torch.int32, device=dev)
+        nuf = int(self._uf_idx.numel())
+        self._uf_states_i32 = torch.zeros(nuf, dtype=torch.int32, device=dev)
+        self._uf_hidx_i32 = torch.arange(nuf, dtype=torch.int32, device=dev)
+        if self._closed is not None:
+            sel = fz.cpu().numpy()
+            self._fz_closed = (self._closed[0][sel].copy(), self._closed[1][sel].copy())
+        else:
+            self._fz_closed = None
         self._wc_key = None
+        self._ws_key = None
         self._fz_dirty = False
 
     def train(self, mode=True):
         self._wc_key = None
+        self._ws_key = None
         return super().train(mode)
+
+    def _split_route(self):
+        """True when this call takes the split route: FROZEN_ATTN_FUSED=0 and
+        some head frozen (with none frozen both routes are one flash call)."""
+        if self._fz_dirty:
+            self._refresh_freeze_cache()
+        return not _FUSED and self._n_frozen > 0
+
+    def _split_weight_cache(self):
+        """Split route, inference: Wv[cperm], [Wq[live]; Wk[live]] and
+        Wc[:, cperm] gathered once per weight version / freeze change
+        (nanogpt/model.py:920-944)."""
+        ws = (self.q_proj.weight, self.k_proj.weight, self.v_proj.weight, self.c_proj.weight)
+        key = tuple((w._version, w.data_ptr()) for w in ws)
+        if self._ws_key != key:
+            qw, kw, vw, cw = ws
+            perm, uf = self._cperm_cols, self._uf_cols
+            self._ws_v = vw.index_select(0, perm).detach()
+            vb = self.v_proj.bias
+            self._ws_vb = None if vb is None else vb.index_select(0, perm).detach()
+            self._ws_qk = self._ws_qkb = None
+            if uf is not None:
+                self._ws_qk = torch.cat([qw.index_select(0, uf), kw.index_select(0, uf)]).detach()
+                if self.q_proj.bias is not None:
+                    self._ws_qkb = torch.cat([self.q_proj.bias.index_select(0, uf),
+                                              self.k_proj.bias.index_select(0, uf)]).detach()
+            self._ws_c = cw.index_select(1, perm).detach()
+            self._ws_key = key
+        return self._ws_v, self._ws_vb, self._ws_qk, self._ws_qkb, self._ws_c
+
+    def split_heads(self, x, rope=None):
+        """Split route (nanogpt/model.py:1017-1061): (B, T, C) head outputs in
+        [live..., frozen...] order and the c_proj weight whose input columns
+        match that order (None on the grad path, which applies
+        linear_permuted_cols itself)."""
+        if self._patterns is not None:
+            raise NotImplementedError("trainable patterns run on the fused route (FROZEN_ATTN_FUSED=1)")
+        B, T, C = x.size()
+        nh, hd = self.n_head, self.head_dim
+        nf = self._n_frozen
+        nuf = nh - nf
+        infer = not torch.is_grad_enabled()
+        if infer:
+            wv, wvb, wqk, wqkb, wc = self._split_weight_cache()
+            v_all = F.linear(x, wv, wvb)
+        else:
+            wc = None
+            v_all = _kernel_mod.linear_rows(x, self.v_proj.weight, self.v_proj.bias, self._cperm_cols)
+        v_all = v_all.view(B, T, nh, hd).transpose(1, 2)
+        vf = v_all[:, nuf:]
+        if self._dec_any:
+            # decomposed heads among the frozen: the frozen-only mixed operator
+            # (dense, decomposed and closed-form kernels) over the frozen group
+            fz = self._fz_idx
+            yf = fused_mixed_attn(vf[:, :0], vf[:, :0], vf, self.dyn_pattern, self._fz_states_i32,
+                                  self._fz_hidx_i32, self._fz_slots_i32 if self.dyn_pattern is not None else None,
+                                  alpha=self.dyn_alpha.index_select(0, fz), rho=self.dyn_rho.index_select(0, fz),
+                                  z=self.dyn_z.index_select(0, fz), validate=False, closed_form=self._fz_closed)
+        else:
+            yf = _kernel_mod.frozen_pv(self.dyn_pattern, vf, self._fz_slots_i32, T)
+        if nuf == 0:
+            return yf.transpose(1, 2).reshape(B, T, C), wc
+        if infer:
+            qk = F.linear(x, wqk, wqkb)
+        else:
+            qk = _kernel_mod.linear_rows2(x, self.q_proj.weight, self.k_proj.weight, self.q_proj.bias,
+                                          self.k_proj.bias, self._uf_cols)
+        qk = qk.view(B, T, 2, nuf, hd)
+        qu, ku = qk[:, :, 0].transpose(1, 2), qk[:, :, 1].transpose(1, 2)
+        if self.position_encoding == "rope":
+            if rope is None:
+                raise ValueError("RoPE Q/K requested without a rotary cache")
+            if infer and qu.dtype in (torch.bfloat16, torch.float16):
+                _kernel_mod.rope_qk_(qu, ku, *rope)
+            else:
+                qu, ku = apply_rotary_pos_emb(qu, ku, *rope)
+        yu = fused_mixed_attn(qu, ku, v_all[:, :nuf], None, self._uf_states_i32, self._uf_hidx_i32,
+                              validate=False)
+        y = torch.cat([yu.transpose(1, 2), yf.transpose(1, 2)], dim=2)
+        return y.reshape(B, T, C), wc
 
     def _infer_weight_cache(self):
         """[Wq[live]; Wk[live]; Wv] gathered once per weight version / freeze
@@ -329,7 +442,19 @@ class CausalSelfAttention(nn.Module):
         return self._wc_qkv, self._wc_qkvb
 
     def forward(self, x, rope=None):
+        if self._split_route():
+            y, wc = self.split_heads(x, rope)
+            if wc is None:
+                return _kernel_mod.linear_permuted_cols(y, self.c_proj.weight, self.c_proj.bias, self._cperm_cols)
+            return F.linear(y, wc, self.c_proj.bias)
         return self.c_proj(self.attend(x, rope))
+
+    def head_outputs(self, x, rope=None):
+        """(y, W): head outputs before c_proj and the c_proj weight whose
+        input columns match their order (inference)."""
+        if self._split_route():
+            return self.split_heads(x, rope)
+        return self.attend(x, rope), self.c_proj.weight
 
     def attend(self, x, rope=None):
         """The block's attention before the output projection: (B, T, C) head outputs."""
@@ -373,12 +498,18 @@ class CausalSelfAttention(nn.Module):
                         qu, ku = apply_rotary_pos_emb(qu, ku, *rope)
         _FUSED_DISPATCH_COUNT += 1
         dec = self._dec_any
+        if dec and self._patterns is not None:
+            # trainable alpha / rho: z of the current parameters, no scan
+            pk = self._patterns.kernel_inputs(self, T)
+        elif dec:
+            pk = dict(alpha=self.dyn_alpha, rho=self.dyn_rho, z=self.dyn_z, closed_form=self._closed)
+        else:
+            pk = dict(alpha=None, rho=None, z=None, closed_form=None)
         y = fused_mixed_attn(qu, ku, v, self.dyn_pattern, self._fz_mask_i32, hidx,
                              self._pidx_i32 if self.dyn_pattern is not None else None,
-                             alpha=self.dyn_alpha if dec else None,
-                             rho=self.dyn_rho if dec else None,
-                             z=self.dyn_z if dec else None,
-                             validate=False, closed_form=self._closed)
+                             validate=False, **pk)
+        if dec and self._patterns is not None:
+            y = self._patterns.attach_gradient(self, y, v, pk["z"])
         return y.transpose(1, 2).reshape(B, T, nh * hd)
 
 
@@ -474,8 +605,8 @@ class GPT(nn.Module):
             for i, block in enumerate(blocks):
                 attn, mlp = block.attn, block.mlp
                 if attn.c_proj.bias is None:
-                    y = attn.attend(h, rope=rope)
-                    x2.addmm_(y.reshape(x2.size(0), -1), attn.c_proj.weight.t())
+                    y, wc = attn.head_outputs(h, rope=rope)
+                    x2.addmm_(y.reshape(x2.size(0), -1), wc.t())
                     h = _kernel_mod.add_layernorm_(x, None, block.ln_2.weight, block.ln_2.bias)
                 else:
                     h = _kernel_mod.add_layernorm_(x, attn(h, rope=rope), block.ln_2.weight, block.ln_2.bias)

@@ -228,3 +228,105 @@ def test_gpu_model_training_gradients_match_oracle():
         assert c >= 0.999, f"{name}: gradient cosine {c:.6f}"
         checked += 1
     assert checked >= 8
+
+
+# ---------------------------------------------------------------------------
+# split route (FROZEN_ATTN_FUSED=0, /root/reference/nanogpt/model.py:1017-1061)
+# ---------------------------------------------------------------------------
+
+@pytest.fixture
+def split_route(monkeypatch):
+    from nanogpt import model as model_mod
+    monkeypatch.setattr(model_mod, "_FUSED", False)
+
+
+def _dense_model(T=128, layers=2, device="cpu", dtype=torch.float32, seed=4):
+    """Dense-frozen heads only, projection biases on: the split route's
+    frozen_pv branch and every bias of the gathered projections."""
+    from nanogpt.model import GPT, GPTConfig
+    torch.manual_seed(seed)
+    cfg = GPTConfig(block_size=T, vocab_size=4096, n_layer=layers, n_head=8, n_embd=512,
+                    bias=True, position_encoding="rope", rand_attn_prior_repr="decomposed")
+    m = GPT(cfg)
+    g = torch.Generator().manual_seed(seed)
+    with torch.no_grad():
+        for n, p in m.named_parameters():
+            if n.endswith(".bias"):
+                p.copy_(torch.randn(p.shape, generator=g) * 0.02)
+    for l, blk in enumerate(m.transformer.h):
+        blk.attn.freeze_heads([1, 4 + l % 3, 7], torch.rand(3, T, T, generator=g))
+    m = m.to(device=device, dtype=dtype).eval()
+    x = torch.randint(0, 4096, (2, T), generator=g).to(device)
+    return m, x
+
+
+def test_split_route_tables():
+    """The split route's column permutation and frozen-group tables."""
+    m, _ = _small_model(T=64, layers=1)
+    a = m.transformer.h[0].attn
+    a._refresh_freeze_cache()
+    hd = a.head_dim
+    order = a._uf_idx.tolist() + a._fz_idx.tolist()
+    assert a._cperm_cols.tolist() == [h * hd + d for h in order for d in range(hd)]
+    assert a._fz_states_i32.tolist() == [int(a._fz_mask_i32[h]) for h in a._fz_idx.tolist()]
+    assert a._fz_slots_i32.tolist() == [max(int(a.dyn_pattern_slot[h]), 0) for h in a._fz_idx.tolist()]
+    assert list(a._fz_closed[0]) == [int(a._closed[0][h]) for h in a._fz_idx.tolist()]
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("kind", ["mixed", "dense"])
+def test_gpu_split_route_logits_match_oracle(split_route, monkeypatch, kind):
+    """Inference on the split route (bf16): all-position and last-position
+    logits against the fp32 oracle's split path, cosine >= 0.9999; dense-only
+    layers go through frozen_pv, layers with decomposed heads through the
+    frozen-only operator, and no fused dispatch is counted."""
+    import kernel
+    from nanogpt import model as model_mod
+    calls = []
+    orig = kernel.frozen_pv
+    monkeypatch.setattr(kernel, "frozen_pv", lambda *a: calls.append(1) or orig(*a))
+    build = _small_model if kind == "mixed" else _dense_model
+    m, x = build(T=256, layers=3, device="cuda", dtype=torch.bfloat16)
+    n0 = model_mod.fused_dispatch_count()
+    with torch.inference_mode():
+        got = m.forward_all_positions(x).float().cpu()
+        last = m(x).float().cpu()
+    assert model_mod.fused_dispatch_count() == n0
+    assert len(calls) == (0 if kind == "mixed" else 2 * 3)
+    sd, ocfg, freeze = _oracle_inputs(m)
+    ref = model_oracle.gpt_forward(sd, ocfg, freeze, x.cpu(), path="split", all_positions=True)
+    c = _cos(got, ref)
+    assert c >= 0.9999, f"{kind}: logits cosine {c:.6f}"
+    assert _cos(last, ref[:, -1:]) >= 0.9999
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("kind", ["mixed", "dense"])
+def test_gpu_split_route_training_gradients_match_oracle(split_route, kind):
+    """One training step on the split route (linear_rows V, linear_rows2 Q/K,
+    the flash backward for live heads, the frozen_pv or frozen-only backward,
+    linear_permuted_cols into c_proj) against the fp32 oracle split path's
+    autograd: cosine >= 0.999 for every attention and MLP weight and bias."""
+    build = _small_model if kind == "mixed" else _dense_model
+    m, x = build(T=128, layers=2, device="cuda", dtype=torch.bfloat16)
+    sd, ocfg, freeze = _oracle_inputs(m)
+    w = torch.randn(x.size(0), 128, m.config.vocab_size, generator=torch.Generator().manual_seed(6))
+    m.zero_grad(set_to_none=True)
+    logits = m.forward_all_positions(x)
+    (logits.float() * w.cuda()).sum().backward()
+    torch.cuda.synchronize()
+    ref_sd = {k: v.clone().requires_grad_(True) for k, v in sd.items()}
+    forward = getattr(model_oracle.gpt_forward, "__wrapped__", model_oracle.gpt_forward)
+    ref = forward(ref_sd, ocfg, freeze, x.cpu(), path="split", all_positions=True)
+    assert _cos(logits.detach().float().cpu(), ref.detach()) >= 0.9999
+    (ref * w).sum().backward()
+    checked = 0
+    for name, p in m.named_parameters():
+        if ".attn." not in name and ".mlp." not in name:
+            continue
+        if p.grad is None or name not in ref_sd or ref_sd[name].grad is None:
+            continue
+        c = _cos(p.grad.float().cpu(), ref_sd[name].grad)
+        assert c >= 0.999, f"{kind} {name}: gradient cosine {c:.6f}"
+        checked += 1
+    assert checked >= (8 if kind == "mixed" else 16)
