@@ -77,13 +77,18 @@ template <typename T, int HD> struct TileDma {
   }
 
   __device__ __forceinline__ void load_k(const T* base, int64_t st, int j0, int T_len, char* tile, int wave) const {
-    const __amdgpu_buffer_rsrc_t r = rows_rsrc(base, st, j0, T_len);
+    load_k_rs(rows_rsrc(base, st, j0, T_len), tile, wave);
+  }
+  __device__ __forceinline__ void load_v(const T* base, int64_t st, int j0, int T_len, char* tile, int wave) const {
+    load_v_rs(rows_rsrc(base, st, j0, T_len), tile, wave);
+  }
+  // the same from a descriptor of the tile's rows (a RowCursor's)
+  __device__ __forceinline__ void load_k_rs(const __amdgpu_buffer_rsrc_t r, char* tile, int wave) const {
 #pragma unroll
     for (int p = 0; p < KN; ++p)
       __builtin_amdgcn_raw_ptr_buffer_load_lds(r, SAF_LDS_PTR(tile + (NW * p + wave) * 1024), 16, koff[p], 0, 0, 0);
   }
-  __device__ __forceinline__ void load_v(const T* base, int64_t st, int j0, int T_len, char* tile, int wave) const {
-    const __amdgpu_buffer_rsrc_t r = rows_rsrc(base, st, j0, T_len);
+  __device__ __forceinline__ void load_v_rs(const __amdgpu_buffer_rsrc_t r, char* tile, int wave) const {
 #pragma unroll
     for (int p = 0; p < VN; ++p)
       __builtin_amdgcn_raw_ptr_buffer_load_lds(r, SAF_LDS_PTR(tile + (NW * p + wave) * 1024), 16, voff[p], 0, 0, 0);
@@ -196,11 +201,13 @@ struct FlashState {
 
   // Rare path: S_u is recomputed from its K tile, the reference moves to
   // max(m, block max) for every query of the wave, O and l are rescaled and
-  // P recomputed.  After it every P of the sub-block is <= 1.
-  __device__ __forceinline__ void redo(f32x16_t (&s)[QT], float (&bs)[QT], const char* ktile, int ks, int j0,
-                                       bool masked) {
+  // P recomputed.  After it every P of the sub-block is <= 1.  The causal
+  // mask is applied whether or not the block holds the diagonal: below it,
+  // every key of the sub-block precedes every query of the workgroup, so the
+  // mask changes nothing there (and no flag has to reach this path).
+  __device__ __forceinline__ void redo(f32x16_t (&s)[QT], float (&bs)[QT], const char* ktile, int ks, int j0) {
     scores(s, ktile, ks);
-    if (masked) mask(s, j0);
+    mask(s, j0);
     rebase(s, bs);
   }
 
@@ -255,7 +262,7 @@ struct FlashState {
   // right after), and the softmax of S_u packs P_u into `cur` (tile kR /
   // sub-block ksR for the rare recompute).
   __device__ __forceinline__ void step(f32x16_t (&cur)[QT], f32x16_t (&nxt)[QT], uint4 (&kpre)[NKT], int u,
-                                       bool masked, const char* kS, int ksS, const char* kN, int ksN,
+                                       int masked, const char* kS, int ksS, const char* kN, int ksN,
                                        const char* kR, int ksR, const char* vP, int ksP) {
     // the mask touches only S_u, complete before the step: applying it first
     // keeps the MFMAs and the softmax below in one basic block.  The empty
@@ -278,7 +285,7 @@ struct FlashState {
     bool bad = false;
 #pragma unroll
     for (int qt = 0; qt < QT; ++qt) bad |= bs[qt] > kRedoSum;
-    if (__builtin_amdgcn_ballot_w64(bad)) redo(cur, bs, kR, ksR, 32 * u, masked);
+    if (__builtin_amdgcn_ballot_w64(bad)) redo(cur, bs, kR, ksR, 32 * u);
 #pragma unroll
     for (int qt = 0; qt < QT; ++qt) l_run[qt] += bs[qt];
   }
@@ -286,7 +293,7 @@ struct FlashState {
   // The step of the two-slot schedule: as step() without the K prefetch,
   // and the rare recompute starts from a register copy of the masked raw
   // scores, so no K tile has to outlive the step that reads it.
-  __device__ __forceinline__ void step_raw(f32x16_t (&cur)[QT], f32x16_t (&nxt)[QT], int u, bool masked,
+  __device__ __forceinline__ void step_raw(f32x16_t (&cur)[QT], f32x16_t (&nxt)[QT], int u, int masked,
                                            const char* kS, int ksS, const char* vP, int ksP) {
     if (masked) {
       asm volatile("" ::: "memory");
@@ -392,6 +399,12 @@ __device__ __forceinline__ void flash_unit(Params& p, const int unit, char* k0, 
   }
   __syncthreads();
 
+  // descriptors of the next K block to load (K_{kb0+2}) and the next V
+  // block (V_{kb0+1}), advanced by 64 rows per block
+  RowCursor kcur, vcur;
+  kcur.init(kbase, p.k_st, 64 * (kb0 + 2), T_len);
+  vcur.init(vbase, p.v_st, 64 * (kb0 + 1), T_len);
+
   // pipeline registers: sA / sB alternate between S_u and P_{u-1} / S_{u+1};
   // P_{-1} = 0 makes the first P.V a no-op
   f32x16_t sA[QT], sB[QT];
@@ -413,12 +426,14 @@ __device__ __forceinline__ void flash_unit(Params& p, const int unit, char* k0, 
       char* const kJ1 = R ? k0 : k1;
       char* const vJ = R ? v1 : v0;
       char* const vJm = R ? v0 : v1;
-      const bool masked = j >= jd;
+      const int masked = j >= jd;
       // u = 2j: S_{2j+1} (K_j sub 1), P_{2j-1} V_{j-1} sub 1, softmax S_{2j}
       st.step_raw(sA, sB, 2 * j, masked, kJ, 1, vJm, 1);
       __syncthreads();  // K_j and V_{j-1} read by every wave; K_{j+1} and V_j landed (vmcnt 0)
-      if (j + 2 < nkb) dma.load_k(kbase, p.k_st, 64 * (j + 2), T_len, kJ, wave);
-      if (j + 1 < nkb) dma.load_v(vbase, p.v_st, 64 * (j + 1), T_len, vJm, wave);
+      if (j + 2 < nkb) dma.load_k_rs(kcur.rsrc(), kJ, wave);
+      if (j + 1 < nkb) dma.load_v_rs(vcur.rsrc(), vJm, wave);
+      kcur.advance(64);
+      vcur.advance(64);
       // u = 2j+1: S_{2j+2} (K_{j+1} sub 0; past the last block a stale slot
       // whose scores are never used), P_{2j} V_j sub 0, softmax S_{2j+1}
       st.step_raw(sB, sA, 2 * j + 1, masked, kJ1, 0, vJ, 0);
@@ -451,9 +466,11 @@ __device__ __forceinline__ void flash_unit(Params& p, const int unit, char* k0, 
       char* const vJm = vs[(R + 2) % 3];
       char* const vJ = vs[R];
       char* const vJ1 = vs[(R + 1) % 3];
-      if (j + 2 < nkb) dma.load_k(kbase, p.k_st, 64 * (j + 2), T_len, kJ2, wave);
-      if (j + 1 < nkb) dma.load_v(vbase, p.v_st, 64 * (j + 1), T_len, vJ1, wave);
-      const bool masked = j >= jd;
+      if (j + 2 < nkb) dma.load_k_rs(kcur.rsrc(), kJ2, wave);
+      if (j + 1 < nkb) dma.load_v_rs(vcur.rsrc(), vJ1, wave);
+      kcur.advance(64);
+      vcur.advance(64);
+      const int masked = j >= jd;
       // u = 2j: S_{2j+1} (K_j sub 1), operands of S_{2j+2} (K_{j+1} sub 0),
       // P_{2j-1} V_{j-1} sub 1, softmax S_{2j}
       st.step(sA, sB, kpre, 2 * j, masked, kJ, 1, kJ1, 0, kJ, 0, vJm, 1);

@@ -63,6 +63,10 @@ int check_act(const saf_tensor_t& t, const char* name, int align) {
     if (t.size[i] > 1 && (t.stride[i] * es) % align != 0)
       return fail(SAF_EALIGN, "%s stride %d (%lld elements) is not a multiple of %d bytes", name, i,
                   (long long)t.stride[i], align);
+  // the kernels walk rows through 32-bit buffer descriptors (RowCursor)
+  if (t.size[2] > 1 && (t.stride[2] < 0 || t.stride[2] * es >= kMaxRowBytes))
+    return fail(SAF_EUNSUPPORTED, "%s row stride (%lld elements) must be below %d bytes", name,
+                (long long)t.stride[2], kMaxRowBytes);
   return SAF_OK;
 }
 

@@ -257,6 +257,34 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t rows_rsrc(const T* base, int64
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<T*>(base + (int64_t)j0 * st), 0, num, kBufferWord3);
 }
 
+// rows_rsrc for a sequence of row blocks walked in order, without a 64-bit
+// multiply or compare per block: the address of the current first row and
+// the rows left before T_len, advanced by a fixed row count.  The record
+// count is the rows left (at least 0, at most lim_rows) times the row pitch,
+// which is below 2^31 whenever the host's limit on row pitches (kMaxRowBytes)
+// holds; it then equals rows_rsrc's count for every row a 64-row tile reads.
+constexpr int kMaxRowBytes = 1 << 24;
+struct RowCursor {
+  const char* ptr;
+  int rows_left, row_bytes, lim_rows;
+
+  template <typename T>
+  __device__ __forceinline__ void init(const T* base, int64_t st, int j0, int T_len) {
+    row_bytes = (int)(st * (int64_t)sizeof(T));
+    lim_rows = 0x7fffffff / (row_bytes > 0 ? row_bytes : 1);
+    ptr = reinterpret_cast<const char*>(base + (int64_t)j0 * st);
+    rows_left = T_len - j0;
+  }
+  __device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc() const {
+    const int r = min(max(rows_left, 0), lim_rows);
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(ptr), 0, r * row_bytes, kBufferWord3);
+  }
+  __device__ __forceinline__ void advance(int rows) {
+    ptr += (int64_t)rows * row_bytes;
+    rows_left -= rows;
+  }
+};
+
 // Stage a 64-key V tile (rows j0..j0+63 of one head) into registers:
 // item idx covers keys 2kp, 2kp+1 and columns 8c..8c+7.  Rows >= T are zero.
 template <typename T, int HD, int NTHR> struct VStager {
