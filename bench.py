@@ -360,6 +360,62 @@ def c2_check(model, x):
             "reference": os.path.relpath(C2_FIXTURE, REPO)}
 
 
+C3_FIXTURE = os.path.join(REPO, "tests", "golden", "c3_check.npz")
+C4_FIXTURE = os.path.join(REPO, "tests", "golden", "c4_check.npz")
+
+
+def _cosine(a, b):
+    a, b = a.double().flatten(), b.double().flatten()
+    return float(a @ b / (a.norm() * b.norm()))
+
+
+def _fixture_for(path, tokens, **shape):
+    """The fixture at `path` if it was made for these tokens and shape."""
+    import hashlib
+    if not os.path.exists(path):
+        return None
+    z = np.load(path)
+    if str(z["tokens_sha256"]) != hashlib.sha256(tokens.cpu().numpy().astype(np.int64).tobytes()).hexdigest():
+        return None
+    if any(int(z[k]) != v for k, v in shape.items()):
+        return None
+    return z
+
+
+def c3_check(model, x):
+    """Cosine of the GPU prefill (last-position logits of both sequences, and
+    the final LayerNorm output at sampled positions) against the fp32 oracle's
+    values stored by tests/golden/make_c3_fixture.py; None if the fixture is
+    absent or was made for another workload."""
+    import torch
+    z = _fixture_for(C3_FIXTURE, x, T=x.size(1), L=model.config.n_layer)
+    if z is None:
+        return None
+    with torch.inference_mode():
+        last = model(x)[:, -1].float().cpu()
+        hid = model.forward_hidden(x)[:, torch.as_tensor(z["positions"], device=x.device)].float().cpu()
+    cl = _cosine(last, torch.from_numpy(z["logits_last"]))
+    ch = _cosine(hid, torch.from_numpy(z["hidden"]))
+    return {"logits_cosine_vs_fp32_oracle": round(cl, 7), "hidden_cosine_vs_fp32_oracle": round(ch, 7),
+            "pass": min(cl, ch) >= 0.9999, "bound": 0.9999, "reference": os.path.relpath(C3_FIXTURE, REPO)}
+
+
+def c4_check(backbone, ids, f, L):
+    """Cosine of the GPU backbone output (final-norm hidden states at sampled
+    positions of every sequence) against the fp32 oracle's, stored per frozen
+    count f by tests/golden/make_c4_fixture.py; None if absent."""
+    import torch
+    import qwen
+    z = _fixture_for(C4_FIXTURE, ids, T=ids.size(1), B=ids.size(0), L=L)
+    if z is None or f"hidden_f{f}" not in z.files:
+        return None
+    with torch.inference_mode():
+        got = qwen.backbone_forward(backbone, ids)[:, torch.as_tensor(z["positions"], device=ids.device)]
+    c = _cosine(got.float().cpu(), torch.from_numpy(z[f"hidden_f{f}"]))
+    return {"hidden_cosine_vs_fp32_oracle": round(c, 7), "pass": c >= 0.9999, "bound": 0.9999,
+            "reference": os.path.relpath(C4_FIXTURE, REPO)}
+
+
 def run_c2(args):
     import torch
     from nanogpt import model as model_mod
@@ -466,6 +522,12 @@ def run_c4(args):
         calls = qwen.fused_dispatch_count() - n0
         if calls != (0 if use_sdpa else L):
             raise RuntimeError(f"dispatch verification failed: {calls} fused calls for {L} layers")
+    check = c4_check(backbone, ids, f, L)
+    if check is not None:
+        log(f"check against the fp32 oracle fixture: {check}")
+        if not check["pass"]:
+            raise RuntimeError(f"C4 output check failed: {check}")
+    with torch.inference_mode():
         step_ms, wall, summ = timed_steps(lambda: qwen.backbone_forward(backbone, ids), args.steps,
                                           args.warmup, not args.no_timer and not use_sdpa)
     total_ms = sum(step_ms)
@@ -492,6 +554,7 @@ def run_c4(args):
                    "median_step_ms": round(statistics.median(step_ms), 3),
                    "wall_s": round(wall, 3)},
         "roofline": roof,
+        "check": check,
         "cpu_baseline": cpu,
     }
     line.update(extra)
@@ -611,7 +674,9 @@ def build_c3_model(T, L, device, seed=1337):
     heads, hd 128, vocab 50304, RoPE, no bias), bf16 random init; per layer
     the heads randperm(16, seed + layer)[:4] are frozen to dense
     lower-triangular row-stochastic patterns softmax(N(0,1) logits masked
-    causally), stored compactly in bf16 as (4, T, T)."""
+    causally), stored compactly in bf16 as (4, T, T).  Weights and pattern
+    logits are drawn on the CPU (seeded), so the host reproduces the device's
+    model exactly (tests/golden/make_c3_fixture.py)."""
     import torch
     from nanogpt.model import GPT, GPTConfig
 
@@ -620,14 +685,14 @@ def build_c3_model(T, L, device, seed=1337):
                     position_encoding="rope", rand_attn_prior_repr="dense", freeze_pattern_dtype="bfloat16",
                     rand_seed=seed)
     model = GPT(cfg).to(device=device, dtype=torch.bfloat16).eval()
-    causal = torch.ones(T, T, dtype=torch.bool, device=device).tril()
+    causal = torch.ones(T, T, dtype=torch.bool).tril()
     plan = {}
     for layer in range(L):
         heads = torch.randperm(cfg.n_head, generator=torch.Generator().manual_seed(seed + layer))[:4].tolist()
-        g = torch.Generator(device=device).manual_seed(seed + layer)
-        logits = torch.randn(len(heads), T, T, generator=g, device=device)
+        g = torch.Generator().manual_seed(seed + layer)
+        logits = torch.randn(len(heads), T, T, generator=g)
         logits.masked_fill_(~causal, float("-inf"))
-        model.transformer.h[layer].attn.freeze_heads(heads, torch.softmax(logits, dim=-1))
+        model.transformer.h[layer].attn.freeze_heads(heads, torch.softmax(logits, dim=-1).to(device))
         del logits
         plan[layer] = [(h, "dense", 0.0) for h in heads]
     x = torch.randint(0, 50257, (2, T), generator=torch.Generator().manual_seed(seed + 1)).to(device)
@@ -655,6 +720,12 @@ def run_c3(args):
         torch.cuda.synchronize()
         if model_mod.fused_dispatch_count() - before != L:
             raise RuntimeError("dispatch verification failed")
+    check = c3_check(model, x)
+    if check is not None:
+        log(f"check against the fp32 oracle fixture: {check}")
+        if not check["pass"]:
+            raise RuntimeError(f"C3 output check failed: {check}")
+    with torch.inference_mode():
         step_ms, wall, summ = timed_steps(lambda: model(x), args.steps, args.warmup, not args.no_timer)
     total_ms = sum(step_ms)
     tok_s = x.numel() * args.steps / (total_ms / 1000.0)
@@ -686,6 +757,7 @@ def run_c3(args):
                    "live_flops": n_live * B * 4 * hd * T * (T + 1) // 2,
                    "median_step_ms": round(statistics.median(step_ms), 3), "wall_s": round(wall, 3)},
         "roofline": roof,
+        "check": check,
         "cpu_baseline": None,
     }
     line.update(extra)

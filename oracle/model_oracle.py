@@ -111,8 +111,10 @@ def block(x, sd, l, fr, cos, sin, n_head, path):
 
 
 @torch.no_grad()
-def gpt_forward(sd, cfg, freeze, idx, path="split", all_positions=False, layers=None, positions=None):
-    """Logits of the reference GPT on CPU fp32.
+def gpt_forward(sd, cfg, freeze, idx, path="split", all_positions=False, layers=None, positions=None,
+                head=True):
+    """Logits of the reference GPT on CPU fp32 (head=False: the final
+    LayerNorm's output at the same positions instead).
 
     sd: float32 state dict; cfg: dict with n_layer, n_head, n_embd,
     position_encoding, rope_base; freeze: per-layer records
@@ -135,4 +137,4 @@ def gpt_forward(sd, cfg, freeze, idx, path="split", all_positions=False, layers=
         x = x[:, torch.as_tensor(positions), :]
     elif not all_positions:
         x = x[:, -1:, :]
-    return F.linear(x, sd["lm_head.weight"])
+    return F.linear(x, sd["lm_head.weight"]) if head else x

@@ -34,12 +34,14 @@ def qwen_config(n_layers=24, hidden=896, n_heads=14, n_kv_heads=2, head_dim=64,
 
 
 def build_model(cfg, device="cuda", dtype=torch.bfloat16, seed=1337):
-    """Random-init Qwen3ForCausalLM (transformers' own N(0, 0.02) init)."""
+    """Random-init Qwen3ForCausalLM (transformers' own N(0, 0.02) init),
+    drawn on the CPU from `seed` and then moved, so the host reproduces the
+    device's weights exactly."""
     from transformers import Qwen3ForCausalLM
     torch.manual_seed(seed)
-    with torch.device(device):
+    with torch.device("cpu"):
         model = Qwen3ForCausalLM(cfg)
-    model = model.to(dtype=dtype).eval()
+    model = model.to(device=device, dtype=dtype).eval()
     model.config.use_cache = False
     return model
 

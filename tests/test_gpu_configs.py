@@ -19,10 +19,17 @@ relative-L2 <= 1e-2 (north_star), as the reference's own grid checks
   C4  B=4, 14 query / 2 KV heads (kvidx), T=4096, hd 64, f in {0, 4, 7, 10}
       causal-mean heads (scan), and f = 7 as dense mean patterns
 
-Model level: C0 (12 layers, T=1024) and C2 (12 layers, T=16384) built exactly
-as bench.py builds them, bf16 on the GPU, against the fp32 oracle of the
-reference's CPU split path on the host: logits cosine >= 0.9999 at every
-position (C0) or at sampled positions plus the last one (C2).
+Model level, every config's whole model built exactly as bench.py builds it,
+bf16 on the GPU, against the fp32 oracle of the reference's CPU split path:
+  C0 (12 layers, T=1024) and C2 (12 layers, T=16384): the oracle runs on the
+      host in the test; logits cosine >= 0.9999 at every position (C0) or at
+      sampled positions plus the last one (C2);
+  C3 (24 layers, d 2048, B=2, T=8192) and C4 (Qwen-style, 24 layers, B=4,
+      T=4096, f in {4, 7, 10}): the oracle's values were computed on the host
+      once (tests/golden/make_c3_fixture.py, make_c4_fixture.py) for the same
+      CPU-seeded models; last-position logits and final-norm outputs at
+      sampled positions (C3), final-norm hidden states at sampled positions
+      (C4), cosine >= 0.9999.
 """
 import numpy as np
 import pytest
@@ -271,3 +278,44 @@ def test_c2_model_logits():
     cl = _cos(last, ref[:, -1:])
     assert c >= 0.9999, f"C2 sampled-position logits cosine {c:.6f}"
     assert cl >= 0.9999, f"C2 last-position logits cosine {cl:.6f}"
+
+
+# ---------------------------------------------------------------------------
+# C3 and C4: the whole model at its config's shape against fp32 oracle values
+# the host computed for the same model (tests/golden/make_c{3,4}_fixture.py)
+# ---------------------------------------------------------------------------
+
+@pytest.mark.timeout(600)
+def test_c3_model_logits():
+    """bench.py's C3 model (24 layers, d 2048, hd 128, B=2, T=8192, 4 dense
+    bf16 heads per layer): last-position logits of both sequences and the
+    final LayerNorm output at sampled positions, cosine >= 0.9999."""
+    import bench
+    print("[case] C3 model build", flush=True)
+    m, x, plan = bench.build_c3_model(8192, 24, DEV)
+    assert sum(len(v) for v in plan.values()) == 96
+    check = bench.c3_check(m, x)
+    assert check is not None, "tests/golden/c3_check.npz missing or made for another workload"
+    print(f"C3 {check}", flush=True)
+    assert check["pass"], check
+
+
+@pytest.mark.timeout(600)
+@pytest.mark.parametrize("rate,f", [(0.25, 4), (0.5, 7), (0.75, 10)])
+def test_c4_model_hidden(rate, f):
+    """bench.py's C4 model (Qwen3-style GQA, 24 layers, hidden 896, 14q/2kv,
+    B=4, T=4096) with f causal-mean query heads per layer on the closed-form
+    scan: final-norm hidden states at sampled positions of every sequence,
+    cosine >= 0.9999."""
+    import bench
+    import qwen
+    print(f"[case] C4 model f={f}", flush=True)
+    cfg = qwen.qwen_config(n_layers=24, max_positions=4096)
+    model = qwen.build_model(cfg, device=DEV, dtype=torch.bfloat16, seed=SEED)
+    _, masks = qwen.convert_with_rate(model, rate, 4096)
+    assert int(masks[0].sum()) == f
+    ids = torch.randint(0, 151643, (4, 4096), generator=torch.Generator().manual_seed(SEED)).to(DEV)
+    check = bench.c4_check(model.model, ids, f, 24)
+    assert check is not None, "tests/golden/c4_check.npz missing or made for another workload"
+    print(f"C4 f={f} {check}", flush=True)
+    assert check["pass"], check
