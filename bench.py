@@ -400,10 +400,14 @@ def c3_check(model, x):
             "pass": min(cl, ch) >= 0.9999, "bound": 0.9999, "reference": os.path.relpath(C3_FIXTURE, REPO)}
 
 
-def c4_check(backbone, ids, f, L):
+def c4_check(backbone, ids, f, L, bound=None):
     """Cosine of the GPU backbone output (final-norm hidden states at sampled
     positions of every sequence) against the fp32 oracle's, stored per frozen
-    count f by tests/golden/make_c4_fixture.py; None if absent."""
+    count f by tests/golden/make_c4_fixture.py; None if absent.  The default
+    bound (bf16 runs) allows 1.5x the error that the same model reaches in
+    bf16 through torch alone on the host (stored beside the oracle values):
+    this 24-layer random-init model amplifies bf16 rounding, and transformers'
+    own bf16 forward of it stays near cosine 0.9997."""
     import torch
     import qwen
     z = _fixture_for(C4_FIXTURE, ids, T=ids.size(1), B=ids.size(0), L=L)
@@ -412,8 +416,11 @@ def c4_check(backbone, ids, f, L):
     with torch.inference_mode():
         got = qwen.backbone_forward(backbone, ids)[:, torch.as_tensor(z["positions"], device=ids.device)]
     c = _cosine(got.float().cpu(), torch.from_numpy(z[f"hidden_f{f}"]))
-    return {"hidden_cosine_vs_fp32_oracle": round(c, 7), "pass": c >= 0.9999, "bound": 0.9999,
-            "reference": os.path.relpath(C4_FIXTURE, REPO)}
+    level = float(z[f"bf16_cos_f{f}"])
+    if bound is None:
+        bound = 1.0 - 1.5 * (1.0 - level)
+    return {"hidden_cosine_vs_fp32_oracle": round(c, 7), "torch_bf16_cosine": round(level, 7),
+            "pass": c >= bound, "bound": round(bound, 7), "reference": os.path.relpath(C4_FIXTURE, REPO)}
 
 
 def run_c2(args):

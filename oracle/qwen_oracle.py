@@ -45,8 +45,12 @@ def rms_norm(x, w, eps):
     return w * (x * torch.rsqrt(x.pow(2).mean(-1, keepdim=True) + eps))
 
 
-def rope_cache(hd, T, theta):
-    inv = 1.0 / (theta ** (torch.arange(0, hd, 2, dtype=torch.int64).float() / hd))
+def rope_cache(hd, T, theta, inv_freq=None):
+    """cos, sin (T, hd) of the default RoPE; inv_freq overrides the
+    frequencies theta^(-2i/hd) (e.g. with those of a model cast to bf16,
+    whose inv_freq buffer transformers rounds along with the weights)."""
+    inv = 1.0 / (theta ** (torch.arange(0, hd, 2, dtype=torch.int64).float() / hd)) if inv_freq is None \
+        else inv_freq.float()
     freqs = torch.outer(torch.arange(T, dtype=torch.float32), inv)
     emb = torch.cat((freqs, freqs), dim=-1)
     return emb.cos(), emb.sin()
@@ -102,15 +106,18 @@ def attention(x, sd, p, cfg, fr, cos, sin):
 
 
 @torch.no_grad()
-def qwen_forward(sd, cfg, freeze, idx, layers=None):
+def qwen_forward(sd, cfg, freeze, idx, layers=None, inv_freq=None):
     """Last hidden state (B, T, hidden) of the hybrid Qwen3 backbone.
 
     sd: float32 state dict (transformers names); cfg: dict with n_layers,
     n_heads, n_kv_heads, head_dim, eps, rope_theta; freeze: per-layer records
-    for frozen_patterns() or None; layers: run only these layer indices."""
+    for frozen_patterns() or None; layers: run only these layer indices;
+    inv_freq: the model's RoPE frequencies if they are not theta's exact ones
+    (transformers' rotary inv_freq buffer is cast with the model, so a bf16
+    model rotates with bf16-rounded frequencies, computed in fp32)."""
     x = sd["model.embed_tokens.weight"][idx].float()
     T = idx.size(1)
-    cos, sin = rope_cache(cfg["head_dim"], T, cfg["rope_theta"])
+    cos, sin = rope_cache(cfg["head_dim"], T, cfg["rope_theta"], inv_freq)
     for l in (range(cfg["n_layers"]) if layers is None else layers):
         p = f"model.layers.{l}."
         h = rms_norm(x, sd[p + "input_layernorm.weight"], cfg["eps"])

@@ -29,7 +29,10 @@ bf16 on the GPU, against the fp32 oracle of the reference's CPU split path:
       once (tests/golden/make_c3_fixture.py, make_c4_fixture.py) for the same
       CPU-seeded models; last-position logits and final-norm outputs at
       sampled positions (C3), final-norm hidden states at sampled positions
-      (C4), cosine >= 0.9999.
+      (C4).  Bounds: cosine >= 0.9999 (C3); C4 cosine >= 0.99999 in fp32, and
+      in bf16 within 1.5x the error of the same model run in bf16 through
+      torch alone on the host (the 24-layer random-init Qwen model amplifies
+      bf16 rounding: transformers' own bf16 forward reaches about 0.9997).
 """
 import numpy as np
 import pytest
@@ -301,21 +304,30 @@ def test_c3_model_logits():
 
 
 @pytest.mark.timeout(600)
+@pytest.mark.parametrize("dtype", ["fp32", "bf16"])
 @pytest.mark.parametrize("rate,f", [(0.25, 4), (0.5, 7), (0.75, 10)])
-def test_c4_model_hidden(rate, f):
+def test_c4_model_hidden(rate, f, dtype):
     """bench.py's C4 model (Qwen3-style GQA, 24 layers, hidden 896, 14q/2kv,
-    B=4, T=4096) with f causal-mean query heads per layer on the closed-form
-    scan: final-norm hidden states at sampled positions of every sequence,
-    cosine >= 0.9999."""
+    B=4, T=4096) with f causal-mean query heads per layer: final-norm hidden
+    states at sampled positions of every sequence against the fp32 oracle.
+      fp32: the bf16 model cast to fp32 (the fp32 kernels, the adapter's
+            torch prologue): cosine >= 0.99999;
+      bf16: the bench's model (closed-form scan for the frozen heads): at most
+            1.5x the error of the same model run in bf16 through torch alone
+            on the host (cosine ~0.9997 there; bench.c4_check)."""
     import bench
     import qwen
-    print(f"[case] C4 model f={f}", flush=True)
+    print(f"[case] C4 model f={f} {dtype}", flush=True)
     cfg = qwen.qwen_config(n_layers=24, max_positions=4096)
     model = qwen.build_model(cfg, device=DEV, dtype=torch.bfloat16, seed=SEED)
+    if dtype == "fp32":
+        model = model.float()
     _, masks = qwen.convert_with_rate(model, rate, 4096)
     assert int(masks[0].sum()) == f
     ids = torch.randint(0, 151643, (4, 4096), generator=torch.Generator().manual_seed(SEED)).to(DEV)
-    check = bench.c4_check(model.model, ids, f, 24)
+    n0 = qwen.fused_dispatch_count()
+    check = bench.c4_check(model.model, ids, f, 24, bound=0.99999 if dtype == "fp32" else None)
+    assert qwen.fused_dispatch_count() - n0 == 24
     assert check is not None, "tests/golden/c4_check.npz missing or made for another workload"
-    print(f"C4 f={f} {check}", flush=True)
+    print(f"C4 f={f} {dtype} {check}", flush=True)
     assert check["pass"], check

@@ -97,29 +97,25 @@ def test_noalloc_matches_workspace_entry_hd64():
 
 def test_noalloc_refuses_oversized_scan():
     """B * n_scan * T large enough that the scan's look-back words exceed the
-    scratch: refused with SAF_EWORKSPACE before any launch (the descriptors
-    point at a small real buffer; nothing reads them)."""
+    scratch (2 x 128 closed-form heads at hd 256, T = 16384: 64 MiB of words
+    plus the 256-byte header): refused with SAF_EWORKSPACE before any launch.
+    v and out are real tensors of that shape (2.1 GB each), so even a
+    regressed size check would run in bounds of them."""
     E = _ext()
     L = E.lib()
-    B, H, T, hd = 64, 64, 16384, 64
-    buf = torch.empty(256, dtype=torch.uint8, device=DEV)
-
-    def desc(shape, dtype):
-        d = E.SafTensor()
-        d.data, d.dtype, d.ndim = buf.data_ptr(), dtype, len(shape)
-        st = 1
-        for i in reversed(range(len(shape))):
-            d.size[i], d.stride[i] = shape[i], st
-            st *= shape[i]
-        return d
-
+    B, H, T, hd = 2, 128, 16384, 256
+    need = 256 + 8 * B * H * (T // 128) * hd
+    assert need > (64 << 20)
+    v = torch.zeros(B, H, T, hd, dtype=torch.bfloat16, device=DEV)
+    out = torch.empty_like(v)
     a = E.SafMixedAttnArgs()
-    a.v = desc((B, H, T, hd), E.SAF_BF16)
-    a.out = desc((B, H, T, hd), E.SAF_BF16)
+    a.v = E.tensor_desc(v)
+    a.out = E.tensor_desc(out)
     a.n_heads = H
     keep = [E.host_i32([2] * H), E.host_i32([1] * H), E.host_f32([0.0] * H)]
     a.frozen, a.closed_kind, a.closed_param = keep
-    a.sm_scale = 0.125
+    a.sm_scale = 0.0625
+    assert L.saf_mixed_attn_workspace_bytes(ctypes.byref(a)) >= need
     rc = L.saf_mixed_attn_fwd_noalloc(ctypes.byref(a), torch.cuda.current_stream().cuda_stream)
     assert rc == E.SAF_EWORKSPACE
     assert b"maximum" in L.saf_last_error()
