@@ -66,6 +66,18 @@ constexpr int decomp_waves_per_eu(int hd) { return hd > 64 ? 2 : 3; }
 // SIMD).  alpha, rho and z are staged pre-multiplied by log2(e), so a cell
 // costs one add, one subtract and one exp2.
 constexpr float kFactorRange = 80.f;
+// fp16 factored form: E and V' as fp16 (unit roundoff 2^-11 each, so a cell
+// carries less rounding than the reference's bf16 P) and one MFMA per
+// operand instead of the hi + lo pair.  fp16's range is short: a factor
+// below 2^-24 flushes to zero and a subnormal one keeps an absolute error of
+// at most 2^-25.  Those errors reach y multiplied by the row factor
+// F = 2^(A + R - z_i) and at most |v|, so over T keys they stay below
+// T F 2^-24 max|v|; the form is used only where F <= 2^(kF16Budget - log2 T),
+// i.e. that sum is at most 2^-10 max|v|, and where every |V'| the workgroup
+// reads is at most kF16Max (no overflow).  Everything else takes the bf16
+// hi + lo form or the rebuild.
+constexpr int kF16Budget = 14;
+constexpr float kF16Max = 65504.f;
 
 // (The body is a device function: the kernel template's host stub is then
 // emitted for every launch site.)
@@ -98,7 +110,7 @@ __device__ __forceinline__ void decomp_body(const FrozenParams& p) {
   __shared__ __align__(16) char vs2[kFactorable ? VB : 16];
   __shared__ __align__(16) char eb0[kE0];
   __shared__ __align__(16) char eb1[kFactorable ? kEBytes : 16];
-  __shared__ float red_lds[3][NW];
+  __shared__ float red_lds[4][NW];
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (SGPR)
@@ -157,15 +169,19 @@ __device__ __forceinline__ void decomp_body(const FrozenParams& p) {
   // over the 64-distance blocks below kend_wg (a superset of what any key
   // segment of this block reaches; both maxima come from the pre-pass) and
   // the smallest z of the block's rows decide it for the whole workgroup
-  bool factored = false;
+  bool factored = false, form16 = false;
   float aoff = 0.f, roff = 0.f;
   const int nblk = (T_len + 63) / 64;
   const float* const ablk = p.a_off + (int64_t)slot * nblk;
   if constexpr (kFactorable) {
     if (p.vp != nullptr) {
       const float* const rblk = p.a_off + (int64_t)(p.n_slots + slot) * nblk;
-      float am = -INFINITY, rm = -INFINITY, zm = INFINITY;
-      for (int k = kb0 + tid; k < nkb; k += NTHR) am = fmaxf(am, ablk[k]);
+      const float* const vblk = p.vmax + ((int64_t)b * p.n_slots + slot) * nblk;
+      float am = -INFINITY, rm = -INFINITY, zm = INFINITY, vm = 0.f;
+      for (int k = kb0 + tid; k < nkb; k += NTHR) {
+        am = fmaxf(am, ablk[k]);
+        vm = fmaxf(vm, vblk[k]);
+      }
       for (int k = tid; k < nkb_qb; k += NTHR) rm = fmaxf(rm, rblk[k]);
       for (int i = q0 + tid; i < kend_wg; i += NTHR)
         zm = fminf(zm, load_as_f32(p.z, (int64_t)ph * p.z_sh + (int64_t)i * p.z_ss, p.z_dtype));
@@ -174,26 +190,37 @@ __device__ __forceinline__ void decomp_body(const FrozenParams& p) {
         am = fmaxf(am, __shfl_xor(am, off));
         rm = fmaxf(rm, __shfl_xor(rm, off));
         zm = fminf(zm, __shfl_xor(zm, off));
+        vm = fmaxf(vm, __shfl_xor(vm, off));
       }
       if (lane == 0) {
         red_lds[0][wave] = am;
         red_lds[1][wave] = rm;
         red_lds[2][wave] = zm;
+        red_lds[3][wave] = vm;
       }
       __syncthreads();
       am = fmaxf(fmaxf(red_lds[0][0], red_lds[0][1]), fmaxf(red_lds[0][2], red_lds[0][3]));
       rm = fmaxf(fmaxf(red_lds[1][0], red_lds[1][1]), fmaxf(red_lds[1][2], red_lds[1][3]));
       zm = fminf(fminf(red_lds[2][0], red_lds[2][1]), fminf(red_lds[2][2], red_lds[2][3])) * kLog2e;
+      vm = fmaxf(fmaxf(red_lds[3][0], red_lds[3][1]), fmaxf(red_lds[3][2], red_lds[3][3]));
       factored = __builtin_isfinite(am) && __builtin_isfinite(rm) && __builtin_isfinite(zm) &&
                  zm >= am + rm - kFactorRange;
+      // fp16 form: every V' this workgroup reads in fp16 range, and the row
+      // factor at most 2^(14 - ceil(log2 T)) (see kF16Budget)
+      const int lgT = T_len > 1 ? 32 - __clz(T_len - 1) : 0;
+      form16 = factored && vm <= kF16Max && zm >= am + rm - (float)(kF16Budget - lgT);
       aoff = am;
       roff = rm;
     }
   }
 
   if constexpr (kFactorable) {
-    if (factored) {
-      const T* vpbase = reinterpret_cast<const T*>(p.vp) + ((int64_t)b * p.n_slots + slot) * T_len * HD;
+    // F16: the fp16 form (E and V' in fp16, one MFMA per operand); else the
+    // bf16 form with E as a hi + lo pair
+    auto run_factored = [&](auto f16tag) {
+      constexpr bool F16 = decltype(f16tag)::value;
+      using TE = typename std::conditional<F16, _Float16, T>::type;
+      const TE* vpbase = reinterpret_cast<const TE*>(F16 ? p.vp16 : p.vp) + ((int64_t)b * p.n_slots + slot) * T_len * HD;
       uint32_t voff[VN];
 #pragma unroll
       for (int pp = 0; pp < VN; ++pp) voff[pp] = vrow_dma_offset<T, HD>((NW * pp + wave) * 64 + lane, HD);
@@ -252,8 +279,13 @@ __device__ __forceinline__ void decomp_body(const FrozenParams& p) {
             const int d = q0 - ej0 + BM - m;
             // A_k - A - R; -inf for a block whose keys all have alpha -inf
             const float x = m < RW && d >= 0 && d < T_len ? fast_exp2(er[u] + (ab - aoff - roff)) : 0.f;
-            hv[u] = Elem<T>::pack2(x, 0.f) & 0xffffu;
-            lv[u] = Elem<T>::pack2(x - Elem<T>::lo(hv[u]), 0.f) & 0xffffu;
+            if constexpr (F16) {
+              hv[u] = Elem<_Float16>::pack2(x, 0.f) & 0xffffu;
+              lv[u] = 0u;
+            } else {
+              hv[u] = Elem<T>::pack2(x, 0.f) & 0xffffu;
+              lv[u] = Elem<T>::pack2(x - Elem<T>::lo(hv[u]), 0.f) & 0xffffu;
+            }
           }
 #pragma unroll
           for (int c = 0; c < 8; ++c) {
@@ -261,7 +293,7 @@ __device__ __forceinline__ void decomp_body(const FrozenParams& p) {
             const int pos = 2 * tid + e0 - c;  // even: its position in copy c
             if (pos >= 0) {
               *reinterpret_cast<uint32_t*>(&ew[0][ecopy(c) + pos]) = hv[e0] | (hv[e0 + 1] << 16);
-              *reinterpret_cast<uint32_t*>(&ew[1][ecopy(c) + pos]) = lv[e0] | (lv[e0 + 1] << 16);
+              if constexpr (!F16) *reinterpret_cast<uint32_t*>(&ew[1][ecopy(c) + pos]) = lv[e0] | (lv[e0 + 1] << 16);
             }
           }
         }
@@ -313,7 +345,7 @@ __device__ __forceinline__ void decomp_body(const FrozenParams& p) {
           for (int ks = 0; ks < 2; ++ks)
 #pragma unroll
             for (int sh = 0; sh < 2; ++sh) {
-              uint4 pb[QT], pl[QT];
+              uint4 pb[QT], pl[QT] = {};
 #pragma unroll
               for (int qt = 0; qt < QT; ++qt) {
                 if (QT == 2 && qt == 1 && ks == 1) {
@@ -321,7 +353,7 @@ __device__ __forceinline__ void decomp_body(const FrozenParams& p) {
                   pl[qt] = keep_l[sh];
                 } else {
                   pb[qt] = *reinterpret_cast<const uint4*>(&ew[0][eo[qt] + 32 * ks + 16 * sh]);
-                  pl[qt] = *reinterpret_cast<const uint4*>(&ew[1][eo[qt] + 32 * ks + 16 * sh]);
+                  if constexpr (!F16) pl[qt] = *reinterpret_cast<const uint4*>(&ew[1][eo[qt] + 32 * ks + 16 * sh]);
                 }
               }
               if (ks == 0) {
@@ -341,11 +373,13 @@ __device__ __forceinline__ void decomp_body(const FrozenParams& p) {
 #pragma unroll
               for (int dt = 0; dt < NDT; ++dt)
 #pragma unroll
-                for (int qt = 0; qt < QT; ++qt) o[qt][dt] = Elem<T>::mfma(a[dt], pb[qt], o[qt][dt]);
+                for (int qt = 0; qt < QT; ++qt) o[qt][dt] = Elem<TE>::mfma(a[dt], pb[qt], o[qt][dt]);
+              if constexpr (!F16) {
 #pragma unroll
-              for (int dt = 0; dt < NDT; ++dt)
+                for (int dt = 0; dt < NDT; ++dt)
 #pragma unroll
-                for (int qt = 0; qt < QT; ++qt) o[qt][dt] = Elem<T>::mfma(a[dt], pl[qt], o[qt][dt]);
+                  for (int qt = 0; qt < QT; ++qt) o[qt][dt] = Elem<TE>::mfma(a[dt], pl[qt], o[qt][dt]);
+              }
             }
         }
         if (j + 1 < nkb) store_er(ENext());
@@ -379,6 +413,12 @@ __device__ __forceinline__ void decomp_body(const FrozenParams& p) {
       __builtin_amdgcn_s_waitcnt(waitcnt_vm_lgkm0(0));
 #pragma unroll
       for (int qt = 0; qt < QT; ++qt) rowscale[qt] = fast_exp2(aoff + roff - zq[qt]);
+    };
+    if (factored) {
+      if (form16)
+        run_factored(std::true_type());
+      else
+        run_factored(std::false_type());
     }
   }
   if (!factored) {
@@ -489,7 +529,8 @@ void frozen_decomp_kernel(const FrozenParams p) {
   decomp_body<T, HD, QT>(p);
 }
 
-// vp[b, slot, j] = 2^(alpha_j log2 e - A_k) v[b, v_head, j] in T, with
+// vp[b, slot, j] = 2^(alpha_j log2 e - A_k) v[b, v_head, j] in T (and in
+// fp16 in vp16, with the block's largest |value| in vmax[(b, slot), k]), with
 // A_k = max alpha log2 e over the 64-key block k = j / 64 of the slot's head
 // (a_off[slot * nblk + k], nblk = ceil(T / 64)).  Batch 0's workgroup also
 // writes r2[slot, d] = rho_d log2 e for the block's 64 distances (the main
@@ -534,7 +575,10 @@ __global__ __launch_bounds__(256) void decomp_prescale_kernel(const FrozenParams
       if (lane == 0) p.a_off[(int64_t)(p.n_slots + slot) * nblk + kb] = rmx;
     }
   }
-  T* vp = reinterpret_cast<T*>(p.vp) + ((int64_t)b * p.n_slots + slot) * p.T * HD;
+  const int64_t row0 = ((int64_t)b * p.n_slots + slot) * p.T;
+  T* vp = reinterpret_cast<T*>(p.vp) + row0 * HD;
+  _Float16* vp16 = reinterpret_cast<_Float16*>(p.vp16) + row0 * HD;
+  float vmx = 0.f;  // largest |V'| of this block (NaN inputs are left to the bf16 copy)
 #pragma unroll
   for (int u = 0; u < PER; ++u) {
     const int idx = tid + 256 * u, rl = idx / CH, c = idx % CH;
@@ -542,12 +586,26 @@ __global__ __launch_bounds__(256) void decomp_prescale_kernel(const FrozenParams
     const float f = ar == -INFINITY ? 0.f : fast_exp2(ar - am);  // am is finite when ar is
     if (j0 + rl < p.T) {
       const uint32_t in[4] = {w[u].x, w[u].y, w[u].z, w[u].w};
-      uint32_t out[4];
+      uint32_t out[4], out16[4];
 #pragma unroll
-      for (int m = 0; m < 4; ++m) out[m] = Elem<T>::pack2(Elem<T>::lo(in[m]) * f, Elem<T>::hi(in[m]) * f);
+      for (int m = 0; m < 4; ++m) {
+        const float x0 = Elem<T>::lo(in[m]) * f, x1 = Elem<T>::hi(in[m]) * f;
+        out[m] = Elem<T>::pack2(x0, x1);
+        out16[m] = Elem<_Float16>::pack2(x0, x1);
+        vmx = fmaxf(vmx, fmaxf(fabsf(x0), fabsf(x1)));
+      }
       *reinterpret_cast<uint4*>(vp + (int64_t)(j0 + rl) * HD + 8 * c) = make_uint4(out[0], out[1], out[2], out[3]);
+      *reinterpret_cast<uint4*>(vp16 + (int64_t)(j0 + rl) * HD + 8 * c) =
+          make_uint4(out16[0], out16[1], out16[2], out16[3]);
     }
   }
+  __shared__ float red[4];
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) vmx = fmaxf(vmx, __shfl_xor(vmx, off));
+  if (lane == 0) red[tid >> 6] = vmx;
+  __syncthreads();
+  if (tid == 0)
+    p.vmax[((int64_t)b * p.n_slots + slot) * ((p.T + 63) / 64) + kb] = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
 }
 
 

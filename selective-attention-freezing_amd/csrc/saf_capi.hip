@@ -507,8 +507,9 @@ int run_dense(const saf_tensor_t& patt, const saf_tensor_t& v, const saf_tensor_
 // blocks (flash, dense and decomposed kernels run one after the other and
 // share them), then the factored decomposed form's per-64-block maxima of
 // alpha and of rho a_off (2 x n_dec x ceil(T / 64) floats), rho log2 e r2
-// (n_dec x T floats) and key-scaled values vp (B, n_dec, T, HD) bf16 (bf16,
-// hd <= 128 only).
+// (n_dec x T floats), key-scaled values vp (B, n_dec, T, HD) in bf16 and
+// again in fp16, and their per-block largest magnitudes vmax (B x n_dec x
+// ceil(T / 64) floats) (bf16, hd <= 128 only).
 int64_t round256(int64_t n) { return (n + 255) / 256 * 256; }
 
 int64_t part_region_bytes(const saf_mixed_attn_args* args, const Plan& pl) {
@@ -534,10 +535,15 @@ int64_t decomp_aoff_bytes(const Plan& pl) {
 }
 int64_t decomp_r2_bytes(const Plan& pl) { return round256((int64_t)pl.decomp.size() * pl.T * 4); }
 
+// key-scaled values in bf16, then in fp16, then their per-block maxima
+int64_t decomp_v1_bytes(const Plan& pl) { return round256((int64_t)pl.B * pl.decomp.size() * pl.T * pl.HD * 2); }
+int64_t decomp_vmax_bytes(const Plan& pl) {
+  return round256((int64_t)pl.B * pl.decomp.size() * ((pl.T + 63) / 64) * 4);
+}
+
 int64_t decomp_vp_bytes(const Plan& pl) {
   if (pl.dtype != SAF_BF16 || pl.HD > 128 || pl.decomp.empty()) return 0;
-  const int64_t nd = (int64_t)pl.decomp.size();
-  return decomp_aoff_bytes(pl) + decomp_r2_bytes(pl) + round256((int64_t)pl.B * nd * pl.T * pl.HD * 2);
+  return decomp_aoff_bytes(pl) + decomp_r2_bytes(pl) + 2 * decomp_v1_bytes(pl) + decomp_vmax_bytes(pl);
 }
 
 // Decomposed P.V (rebuilt in registers), causally balanced like run_dense
@@ -581,6 +587,8 @@ int run_decomp(const saf_mixed_attn_args* a, const Plan& pl, hipStream_t s) {
     p.a_off = reinterpret_cast<float*>(w);
     p.r2 = reinterpret_cast<float*>(w + decomp_aoff_bytes(pl));
     p.vp = w + decomp_aoff_bytes(pl) + decomp_r2_bytes(pl);
+    p.vp16 = reinterpret_cast<char*>(p.vp) + decomp_v1_bytes(pl);
+    p.vmax = reinterpret_cast<float*>(reinterpret_cast<char*>(p.vp16) + decomp_v1_bytes(pl));
   }
   if (int rc = launched(timed([&] {
                           if (factored) {

@@ -98,6 +98,12 @@ struct FrozenParams {
   float* a_off;
   void* vp;
   float* r2;
+  // the same key-scaled values in fp16 (vp16, null: no fp16 factored form)
+  // and their largest magnitude per (batch, slot, 64-key block) (vmax,
+  // B x n_slots x ceil(T / 64)): the fp16 form needs every |V'| it reads
+  // below the fp16 range limit
+  void* vp16;
+  float* vmax;
   int16_t out_head[kMaxHeads];
   int16_t v_head[kMaxHeads];
   int16_t pat_head[kMaxHeads];  // dense: pattern row; decomposed: buffer row

@@ -155,6 +155,63 @@ def test_decomposed_extreme_logits(case):
     run_case(B, H, T, hd, S, fz, dec, no_patt=np_, dec_scale=40.0)
 
 
+def test_decomposed_fp16_bf16_and_rebuilt_forms():
+    """The three decomposed forms in one call (bf16 inputs), each against the
+    float64 oracle.  Head 0: a decay (alpha = 0, so the row factor is <= 1
+    and every workgroup takes the fp16 form); head 1: moderate random
+    alpha / rho (fp16 where the row factor allows, bf16 hi + lo elsewhere);
+    head 2: an attention sink alpha[0] = +12 with a steep decay (row factors
+    up to 2^17: the bf16 hi + lo form); head 3: an alpha spike of +150 at key
+    1200 (workgroups past it rebuild cell by cell).  T = 2500 (so the fp16
+    form needs row factors <= 2^2)."""
+    import kernel
+    B, H, T, hd, S = 2, 4, 2500, 64, 2560
+    g = torch.Generator().manual_seed(91)
+    d = torch.arange(S, dtype=torch.float32)
+    alpha = torch.zeros(H, S)
+    rho = torch.zeros(H, S)
+    rho[0] = -0.03 * d
+    alpha[1] = torch.randn(S, generator=g) * 0.7
+    rho[1] = torch.randn(S, generator=g) * 0.7
+    alpha[2, 0] = 12.0
+    rho[2] = -0.5 * d
+    alpha[3] = torch.randn(S, generator=g) * 0.5
+    alpha[3, 1200] = 150.0
+    rho[3] = -0.01 * d
+    z = torch.from_numpy(orc.decomposed_logz(alpha.double().numpy(), rho.double().numpy())).float()
+    frozen = torch.full((H,), 2, dtype=torch.int32)
+    q, k, v = qkv(B, H, T, hd, seed=8, dtype=torch.bfloat16)
+    y = kernel.fused_mixed_attn(q[:, :0].to(DEV), k[:, :0].to(DEV), v.to(DEV), None, frozen.to(DEV),
+                                alpha=alpha.to(DEV), rho=rho.to(DEV), z=z.to(DEV))
+    torch.cuda.synchronize()
+    ref = orc.eager_mixed_attention(None, None, f64(v), frozen.numpy(), alpha=f64(alpha), rho=f64(rho),
+                                    z=f64(z))
+    for h in range(H):
+        compare(y[:, h:h + 1], ref[:, h:h + 1], what=f"decomposed forms head {h}")
+
+
+def test_decomposed_large_values_keep_the_bf16_form():
+    """Values of magnitude ~1e5 scale to key-scaled values past the fp16
+    range, so the workgroups of a decay head (row factor <= 1, otherwise an
+    fp16 candidate) keep the bf16 form: finite outputs within bf16 rounding
+    of the float64 oracle (relative bounds: the outputs are ~1e5)."""
+    import kernel
+    B, H, T, hd, S = 1, 2, 1200, 64, 1280
+    d = torch.arange(S, dtype=torch.float32)
+    alpha = torch.zeros(H, S)
+    rho = torch.stack([-0.02 * d, -0.2 * d])
+    z = torch.from_numpy(orc.decomposed_logz(alpha.double().numpy(), rho.double().numpy())).float()
+    frozen = torch.full((H,), 2, dtype=torch.int32)
+    _, _, v = qkv(B, H, T, hd, seed=12, dtype=torch.float32)
+    v = (v * 1e5).bfloat16()
+    y = kernel.fused_mixed_attn(v[:, :0].to(DEV), v[:, :0].to(DEV), v.to(DEV), None, frozen.to(DEV),
+                                alpha=alpha.to(DEV), rho=rho.to(DEV), z=z.to(DEV))
+    torch.cuda.synchronize()
+    ref = orc.eager_mixed_attention(None, None, f64(v), frozen.numpy(), alpha=f64(alpha), rho=f64(rho),
+                                    z=f64(z))
+    compare(y.float() / 1e5, ref / 1e5, what="decomposed, |v| ~ 1e5")
+
+
 def test_decomposed_factored_and_rebuilt_workgroups():
     """The decomposed kernel picks, per workgroup, the factored form (key and
     row factors around a Toeplitz operand) when every row's z lies within
