@@ -56,24 +56,25 @@ inline int rope_lanes(int hd) {
 //   x <- w * round(x * rsqrt(mean(x^2) + eps)),  rounded to the activation dtype
 // (fp32 statistics; the two roundings of the reference module are kept), then
 // rotated.  The row's sum of squares is reduced across its lane group.
-template <typename T, bool NORM>
-__global__ __launch_bounds__(256) void rope_kernel(const RopeParams p, const int lanes) {
+//
+// Grid: blockIdx.y = one (batch, head) of q (the first B Uq) or of k, so the
+// head's base address is wave-uniform scalar arithmetic; blockIdx.x covers
+// the head's rows, LANES threads per row (a shift, no integer division).
+template <typename T, bool NORM, int LANES>
+__global__ __launch_bounds__(256) void rope_kernel(const RopeParams p) {
   const int np = p.hd / 16;  // chunk pairs per row
-  const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  const int64_t rows_q = (int64_t)p.B * p.Uq * p.T;
-  const int64_t rows = rows_q + (int64_t)p.B * p.Uk * p.T;
-  const int64_t row = gid / lanes;
-  const int c = (int)(gid & (lanes - 1));
-  const bool active = row < rows && c < np;
-  const bool is_k = row >= rows_q;
-  const int64_t rr = active ? (is_k ? row - rows_q : row) : 0;
-  const int U = max(is_k ? p.Uk : p.Uq, 1);
-  const int t = (int)(rr % p.T);
-  const int64_t bu = rr / p.T;
-  const int u = (int)(bu % U), b = (int)(bu / U);
+  const int head = blockIdx.y;
+  const bool is_k = head >= p.B * p.Uq;
+  const int hh = is_k ? head - p.B * p.Uq : head;
+  const int U = is_k ? p.Uk : p.Uq;
+  const int b = hh / U, u = hh - b * U;
+  const int gid = (int)blockIdx.x * 256 + (int)threadIdx.x;
+  const int t = gid / LANES;
+  const int c = gid & (LANES - 1);
+  const bool active = t < p.T && c < np;
   T* x = reinterpret_cast<T*>(is_k ? p.k : p.q) +
-         (is_k ? b * p.k_sb + (int64_t)u * p.k_sh + (int64_t)t * p.k_st
-               : b * p.q_sb + (int64_t)u * p.q_sh + (int64_t)t * p.q_st);
+         (is_k ? b * p.k_sb + (int64_t)u * p.k_sh + (int64_t)(active ? t : 0) * p.k_st
+               : b * p.q_sb + (int64_t)u * p.q_sh + (int64_t)(active ? t : 0) * p.q_st);
   const int d0 = 8 * c, half = p.hd / 2;
   uint4* lo_p = reinterpret_cast<uint4*>(x + d0);
   uint4* hi_p = reinterpret_cast<uint4*>(x + d0 + half);
@@ -95,7 +96,8 @@ __global__ __launch_bounds__(256) void rope_kernel(const RopeParams p, const int
     float ss = 0.f;
 #pragma unroll
     for (int m = 0; m < 8; ++m) ss = fmaf(a[m], a[m], fmaf(bv[m], bv[m], ss));
-    for (int m = 1; m < lanes; m <<= 1) ss += __shfl_xor(ss, m, lanes);
+#pragma unroll
+    for (int m = 1; m < LANES; m <<= 1) ss += __shfl_xor(ss, m, LANES);
     const float r = rsqrtf(ss / (float)p.hd + p.eps);
     if (active) {
       float wl[8], wh[8];
@@ -126,27 +128,32 @@ __global__ __launch_bounds__(256) void rope_kernel(const RopeParams p, const int
   *hi_p = make_uint4(oh[0], oh[1], oh[2], oh[3]);
 }
 
-template <typename T>
-static void launch_rope_t(const RopeParams& p, dim3 grid, int lanes, hipStream_t s) {
+template <typename T, int LANES>
+static void launch_rope_l(const RopeParams& p, hipStream_t s) {
+  const dim3 grid((unsigned)(((int64_t)p.T * LANES + 255) / 256), (unsigned)(p.B * (p.Uq + p.Uk)));
   if (p.q_w != nullptr)
-    hipLaunchKernelGGL((rope_kernel<T, true>), grid, dim3(256), 0, s, p, lanes);
+    hipLaunchKernelGGL((rope_kernel<T, true, LANES>), grid, dim3(256), 0, s, p);
   else
-    hipLaunchKernelGGL((rope_kernel<T, false>), grid, dim3(256), 0, s, p, lanes);
+    hipLaunchKernelGGL((rope_kernel<T, false, LANES>), grid, dim3(256), 0, s, p);
+}
+
+template <typename T>
+static hipError_t launch_rope_t(const RopeParams& p, hipStream_t s) {
+  switch (rope_lanes(p.hd)) {
+    case 2: launch_rope_l<T, 2>(p, s); break;
+    case 4: launch_rope_l<T, 4>(p, s); break;
+    case 8: launch_rope_l<T, 8>(p, s); break;
+    case 16: launch_rope_l<T, 16>(p, s); break;
+    default: return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
 }
 
 hipError_t launch_rope(const RopeParams& p, int dtype, hipStream_t s) {
-  const int64_t rows = (int64_t)p.B * (p.Uq + p.Uk) * p.T;
-  const int lanes = rope_lanes(p.hd);
-  const int64_t threads = rows * lanes;
-  if (threads == 0) return hipSuccess;
-  const dim3 grid((unsigned)((threads + 255) / 256));
-  if (dtype == kBF16)
-    launch_rope_t<__bf16>(p, grid, lanes, s);
-  else if (dtype == kF16)
-    launch_rope_t<_Float16>(p, grid, lanes, s);
-  else
-    return hipErrorInvalidValue;
-  return hipGetLastError();
+  if ((int64_t)p.B * (p.Uq + p.Uk) * p.T == 0) return hipSuccess;
+  if (dtype == kBF16) return launch_rope_t<__bf16>(p, s);
+  if (dtype == kF16) return launch_rope_t<_Float16>(p, s);
+  return hipErrorInvalidValue;
 }
 
 }  // namespace saf

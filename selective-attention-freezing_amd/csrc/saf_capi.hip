@@ -810,6 +810,9 @@ static int rope_common(const saf_tensor_t* q, const saf_tensor_t* k, const saf_t
   }
   if (int rc = check_act(*q, "q", 16)) return rc;
   if (int rc = check_act(*k, "k", 16)) return rc;
+  // one grid row per (batch, head) of q and k; T x 16 threads per grid row
+  if (B * (q->size[1] + k->size[1]) > 65535 || T > (int64_t(1) << 26))
+    return fail(SAF_EUNSUPPORTED, "rope: B x (Uq + Uk) must be at most 65535 and T at most 2^26");
   RopeParams p{};
   p.q = q->data; p.k = k->data;
   p.q_sb = q->stride[0]; p.q_sh = q->stride[1]; p.q_st = q->stride[2];
@@ -883,6 +886,12 @@ int saf_add_layernorm(const saf_tensor_t* x, const saf_tensor_t* delta, const sa
   p.y_rs = out->stride[0];
   p.eps = eps;
   p.wb_dtype = weight->dtype;
+  auto al16 = [&](const saf_tensor_t& t) {
+    return reinterpret_cast<uintptr_t>(t.data) % 16 == 0 && (t.size[0] <= 1 || (t.stride[0] * 2) % 16 == 0);
+  };
+  p.vec16 = C % 256 == 0 && al16(*x) && al16(*out) && (!has_d || al16(*delta)) &&
+            reinterpret_cast<uintptr_t>(weight->data) % 16 == 0 &&
+            (!has_b || reinterpret_cast<uintptr_t>(bias->data) % 16 == 0);
   return launched(launch_add_layernorm(p, x->dtype, reinterpret_cast<hipStream_t>(stream)), "add_layernorm");
 }
 

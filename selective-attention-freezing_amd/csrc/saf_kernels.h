@@ -170,6 +170,9 @@ struct AddLnParams {
   int64_t x_rs, d_rs, y_rs;  // row strides in elements
   float eps;
   int wb_dtype;
+  // C % 256 == 0, every row and the weight / bias 16-byte aligned: the
+  // half-wave-per-row kernel with 16-byte pieces
+  int vec16;
 };
 
 // Rows of one scan chunk for a head dimension (must match ScanShape in the

@@ -58,3 +58,28 @@ def test_add_layernorm_3d_view_and_rejections():
     with pytest.raises(ValueError, match="weight and bias"):
         kernel.add_layernorm_(torch.zeros(4, 768, dtype=torch.bfloat16, device="cuda"), None,
                               torch.ones(767, device="cuda"))
+
+
+@pytest.mark.parametrize("C,rows,offset", [(768, 1001, 0), (768, 999, 4), (2048, 7, 0), (256, 3, 4)])
+def test_add_layernorm_alignment_paths(C, rows, offset):
+    """Rows 16-byte aligned (half-wave rows, 16-byte pieces; odd row counts
+    leave half a wave idle) and rows only 8-byte aligned (a view offset by
+    four channels: the one-wave-per-row kernel) give the same results."""
+    import kernel
+    g = torch.Generator().manual_seed(C + rows + offset)
+    base = (torch.randn(rows, C + offset, generator=g) * 2 + 0.5).bfloat16()
+    dbase = torch.randn(rows, C + offset, generator=g).bfloat16()
+    x, d = base[:, offset:], dbase[:, offset:]
+    w = (1 + 0.1 * torch.randn(C, generator=g)).bfloat16()
+    b = (0.1 * torch.randn(C, generator=g)).bfloat16()
+    xb = base.cuda()
+    y = kernel.add_layernorm_(xb[:, offset:], dbase.cuda()[:, offset:], w.cuda(), b.cuda())
+    torch.cuda.synchronize()
+    ref_x = (x.cuda() + d.cuda()).cpu()
+    assert torch.equal(xb[:, offset:].cpu(), ref_x)
+    if offset:
+        assert torch.equal(xb[:, :offset].cpu(), base[:, :offset]), "channels outside the view changed"
+    _, yr = orc.add_layernorm(x.double().numpy(), d.double().numpy(), w.double().numpy(), b.double().numpy(),
+                              round_fn=_round(torch.bfloat16))
+    err = np.abs(y.double().cpu().numpy() - yr).max()
+    assert err <= 3e-2, f"C={C} rows={rows} offset={offset}: max-abs {err:.3e}"
