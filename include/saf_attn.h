@@ -116,6 +116,13 @@ typedef struct saf_mixed_attn_args {
   int32_t scan_spin_limit;      /* 0 = default bound of each look-back wait; < 0 = give-up
                                    drill: every scan chunk after the first gives up at once
                                    (tests of the error path) */
+  int32_t decomp_unsplit;       /* 0 = the decomposed heads' query blocks are split into key
+                                   segments for balance (fp32 partials in the workspace region
+                                   the live-head and dense kernels also use, then a combine);
+                                   1 = one workgroup per query block, no partials: for a
+                                   saf_frozen_decomp_fwd call on a second stream beside
+                                   saf_flash_fwd, whose workgroups fill the slots the causal
+                                   imbalance leaves idle (same results to fp32 rounding) */
 } saf_mixed_attn_args;
 
 /* All head kinds: live flash, dense P.V, decomposed rebuild, closed-form scan. */

@@ -546,9 +546,11 @@ int64_t decomp_vp_bytes(const Plan& pl) {
   return decomp_aoff_bytes(pl) + decomp_r2_bytes(pl) + 2 * decomp_v1_bytes(pl) + decomp_vmax_bytes(pl);
 }
 
-// Decomposed P.V (rebuilt in registers), causally balanced like run_dense
-// when the workspace holds the plan's partials (same region as the flash and
-// dense partials: the kernels run one after the other on the stream).
+// Decomposed P.V, causally balanced like run_dense when the workspace holds
+// the plan's partials (same region as the flash and dense partials: the
+// kernels run one after the other on the stream) unless args->decomp_unsplit
+// asks for one workgroup per query block (the call then shares no workspace
+// region with the live-head and dense kernels and may run beside them).
 int run_decomp(const saf_mixed_attn_args* a, const Plan& pl, hipStream_t s) {
   if (pl.decomp.empty() || pl.T == 0 || pl.B == 0) return SAF_OK;
   FrozenParams p{};
@@ -567,8 +569,8 @@ int run_decomp(const saf_mixed_attn_args* a, const Plan& pl, hipStream_t s) {
   const int BM = block_rows(frozen_qtiles(pl.HD));
   FlashPlan fp = plan_flash(pl.B, p.n_slots, pl.T, pl.HD, BM, decomp_resident(pl.HD));
   const int64_t part_off = scan_ws_bytes(pl);
-  if (pl.dtype != SAF_F32 && fp.n_items && a->workspace != nullptr && a->workspace_bytes >= part_off + fp.part_bytes &&
-      reinterpret_cast<uintptr_t>(a->workspace) % 16 == 0) {
+  if (pl.dtype != SAF_F32 && fp.n_items && !a->decomp_unsplit && a->workspace != nullptr &&
+      a->workspace_bytes >= part_off + fp.part_bytes && reinterpret_cast<uintptr_t>(a->workspace) % 16 == 0) {
     p.n_items = fp.n_items;
     p.seg_len = fp.seg_len;
     p.n_part_per_head = fp.n_part_per_head;

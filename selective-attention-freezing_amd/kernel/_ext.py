@@ -50,7 +50,8 @@ class SafMixedAttnArgs(ctypes.Structure):
                 ("workspace", ctypes.c_void_p),
                 ("workspace_bytes", ctypes.c_int64),
                 ("flash_qtiles", ctypes.c_int32),
-                ("scan_spin_limit", ctypes.c_int32)]
+                ("scan_spin_limit", ctypes.c_int32),
+                ("decomp_unsplit", ctypes.c_int32)]
 
 
 _lib = None

@@ -9,10 +9,12 @@ Drop-in for the reference operator ``fused_mixed_attn``
     2  frozen, decomposed y_i = sum_{j<=i} exp(alpha[j] + rho[i-j] - z[i]) v_j
 
 The work runs in libsafattn.so on the current HIP stream: a live-head flash
-kernel on bf16/fp16 MFMA, a dense P.V MFMA kernel, an in-register decomposed
-rebuild kernel, and, for decomposed heads whose pattern is the causal mean, an
-exponential decay or a sliding window (``closed_form=``), a single-pass scan
-that reads V once.  Output is in natural head order.
+kernel on bf16/fp16 MFMA, a dense P.V MFMA kernel, a decomposed P.V kernel
+(factored Toeplitz form or P rebuilt per cell), and, for decomposed heads
+whose pattern is the causal mean, an exponential decay or a sliding window
+(``closed_form=``), a single-pass scan that reads V once.  The scan and the
+decomposed heads run on a second stream beside the live-head kernel, joined
+before the call returns.  Output is in natural head order.
 
 Pattern helpers (``make_rho_band``, ``decomp_logits``, ``decomposed_logz``)
 follow the reference's definitions (/root/reference/kernel/fused_attn.py:50-116).
@@ -171,7 +173,7 @@ def classify_closed_form(alpha, rho, z=None, heads=None, rtol=1e-5):
     c > 0; param = c) or CLOSED_WINDOW (alpha = 0, rho[d] = 0 for d < w and
     -inf beyond; param = w), else CLOSED_NONE.  If z is given it must be the
     pattern's own normaliser (checked against the closed form), otherwise the
-    head is left to the in-register rebuild, which uses z as given.  Runs once
+    head is left to the decomposed P.V kernel, which uses z as given.  Runs once
     per freeze change (one host sync)."""
     H, S = alpha.shape
     a = alpha.detach().float().cpu()
@@ -282,8 +284,9 @@ _SIDE_STREAMS = {}
 
 
 def _side_stream(device):
-    """A second stream per device (default priority) for the closed-form scan,
-    which runs beside the MFMA-bound kernels of the same call."""
+    """A second stream per device (default priority) for the closed-form scan
+    and the decomposed heads, which run beside the live-head kernel of the
+    same call."""
     idx = device.index if device.index is not None else torch.cuda.current_device()
     if idx not in _SIDE_STREAMS:
         _SIDE_STREAMS[idx] = torch.cuda.Stream(device=idx)
@@ -325,7 +328,8 @@ class _MixedAttnFn(torch.autograd.Function):
 def fused_mixed_attn(q, k, v, patt, frozen, hidx=None, pidx=None,
                      sm_scale=None, alpha=None, rho=None, z=None,
                      rho_band=None, validate=True, kvidx=None,
-                     closed_form=None, lse=None, flash_qtiles=0, scan_spin_limit=0):
+                     closed_form=None, lse=None, flash_qtiles=0, scan_spin_limit=0,
+                     decomp_unsplit=None):
     """Causal attention over all heads, frozen heads using a fixed prior.
 
     Arguments follow /root/reference/kernel/fused_attn.py:650-680 (and
@@ -341,7 +345,7 @@ def fused_mixed_attn(q, k, v, patt, frozen, hidx=None, pidx=None,
     Extensions of this build:
       closed_form  (kind int32[H], param float32[H]) from
                classify_closed_form(): state-2 heads with a non-zero kind run
-               the closed-form scan instead of the in-register rebuild
+               the closed-form scan instead of the decomposed P.V kernel
       lse      optional (B, H, T) fp32 output for the live heads' base-2 LSE
       flash_qtiles 0 (auto: 1) / 1 / 2 query tiles per wave of the flash kernel
                (2 applies up to hd 64; larger heads use 1)
@@ -349,6 +353,11 @@ def fused_mixed_attn(q, k, v, patt, frozen, hidx=None, pidx=None,
                is the give-up drill that tests the error path (every scan
                chunk after the first gives up: NaN rows, and with validate
                a RuntimeError)
+      decomp_unsplit  None (auto) = True when live heads share the call;
+               True: decomposed heads run one workgroup per query block,
+               beside the live-head kernel on a side stream when there is
+               one; False: key-segment split with partials and a combine,
+               after the live-head kernel on the current stream
     Returns (B, H, T, HD) in natural head order, strided like v (like the
     reference's empty_like(v)).
     """
@@ -467,15 +476,26 @@ def fused_mixed_attn(q, k, v, patt, frozen, hidx=None, pidx=None,
             _ext.check(rc)
             timer.records[kind].append((e0, e1, w))
 
-        if n_scan and (n_live or n_dense or n_dec):
-            # the HBM-bound scan of the closed-form heads on a side stream
-            # beside the MFMA-bound kernels: disjoint output rows and disjoint
-            # workspace regions; joined before returning
+        # decomposed heads beside live ones: one workgroup per query block
+        # (decomp_unsplit) on the side stream, so the live-head kernel's
+        # workgroups fill the slots their causal imbalance leaves idle and
+        # no key-segment partials or combine are needed
+        unsplit = bool(n_live) if decomp_unsplit is None else bool(decomp_unsplit)
+        args.decomp_unsplit = int(unsplit)
+        dec_side = bool(n_dec and n_live and unsplit)
+        if (n_scan and (n_live or n_dense or n_dec)) or dec_side:
+            # the HBM-bound scan of the closed-form heads (and the decomposed
+            # heads) on a side stream beside the MFMA-bound kernels: disjoint
+            # output rows and disjoint workspace regions; joined before
+            # returning
             side = _side_stream(v.device)
             side.wait_stream(cur)
-            launch("scan", side)
+            if dec_side:
+                launch("decomp", side)
+            if n_scan:
+                launch("scan", side)
             for kind in ("flash", "dense", "decomp"):
-                if work[kind][1]:
+                if work[kind][1] and not (kind == "decomp" and dec_side):
                     launch(kind, cur)
             cur.wait_stream(side)
         elif timer is not None:

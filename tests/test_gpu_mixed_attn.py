@@ -448,3 +448,44 @@ def test_invalid_args_raise():
     with pytest.raises(AssertionError, match="dense-frozen heads require patt"):
         K.fused_mixed_attn(q.to(DEV), k.to(DEV), v.to(DEV), None,
                            torch.tensor([1, 0, 0, 0], dtype=torch.int32, device=DEV))
+
+
+@pytest.mark.parametrize("with_scan", [False, True])
+def test_decomposed_beside_live_heads_unsplit_vs_split(with_scan):
+    """Decomposed heads next to live heads run one workgroup per query block
+    on the side stream, beside the live-head kernel (the default); forced
+    back to the key-segment split with partials and a combine on the current
+    stream (decomp_unsplit=False) they give the same rows to fp32 rounding,
+    both within the bound of the float64 oracle.  The live rows are
+    bit-identical.  T = 3000 at B = 4 makes the split plan cut the long
+    query blocks; with_scan adds a closed-form decay head, which shares the
+    side stream with the decomposed heads."""
+    K = _kernel()
+    B, H, T, hd, S = 4, 6, 3000, 64, 3008
+    dec = [1, 4]
+    closed = {2: ("decay", 0.02)} if with_scan else {}
+    states = {h: 2 for h in dec}
+    states.update({h: 2 for h in closed})
+    frozen, hidx, live = routing(H, states)
+    alpha, rho, z = make_decomp(H, S, seed=77, scale=0.6)
+    if closed:
+        ca, cr, cz = closed_params(H, S, closed)
+        for h in closed:
+            alpha[h], rho[h], z[h] = ca[h], cr[h], cz[h]
+    q, k, v = qkv(B, H, T, hd, seed=5, dtype=torch.bfloat16)
+    cf = K.classify_closed_form(alpha, rho, z) if closed else None
+    args = (q[:, live].to(DEV), k[:, live].to(DEV), v.to(DEV), None, frozen.to(DEV), hidx.to(DEV))
+    kw = dict(alpha=alpha.to(DEV), rho=rho.to(DEV), z=z.to(DEV), closed_form=cf)
+    y_side = K.fused_mixed_attn(*args, **kw)
+    y_split = K.fused_mixed_attn(*args, decomp_unsplit=False, **kw)
+    torch.cuda.synchronize()
+    assert torch.equal(y_side[:, live], y_split[:, live])
+    # one bf16 step of the value, or 2^-10 where a row's terms cancel to a
+    # small sum (the fp32 orders differ by rounding of the terms' magnitude)
+    d = (y_side[:, dec].float() - y_split[:, dec].float()).abs()
+    step = (y_split[:, dec].float().abs() * 2.0 ** -7).clamp_min(2.0 ** -10)
+    assert bool((d <= step).all()), f"unsplit and split differ by {d.max().item():.3e}"
+    ref = orc.eager_mixed_attention(f64(q[:, live]), f64(k[:, live]), f64(v), frozen.numpy(), hidx.numpy(),
+                                    None, None, alpha=f64(alpha), rho=f64(rho), z=f64(z), sm_scale=scale_of(hd))
+    compare(y_side, ref, what="decomposed beside live (unsplit)")
+    compare(y_split, ref, what="decomposed after live (split)")
