@@ -641,6 +641,12 @@ def run_c1(args):
         "decomp_alone": lambda: kernel.fused_mixed_attn(q0, q0, vd, None, frozen_d, None, alpha=alpha_d,
                                                          rho=rho_d, z=z_d, validate=False),
     }
+    if args.c1_legs:
+        keep = set(args.c1_legs.split(",")) | {"scan"}
+        unknown = keep - set(runs)
+        if unknown:
+            raise SystemExit(f"--c1-legs: unknown legs {sorted(unknown)}")
+        runs = {k2: fn for k2, fn in runs.items() if k2 in keep}
     n_live, nf = len(live), len(fz)
     flops_live = n_live * B * 4 * hd * T * (T + 1) // 2
     res = {}
@@ -665,13 +671,14 @@ def run_c1(args):
             if "frozen_scan" in extra:
                 entry["frozen_scan"] = {k2: extra["frozen_scan"][k2] for k2 in ("achieved", "frac", "avg_launch_ms")}
             res[name] = entry
-        vf = v[:, fz].contiguous()
-        fz_idx = torch.arange(nf, dtype=torch.int32, device="cuda")
-        step_ms, _, _ = timed_steps(lambda: kernel.frozen_pv(patt, vf, fz_idx, T), args.steps, args.warmup, False)
-        res["frozen_pv_split"] = {"ms_per_op": round(sum(step_ms) / args.steps, 4)}
+        if not args.c1_legs:
+            vf = v[:, fz].contiguous()
+            fz_idx = torch.arange(nf, dtype=torch.int32, device="cuda")
+            step_ms, _, _ = timed_steps(lambda: kernel.frozen_pv(patt, vf, fz_idx, T), args.steps, args.warmup,
+                                        False)
+            res["frozen_pv_split"] = {"ms_per_op": round(sum(step_ms) / args.steps, 4)}
     prim = res["scan"]
-    log(f"GPU: C1 op {prim['ms_per_op']:.3f} ms (scan), {res['decomp']['ms_per_op']:.3f} (decomposed beside the "
-        f"live heads; {res['decomp_split']['ms_per_op']:.3f} after them), {res['dense']['ms_per_op']:.3f} (dense)")
+    log("GPU: C1 op " + ", ".join(f"{k2} {e['ms_per_op']:.3f} ms" for k2, e in res.items()))
     roof, _ = None, None
     line = {
         "metric": "isolated mixed-head attention op (C1), tokens/s through the op",
@@ -1189,6 +1196,9 @@ def main():
     ap.add_argument("--batch", type=int, default=None, help="c1 / c4 / scan / ckpt batch (defaults 8 / 4 / 8 / 8)")
     ap.add_argument("--layers", type=int, default=None)
     ap.add_argument("--rate", type=float, default=0.25, help="c4: frozen fraction of query heads")
+    ap.add_argument("--c1-legs", default=None,
+                    help="c1: comma list of legs to run (scan, decomp, dense, decomp_split, decomp_alone); "
+                         "default all, the scan leg always")
     ap.add_argument("--prior-repr", choices=["decomposed", "dense"], default="decomposed",
                     help="c4: causal-mean prior as alpha = rho = 0 (scan) or a dense (T, T) pattern")
     ap.add_argument("--sdpa-live", action="store_true",
