@@ -676,6 +676,52 @@ int run(const saf_mixed_attn_args* a, unsigned which, void* stream) {
   return SAF_OK;
 }
 
+// A second stream per device (default priority, non-blocking) with a fork
+// and a join event, for kernels of one call that run beside each other: the
+// caller's stream records `fork` and the side stream waits for it; after the
+// side kernels the side stream records `join` and the caller's stream waits
+// for it before the call returns.  g_side_mu is held from the fork to the
+// join, so calls from several host threads do not interleave their records.
+struct SideStream {
+  hipStream_t s = nullptr;
+  hipEvent_t fork = nullptr, join = nullptr;
+};
+constexpr int kMaxSideDevices = 64;
+std::mutex g_side_mu;
+SideStream g_side[kMaxSideDevices];
+
+// With g_side_mu held: the current device's side stream (created on first
+// use) made to wait for the work enqueued so far on `s`.
+int side_fork_locked(hipStream_t s, SideStream** out) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return fail(SAF_ELAUNCH, "hipGetDevice failed: %s", hipGetErrorString(e));
+  if (dev < 0 || dev >= kMaxSideDevices)
+    return fail(SAF_EUNSUPPORTED, "device %d beyond %d devices", dev, kMaxSideDevices);
+  SideStream& ss = g_side[dev];
+  if (ss.s == nullptr) {
+    SideStream n;
+    e = hipStreamCreateWithFlags(&n.s, hipStreamNonBlocking);
+    if (e == hipSuccess) e = hipEventCreateWithFlags(&n.fork, hipEventDisableTiming);
+    if (e == hipSuccess) e = hipEventCreateWithFlags(&n.join, hipEventDisableTiming);
+    if (e != hipSuccess) return fail(SAF_ELAUNCH, "side stream set-up failed: %s", hipGetErrorString(e));
+    ss = n;
+  }
+  e = hipEventRecord(ss.fork, s);
+  if (e == hipSuccess) e = hipStreamWaitEvent(ss.s, ss.fork, 0);
+  if (e != hipSuccess) return fail(SAF_ELAUNCH, "side stream fork failed: %s", hipGetErrorString(e));
+  *out = &ss;
+  return SAF_OK;
+}
+
+// With g_side_mu held: `s` waits for everything enqueued on the side stream.
+int side_join_locked(SideStream* ss, hipStream_t s) {
+  hipError_t e = hipEventRecord(ss->join, ss->s);
+  if (e == hipSuccess) e = hipStreamWaitEvent(s, ss->join, 0);
+  if (e != hipSuccess) return fail(SAF_ELAUNCH, "side stream join failed: %s", hipGetErrorString(e));
+  return SAF_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -1048,9 +1094,6 @@ int saf_mixed_attn_bwd(const saf_mixed_attn_args* a, const saf_tensor_t* dout, c
       p.out_head[i] = (int16_t)h;
       p.q_head[i] = (int16_t)(a->hidx ? a->hidx[h] : h);
     }
-    if (int rc = launched(launch_bwd_delta(p, pl.dtype, pl.HD, s), "backward delta")) return rc;
-    if (int rc = launched(launch_bwd_dq(p, pl.dtype, pl.HD, s), "backward dq")) return rc;
-    if (int rc = launched(launch_bwd_dkdv(p, pl.dtype, pl.HD, s), "backward dk/dv")) return rc;
   }
   if (nf > 0) {
     p.n_frozen = nf;
@@ -1078,9 +1121,30 @@ int saf_mixed_attn_bwd(const saf_mixed_attn_args* a, const saf_tensor_t* dout, c
       p.r_sh = a->rho.stride[0]; p.r_ss = a->rho.stride[1];
       p.z_sh = a->z.stride[0]; p.z_ss = a->z.stride[1];
     }
-    if (int rc = launched(launch_bwd_frozen_dv(p, pl.dtype, pl.HD, s), "backward frozen dv")) return rc;
   }
-  return SAF_OK;
+  // the frozen heads' dV (its own rows of dv, no workspace) on the side
+  // stream beside the live heads' kernels, whose tails leave slots idle
+  const bool fork = !pl.live.empty() && nf > 0;
+  std::unique_lock<std::mutex> lock(g_side_mu, std::defer_lock);
+  SideStream* ss = nullptr;
+  if (fork) {
+    lock.lock();
+    if (int rc = side_fork_locked(s, &ss)) return rc;
+  }
+  int rc = SAF_OK;
+  if (nf > 0) rc = launched(launch_bwd_frozen_dv(p, pl.dtype, pl.HD, fork ? ss->s : s), "backward frozen dv");
+  if (rc == SAF_OK && !pl.live.empty()) {
+    rc = launched(launch_bwd_delta(p, pl.dtype, pl.HD, s), "backward delta");
+    if (rc == SAF_OK) rc = launched(launch_bwd_dq(p, pl.dtype, pl.HD, s), "backward dq");
+    if (rc == SAF_OK) rc = launched(launch_bwd_dkdv(p, pl.dtype, pl.HD, s), "backward dk/dv");
+  }
+  if (fork) {
+    // joined on every path, so the side stream never outlives the call's
+    // ordering on the caller's stream
+    const int jrc = side_join_locked(ss, s);
+    if (rc == SAF_OK) rc = jrc;
+  }
+  return rc;
 }
 
 static std::vector<int> decomp_heads_all(const Plan& pl) {
