@@ -31,9 +31,13 @@
  *   - Head-routing tables (frozen, hidx, pidx, kvidx, closed_kind,
  *     closed_param) are HOST arrays of n_heads entries, read during the call.
  *   - Kernels are enqueued on `stream` (a hipStream_t) without any host
- *     synchronisation.  Calls are re-entrant; the only mutable global state is
- *     the thread-local error string (and the noalloc scratch array, shared by
- *     the calls of that one entry point).
+ *     synchronisation.  saf_mixed_attn_fwd and saf_mixed_attn_bwd also use a
+ *     second stream of the library per device (created at first use, default
+ *     priority), forked from `stream` and joined back into it by events within
+ *     the call, under a mutex, so each call stays ordered on `stream`.  Calls
+ *     are re-entrant; the other mutable global state is the thread-local error
+ *     string (and the noalloc scratch array, shared by the calls of that one
+ *     entry point).
  *   - Head dims: the forward entry points take HD in {32, 64, 96, 128, 256}
  *     (the reference's Triton kernels take any power of two; 256 is
  *     Qwen3.5's); the bf16 / fp16 backward entry points and the fused RoPE /
@@ -116,16 +120,27 @@ typedef struct saf_mixed_attn_args {
   int32_t scan_spin_limit;      /* 0 = default bound of each look-back wait; < 0 = give-up
                                    drill: every scan chunk after the first gives up at once
                                    (tests of the error path) */
-  int32_t decomp_unsplit;       /* 0 = the decomposed heads' query blocks are split into key
-                                   segments for balance (fp32 partials in the workspace region
-                                   the live-head and dense kernels also use, then a combine);
-                                   1 = one workgroup per query block, no partials: for a
-                                   saf_frozen_decomp_fwd call on a second stream beside
-                                   saf_flash_fwd, whose workgroups fill the slots the causal
-                                   imbalance leaves idle (same results to fp32 rounding) */
+  int32_t decomp_unsplit;       /* schedule of the decomposed heads (same results to fp32
+                                   rounding):
+                                   0 = automatic: saf_mixed_attn_fwd runs them with one
+                                   workgroup per query block on the library's side stream
+                                   beside the live-head kernel when live heads share the call
+                                   (its workgroups fill the slots the causal imbalance leaves
+                                   idle); otherwise, and in saf_frozen_decomp_fwd, their long
+                                   query blocks are split into key segments (fp32 partials in
+                                   the workspace region the live-head and dense kernels also
+                                   use, then a combine);
+                                   1 = one workgroup per query block, no partials, so a
+                                   saf_frozen_decomp_fwd call may run on a caller's second
+                                   stream beside saf_flash_fwd;
+                                   -1 = always split, after the live-head kernel */
 } saf_mixed_attn_args;
 
-/* All head kinds: live flash, dense P.V, decomposed rebuild, closed-form scan. */
+/* All head kinds: live flash, dense P.V, decomposed P.V, closed-form scan.
+ * The closed-form scan and (see decomp_unsplit) the decomposed heads run on a
+ * second stream of the library (one per device, default priority), forked
+ * from and joined back into `stream` by events within the call, so the call
+ * is ordered on `stream` like a single kernel. */
 int saf_mixed_attn_fwd(const saf_mixed_attn_args* args, void* stream);
 
 /* saf_mixed_attn_fwd without a caller workspace, for callers that cannot

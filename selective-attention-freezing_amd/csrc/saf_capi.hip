@@ -548,10 +548,10 @@ int64_t decomp_vp_bytes(const Plan& pl) {
 
 // Decomposed P.V, causally balanced like run_dense when the workspace holds
 // the plan's partials (same region as the flash and dense partials: the
-// kernels run one after the other on the stream) unless args->decomp_unsplit
-// asks for one workgroup per query block (the call then shares no workspace
-// region with the live-head and dense kernels and may run beside them).
-int run_decomp(const saf_mixed_attn_args* a, const Plan& pl, hipStream_t s) {
+// kernels run one after the other on the stream) unless `unsplit` asks for
+// one workgroup per query block (the call then shares no workspace region
+// with the live-head and dense kernels and may run beside them).
+int run_decomp(const saf_mixed_attn_args* a, const Plan& pl, hipStream_t s, bool unsplit) {
   if (pl.decomp.empty() || pl.T == 0 || pl.B == 0) return SAF_OK;
   FrozenParams p{};
   fill_frozen_common(p, a->v, a->out, pl.B, pl.T);
@@ -569,7 +569,7 @@ int run_decomp(const saf_mixed_attn_args* a, const Plan& pl, hipStream_t s) {
   const int BM = block_rows(frozen_qtiles(pl.HD));
   FlashPlan fp = plan_flash(pl.B, p.n_slots, pl.T, pl.HD, BM, decomp_resident(pl.HD));
   const int64_t part_off = scan_ws_bytes(pl);
-  if (pl.dtype != SAF_F32 && fp.n_items && !a->decomp_unsplit && a->workspace != nullptr &&
+  if (pl.dtype != SAF_F32 && fp.n_items && !unsplit && a->workspace != nullptr &&
       a->workspace_bytes >= part_off + fp.part_bytes && reinterpret_cast<uintptr_t>(a->workspace) % 16 == 0) {
     p.n_items = fp.n_items;
     p.seg_len = fp.seg_len;
@@ -661,21 +661,6 @@ int run_dense_mixed(const saf_mixed_attn_args* a, const Plan& pl, hipStream_t s)
   return run_dense(a->patt, a->v, a->out, pl.B, pl.T, pl.HD, pl.dtype, pl.dense, vh, ph, ws, ws_bytes, s);
 }
 
-int run(const saf_mixed_attn_args* a, unsigned which, void* stream) {
-  Plan pl;
-  if (int rc = plan_and_validate(a, which, pl)) return rc;
-  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-  if (which & kDoFlash)
-    if (int rc = run_flash(a, pl, s)) return rc;
-  if (which & kDoScan)
-    if (int rc = run_scan(a, pl, s)) return rc;
-  if (which & kDoDense)
-    if (int rc = run_dense_mixed(a, pl, s)) return rc;
-  if (which & kDoDecomp)
-    if (int rc = run_decomp(a, pl, s)) return rc;
-  return SAF_OK;
-}
-
 // A second stream per device (default priority, non-blocking) with a fork
 // and a join event, for kernels of one call that run beside each other: the
 // caller's stream records `fork` and the side stream waits for it; after the
@@ -691,8 +676,12 @@ std::mutex g_side_mu;
 SideStream g_side[kMaxSideDevices];
 
 // With g_side_mu held: the current device's side stream (created on first
-// use) made to wait for the work enqueued so far on `s`.
+// use) made to wait for the work enqueued so far on `s`.  *out stays null
+// (and the caller runs everything on `s`) when the side stream does not
+// exist yet and `s` is being captured into a HIP graph: creating streams and
+// events is left out of captures.
 int side_fork_locked(hipStream_t s, SideStream** out) {
+  *out = nullptr;
   int dev = 0;
   hipError_t e = hipGetDevice(&dev);
   if (e != hipSuccess) return fail(SAF_ELAUNCH, "hipGetDevice failed: %s", hipGetErrorString(e));
@@ -700,6 +689,10 @@ int side_fork_locked(hipStream_t s, SideStream** out) {
     return fail(SAF_EUNSUPPORTED, "device %d beyond %d devices", dev, kMaxSideDevices);
   SideStream& ss = g_side[dev];
   if (ss.s == nullptr) {
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    e = hipStreamIsCapturing(s, &cs);
+    if (e != hipSuccess) return fail(SAF_ELAUNCH, "hipStreamIsCapturing failed: %s", hipGetErrorString(e));
+    if (cs != hipStreamCaptureStatusNone) return SAF_OK;
     SideStream n;
     e = hipStreamCreateWithFlags(&n.s, hipStreamNonBlocking);
     if (e == hipSuccess) e = hipEventCreateWithFlags(&n.fork, hipEventDisableTiming);
@@ -722,11 +715,58 @@ int side_join_locked(SideStream* ss, hipStream_t s) {
   return SAF_OK;
 }
 
+// The head kinds of `which`.  With may_fork (saf_mixed_attn_fwd), the
+// HBM-bound closed-form scan and, when live heads share the call, the
+// decomposed heads (one workgroup per query block, unless decomp_unsplit < 0)
+// run on the side stream beside the live-head and dense kernels: disjoint
+// output rows and workspace regions, joined before returning.  Otherwise
+// everything runs in order on `stream`.
+int run(const saf_mixed_attn_args* a, unsigned which, void* stream, bool may_fork = false) {
+  Plan pl;
+  if (int rc = plan_and_validate(a, which, pl)) return rc;
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  const bool has_dec = (which & kDoDecomp) && !pl.decomp.empty();
+  const bool has_live = (which & kDoFlash) && !pl.live.empty();
+  const bool dec_side = may_fork && has_dec && has_live && a->decomp_unsplit >= 0;
+  const bool scan_side = may_fork && (which & kDoScan) && !pl.scan.empty() &&
+                         (has_live || has_dec || ((which & kDoDense) && !pl.dense.empty()));
+  const bool dec_unsplit = a->decomp_unsplit > 0;
+  if (!dec_side && !scan_side) {
+    if (which & kDoFlash)
+      if (int rc = run_flash(a, pl, s)) return rc;
+    if (which & kDoScan)
+      if (int rc = run_scan(a, pl, s)) return rc;
+    if (which & kDoDense)
+      if (int rc = run_dense_mixed(a, pl, s)) return rc;
+    if (which & kDoDecomp)
+      if (int rc = run_decomp(a, pl, s, dec_unsplit)) return rc;
+    return SAF_OK;
+  }
+  std::lock_guard<std::mutex> lock(g_side_mu);
+  SideStream* ss = nullptr;
+  if (int rc = side_fork_locked(s, &ss)) return rc;
+  // without a side stream (first use inside a graph capture) the same
+  // kernels run in order on `s`
+  hipStream_t t = ss != nullptr ? ss->s : s;
+  int rc = SAF_OK;
+  if (dec_side) rc = run_decomp(a, pl, t, true);
+  if (rc == SAF_OK && scan_side) rc = run_scan(a, pl, t);
+  if (rc == SAF_OK && (which & kDoFlash)) rc = run_flash(a, pl, s);
+  if (rc == SAF_OK && (which & kDoScan) && !scan_side) rc = run_scan(a, pl, s);
+  if (rc == SAF_OK && (which & kDoDense)) rc = run_dense_mixed(a, pl, s);
+  if (rc == SAF_OK && (which & kDoDecomp) && !dec_side) rc = run_decomp(a, pl, s, dec_unsplit);
+  if (ss == nullptr) return rc;
+  // joined on every path, so the side stream's work is ordered before
+  // whatever the caller enqueues next
+  const int jrc = side_join_locked(ss, s);
+  return rc == SAF_OK ? jrc : rc;
+}
+
 }  // namespace
 
 extern "C" {
 
-int saf_mixed_attn_fwd(const saf_mixed_attn_args* args, void* stream) { return run(args, kDoAll, stream); }
+int saf_mixed_attn_fwd(const saf_mixed_attn_args* args, void* stream) { return run(args, kDoAll, stream, true); }
 int saf_flash_fwd(const saf_mixed_attn_args* args, void* stream) { return run(args, kDoFlash, stream); }
 int saf_frozen_dense_pv_fwd(const saf_mixed_attn_args* args, void* stream) { return run(args, kDoDense, stream); }
 int saf_frozen_decomp_fwd(const saf_mixed_attn_args* args, void* stream) { return run(args, kDoDecomp, stream); }
@@ -1132,13 +1172,13 @@ int saf_mixed_attn_bwd(const saf_mixed_attn_args* a, const saf_tensor_t* dout, c
     if (int rc = side_fork_locked(s, &ss)) return rc;
   }
   int rc = SAF_OK;
-  if (nf > 0) rc = launched(launch_bwd_frozen_dv(p, pl.dtype, pl.HD, fork ? ss->s : s), "backward frozen dv");
+  if (nf > 0) rc = launched(launch_bwd_frozen_dv(p, pl.dtype, pl.HD, ss != nullptr ? ss->s : s), "backward frozen dv");
   if (rc == SAF_OK && !pl.live.empty()) {
     rc = launched(launch_bwd_delta(p, pl.dtype, pl.HD, s), "backward delta");
     if (rc == SAF_OK) rc = launched(launch_bwd_dq(p, pl.dtype, pl.HD, s), "backward dq");
     if (rc == SAF_OK) rc = launched(launch_bwd_dkdv(p, pl.dtype, pl.HD, s), "backward dk/dv");
   }
-  if (fork) {
+  if (ss != nullptr) {
     // joined on every path, so the side stream never outlives the call's
     // ordering on the caller's stream
     const int jrc = side_join_locked(ss, s);

@@ -285,8 +285,8 @@ _SIDE_STREAMS = {}
 
 def _side_stream(device):
     """A second stream per device (default priority) for the closed-form scan
-    and the decomposed heads, which run beside the live-head kernel of the
-    same call."""
+    and the decomposed heads when each kernel of a call is timed
+    (KernelTimer); untimed calls use the library's own side stream."""
     idx = device.index if device.index is not None else torch.cuda.current_device()
     if idx not in _SIDE_STREAMS:
         _SIDE_STREAMS[idx] = torch.cuda.Stream(device=idx)
@@ -461,11 +461,8 @@ def fused_mixed_attn(q, k, v, patt, frozen, hidx=None, pidx=None,
         timer = _TIMER
         cur = torch.cuda.current_stream(v.device)
 
-        def launch(kind, strm):
+        def launch(kind, strm):  # one timed per-kind call
             fn, w = work[kind]
-            if timer is None:
-                _ext.check(fn(args, strm.cuda_stream))
-                return
             e0 = torch.cuda.Event(enable_timing=True)
             e1 = torch.cuda.Event(enable_timing=True)
             e0.record(strm)  # creates the HIP events; the library re-records them
@@ -476,34 +473,37 @@ def fused_mixed_attn(q, k, v, patt, frozen, hidx=None, pidx=None,
             _ext.check(rc)
             timer.records[kind].append((e0, e1, w))
 
-        # decomposed heads beside live ones: one workgroup per query block
-        # (decomp_unsplit) on the side stream, so the live-head kernel's
-        # workgroups fill the slots their causal imbalance leaves idle and
-        # no key-segment partials or combine are needed
-        unsplit = bool(n_live) if decomp_unsplit is None else bool(decomp_unsplit)
-        args.decomp_unsplit = int(unsplit)
-        dec_side = bool(n_dec and n_live and unsplit)
-        if (n_scan and (n_live or n_dense or n_dec)) or dec_side:
-            # the HBM-bound scan of the closed-form heads (and the decomposed
-            # heads) on a side stream beside the MFMA-bound kernels: disjoint
-            # output rows and disjoint workspace regions; joined before
-            # returning
-            side = _side_stream(v.device)
-            side.wait_stream(cur)
-            if dec_side:
-                launch("decomp", side)
-            if n_scan:
-                launch("scan", side)
-            for kind in ("flash", "dense", "decomp"):
-                if work[kind][1] and not (kind == "decomp" and dec_side):
-                    launch(kind, cur)
-            cur.wait_stream(side)
-        elif timer is not None:
-            for kind in KernelTimer.KINDS:
-                if work[kind][1]:
-                    launch(kind, cur)
-        else:
+        if timer is None:
+            # one call: the library runs the closed-form scan and the
+            # decomposed heads on its side stream beside the live-head kernel
+            args.decomp_unsplit = {None: 0, True: 1, False: -1}[decomp_unsplit]
             _ext.check(L.saf_mixed_attn_fwd(args, cur.cuda_stream))
+        else:
+            # the same schedule through the per-kind entry points, each kernel
+            # timed on its own stream: decomposed heads beside live ones run
+            # one workgroup per query block (decomp_unsplit = 1), so the
+            # live-head kernel's workgroups fill the slots their causal
+            # imbalance leaves idle and no key-segment partials are needed
+            unsplit = bool(n_live) if decomp_unsplit is None else bool(decomp_unsplit)
+            args.decomp_unsplit = 1 if unsplit else -1
+            dec_side = bool(n_dec and n_live and unsplit)
+            if (n_scan and (n_live or n_dense or n_dec)) or dec_side:
+                # disjoint output rows and workspace regions; joined before
+                # returning
+                side = _side_stream(v.device)
+                side.wait_stream(cur)
+                if dec_side:
+                    launch("decomp", side)
+                if n_scan:
+                    launch("scan", side)
+                for kind in ("flash", "dense", "decomp"):
+                    if work[kind][1] and not (kind == "decomp" and dec_side):
+                        launch(kind, cur)
+                cur.wait_stream(side)
+            else:
+                for kind in KernelTimer.KINDS:
+                    if work[kind][1]:
+                        launch(kind, cur)
         if n_scan and validate:
             # a look-back wait that gave up leaves NaN rows (never a silently
             # incomplete sum); with validate the call also raises
