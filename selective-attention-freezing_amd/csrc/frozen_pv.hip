@@ -56,9 +56,9 @@ constexpr int decomp_waves_per_eu(int hd) { return hd > 64 ? 2 : 3; }
 // Every factor is <= 1 before the row factor, and the form is used only when
 // every row's z is within kFactorRange of A + R, so every cell that matters
 // (P > 2^-24) has both bf16 factors far above the normal range limit and the
-// products stay normal in fp32; otherwise (and for fp16, whose exponent range
-// is too short, or without the workspace) the workgroup rebuilds P cell by
-// cell.
+// products stay normal in fp32; otherwise (and without the workspace) the
+// workgroup rebuilds P cell by cell.  That bf16 hi + lo form needs bf16
+// activations; fp16 activations have the fp16 form below or the rebuild.
 //
 // Rebuild form: P^T rebuilt in registers, one 16-key operand at a time and
 // consumed by its MFMAs right away (building a whole 64-key block of
@@ -75,7 +75,8 @@ constexpr float kFactorRange = 80.f;
 // T F 2^-24 max|v|; the form is used only where F <= 2^(kF16Budget - log2 T),
 // i.e. that sum is at most 2^-10 max|v|, and where every |V'| the workgroup
 // reads is at most kF16Max (no overflow).  Everything else takes the bf16
-// hi + lo form or the rebuild.
+// hi + lo form (bf16 activations) or the rebuild.  The form serves fp16
+// activations as well: their V' is fp16 already in range.
 constexpr int kF16Budget = 14;
 constexpr float kF16Max = 65504.f;
 
@@ -93,7 +94,10 @@ __device__ __forceinline__ void decomp_body(const FrozenParams& p) {
   constexpr int RWL = RW + 16;
   constexpr int ERN = (RW + NTHR - 1) / NTHR;
   static_assert(RW % 2 == 0 && RW / 2 <= NTHR, "one thread per pair of factored-window elements");
-  constexpr bool kFactorable = std::is_same<T, __bf16>::value && HD <= 128;
+  // bf16 activations: the fp16 form, else the bf16 hi + lo form, else the
+  // rebuild; fp16 activations: the fp16 form, else the rebuild
+  constexpr bool kBf16 = std::is_same<T, __bf16>::value;
+  constexpr bool kFactorable = (kBf16 || std::is_same<T, _Float16>::value) && HD <= 128;
   // LDS: the factored form's three V' tiles (vs0..vs2) and two distance
   // windows of hi and lo copies (eb0, eb1), or the rebuild form's two V^T
   // tiles (vs0, vs1) and alpha / rho windows (eb0).  Separate objects, so the
@@ -209,6 +213,7 @@ __device__ __forceinline__ void decomp_body(const FrozenParams& p) {
       // factor at most 2^(14 - ceil(log2 T)) (see kF16Budget)
       const int lgT = T_len > 1 ? 32 - __clz(T_len - 1) : 0;
       form16 = factored && vm <= kF16Max && zm >= am + rm - (float)(kF16Budget - lgT);
+      if constexpr (!kBf16) factored = form16;
       aoff = am;
       roff = rm;
     }
@@ -415,10 +420,14 @@ __device__ __forceinline__ void decomp_body(const FrozenParams& p) {
       for (int qt = 0; qt < QT; ++qt) rowscale[qt] = fast_exp2(aoff + roff - zq[qt]);
     };
     if (factored) {
-      if (form16)
+      if constexpr (kBf16) {
+        if (form16)
+          run_factored(std::true_type());
+        else
+          run_factored(std::false_type());
+      } else {
         run_factored(std::true_type());
-      else
-        run_factored(std::false_type());
+      }
     }
   }
   if (!factored) {
@@ -594,7 +603,8 @@ __global__ __launch_bounds__(256) void decomp_prescale_kernel(const FrozenParams
         out16[m] = Elem<_Float16>::pack2(x0, x1);
         vmx = fmaxf(vmx, fmaxf(fabsf(x0), fabsf(x1)));
       }
-      *reinterpret_cast<uint4*>(vp + (int64_t)(j0 + rl) * HD + 8 * c) = make_uint4(out[0], out[1], out[2], out[3]);
+      if constexpr (std::is_same<T, __bf16>::value)  // the bf16 forms' copy (fp16 inputs have only the fp16 form)
+        *reinterpret_cast<uint4*>(vp + (int64_t)(j0 + rl) * HD + 8 * c) = make_uint4(out[0], out[1], out[2], out[3]);
       *reinterpret_cast<uint4*>(vp16 + (int64_t)(j0 + rl) * HD + 8 * c) =
           make_uint4(out16[0], out16[1], out16[2], out16[3]);
     }
@@ -1020,22 +1030,28 @@ static hipError_t launch_frozen_hd(const FrozenParams& p, int hd, int mode, hipS
 }
 
 
-template <int HD>
+template <typename T, int HD>
 static hipError_t launch_prescale_hd(const FrozenParams& p, hipStream_t s) {
   const dim3 grid((unsigned)((p.T + 63) / 64), (unsigned)p.n_slots, (unsigned)p.B);
-  hipLaunchKernelGGL((decomp_prescale_kernel<__bf16, HD>), grid, dim3(256), 0, s, p);
+  hipLaunchKernelGGL((decomp_prescale_kernel<T, HD>), grid, dim3(256), 0, s, p);
   return hipGetLastError();
 }
 
-hipError_t launch_decomp_prescale(const FrozenParams& p, int dtype, int hd, hipStream_t s) {
-  if (dtype != kBF16) return hipErrorInvalidValue;
+template <typename T>
+static hipError_t launch_prescale_t(const FrozenParams& p, int hd, hipStream_t s) {
   switch (hd) {
-    case 32: return launch_prescale_hd<32>(p, s);
-    case 64: return launch_prescale_hd<64>(p, s);
-    case 96: return launch_prescale_hd<96>(p, s);
-    case 128: return launch_prescale_hd<128>(p, s);
+    case 32: return launch_prescale_hd<T, 32>(p, s);
+    case 64: return launch_prescale_hd<T, 64>(p, s);
+    case 96: return launch_prescale_hd<T, 96>(p, s);
+    case 128: return launch_prescale_hd<T, 128>(p, s);
     default: return hipErrorInvalidValue;
   }
+}
+
+hipError_t launch_decomp_prescale(const FrozenParams& p, int dtype, int hd, hipStream_t s) {
+  if (dtype == kBF16) return launch_prescale_t<__bf16>(p, hd, s);
+  if (dtype == kF16) return launch_prescale_t<_Float16>(p, hd, s);
+  return hipErrorInvalidValue;
 }
 
 hipError_t launch_frozen_pv(const FrozenParams& p, int dtype, int hd, int mode, hipStream_t s) {

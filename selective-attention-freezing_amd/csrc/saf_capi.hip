@@ -507,9 +507,9 @@ int run_dense(const saf_tensor_t& patt, const saf_tensor_t& v, const saf_tensor_
 // blocks (flash, dense and decomposed kernels run one after the other and
 // share them), then the factored decomposed form's per-64-block maxima of
 // alpha and of rho a_off (2 x n_dec x ceil(T / 64) floats), rho log2 e r2
-// (n_dec x T floats), key-scaled values vp (B, n_dec, T, HD) in bf16 and
-// again in fp16, and their per-block largest magnitudes vmax (B x n_dec x
-// ceil(T / 64) floats) (bf16, hd <= 128 only).
+// (n_dec x T floats), key-scaled values vp (B, n_dec, T, HD) in bf16 (bf16
+// activations only) and in fp16, and their per-block largest magnitudes vmax
+// (B x n_dec x ceil(T / 64) floats) (bf16 and fp16, hd <= 128 only).
 int64_t round256(int64_t n) { return (n + 255) / 256 * 256; }
 
 int64_t part_region_bytes(const saf_mixed_attn_args* args, const Plan& pl) {
@@ -542,7 +542,7 @@ int64_t decomp_vmax_bytes(const Plan& pl) {
 }
 
 int64_t decomp_vp_bytes(const Plan& pl) {
-  if (pl.dtype != SAF_BF16 || pl.HD > 128 || pl.decomp.empty()) return 0;
+  if ((pl.dtype != SAF_BF16 && pl.dtype != SAF_F16) || pl.HD > 128 || pl.decomp.empty()) return 0;
   return decomp_aoff_bytes(pl) + decomp_r2_bytes(pl) + 2 * decomp_v1_bytes(pl) + decomp_vmax_bytes(pl);
 }
 

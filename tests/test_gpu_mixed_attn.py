@@ -190,6 +190,45 @@ def test_decomposed_fp16_bf16_and_rebuilt_forms():
         compare(y[:, h:h + 1], ref[:, h:h + 1], what=f"decomposed forms head {h}")
 
 
+def test_decomposed_fp16_activations_fp16_form_and_rebuild():
+    """fp16 activations: the decomposed heads take the fp16 factored form
+    where the row factor allows and rebuild P cell by cell elsewhere (the
+    bf16 hi + lo form needs bf16 inputs), against the float64 oracle.  Head
+    0: a decay (fp16 form everywhere); head 1: moderate random alpha / rho
+    (both); head 2: an attention sink with a steep decay (rebuild); head 3:
+    an alpha spike (rebuild past it).  Alone and beside live heads."""
+    import kernel
+    B, H, T, hd, S = 2, 6, 2500, 64, 2560
+    g = torch.Generator().manual_seed(93)
+    d = torch.arange(S, dtype=torch.float32)
+    alpha = torch.zeros(H, S)
+    rho = torch.zeros(H, S)
+    rho[0] = -0.03 * d
+    alpha[1] = torch.randn(S, generator=g) * 0.7
+    rho[1] = torch.randn(S, generator=g) * 0.7
+    alpha[2, 0] = 12.0
+    rho[2] = -0.5 * d
+    alpha[3] = torch.randn(S, generator=g) * 0.5
+    alpha[3, 1200] = 150.0
+    rho[3] = -0.01 * d
+    z = torch.from_numpy(orc.decomposed_logz(alpha.double().numpy(), rho.double().numpy())).float()
+    q, k, v = qkv(B, H, T, hd, seed=9, dtype=torch.float16)
+    # decomposed only (heads 0-3), then heads 4 and 5 live beside them
+    for n_live in (0, 2):
+        Hc = 4 + n_live
+        st = {h: 2 for h in range(4)}
+        frozen, hidx, live = routing(Hc, st)
+        y = kernel.fused_mixed_attn(q[:, live].to(DEV), k[:, live].to(DEV), v[:, :Hc].to(DEV), None,
+                                    frozen.to(DEV), hidx.to(DEV), alpha=alpha[:Hc].to(DEV), rho=rho[:Hc].to(DEV),
+                                    z=z[:Hc].to(DEV))
+        torch.cuda.synchronize()
+        ref = orc.eager_mixed_attention(f64(q[:, live]), f64(k[:, live]), f64(v[:, :Hc]), frozen.numpy(),
+                                        hidx.numpy(), None, None, alpha=f64(alpha[:Hc]), rho=f64(rho[:Hc]),
+                                        z=f64(z[:Hc]), sm_scale=scale_of(hd))
+        for h in range(Hc):
+            compare(y[:, h:h + 1], ref[:, h:h + 1], what=f"fp16 activations, {n_live} live, head {h}")
+
+
 def test_decomposed_large_values_keep_the_bf16_form():
     """Values of magnitude ~1e5 scale to key-scaled values past the fp16
     range, so the workgroups of a decay head (row factor <= 1, otherwise an
