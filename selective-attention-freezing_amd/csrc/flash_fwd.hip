@@ -181,21 +181,24 @@ struct FlashState {
 
   // P = 2^(s c - m) rounded to T, packed in place into registers 0..7 of s
   // (word 4 sh + u = keys 16 sh + 8g + 2u, 2u + 1); bs = the lane's sum of
-  // its rounded P values
+  // its rounded P values, added on the matrix pipe (four 4x4x4 MFMAs with an
+  // all-ones operand), which has issue slots to spare where the VALU has none
   __device__ __forceinline__ void exp_pack(f32x16_t (&s)[QT], float (&bs)[QT]) const {
 #pragma unroll
     for (int qt = 0; qt < QT; ++qt) {
       const float mneg = -m_run[qt];
-      float sum = 0.f;
+      uint32_t wd[8];
 #pragma unroll
       for (int w = 0; w < 8; ++w) {
         const float e0 = fast_exp2(fmaf(s[qt][2 * w], c, mneg));
         const float e1 = fast_exp2(fmaf(s[qt][2 * w + 1], c, mneg));
-        const uint32_t word = Elem<T>::pack2(e0, e1);
-        sum = Elem<T>::sum2(word, sum);
-        s[qt][w] = __uint_as_float(word);
+        wd[w] = Elem<T>::pack2(e0, e1);
+        s[qt][w] = __uint_as_float(wd[w]);
       }
-      bs[qt] = sum;
+      f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int w = 0; w < 8; w += 2) acc = Elem<T>::sum4(make_uint2(wd[w], wd[w + 1]), acc);
+      bs[qt] = acc[0];
     }
   }
 

@@ -36,6 +36,9 @@ typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
 typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
 typedef float f32x16_t __attribute__((ext_vector_type(16)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+typedef short i16x4_t __attribute__((ext_vector_type(4)));
+typedef _Float16 f16x4_t __attribute__((ext_vector_type(4)));
 
 constexpr float kLog2e = 1.4426950408889634f;  // 1 / ln(2)
 
@@ -68,6 +71,14 @@ template <> struct Elem<__bf16> {
     const bf16x2_t one = {(__bf16)1.f, (__bf16)1.f};
     return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, w), one, acc, false);
   }
+  // acc + the sum of this lane's four values in w (two dwords), on the
+  // matrix pipe: in a 4x4x4 MFMA block, lane 4b + j supplies column j of B
+  // and receives column j of D, so with an all-ones A every register of the
+  // lane's result holds acc + its own four values
+  __device__ static inline f32x4_t sum4(uint2 w, f32x4_t acc) {
+    const i16x4_t ones = {0x3f80, 0x3f80, 0x3f80, 0x3f80};
+    return __builtin_amdgcn_mfma_f32_4x4x4bf16_1k(ones, __builtin_bit_cast(i16x4_t, w), acc, 0, 0, 0);
+  }
 };
 
 template <> struct Elem<_Float16> {
@@ -91,6 +102,10 @@ template <> struct Elem<_Float16> {
   __device__ static inline float sum2(uint32_t w, float acc) {
     const f16x2_t one = {(_Float16)1.f, (_Float16)1.f};
     return __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2_t, w), one, acc, false);
+  }
+  __device__ static inline f32x4_t sum4(uint2 w, f32x4_t acc) {
+    const f16x4_t ones = {(_Float16)1.f, (_Float16)1.f, (_Float16)1.f, (_Float16)1.f};
+    return __builtin_amdgcn_mfma_f32_4x4x4f16(ones, __builtin_bit_cast(f16x4_t, w), acc, 0, 0, 0);
   }
 };
 
