@@ -677,9 +677,11 @@ SideStream g_side[kMaxSideDevices];
 
 // With g_side_mu held: the current device's side stream (created on first
 // use) made to wait for the work enqueued so far on `s`.  *out stays null
-// (and the caller runs everything on `s`) when the side stream does not
-// exist yet and `s` is being captured into a HIP graph: creating streams and
-// events is left out of captures.
+// (and the caller runs everything on `s`) where a fork could mix graph
+// captures: when `s` is being captured and the side stream does not exist
+// yet (creating streams and events is left out of captures), and when the
+// side stream is still part of a capture (a stream that joined one stays in
+// it until it ends) other than the one `s` is in.
 int side_fork_locked(hipStream_t s, SideStream** out) {
   *out = nullptr;
   int dev = 0;
@@ -688,10 +690,18 @@ int side_fork_locked(hipStream_t s, SideStream** out) {
   if (dev < 0 || dev >= kMaxSideDevices)
     return fail(SAF_EUNSUPPORTED, "device %d beyond %d devices", dev, kMaxSideDevices);
   SideStream& ss = g_side[dev];
-  if (ss.s == nullptr) {
-    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
-    e = hipStreamIsCapturing(s, &cs);
-    if (e != hipSuccess) return fail(SAF_ELAUNCH, "hipStreamIsCapturing failed: %s", hipGetErrorString(e));
+  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+  unsigned long long cid = 0;
+  e = hipStreamGetCaptureInfo(s, &cs, &cid);
+  if (e != hipSuccess) return fail(SAF_ELAUNCH, "hipStreamGetCaptureInfo failed: %s", hipGetErrorString(e));
+  if (ss.s != nullptr) {
+    hipStreamCaptureStatus side_cs = hipStreamCaptureStatusNone;
+    unsigned long long side_cid = 0;
+    e = hipStreamGetCaptureInfo(ss.s, &side_cs, &side_cid);
+    if (e != hipSuccess) return fail(SAF_ELAUNCH, "hipStreamGetCaptureInfo failed: %s", hipGetErrorString(e));
+    if (side_cs != hipStreamCaptureStatusNone && (cs != hipStreamCaptureStatusActive || side_cid != cid))
+      return SAF_OK;
+  } else {
     if (cs != hipStreamCaptureStatusNone) return SAF_OK;
     SideStream n;
     e = hipStreamCreateWithFlags(&n.s, hipStreamNonBlocking);
