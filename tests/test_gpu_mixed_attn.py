@@ -528,3 +528,47 @@ def test_decomposed_beside_live_heads_unsplit_vs_split(with_scan):
                                     None, None, alpha=f64(alpha), rho=f64(rho), z=f64(z), sm_scale=scale_of(hd))
     compare(y_side, ref, what="decomposed beside live (unsplit)")
     compare(y_split, ref, what="decomposed after live (split)")
+
+
+def test_timed_per_kind_path_matches_single_call():
+    """With a KernelTimer installed, fused_mixed_attn runs each head kind
+    through its own entry point (saf_flash_fwd, saf_frozen_dense_pv_fwd,
+    saf_frozen_decomp_fwd, saf_frozen_scan_fwd; scan and decomposed heads on
+    a second stream) and times each kernel; without one it makes the single
+    saf_mixed_attn_fwd call, which forks the library's own side stream.  Both
+    give the same rows (the scan's look-back order may move a last fp32 bit,
+    so one bf16 step is allowed) and the timer records every kind."""
+    K = _kernel()
+    B, H, T, hd, S = 2, 8, 1500, 64, 1536
+    dense, dec = [1, 6], [2, 5]
+    closed = {3: ("decay", 0.05)}
+    states = {h: 1 for h in dense}
+    states.update({h: 2 for h in dec})
+    states.update({h: 2 for h in closed})
+    frozen, hidx, live = routing(H, states)
+    patt = make_pattern(H, S, seed=5)
+    alpha, rho, z = make_decomp(H, S, seed=6, scale=0.6)
+    ca, cr, cz = closed_params(H, S, closed)
+    for h in closed:
+        alpha[h], rho[h], z[h] = ca[h], cr[h], cz[h]
+    cf = K.classify_closed_form(alpha, rho, z)
+    q, k, v = qkv(B, H, T, hd, seed=4, dtype=torch.bfloat16)
+    args = (q[:, live].to(DEV), k[:, live].to(DEV), v.to(DEV), patt.to(DEV), frozen.to(DEV), hidx.to(DEV))
+    kw = dict(alpha=alpha.to(DEV), rho=rho.to(DEV), z=z.to(DEV), closed_form=cf)
+    y_one = K.fused_mixed_attn(*args, **kw)
+    timer = K.KernelTimer()
+    K.set_kernel_timer(timer)
+    try:
+        y_timed = K.fused_mixed_attn(*args, **kw)
+    finally:
+        K.set_kernel_timer(None)
+    torch.cuda.synchronize()
+    summary = timer.summary()
+    assert {"flash", "dense", "decomp", "scan"} <= set(summary), summary
+    d = (y_one.float() - y_timed.float()).abs()
+    step = (y_one.float().abs() * 2.0 ** -7).clamp_min(2.0 ** -12)
+    assert bool((d <= step).all()), f"timed and single-call paths differ by {d.max().item():.3e}"
+    ref = orc.eager_mixed_attention(f64(q[:, live]), f64(k[:, live]), f64(v), frozen.numpy(), hidx.numpy(),
+                                    None, None, patt=patt.numpy(), alpha=f64(alpha), rho=f64(rho), z=f64(z),
+                                    sm_scale=scale_of(hd))
+    compare(y_one, ref, what="single call")
