@@ -114,29 +114,26 @@ __device__ __forceinline__ void decomp_body(const FrozenParams& p) {
   __shared__ __align__(16) char vs2[kFactorable ? VB : 16];
   __shared__ __align__(16) char eb0[kE0];
   __shared__ __align__(16) char eb1[kFactorable ? kEBytes : 16];
-  __shared__ float red_lds[4][NW];
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (SGPR)
   const int n = lane & 31, g = lane >> 5;
 
   // work item (query block, key segment) of one (batch, head), heaviest
-  // first, (batch, head) fastest; without items one per query block
+  // first, (batch, head) fastest; without items one per query block.  The
+  // item word is read unconditionally (index clamped), so the compiler can
+  // issue it together with the head-table reads below
   const int nbh = p.B * p.n_slots;
   const int r = blockIdx.x % nbh;
-  int qb, seg = 0;
-  if (p.n_items) {
-    const int w = p.items[blockIdx.x / nbh];
-    qb = w >> 8;
-    seg = w & 255;
-  } else {
-    qb = p.n_qblk - 1 - (int)(blockIdx.x / nbh);
-  }
+  const int iu = (int)(blockIdx.x / nbh);
+  const int w_item = p.items[min(iu, kMaxItems - 1)];
+  const int qb = p.n_items ? w_item >> 8 : p.n_qblk - 1 - iu;
+  const int seg = p.n_items ? w_item & 255 : 0;
   const int b = r / p.n_slots, slot = r % p.n_slots;
-  const int h = p.out_head[slot];
-  const int ph = p.pat_head[slot];
+  const int h = arg_i16(p.out_head, slot);
+  const int ph = arg_i16(p.pat_head, slot);
 
-  const T* vbase = reinterpret_cast<const T*>(p.v) + b * p.v_sb + (int64_t)p.v_head[slot] * p.v_sh;
+  const T* vbase = reinterpret_cast<const T*>(p.v) + b * p.v_sb + (int64_t)arg_i16(p.v_head, slot) * p.v_sh;
   T* obase = reinterpret_cast<T*>(p.out) + b * p.o_sb + (int64_t)h * p.o_sh;
 
   const int T_len = p.T;
@@ -144,24 +141,19 @@ __device__ __forceinline__ void decomp_body(const FrozenParams& p) {
   const int q0w = q0 + wave * 32 * QT;
   const int kend_wg = min(q0 + BM, T_len);
   const int nkb_qb = (kend_wg + 63) / 64;
-  const bool split = p.n_items != 0 && p.part_base[qb] >= 0;
-  const int kb0 = split ? seg * p.seg_len : 0;
-  const int nkb = split ? min(nkb_qb, kb0 + p.seg_len) : nkb_qb;
+  // an unsplit query block's item is segment 0 and spans at most seg_len
+  // blocks, so the range needs no part_base lookup (that is read for the
+  // epilogue only)
+  const int kb0 = p.n_items ? seg * p.seg_len : 0;
+  const int nkb = p.n_items ? min(nkb_qb, kb0 + p.seg_len) : nkb_qb;
   const int kend_w = min(q0w + 32 * QT, T_len);
   const int nkb_w = min(nkb, kend_w > 0 ? (kend_w + 63) / 64 : 0);  // blocks this wave's rows reach
 
   auto alpha_at = [&](int j) { return load_as_f32(p.alpha, (int64_t)ph * p.a_sh + (int64_t)j * p.a_ss, p.a_dtype); };
   auto rho_at = [&](int d) { return load_as_f32(p.rho, (int64_t)ph * p.r_sh + (int64_t)d * p.r_ss, p.r_dtype); };
 
-  // per-lane row normaliser; rows >= T get +inf -> exact zeros
+  // per-lane row normalisers in log2 units; rows >= T get +inf -> exact zeros
   float zq[QT];
-#pragma unroll
-  for (int qt = 0; qt < QT; ++qt) {
-    const int i = q0w + 32 * qt + n;
-    zq[qt] = i < T_len ? load_as_f32(p.z, (int64_t)ph * p.z_sh + (int64_t)i * p.z_ss, p.z_dtype) * kLog2e
-                       : INFINITY;
-  }
-
   f32x16_t o[QT][NDT];
 #pragma unroll
   for (int qt = 0; qt < QT; ++qt)
@@ -169,44 +161,85 @@ __device__ __forceinline__ void decomp_body(const FrozenParams& p) {
     for (int dt = 0; dt < NDT; ++dt) o[qt][dt] = zero16();
   float rowscale[QT];
 
-  // factored form: A = max A_k over this segment's key blocks, R = max r
+  // Factored form: A = max A_k over this segment's key blocks, R = max r
   // over the 64-distance blocks below kend_wg (a superset of what any key
-  // segment of this block reaches; both maxima come from the pre-pass) and
-  // the smallest z of the block's rows decide it for the whole workgroup
-  bool factored = false, form16 = false;
+  // segment of this block reaches) and the smallest z of the block's rows
+  // decide it for the whole workgroup.  Every input comes from the pre-pass,
+  // so the prologue issues all its loads before the first wait: the fp16 V'
+  // of the first two blocks (the usual form; the others reload them), the
+  // first window's rho values, the rows' normalisers and the per-block
+  // maxima and minima.  Each wave reduces the same values itself (DPP, no LDS
+  // and no barrier), so the four waves reach the same decision.
+  bool factored = false, form16 = false, spec = false;
   float aoff = 0.f, roff = 0.f;
   const int nblk = (T_len + 63) / 64;
   const float* const ablk = p.a_off + (int64_t)slot * nblk;
+  uint32_t voff[VN];
+#pragma unroll
+  for (int pp = 0; pp < VN; ++pp) voff[pp] = vrow_dma_offset<T, HD>((NW * pp + wave) * 64 + lane, HD);
+  // V'_j from the copy at vpb into V slot `slot`; a block past this segment
+  // gets an empty descriptor (no memory read, the slot is filled with
+  // zeros), so every block issues the same loads and the vmcnt counts of the
+  // block loop are static
+  auto load_v = [&](const auto* vpb, int j, auto slot) {
+    constexpr int V = decltype(slot)::value;
+    char* const tile = V == 0 ? vs0 : (V == 1 ? vs1 : vs2);
+    const __amdgpu_buffer_rsrc_t rs = rows_rsrc(vpb, (int64_t)HD, 64 * j, j < nkb ? T_len : 0);
+#pragma unroll
+    for (int pp = 0; pp < VN; ++pp)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, SAF_LDS_PTR(tile + (NW * pp + wave) * 1024), 16, voff[pp], 0, 0, 0);
+  };
+  // the fp32 rho log2 e values (r2) of block jb's distance window (elements
+  // 2t, 2t + 1 and 2t + 2 for thread t) and the block's alpha maximum,
+  // loaded unconditionally with indices clamped past the end
+  float er[3], ab = 0.f;
+  int ej0 = 0;
+  const float* const r2 = p.r2 + (int64_t)slot * T_len;
+  auto load_er = [&](int jb) {
+    const int j0 = 64 * jb;
+#pragma unroll
+    for (int u = 0; u < 3; ++u) er[u] = r2[min(max(q0 - j0 + BM - (2 * tid + u), 0), T_len - 1)];
+    ab = ablk[min(jb, nblk - 1)];
+    ej0 = j0;
+  };
+  using S0 = std::integral_constant<int, 0>;
+  using S1 = std::integral_constant<int, 1>;
+  const int64_t vrow0 = ((int64_t)b * p.n_slots + slot) * T_len * HD;
+  const _Float16* const vp16base = reinterpret_cast<const _Float16*>(p.vp16) + vrow0;
+  const T* const vpbase = reinterpret_cast<const T*>(p.vp) + vrow0;
   if constexpr (kFactorable) {
     if (p.vp != nullptr) {
+      load_v(vp16base, kb0, S0());
+      load_v(vp16base, kb0 + 1, S1());
+      spec = true;
+      load_er(kb0);
+      const float* const z2 = p.z2 + (int64_t)slot * T_len;
+#pragma unroll
+      for (int qt = 0; qt < QT; ++qt) {
+        const int i = q0w + 32 * qt + n;
+        zq[qt] = i < T_len ? z2[i] : INFINITY;
+      }
       const float* const rblk = p.a_off + (int64_t)(p.n_slots + slot) * nblk;
+      const float* const zblk = p.a_off + (int64_t)(2 * p.n_slots + slot) * nblk;
       const float* const vblk = p.vmax + ((int64_t)b * p.n_slots + slot) * nblk;
-      float am = -INFINITY, rm = -INFINITY, zm = INFINITY, vm = 0.f;
-      for (int k = kb0 + tid; k < nkb; k += NTHR) {
+      // each lane's first element of every range is read before any wait
+      // (more than 64 blocks per range only at T above 4096 rows per
+      // query block's reach)
+      const int ka = kb0 + lane, kz = q0 / 64 + lane;
+      float am = ka < nkb ? ablk[ka] : -INFINITY;
+      float vm = ka < nkb ? vblk[ka] : 0.f;
+      float rm = lane < nkb_qb ? rblk[lane] : -INFINITY;
+      float zm = kz < nkb_qb ? zblk[kz] : INFINITY;
+      for (int k = ka + 64; k < nkb; k += 64) {
         am = fmaxf(am, ablk[k]);
         vm = fmaxf(vm, vblk[k]);
       }
-      for (int k = tid; k < nkb_qb; k += NTHR) rm = fmaxf(rm, rblk[k]);
-      for (int i = q0 + tid; i < kend_wg; i += NTHR)
-        zm = fminf(zm, load_as_f32(p.z, (int64_t)ph * p.z_sh + (int64_t)i * p.z_ss, p.z_dtype));
-#pragma unroll
-      for (int off = 32; off >= 1; off >>= 1) {
-        am = fmaxf(am, __shfl_xor(am, off));
-        rm = fmaxf(rm, __shfl_xor(rm, off));
-        zm = fminf(zm, __shfl_xor(zm, off));
-        vm = fmaxf(vm, __shfl_xor(vm, off));
-      }
-      if (lane == 0) {
-        red_lds[0][wave] = am;
-        red_lds[1][wave] = rm;
-        red_lds[2][wave] = zm;
-        red_lds[3][wave] = vm;
-      }
-      __syncthreads();
-      am = fmaxf(fmaxf(red_lds[0][0], red_lds[0][1]), fmaxf(red_lds[0][2], red_lds[0][3]));
-      rm = fmaxf(fmaxf(red_lds[1][0], red_lds[1][1]), fmaxf(red_lds[1][2], red_lds[1][3]));
-      zm = fminf(fminf(red_lds[2][0], red_lds[2][1]), fminf(red_lds[2][2], red_lds[2][3])) * kLog2e;
-      vm = fmaxf(fmaxf(red_lds[3][0], red_lds[3][1]), fmaxf(red_lds[3][2], red_lds[3][3]));
+      for (int k = lane + 64; k < nkb_qb; k += 64) rm = fmaxf(rm, rblk[k]);
+      for (int k = kz + 64; k < nkb_qb; k += 64) zm = fminf(zm, zblk[k]);
+      am = wave_max(am);
+      rm = wave_max(rm);
+      zm = wave_min(zm);
+      vm = wave_max(vm);
       factored = __builtin_isfinite(am) && __builtin_isfinite(rm) && __builtin_isfinite(zm) &&
                  zm >= am + rm - kFactorRange;
       // fp16 form: every V' this workgroup reads in fp16 range, and the row
@@ -218,37 +251,29 @@ __device__ __forceinline__ void decomp_body(const FrozenParams& p) {
       roff = rm;
     }
   }
+  if (!spec) {
+#pragma unroll
+    for (int qt = 0; qt < QT; ++qt) {
+      const int i = q0w + 32 * qt + n;
+      zq[qt] = i < T_len ? load_as_f32(p.z, (int64_t)ph * p.z_sh + (int64_t)i * p.z_ss, p.z_dtype) * kLog2e
+                         : INFINITY;
+    }
+  }
 
   if constexpr (kFactorable) {
     // F16: the fp16 form (E and V' in fp16, one MFMA per operand); else the
-    // bf16 form with E as a hi + lo pair
-    auto run_factored = [&](auto f16tag) {
+    // bf16 form with E as a hi + lo pair.  vpb is the V' copy of the form,
+    // whose blocks kb0 and kb0 + 1 are already on their way to V slots 0 and
+    // 1, as are the rho values of block kb0's window.
+    auto run_factored = [&](auto f16tag, const auto* vpb) {
       constexpr bool F16 = decltype(f16tag)::value;
       using TE = typename std::conditional<F16, _Float16, T>::type;
-      const TE* vpbase = reinterpret_cast<const TE*>(F16 ? p.vp16 : p.vp) + ((int64_t)b * p.n_slots + slot) * T_len * HD;
-      uint32_t voff[VN];
-#pragma unroll
-      for (int pp = 0; pp < VN; ++pp) voff[pp] = vrow_dma_offset<T, HD>((NW * pp + wave) * 64 + lane, HD);
       int vro[NDT], vroh[NDT];
 #pragma unroll
       for (int dt = 0; dt < NDT; ++dt) {
         vro[dt] = vt_read_offset<HD>(lane, dt, 0);
         vroh[dt] = vt_read_offset<HD>(lane, dt, 1);
       }
-      using S0 = std::integral_constant<int, 0>;
-      using S1 = std::integral_constant<int, 1>;
-      // V'_j into V slot `slot`; a block past this segment gets an empty
-      // descriptor (no memory read, the slot is filled with zeros), so every
-      // block issues the same loads and the vmcnt counts below are static
-      auto load_v = [&](int j, auto slot) {
-        constexpr int V = decltype(slot)::value;
-        char* const tile = V == 0 ? vs0 : (V == 1 ? vs1 : vs2);
-        const __amdgpu_buffer_rsrc_t rs = rows_rsrc(vpbase, (int64_t)HD, 64 * j, j < nkb ? T_len : 0);
-#pragma unroll
-        for (int pp = 0; pp < VN; ++pp)
-          __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, SAF_LDS_PTR(tile + (NW * pp + wave) * 1024), 16, voff[pp], 0,
-                                                   0, 0);
-      };
       // distance window of block j0: m in [0, RW) holds E(d), d = q0 - j0 + BM - m
       // (the window reversed), as a bf16 pair hi + lo (E - hi rounded), so E
       // costs no rounding beyond V''s; copy c holds window element c + k at k.
@@ -260,16 +285,6 @@ __device__ __forceinline__ void decomp_body(const FrozenParams& p) {
       // copy c stores (2t, 2t + 1) at its position 2t - c, an odd one
       // (2t + 1, 2t + 2) at 2t + 1 - c (16-bit stores put two lanes on one
       // bank word).
-      float er[3], ab = 0.f;
-      int ej0 = 0;
-      const float* const r2 = p.r2 + (int64_t)slot * T_len;
-      auto load_er = [&](int jb) {  // unconditional: indices clamped past the end
-        const int j0 = 64 * jb;
-#pragma unroll
-        for (int u = 0; u < 3; ++u) er[u] = r2[min(max(q0 - j0 + BM - (2 * tid + u), 0), T_len - 1)];
-        ab = ablk[min(jb, nblk - 1)];
-        ej0 = j0;
-      };
       auto e_slot = [&](auto slot) {
         return reinterpret_cast<uint16_t(*)[8 * RWL]>(decltype(slot)::value ? eb1 : eb0);
       };
@@ -315,10 +330,8 @@ __device__ __forceinline__ void decomp_body(const FrozenParams& p) {
         eo[qt] = ecopy(ec) + BM - il - ec + 8 * g;
       }
 
-      // prologue: E of block kb0 in E slot 0, V' of kb0 and kb0+1 in V slots 0, 1
-      load_er(kb0);
-      load_v(kb0, S0());
-      load_v(kb0 + 1, S1());
+      // prologue: E of block kb0 in E slot 0 (V' of kb0 and kb0+1 land in V
+      // slots 0, 1)
       store_er(S0());
       asm volatile("" ::: "memory");
       __builtin_amdgcn_s_waitcnt(waitcnt_vm_lgkm0(VN));
@@ -341,7 +354,7 @@ __device__ __forceinline__ void decomp_body(const FrozenParams& p) {
         const char* const vt = R == 0 ? vs0 : (R == 1 ? vs1 : vs2);
         uint16_t(*const ew)[8 * RWL] = e_slot(ESlot());
         load_er(j + 1);
-        load_v(j + 2, VAhead());
+        load_v(vpb, j + 2, VAhead());
         if (j < nkb_w) {
           // Toeplitz reuse: query tile 1 sits 32 rows below tile 0, so its
           // operand of key step (1, sh) is tile 0's of step (0, sh)
@@ -421,16 +434,29 @@ __device__ __forceinline__ void decomp_body(const FrozenParams& p) {
     };
     if (factored) {
       if constexpr (kBf16) {
-        if (form16)
-          run_factored(std::true_type());
-        else
-          run_factored(std::false_type());
+        if (form16) {
+          run_factored(std::true_type(), vp16base);
+        } else {
+          // the bf16 copy replaces the fp16 one in V slots 0 and 1: each
+          // thread's DMA chunks are its own, so its own earlier loads landing
+          // first is all the order needed
+          __builtin_amdgcn_s_waitcnt(waitcnt_vm_lgkm0(0));
+          load_v(vpbase, kb0, S0());
+          load_v(vpbase, kb0 + 1, S1());
+          run_factored(std::false_type(), vpbase);
+        }
       } else {
-        run_factored(std::true_type());
+        run_factored(std::true_type(), vp16base);
       }
     }
   }
   if (!factored) {
+    if (spec) {
+      // the rebuild writes V slots 0 and 1 from every thread: the fp16 V'
+      // loaded there for the factored form lands first
+      __builtin_amdgcn_s_waitcnt(waitcnt_vm_lgkm0(0));
+      __syncthreads();
+    }
     // alpha[j0 + t] for t < 64 and rho[d] for d = dmin + t, t < RW,
     // dmin = q0 - j0 - 63.  Out-of-range distances are -inf (exact zero cells).
     auto v_lds = [&](int buf) { return reinterpret_cast<uint4*>(buf ? vs1 : vs0); };
@@ -511,6 +537,7 @@ __device__ __forceinline__ void decomp_body(const FrozenParams& p) {
     for (int qt = 0; qt < QT; ++qt) rowscale[qt] = 1.f;
   }
 
+  const bool split = p.n_items != 0 && p.part_base[qb] >= 0;
 #pragma unroll
   for (int qt = 0; qt < QT; ++qt) {
     const int i = q0w + 32 * qt + n;
@@ -545,8 +572,11 @@ void frozen_decomp_kernel(const FrozenParams p) {
 // writes r2[slot, d] = rho_d log2 e for the block's 64 distances (the main
 // kernel then reads rho as plain fp32) and their maximum
 // a_off[(n_slots + slot) * nblk + k] (so a workgroup's R is a maximum over
-// at most nblk values).  One workgroup per (key block, slot, batch); every
-// wave reduces the block's alpha itself, so nothing orders workgroups.  vp
+// at most nblk values), and z2[slot, i] = z_i log2 e for the block's 64 rows
+// with their minimum a_off[(2 n_slots + slot) * nblk + k] (the main kernel's
+// row normalisers and the smallest z of its rows).  One workgroup per (key
+// block, slot, batch); every wave reduces the block's alpha itself, so
+// nothing orders workgroups.  vp
 // holds T rows per (batch, slot); the main kernel's buffer-resource bound
 // reads rows past T as zero.
 template <typename T, int HD>
@@ -567,9 +597,7 @@ __global__ __launch_bounds__(256) void decomp_prescale_kernel(const FrozenParams
   const float al =
       j0 + lane < p.T ? load_as_f32(p.alpha, (int64_t)ph * p.a_sh + (int64_t)(j0 + lane) * p.a_ss, p.a_dtype) * kLog2e
                       : -INFINITY;
-  float am = al;
-#pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) am = fmaxf(am, __shfl_xor(am, off));
+  const float am = wave_max(al);
   if (b == 0) {
     const int nblk = (p.T + 63) / 64;
     if (tid == 0) p.a_off[(int64_t)slot * nblk + kb] = am;
@@ -578,10 +606,16 @@ __global__ __launch_bounds__(256) void decomp_prescale_kernel(const FrozenParams
                            ? load_as_f32(p.rho, (int64_t)ph * p.r_sh + (int64_t)(j0 + lane) * p.r_ss, p.r_dtype) * kLog2e
                            : -INFINITY;
       if (j0 + lane < p.T) p.r2[(int64_t)slot * p.T + j0 + lane] = rv;
-      float rmx = rv;
-#pragma unroll
-      for (int off = 32; off >= 1; off >>= 1) rmx = fmaxf(rmx, __shfl_xor(rmx, off));
+      const float rmx = wave_max(rv);
       if (lane == 0) p.a_off[(int64_t)(p.n_slots + slot) * nblk + kb] = rmx;
+    }
+    if (tid >= 128 && tid < 192) {  // wave 2: the block's rows
+      const float zv = j0 + lane < p.T
+                           ? load_as_f32(p.z, (int64_t)ph * p.z_sh + (int64_t)(j0 + lane) * p.z_ss, p.z_dtype) * kLog2e
+                           : INFINITY;
+      if (j0 + lane < p.T) p.z2[(int64_t)slot * p.T + j0 + lane] = zv;
+      const float zmn = wave_min(zv);
+      if (lane == 0) p.a_off[(int64_t)(2 * p.n_slots + slot) * nblk + kb] = zmn;
     }
   }
   const int64_t row0 = ((int64_t)b * p.n_slots + slot) * p.T;
@@ -610,8 +644,7 @@ __global__ __launch_bounds__(256) void decomp_prescale_kernel(const FrozenParams
     }
   }
   __shared__ float red[4];
-#pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) vmx = fmaxf(vmx, __shfl_xor(vmx, off));
+  vmx = wave_max(vmx);
   if (lane == 0) red[tid >> 6] = vmx;
   __syncthreads();
   if (tid == 0)

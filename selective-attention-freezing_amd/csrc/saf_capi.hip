@@ -506,10 +506,11 @@ int run_dense(const saf_tensor_t& patt, const saf_tensor_t& v, const saf_tensor_
 // Workspace regions after the scan's: the fp32 partials of split query
 // blocks (flash, dense and decomposed kernels run one after the other and
 // share them), then the factored decomposed form's per-64-block maxima of
-// alpha and of rho a_off (2 x n_dec x ceil(T / 64) floats), rho log2 e r2
-// (n_dec x T floats), key-scaled values vp (B, n_dec, T, HD) in bf16 (bf16
-// activations only) and in fp16, and their per-block largest magnitudes vmax
-// (B x n_dec x ceil(T / 64) floats) (bf16 and fp16, hd <= 128 only).
+// alpha and of rho and minima of z log2 e a_off (3 x n_dec x ceil(T / 64)
+// floats), rho log2 e r2 and z log2 e z2 (n_dec x T floats each), key-scaled
+// values vp (B, n_dec, T, HD) in bf16 (bf16 activations only) and in fp16,
+// and their per-block largest magnitudes vmax (B x n_dec x ceil(T / 64)
+// floats) (bf16 and fp16, hd <= 128 only).
 int64_t round256(int64_t n) { return (n + 255) / 256 * 256; }
 
 int64_t part_region_bytes(const saf_mixed_attn_args* args, const Plan& pl) {
@@ -528,10 +529,11 @@ int64_t part_region_bytes(const saf_mixed_attn_args* args, const Plan& pl) {
   return round256(part);
 }
 
-// Per-64-block maxima of alpha and of rho (2 x n_dec x ceil(T / 64) floats),
-// rho log2 e in fp32 (n_dec x T), then the key-scaled values.
+// Per-64-block maxima of alpha and of rho and minima of z (3 x n_dec x
+// ceil(T / 64) floats), rho log2 e and z log2 e in fp32 (n_dec x T each),
+// then the key-scaled values.
 int64_t decomp_aoff_bytes(const Plan& pl) {
-  return round256(2 * (int64_t)pl.decomp.size() * ((pl.T + 63) / 64) * 4);
+  return round256(3 * (int64_t)pl.decomp.size() * ((pl.T + 63) / 64) * 4);
 }
 int64_t decomp_r2_bytes(const Plan& pl) { return round256((int64_t)pl.decomp.size() * pl.T * 4); }
 
@@ -543,7 +545,7 @@ int64_t decomp_vmax_bytes(const Plan& pl) {
 
 int64_t decomp_vp_bytes(const Plan& pl) {
   if ((pl.dtype != SAF_BF16 && pl.dtype != SAF_F16) || pl.HD > 128 || pl.decomp.empty()) return 0;
-  return decomp_aoff_bytes(pl) + decomp_r2_bytes(pl) + 2 * decomp_v1_bytes(pl) + decomp_vmax_bytes(pl);
+  return decomp_aoff_bytes(pl) + 2 * decomp_r2_bytes(pl) + 2 * decomp_v1_bytes(pl) + decomp_vmax_bytes(pl);
 }
 
 // Decomposed P.V, causally balanced like run_dense when the workspace holds
@@ -588,7 +590,8 @@ int run_decomp(const saf_mixed_attn_args* a, const Plan& pl, hipStream_t s, bool
     char* w = reinterpret_cast<char*>(a->workspace) + vp_off;
     p.a_off = reinterpret_cast<float*>(w);
     p.r2 = reinterpret_cast<float*>(w + decomp_aoff_bytes(pl));
-    p.vp = w + decomp_aoff_bytes(pl) + decomp_r2_bytes(pl);
+    p.z2 = reinterpret_cast<float*>(w + decomp_aoff_bytes(pl) + decomp_r2_bytes(pl));
+    p.vp = w + decomp_aoff_bytes(pl) + 2 * decomp_r2_bytes(pl);
     p.vp16 = reinterpret_cast<char*>(p.vp) + decomp_v1_bytes(pl);
     p.vmax = reinterpret_cast<float*>(reinterpret_cast<char*>(p.vp16) + decomp_v1_bytes(pl));
   }

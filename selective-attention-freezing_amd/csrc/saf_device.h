@@ -150,6 +150,36 @@ __device__ inline float half_swap_sum(float x) {
   return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 
+// Maximum of x over the 64 lanes of a wave (every lane active), as a
+// wave-uniform value.  GFX9 DPP moves (a few cycles each, no LDS round trip
+// as __shfl_xor's ds_bpermute has): lane pairs and quads (quad_perm), then
+// 8- and 16-lane rows (row_half_mirror, row_mirror), then lane 15 of rows 0
+// and 2 into rows 1 and 3 (row_bcast:15) and lane 31 into rows 2 and 3
+// (row_bcast:31), after which lane 63 holds the maximum of all 64.
+template <int CTRL, int ROWMASK>
+__device__ __forceinline__ float dpp_move(float x) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(x), __float_as_int(x), CTRL, ROWMASK, 0xf, false));
+}
+__device__ inline float wave_max(float x) {
+  x = fmaxf(x, dpp_move<0xb1, 0xf>(x));   // quad_perm [1, 0, 3, 2]
+  x = fmaxf(x, dpp_move<0x4e, 0xf>(x));   // quad_perm [2, 3, 0, 1]
+  x = fmaxf(x, dpp_move<0x141, 0xf>(x));  // row_half_mirror
+  x = fmaxf(x, dpp_move<0x140, 0xf>(x));  // row_mirror
+  x = fmaxf(x, dpp_move<0x142, 0xa>(x));  // row_bcast:15, rows 1 and 3
+  x = fmaxf(x, dpp_move<0x143, 0xc>(x));  // row_bcast:31, rows 2 and 3
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), 63));
+}
+__device__ inline float wave_min(float x) { return -wave_max(-x); }
+
+// Entry i (wave-uniform) of an int16 table in the kernel arguments, read as
+// its aligned 32-bit word: the compiler then reads it with a scalar load
+// (waited with the other argument reads) instead of a 16-bit vector load
+// that the next use has to wait for.  The table must start 4-byte aligned.
+__device__ inline int arg_i16(const int16_t* t, int i) {
+  const int32_t w = reinterpret_cast<const int32_t*>(t)[i >> 1];
+  return (int)(int16_t)(uint32_t)(w >> (16 * (i & 1)));
+}
+
 // Row permutation of the S^T product (see header comment).  A-lane row
 // m = 8a + 4g + r  loads key 16*(a/2) + 8g + 4*(a%2) + r.
 __device__ inline int kperm(int m) {

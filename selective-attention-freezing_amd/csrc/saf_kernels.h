@@ -91,13 +91,15 @@ struct FrozenParams {
   // decomposed heads, factored form (null: cell-by-cell rebuild only):
   // a_off[slot][k] = max alpha log2 e over 64-key block k of the slot's head
   // (n_slots x ceil(T / 64)), followed by the same layout of maxima of
-  // rho log2 e over 64-distance blocks, vp = the key-scaled values
-  // 2^(alpha_j log2 e - a_off[slot][j / 64]) v_j, (B, n_slots, T, HD) in the
-  // input dtype, r2[slot][d] = rho_d log2 e (n_slots x T) (workspace, all
-  // written by launch_decomp_prescale)
+  // rho log2 e over 64-distance blocks and of minima of z log2 e over 64-row
+  // blocks, vp = the key-scaled values 2^(alpha_j log2 e - a_off[slot][j / 64]) v_j,
+  // (B, n_slots, T, HD) in the input dtype, r2[slot][d] = rho_d log2 e and
+  // z2[slot][i] = z_i log2 e (n_slots x T each) (workspace, all written by
+  // launch_decomp_prescale)
   float* a_off;
   void* vp;
   float* r2;
+  float* z2;
   // the same key-scaled values in fp16 (vp16, null: no fp16 factored form)
   // and their largest magnitude per (batch, slot, 64-key block) (vmax,
   // B x n_slots x ceil(T / 64)): the fp16 form needs every |V'| it reads
@@ -116,6 +118,9 @@ struct FrozenParams {
   int16_t part_base[kMaxQblk];
 };
 static_assert(sizeof(FrozenParams) <= 4096, "FrozenParams must fit the kernel argument segment");
+static_assert(offsetof(FrozenParams, out_head) % 4 == 0 && offsetof(FrozenParams, v_head) % 4 == 0 &&
+                  offsetof(FrozenParams, pat_head) % 4 == 0,
+              "the head tables are read as aligned 32-bit words (arg_i16)");
 
 // Closed-form frozen heads (state 2 heads recognised as causal mean,
 // exponential decay or sliding window): a single-pass chunked scan along T
