@@ -587,7 +587,7 @@ __global__ __launch_bounds__(256) void decomp_prescale_kernel(const FrozenParams
   const int kb = blockIdx.x, slot = blockIdx.y, b = blockIdx.z, j0 = 64 * kb;
   const int tid = threadIdx.x, lane = tid & 63;
   const int ph = p.pat_head[slot];
-  const T* vbase = reinterpret_cast<const T*>(p.v) + b * p.v_sb + (int64_t)p.v_head[slot] * p.v_sh;
+  const T* vbase = reinterpret_cast<const T*>(p.v) + b * p.v_sb + (int64_t)arg_i16(p.v_head, slot) * p.v_sh;
   uint4 w[PER];
 #pragma unroll
   for (int u = 0; u < PER; ++u) {
@@ -896,32 +896,27 @@ void frozen_dense_kernel(const FrozenParams p) {
   const int n_work = p.n_items ? p.n_items : p.n_qblk;
   if (grp >= n_work * p.n_slots) return;
   const int it = grp / p.n_slots, slot = grp % p.n_slots;
-  int qb, seg;
-  if (p.n_items) {
-    const int w = p.items[it];
-    qb = w >> 8;
-    seg = w & 255;
-  } else {
-    qb = p.n_qblk - 1 - it;
-    seg = 0;
-  }
-  qb = __builtin_amdgcn_readfirstlane(qb);
-  seg = __builtin_amdgcn_readfirstlane(seg);
-  const int h = p.out_head[slot];
-  const int64_t pat_off = (int64_t)p.pat_head[slot] * p.p_sh;
+  // item word (index clamped, no branch) and head tables (scalar word
+  // reads) issued together, ahead of any wait
+  const int w_item = p.items[min(it, kMaxItems - 1)];
+  const int qb = __builtin_amdgcn_readfirstlane(p.n_items ? w_item >> 8 : p.n_qblk - 1 - it);
+  const int seg = __builtin_amdgcn_readfirstlane(p.n_items ? w_item & 255 : 0);
+  const int h = arg_i16(p.out_head, slot);
+  const int64_t pat_off = (int64_t)arg_i16(p.pat_head, slot) * p.p_sh;
   const PT* pbase = reinterpret_cast<const PT*>(p.patt) + pat_off;
 
   const int T_len = p.T;
   const int q0 = qb * BM;
   const int nkb = (min(q0 + BM, T_len) + 63) / 64;
-  const bool split = p.n_items != 0 && p.part_base[qb] >= 0;
-  const int kb0 = split ? seg * p.seg_len : 0;
-  const int kb1 = split ? min(nkb, kb0 + p.seg_len) : nkb;
+  // an unsplit query block's item is segment 0 and spans at most seg_len
+  // blocks: the range needs no part_base lookup (read for the epilogue)
+  const int kb0 = p.n_items ? seg * p.seg_len : 0;
+  const int kb1 = p.n_items ? min(nkb, kb0 + p.seg_len) : nkb;
 
   St st;
 #pragma unroll
   for (int nb = 0; nb < NB; ++nb)
-    st.vbase[nb] = reinterpret_cast<const T*>(p.v) + (int64_t)(bg * NB + nb) * p.v_sb + (int64_t)p.v_head[slot] * p.v_sh;
+    st.vbase[nb] = reinterpret_cast<const T*>(p.v) + (int64_t)(bg * NB + nb) * p.v_sb + (int64_t)arg_i16(p.v_head, slot) * p.v_sh;
   st.v_st = p.v_st;
   st.T_len = T_len;
   st.wave = wave;
@@ -978,6 +973,7 @@ void frozen_dense_kernel(const FrozenParams p) {
     st.block(p, j + 2, kb1, kb1_w, vs2, vs1, pC, pB);
   }
 
+  const bool split = p.n_items != 0 && p.part_base[qb] >= 0;
 #pragma unroll
   for (int nb = 0; nb < NB; ++nb) {
     const int b = bg * NB + nb;
