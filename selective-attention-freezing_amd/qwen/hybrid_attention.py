@@ -233,12 +233,25 @@ class HybridAttentionBase(nn.Module):
 
     # -- the single gathered projection of the fused path ------------------
     def _projection_weights(self):
+        """[Wq[live]; Wk; Wv (; gates)] gathered once per weight version, its
+        rows padded with zeros to a multiple of 256 when the padding is whole
+        heads: hipBLASLt's bf16 kernels for an odd multiple of 128 output
+        columns run about 1.5x as long as for the next multiple of 256 (the
+        columns past the heads are never read)."""
         mods = [m for m in (self.q_live, self.k_proj, self.v_proj, self.gate) if m is not None]
         key = tuple((m.weight._version, m.weight.data_ptr()) for m in mods)
         if self._cache_key != key:
             with torch.no_grad():
-                self._w_cat = torch.cat([m.weight.detach() for m in mods])
-                self._b_cat = None if mods[0].bias is None else torch.cat([m.bias.detach() for m in mods])
+                ws = [m.weight.detach() for m in mods]
+                bs = None if mods[0].bias is None else [m.bias.detach() for m in mods]
+                rows = sum(w.size(0) for w in ws)
+                pad = -rows % 256
+                if pad and pad % self.head_dim == 0:
+                    ws.append(ws[0].new_zeros(pad, ws[0].size(1)))
+                    if bs is not None:
+                        bs.append(bs[0].new_zeros(pad))
+                self._w_cat = torch.cat(ws)
+                self._b_cat = None if bs is None else torch.cat(bs)
             self._cache_key = key
         return self._w_cat, self._b_cat
 
@@ -272,7 +285,7 @@ class HybridAttentionBase(nn.Module):
         q = y[:, :, :U].transpose(1, 2)
         k = y[:, :, U:U + HKV].transpose(1, 2)
         v = y[:, :, U + HKV:U + 2 * HKV].transpose(1, 2)
-        gate = y[:, :, U + 2 * HKV:] if self.SPEC.gated else None
+        gate = y[:, :, U + 2 * HKV:U + 2 * HKV + H] if self.SPEC.gated else None
         if U:
             if (self.SPEC.hip_prologue and hd in _PROLOGUE_HEAD_DIMS and q.dtype != torch.float32
                     and (cos.dim() == 2 or cos.size(0) == 1)):
