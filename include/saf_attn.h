@@ -272,8 +272,10 @@ int64_t saf_workspace_bytes(int32_t B, int32_t T, int32_t head_dim, int32_t n_sc
  * scan's look-back words, then one region of fp32 partials shared by the
  * live-head, dense P.V and decomposed kernels' causal load balancing (long
  * query blocks split into key segments and merged by a combine kernel; the
- * kernels run one after the other on the stream), then the decomposed heads'
- * key-scaled values for their factored form (bf16, hd <= 128).  A smaller
+ * kernels run one after the other on the stream), then the inputs of the
+ * decomposed heads' factored form (bf16 / fp16, hd <= 128: key-scaled values,
+ * rho and z in log2 units and their per-64-block maxima and minima, written
+ * by a pre-pass).  A smaller
  * workspace still works if it covers the scan: those kernels then run
  * unsplit, and decomposed heads rebuild P cell by cell (equal to rounding).
  * Partials need a 16-byte aligned workspace, the factored form a 256-byte
