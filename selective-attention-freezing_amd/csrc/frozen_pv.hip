@@ -189,18 +189,30 @@ __device__ __forceinline__ void decomp_body(const FrozenParams& p) {
     for (int pp = 0; pp < VN; ++pp)
       __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, SAF_LDS_PTR(tile + (NW * pp + wave) * 1024), 16, voff[pp], 0, 0, 0);
   };
-  // the fp32 rho log2 e values (r2) of block jb's distance window (elements
-  // 2t, 2t + 1 and 2t + 2 for thread t) and the block's alpha maximum,
-  // loaded unconditionally with indices clamped past the end
-  float er[3], ab = 0.f;
-  int ej0 = 0;
+  // The fp32 rho log2 e values (r2) of block jb's distance window (elements
+  // 2t, 2t + 1 and 2t + 2 of thread t: distances d0, d0 - 1, d0 - 2 with
+  // d0 = q0 - 64 jb + BM - 2t) and the block's alpha maximum, into register
+  // set `set` (two sets: the block loop loads them two blocks ahead).  One
+  // explicit 12-byte buffer load and one 4-byte load per block, so the
+  // block loop's vmcnt count is exact: the descriptor starts two elements
+  // before the slot's row, so byte offset 4 d0 covers d0 - 2 .. d0; below
+  // zero the offset wraps and reads zeros, past the row it reads the
+  // workspace that follows (within BM + 64 elements), and every such
+  // distance (d < 0 or d >= T) is masked where the window is written.
+  float er[2][3], ab[2] = {0.f, 0.f};
   const float* const r2 = p.r2 + (int64_t)slot * T_len;
-  auto load_er = [&](int jb) {
-    const int j0 = 64 * jb;
-#pragma unroll
-    for (int u = 0; u < 3; ++u) er[u] = r2[min(max(q0 - j0 + BM - (2 * tid + u), 0), T_len - 1)];
-    ab = ablk[min(jb, nblk - 1)];
-    ej0 = j0;
+  const __amdgpu_buffer_rsrc_t r2rs = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<float*>(r2 - 2), 0, (T_len + BM + 66) * 4, kBufferWord3);
+  const __amdgpu_buffer_rsrc_t abrs = __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(ablk), 0, nblk * 4,
+                                                                        kBufferWord3);
+  auto load_er = [&](auto set, int jb) {
+    constexpr int S = decltype(set)::value;
+    const int d0 = q0 - 64 * jb + BM - 2 * tid;
+    const auto w3 = __builtin_amdgcn_raw_buffer_load_b96(r2rs, d0 * 4, 0, 0);
+    er[S][0] = __uint_as_float(w3[2]);
+    er[S][1] = __uint_as_float(w3[1]);
+    er[S][2] = __uint_as_float(w3[0]);
+    ab[S] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(abrs, min(jb, nblk - 1) * 4, 0, 0));
   };
   using S0 = std::integral_constant<int, 0>;
   using S1 = std::integral_constant<int, 1>;
@@ -212,7 +224,7 @@ __device__ __forceinline__ void decomp_body(const FrozenParams& p) {
       load_v(vp16base, kb0, S0());
       load_v(vp16base, kb0 + 1, S1());
       spec = true;
-      load_er(kb0);
+      load_er(S0(), kb0);
       const float* const z2 = p.z2 + (int64_t)slot * T_len;
 #pragma unroll
       for (int qt = 0; qt < QT; ++qt) {
@@ -249,6 +261,7 @@ __device__ __forceinline__ void decomp_body(const FrozenParams& p) {
       if constexpr (!kBf16) factored = form16;
       aoff = am;
       roff = rm;
+      load_er(S1(), kb0 + 1);
     }
   }
   if (!spec) {
@@ -289,16 +302,18 @@ __device__ __forceinline__ void decomp_body(const FrozenParams& p) {
         return reinterpret_cast<uint16_t(*)[8 * RWL]>(decltype(slot)::value ? eb1 : eb0);
       };
       auto ecopy = [](int c) { return c * RWL + (c ? 8 : 0); };
-      auto store_er = [&](auto slot) {
+      // window of block jb into E slot `slot` from register set `set`
+      auto store_er = [&](auto slot, auto set, int jb) {
+        constexpr int S = decltype(set)::value;
         uint16_t(*const ew)[8 * RWL] = e_slot(slot);
         if (tid < RW / 2) {
           uint32_t hv[3], lv[3];  // hi and lo bits of window elements 2t, 2t + 1, 2t + 2
 #pragma unroll
           for (int u = 0; u < 3; ++u) {
             const int m = 2 * tid + u;
-            const int d = q0 - ej0 + BM - m;
+            const int d = q0 - 64 * jb + BM - m;
             // A_k - A - R; -inf for a block whose keys all have alpha -inf
-            const float x = m < RW && d >= 0 && d < T_len ? fast_exp2(er[u] + (ab - aoff - roff)) : 0.f;
+            const float x = m < RW && d >= 0 && d < T_len ? fast_exp2(er[S][u] + (ab[S] - aoff - roff)) : 0.f;
             if constexpr (F16) {
               hv[u] = Elem<_Float16>::pack2(x, 0.f) & 0xffffu;
               lv[u] = 0u;
@@ -330,31 +345,35 @@ __device__ __forceinline__ void decomp_body(const FrozenParams& p) {
         eo[qt] = ecopy(ec) + BM - il - ec + 8 * g;
       }
 
-      // prologue: E of block kb0 in E slot 0 (V' of kb0 and kb0+1 land in V
-      // slots 0, 1)
-      store_er(S0());
+      // prologue: E of block kb0 in E slot 0 from register set 0 (V' of kb0
+      // and kb0+1 land in V slots 0, 1; set 1 holds block kb0 + 1's inputs)
+      store_er(S0(), S0(), kb0);
       asm volatile("" ::: "memory");
       __builtin_amdgcn_s_waitcnt(waitcnt_vm_lgkm0(VN));
       __builtin_amdgcn_s_barrier();
       asm volatile("" ::: "memory");
       // block j in phase P: V'_j in V slot P % 3, E_j in E slot P % 2 (both
       // compile-time, so every LDS access names one array and none waits on
-      // another slot's DMA).  E_{j+1} goes to the other E slot and V'_{j+2}
-      // to V slot (P + 2) % 3, both last read in block j-1.  The rho loads are
-      // issued before the DMA, so the wait for them leaves the DMA in flight;
-      // the closing barrier waits for V'_{j+1} alone (vmcnt VN, the DMA of
-      // V'_{j+2} stays in flight; a __syncthreads would drain it) and for this
-      // block's LDS writes (lgkmcnt 0).
+      // another slot's DMA).  E_{j+1} goes to the other E slot (from register
+      // set (P + 1) % 2, loaded in block j - 1) and V'_{j+2} to V slot
+      // (P + 2) % 3, both last read in block j-1; block j + 2's window inputs
+      // go to register set P % 2 after that DMA.  The closing barrier waits
+      // for everything issued before this block (vmcnt VN + 2: V'_{j+1} and
+      // block j + 1's inputs; V'_{j+2} and block j + 2's inputs stay in
+      // flight, a __syncthreads would drain them) and for this block's LDS
+      // writes (lgkmcnt 0).
       auto block = [&](const int j, auto phase) {
         constexpr int PH = decltype(phase)::value;
         constexpr int R = PH % 3;
         using ESlot = std::integral_constant<int, PH % 2>;
         using ENext = std::integral_constant<int, 1 - PH % 2>;
         using VAhead = std::integral_constant<int, (R + 2) % 3>;
+        using SetNow = std::integral_constant<int, (PH + 1) % 2>;
+        using SetAhead = std::integral_constant<int, PH % 2>;
         const char* const vt = R == 0 ? vs0 : (R == 1 ? vs1 : vs2);
         uint16_t(*const ew)[8 * RWL] = e_slot(ESlot());
-        load_er(j + 1);
         load_v(vpb, j + 2, VAhead());
+        load_er(SetAhead(), j + 2);
         if (j < nkb_w) {
           // Toeplitz reuse: query tile 1 sits 32 rows below tile 0, so its
           // operand of key step (1, sh) is tile 0's of step (0, sh)
@@ -400,9 +419,9 @@ __device__ __forceinline__ void decomp_body(const FrozenParams& p) {
               }
             }
         }
-        if (j + 1 < nkb) store_er(ENext());
+        if (j + 1 < nkb) store_er(ENext(), SetNow(), j + 1);
         asm volatile("" ::: "memory");
-        __builtin_amdgcn_s_waitcnt(waitcnt_vm_lgkm0(VN));
+        __builtin_amdgcn_s_waitcnt(waitcnt_vm_lgkm0(VN + 2));
         __builtin_amdgcn_s_barrier();
         asm volatile("" ::: "memory");
       };
