@@ -127,6 +127,8 @@ DEC_CASES = [
     (2, 12, 1024, 64, 1024, [], list(range(12)), True),
     (2, 12, 700, 64, 1024, [3], [0, 7], False),
     (2, 12, 37, 64, 1024, [5], [0, 2], False),
+    (3, 12, 1, 64, 64, [], [0, 2], False),
+    (2, 12, 65, 64, 128, [], [1, 4, 9], False),
     (1, 16, 2048, 96, 2048, [0, 8], [7, 15], False),
     (4, 12, 2048, 64, 2048, [1], [0, 2], False),
     (1, 8, 1000, 128, 1024, [2], [3, 5], False),
