@@ -241,6 +241,16 @@ int saf_qk_rmsnorm_rope_inplace(const saf_tensor_t* q, const saf_tensor_t* k, co
 int saf_add_layernorm(const saf_tensor_t* x, const saf_tensor_t* delta, const saf_tensor_t* weight,
                       const saf_tensor_t* bias, float eps, const saf_tensor_t* out, void* stream);
 
+/* MLP up-projection and activation of the GPT block in one kernel:
+ * out = gelu(x weight^T) with gelu(u) = u / 2 (1 + erf(u / sqrt 2)) (the exact
+ * GELU, nn.GELU's default), for x (M, K), weight (N, K) (an nn.Linear weight
+ * without bias) and out (M, N), all bf16 or all fp16 with unit column stride;
+ * fp32 accumulation, the GELU in fp32 on the accumulator, one rounding of out.
+ * N is a multiple of 256 and K of 128 (any M); x and weight rows 16-byte
+ * aligned, out rows 8-byte aligned.  No workspace.  Replaces c_fc followed by
+ * gelu in MLP.forward (nanogpt/model.py:1202-1204) on the prefill path. */
+int saf_linear_gelu(const saf_tensor_t* x, const saf_tensor_t* weight, const saf_tensor_t* out, void* stream);
+
 /* Row normalisers of decomposed patterns: z[h, i] = logsumexp over j <= i of
  * alpha[h, j] + rho[h, i - j], for (H, S) fp32 alpha, rho and z with unit
  * column stride (any row stride).  Rows whose logits are all -inf get -inf.

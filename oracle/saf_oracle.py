@@ -30,10 +30,13 @@ Each function restates the reference's algorithm from its source
   rope                    nanogpt/model.py:57-99
   add_layernorm           nanogpt/model.py:45-54 (LayerNorm, eps 1e-5) with the
                           residual additions of Block.forward (:1214-1240)
+  linear_gelu             nanogpt/model.py:1193-1207 (MLP: c_fc without bias,
+                          then nn.GELU(), the exact erf form)
 
 How each is pinned (tests/test_oracle.py): torch SDPA as the library special
 case of the all-live case (torch.nn.functional.layer_norm likewise for
-add_layernorm); brute-force pure-Python loops on tiny inputs;
+add_layernorm, torch.nn.functional.gelu and the normal CDF's closed values
+for linear_gelu); brute-force pure-Python loops on tiny inputs;
 closed forms (prefix sums, IIR recurrences, box filters) against the dense
 patterns; invariants (rows sum to 1, T = 1 gives y = v, frozen heads ignore
 Q/K, head-permutation equivariance); routing tables brute-forced over every
@@ -449,6 +452,15 @@ def apply_rope(x, cos, sin):
     half = x.shape[-1] // 2
     rot = np.concatenate([-x[..., half:], x[..., :half]], axis=-1)
     return x * cos + rot * sin
+
+
+def linear_gelu(x, weight):
+    """MLP up-projection and activation of the GPT block (nanogpt/model.py:
+    1193-1207, bias-free c_fc then nn.GELU()): u = x w^T, gelu(u) =
+    u / 2 (1 + erf(u / sqrt 2)), in float64."""
+    from scipy.special import erf
+    u = _f64(x) @ _f64(weight).T
+    return u * 0.5 * (1.0 + erf(u / math.sqrt(2.0)))
 
 
 def add_layernorm(x, delta, weight, bias=None, eps=1e-5, round_fn=None):

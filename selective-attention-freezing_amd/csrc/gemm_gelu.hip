@@ -1,0 +1,290 @@
+// MLP up-projection with the exact GELU fused into the GEMM's epilogue, on
+// gfx950 (the caller side of the attention path: /root/reference/nanogpt/
+// model.py:1193-1207, c_fc followed by nn.GELU()):
+//
+//   C[m][n] = gelu(sum_k A[m][k] W[n][k]),  gelu(u) = u Phi(u) = u (1 + erf(u / sqrt 2)) / 2
+//
+// A (M x K) the LayerNorm output, W (N x K) the nn.Linear weight, C (M x N),
+// all bf16 / fp16 and row-major (N a multiple of 256, K of 128, any M); fp32
+// accumulation, the GELU in fp32 on the accumulator, one rounding of C.
+// Fusing the activation removes the separate pass that reads and writes C
+// again.  erf comes from Abramowitz and Stegun's rational approximation
+// 7.1.26 (Handbook of Mathematical Functions, 1964), absolute error at most
+// 1.5e-7, far below the output's half-ulp.
+//
+// Tiling: 256 x 256 tiles of C, one persistent workgroup of 8 waves per CU
+// walking its tiles in turn; wave w computes the 64 (rows of A) x 128 (rows
+// of W) block (64 (w / 2), 128 (w % 2)).  The product runs transposed
+// (C^T = W A^T on v_mfma_f32_32x32x16): W rows are the MFMA's A operand, A
+// rows its B operand, both read with ds_read_b128 (8 consecutive k of a row)
+// from LDS tiles of 256 rows x 32 k, so each lane's accumulator holds 4 runs
+// of 4 consecutive columns of one row of C, paired across the wave's halves
+// into 16-byte pieces for the stores.  The k
+// tiles arrive by buffer_load ... lds DMA into four LDS stages, three k steps
+// ahead, as one stream over the workgroup's tiles: the last steps of a tile
+// load the first k tiles of the next, which land while the epilogue runs.
+// The 16-byte chunks of a tile row are XOR-swizzled by the row so that the
+// reads of a 16-lane group hit distinct banks.
+#include "saf_kernels.h"
+
+namespace saf {
+
+namespace {
+
+constexpr int kGBM = 256, kGBN = 256, kGBK = 32, kGStages = 4, kGWaves = 8;
+constexpr int kGRowBytes = kGBK * 2;          // one k-tile row (64 bytes)
+constexpr int kGTileBytes = kGBM * kGRowBytes;  // one operand's k tile (16 KB)
+constexpr int kGChunks = kGBK / 8;            // 16-byte chunks per row
+constexpr int kGDma = kGBM * kGChunks / (64 * kGWaves);  // DMA loads per thread, operand and step
+static_assert(kGBM == kGBN, "both operand tiles have kGBM rows");
+static_assert(kGDma * 64 * kGWaves == kGBM * kGChunks, "DMA chunks split evenly over the threads");
+
+// logical chunk c of row r sits at chunk c ^ swz(r): rows r .. r + 15 of one
+// chunk land on 16 distinct 4-bank groups (row pitch 64 bytes); the swizzle
+// depends on r % 16 only
+__device__ __forceinline__ int gswz(int r) { return (r >> 2) & 3; }
+
+// byte offset in a k tile of row r, logical chunk c
+__device__ __forceinline__ int gtile_off(int r, int c) { return r * kGRowBytes + 16 * (c ^ gswz(r)); }
+
+// gelu(u) = u Phi(u) with Phi(u) = 1 - erfc(u / sqrt 2) / 2 for u >= 0 and
+// erfc(|u| / sqrt 2) / 2 below, erfc(z) = t (a1 + t (a2 + ... + t a5)) e^{-z^2},
+// t = 1 / (1 + p z) (A&S 7.1.26; the 1/2 folded into the a_i)
+__device__ __forceinline__ float gelu_f(float u) {
+  constexpr float kSqrtHalf = 0.70710678118654752440f;
+  const float z = fabsf(u) * kSqrtHalf;
+  const float t = __builtin_amdgcn_rcpf(fmaf(0.3275911f, z, 1.f));
+  float pol = fmaf(t, 0.5f * 1.061405429f, 0.5f * -1.453152027f);
+  pol = fmaf(t, pol, 0.5f * 1.421413741f);
+  pol = fmaf(t, pol, 0.5f * -0.284496736f);
+  pol = fmaf(t, pol, 0.5f * 0.254829592f);
+  const float h = pol * t * __builtin_amdgcn_exp2f(z * (z * -kLog2e));
+  return u * (u >= 0.f ? 1.f - h : h);
+}
+
+template <typename T>
+__global__ __launch_bounds__(64 * kGWaves) __attribute__((amdgpu_waves_per_eu(2, 2)))
+void gemm_gelu_kernel(const GemmGeluParams p) {
+  // one array per operand and stage, so that the compiler's wait insertion
+  // sees that a read of one stage does not depend on the DMAs into the others
+  __shared__ __align__(16) char sw0[kGTileBytes], sw1[kGTileBytes], sw2[kGTileBytes], sw3[kGTileBytes];
+  __shared__ __align__(16) char sa0[kGTileBytes], sa1[kGTileBytes], sa2[kGTileBytes], sa3[kGTileBytes];
+  auto wst = [&](auto stage) -> char* {
+    constexpr int S = decltype(stage)::value;
+    return S == 0 ? sw0 : (S == 1 ? sw1 : (S == 2 ? sw2 : sw3));
+  };
+  auto ast = [&](auto stage) -> char* {
+    constexpr int S = decltype(stage)::value;
+    return S == 0 ? sa0 : (S == 1 ? sa1 : (S == 2 ? sa2 : sa3));
+  };
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int n32 = lane & 31, g = lane >> 5;
+  const int wm = wave >> 1, wn = wave & 1;
+
+  // tile order: workgroup b runs on XCD b % 8; each XCD owns a contiguous
+  // run of per_xcd tiles (columns fastest), which its gridDim / 8 workgroups
+  // take in strides, so the tiles in flight on an XCD stay contiguous and the
+  // A rows of a tile row stay in that XCD's L2
+  const int tiles_n = p.N / kGBN, tiles = ((p.M + kGBM - 1) / kGBM) * tiles_n;
+  const int per_xcd = (tiles + 7) / 8;
+  const int xcd = (int)(blockIdx.x % 8), local = (int)(blockIdx.x / 8), n_local = (int)(gridDim.x / 8);
+  auto tile_of = [&](int i) {
+    const int v = local + i * n_local, t = xcd * per_xcd + v;
+    return v < per_xcd && t < tiles ? t : -1;
+  };
+  int cur = tile_of(0);
+  if (cur < 0) return;
+  int nxt = tile_of(1);
+
+  // DMA: load q of a thread writes chunk X = (8 q + wave) * 64 + lane of a
+  // tile, i.e. row X / 4, stored chunk X % 4 = logical chunk (X % 4) ^ swz(row);
+  // source offsets from the tile's first row at k = 0
+  uint32_t aoff[kGDma], woff[kGDma];
+#pragma unroll
+  for (int q = 0; q < kGDma; ++q) {
+    const int X = (kGWaves * q + wave) * 64 + lane;
+    const int r = X / kGChunks, c = (X % kGChunks) ^ gswz(r);
+    aoff[q] = (uint32_t)(r * p.a_rs * 2 + 16 * c);
+    woff[q] = (uint32_t)(r * p.w_rs * 2 + 16 * c);
+  }
+  const int nk = p.K / kGBK;  // a multiple of kGStages
+  // descriptors over a tile's rows of A (rows past M read as zero) and W; a
+  // missing tile gets empty ones, whose loads write zeros
+  auto a_rsrc = [&](int t) {
+    const int m0 = t < 0 ? 0 : (t / tiles_n) * kGBM;
+    const T* base = reinterpret_cast<const T*>(p.a) + (int64_t)m0 * p.a_rs;
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<T*>(base), 0, t < 0 ? 0 : min(kGBM, p.M - m0) * p.a_rs * 2,
+                                             kBufferWord3);
+  };
+  auto w_rsrc = [&](int t) {
+    const int n0 = t < 0 ? 0 : (t % tiles_n) * kGBN;
+    const T* base = reinterpret_cast<const T*>(p.w) + (int64_t)n0 * p.w_rs;
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<T*>(base), 0, t < 0 ? 0 : kGBN * p.w_rs * 2, kBufferWord3);
+  };
+  __amdgpu_buffer_rsrc_t ars = a_rsrc(cur), wrs = w_rsrc(cur), arn = a_rsrc(nxt), wrn = w_rsrc(nxt);
+
+  // the DMA of k step j of the stream position: j < nk reads the current
+  // tile at k step j, j >= nk the next tile at k step j - nk
+  auto load_step = [&](int j, auto stage) {
+    char* const tw = wst(stage);
+    char* const ta = ast(stage);
+    const bool here = j < nk;
+    const int so = kGRowBytes * (here ? j : j - nk);
+#pragma unroll
+    for (int q = 0; q < kGDma; ++q)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(here ? ars : arn, SAF_LDS_PTR(ta + (kGWaves * q + wave) * 1024), 16,
+                                               aoff[q], so, 0, 0);
+#pragma unroll
+    for (int q = 0; q < kGDma; ++q)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(here ? wrs : wrn, SAF_LDS_PTR(tw + (kGWaves * q + wave) * 1024), 16,
+                                               woff[q], so, 0, 0);
+  };
+
+  // read offsets of this lane: W rows 128 wn + 32 nt + n32, A rows
+  // 64 wm + 32 mt + n32, logical chunk 2 s + g for k substep s; the 32-row
+  // subtiles nt / mt sit 2 KB apart
+  int wrd[2], ard[2];
+#pragma unroll
+  for (int s = 0; s < 2; ++s) {
+    wrd[s] = gtile_off(128 * wn + n32, 2 * s + g);
+    ard[s] = gtile_off(64 * wm + n32, 2 * s + g);
+  }
+  constexpr int kSub = 32 * kGRowBytes;
+
+  f32x16_t acc[4][2];
+  auto read_sub = [&](auto stage, auto sub, uint4 (&wa)[4], uint4 (&ab)[2]) {
+    constexpr int s = decltype(sub)::value;
+#pragma unroll
+    for (int nt = 0; nt < 4; ++nt) wa[nt] = *reinterpret_cast<const uint4*>(wst(stage) + wrd[s] + nt * kSub);
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt) ab[mt] = *reinterpret_cast<const uint4*>(ast(stage) + ard[s] + mt * kSub);
+  };
+  auto mma = [&](const uint4 (&wa)[4], const uint4 (&ab)[2]) {
+#pragma unroll
+    for (int nt = 0; nt < 4; ++nt)
+#pragma unroll
+      for (int mt = 0; mt < 2; ++mt) acc[nt][mt] = Elem<T>::mfma(wa[nt], ab[mt], acc[nt][mt]);
+  };
+
+  using G0 = std::integral_constant<int, 0>;
+  using G1 = std::integral_constant<int, 1>;
+  using G2 = std::integral_constant<int, 2>;
+  using G3 = std::integral_constant<int, 3>;
+  using Sub0 = std::integral_constant<int, 0>;
+  using Sub1 = std::integral_constant<int, 1>;
+  load_step(0, G0());
+  load_step(1, G1());
+  load_step(2, G2());
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_waitcnt(waitcnt_vm_lgkm0(4 * kGDma));  // step 0 landed, steps 1, 2 in flight
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+  uint4 wa0[4], ab0[2], wa1[4], ab1[2];
+  read_sub(G0(), Sub0(), wa0, ab0);
+
+  // k step j in stage j % 4 (nk is a multiple of 4, so every tile starts at
+  // stage 0), its substep 0 operands already in registers: the DMA of stream
+  // step j + 3 goes to stage (j + 3) % 4, last read in step j - 1 (every
+  // wave's reads of it completed before the previous barrier); substep 1's
+  // reads run under substep 0's products; the barrier follows the wait for
+  // step j + 1's DMA (steps j + 2, j + 3 stay in flight) and for this wave's
+  // reads of stage j, and step j + 1's substep 0 reads (the next tile's
+  // first k tile after a tile's last step) run under substep 1's products.
+  // The scheduling barriers keep each group of reads ahead of the products
+  // it overlaps.
+  auto step = [&](int j, auto stage) {
+    constexpr int S = decltype(stage)::value;
+    using Ahead = std::integral_constant<int, (S + 3) % kGStages>;
+    using Next = std::integral_constant<int, (S + 1) % kGStages>;
+    load_step(j + 3, Ahead());
+    read_sub(stage, Sub1(), wa1, ab1);
+    __builtin_amdgcn_sched_barrier(0);
+    mma(wa0, ab0);
+    __builtin_amdgcn_sched_barrier(0);
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_waitcnt(waitcnt_vm_lgkm0(4 * kGDma));
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+    read_sub(Next(), Sub0(), wa0, ab0);
+    __builtin_amdgcn_sched_barrier(0);
+    mma(wa1, ab1);
+    __builtin_amdgcn_sched_barrier(0);
+  };
+
+  for (int i = 1;; ++i) {
+#pragma unroll
+    for (int nt = 0; nt < 4; ++nt)
+#pragma unroll
+      for (int mt = 0; mt < 2; ++mt) acc[nt][mt] = zero16();
+    for (int j = 0; j < nk; j += kGStages) {
+      step(j, G0());
+      step(j + 1, G1());
+      step(j + 2, G2());
+      step(j + 3, G3());
+    }
+
+    // epilogue of tile cur (the next tile's first k tiles are in flight):
+    // lane (n32, g), tile (nt, mt), register 4 q + e holds C[row][col],
+    // row = m0 + 64 wm + 32 mt + n32, col = n0 + 128 wn + 32 nt + 8 q + 4 g + e.
+    // v_permlane32_swap(vdst, vsrc) exchanges vdst of lanes 32..63 with vsrc
+    // of lanes 0..31: with vdst = piece q = 2 r and vsrc = piece 2 r + 1, lane
+    // (n32, 0) ends with columns 16 r + 0..7 and lane (n32, 1) with
+    // 16 r + 8..15 of the row, one 16-byte store each
+    const int m0 = (cur / tiles_n) * kGBM, n0 = (cur % tiles_n) * kGBN;
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt) {
+      const int row = m0 + 64 * wm + 32 * mt + n32;
+      T* crow = reinterpret_cast<T*>(p.c) + (int64_t)row * p.c_rs + n0 + 128 * wn + 8 * g;
+#pragma unroll
+      for (int nt = 0; nt < 4; ++nt)
+#pragma unroll
+        for (int r = 0; r < 2; ++r) {
+          const f32x16_t& a = acc[nt][mt];
+          uint32_t pc[2][2];
+#pragma unroll
+          for (int h = 0; h < 2; ++h) {
+            const int q = 2 * r + h;
+            pc[h][0] = Elem<T>::pack2(gelu_f(a[4 * q]), gelu_f(a[4 * q + 1]));
+            pc[h][1] = Elem<T>::pack2(gelu_f(a[4 * q + 2]), gelu_f(a[4 * q + 3]));
+          }
+          const auto s0 = __builtin_amdgcn_permlane32_swap(pc[0][0], pc[1][0], false, false);
+          const auto s1 = __builtin_amdgcn_permlane32_swap(pc[0][1], pc[1][1], false, false);
+          if (row < p.M) *reinterpret_cast<uint4*>(crow + 32 * nt + 16 * r) = make_uint4(s0[0], s1[0], s0[1], s1[1]);
+        }
+    }
+    if (nxt < 0) break;
+    cur = nxt;
+    nxt = tile_of(i + 1);
+    ars = arn;
+    wrs = wrn;
+    arn = a_rsrc(nxt);
+    wrn = w_rsrc(nxt);
+  }
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_waitcnt(waitcnt_vm_lgkm0(0));  // the trailing (empty) DMAs land before exit
+}
+
+}  // namespace
+
+bool gemm_gelu_shape_ok(int64_t M, int64_t N, int64_t K) {
+  return M > 0 && N > 0 && K > 0 && N % kGBN == 0 && K % (kGBK * kGStages) == 0;
+}
+
+hipError_t launch_gemm_gelu(const GemmGeluParams& p, int dtype, hipStream_t s) {
+  // one workgroup per CU (a multiple of the 8 XCDs), fewer for small problems
+  const int tiles = ((p.M + kGBM - 1) / kGBM) * (p.N / kGBN);
+  const int per_xcd = (tiles + 7) / 8;
+  const int n_local = max(1, min(p.n_cu / 8, per_xcd));
+  const dim3 grid((unsigned)(8 * n_local));
+  if (dtype == kBF16)
+    hipLaunchKernelGGL(gemm_gelu_kernel<__bf16>, grid, dim3(64 * kGWaves), 0, s, p);
+  else if (dtype == kF16)
+    hipLaunchKernelGGL(gemm_gelu_kernel<_Float16>, grid, dim3(64 * kGWaves), 0, s, p);
+  else
+    return hipErrorInvalidValue;
+  return hipGetLastError();
+}
+
+}  // namespace saf

@@ -996,6 +996,50 @@ int saf_add_layernorm(const saf_tensor_t* x, const saf_tensor_t* delta, const sa
   return launched(launch_add_layernorm(p, x->dtype, reinterpret_cast<hipStream_t>(stream)), "add_layernorm");
 }
 
+int saf_linear_gelu(const saf_tensor_t* x, const saf_tensor_t* weight, const saf_tensor_t* out, void* stream) {
+  if (x == nullptr || weight == nullptr || out == nullptr || !present(*x) || !present(*weight) || !present(*out))
+    return fail(SAF_EINVAL, "x, weight and out are required");
+  if (x->ndim != 2 || weight->ndim != 2 || out->ndim != 2)
+    return fail(SAF_EINVAL, "x (M, K), weight (N, K) and out (M, N) must be 2-D");
+  if (x->dtype != SAF_BF16 && x->dtype != SAF_F16)
+    return fail(SAF_EUNSUPPORTED, "linear_gelu supports bf16 / fp16 (got %s)", dtype_name(x->dtype));
+  if (weight->dtype != x->dtype || out->dtype != x->dtype)
+    return fail(SAF_EINVAL, "x, weight and out must share one dtype");
+  const int64_t M = x->size[0], K = x->size[1], N = weight->size[0];
+  if (weight->size[1] != K || out->size[0] != M || out->size[1] != N)
+    return fail(SAF_EINVAL, "shapes do not chain: x (%lld, %lld), weight (%lld, %lld), out (%lld, %lld)",
+                (long long)M, (long long)K, (long long)weight->size[0], (long long)weight->size[1],
+                (long long)out->size[0], (long long)out->size[1]);
+  if (x->stride[1] != 1 || weight->stride[1] != 1 || out->stride[1] != 1)
+    return fail(SAF_EALIGN, "x, weight and out need a unit column stride");
+  if (M == 0) return SAF_OK;
+  if (!gemm_gelu_shape_ok(M, N, K) || M > 0x7fffffff)
+    return fail(SAF_EUNSUPPORTED, "linear_gelu: N = %lld must be a multiple of 256 and K = %lld of 128",
+                (long long)N, (long long)K);
+  // 16-byte pieces of x and weight rows, 8-byte pieces of out rows; the
+  // buffer descriptors span 256 rows of x and weight
+  auto rows_ok = [](const saf_tensor_t& t, int align) {
+    return reinterpret_cast<uintptr_t>(t.data) % align == 0 && (t.stride[0] * 2) % align == 0 &&
+           t.stride[0] >= t.size[1] && t.stride[0] < (1 << 22);
+  };
+  if (!rows_ok(*x, 16) || !rows_ok(*weight, 16) || !rows_ok(*out, 8))
+    return fail(SAF_EALIGN, "x and weight rows must be 16-byte aligned and out rows 8-byte aligned "
+                            "(row strides below 2^22 elements)");
+  GemmGeluParams p{};
+  p.a = x->data;
+  p.w = weight->data;
+  p.c = out->data;
+  p.M = (int)M;
+  p.N = (int)N;
+  p.K = (int)K;
+  p.a_rs = (int)x->stride[0];
+  p.w_rs = (int)weight->stride[0];
+  p.c_rs = (int)out->stride[0];
+  p.n_cu = cu_count();
+  const hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  return launched(timed([&] { return launch_gemm_gelu(p, x->dtype, s); }, s), "linear_gelu");
+}
+
 int saf_decomposed_logz(const saf_tensor_t* alpha, const saf_tensor_t* rho, const saf_tensor_t* z, void* stream) {
   if (alpha == nullptr || rho == nullptr || z == nullptr || !present(*alpha) || !present(*rho) || !present(*z))
     return fail(SAF_EINVAL, "alpha, rho and z are required");

@@ -231,6 +231,23 @@ def test_add_layernorm_matches_torch_layer_norm():
     assert np.allclose(y1.mean(-1), 0, atol=1e-12) and np.allclose(y1.var(-1), 1 / (1 + 1e-5 / (x + d).numpy().var(-1)))
 
 
+def test_linear_gelu_matches_torch_and_the_normal_cdf():
+    # the library special case: torch's exact GELU of the float64 product
+    g = torch.Generator().manual_seed(11)
+    x, w = torch.randn(7, 48, generator=g, dtype=torch.float64), torch.randn(40, 48, generator=g, dtype=torch.float64)
+    y = orc.linear_gelu(x.numpy(), w.numpy())
+    ref = torch.nn.functional.gelu(x @ w.T, approximate="none")
+    assert np.allclose(y, ref.numpy(), atol=1e-12, rtol=1e-12)
+    # gelu(u) = u Phi(u): identity weight rows give the closed values
+    # Phi(0) = 1/2, Phi(1) = 0.841344746068543, Phi(-2) = 0.022750131948179
+    u = np.array([[0.0, 1.0, -2.0, 30.0]])
+    y = orc.linear_gelu(u, np.eye(4))
+    assert np.allclose(y, [[0.0, 0.841344746068543, -2 * 0.022750131948179, 30.0]], atol=1e-14)
+    # gelu(u) - gelu(-u) = u (the odd part); a dropped 1/2 or sqrt 2 breaks it
+    v = np.linspace(-6, 6, 97)[None, :]
+    assert np.allclose(orc.linear_gelu(v, np.eye(97)) - orc.linear_gelu(-v, np.eye(97)), v, atol=1e-13)
+
+
 def test_planted_oracle_mistake_is_caught():
     """A transposed pattern (a plausible slip) breaks the causal-mean check."""
     T = 12
