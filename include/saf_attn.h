@@ -247,9 +247,28 @@ int saf_add_layernorm(const saf_tensor_t* x, const saf_tensor_t* delta, const sa
  * without bias) and out (M, N), all bf16 or all fp16 with unit column stride;
  * fp32 accumulation, the GELU in fp32 on the accumulator, one rounding of out.
  * N is a multiple of 256 and K of 128 (any M); x and weight rows 16-byte
- * aligned, out rows 8-byte aligned.  No workspace.  Replaces c_fc followed by
+ * aligned, out rows 16-byte aligned.  No workspace.  Replaces c_fc followed by
  * gelu in MLP.forward (nanogpt/model.py:1202-1204) on the prefill path. */
 int saf_linear_gelu(const saf_tensor_t* x, const saf_tensor_t* weight, const saf_tensor_t* out, void* stream);
+
+/* Indexed QKV projection with the rotary embedding in one kernel:
+ * out = x weight^T for x (M, K) = (B T, K) and weight (N, K) the gathered
+ * [Wq[live]; Wk[live]; Wv] rows (zero rows may pad N), with the first n_rope
+ * columns (the live heads' q and k, heads of head_dim columns) rotated at
+ * position t = row mod seq_len by the Llama half rotation
+ *   out[d] = u[d] cos[t][d] - u[d + hd/2] sin[t][d]   (d < hd/2),
+ *   out[d] = u[d] cos[t][d] + u[d - hd/2] sin[t][d]   (d >= hd/2),
+ * computed in fp32 on the accumulator and rounded once; the other columns are
+ * the plain product.  bf16 / fp16 throughout (cos / sin (>= seq_len, >= hd)
+ * in x's dtype, unit column stride, 8-byte aligned rows); N a multiple of 256,
+ * K of 128, n_rope a multiple of 128, head_dim 64 or 128, M a multiple of
+ * seq_len; x, weight and out rows 16-byte aligned.  No workspace.  Replaces
+ * the projection of the gathered weight (nanogpt/model.py:920-944,
+ * :1003-1004) and apply_rotary_pos_emb on the live q / k (:57-99,
+ * :1007-1008) on the prefill path. */
+int saf_linear_rope(const saf_tensor_t* x, const saf_tensor_t* weight, const saf_tensor_t* out, int32_t n_rope,
+                    int32_t head_dim, int32_t seq_len, const saf_tensor_t* cos, const saf_tensor_t* sin,
+                    void* stream);
 
 /* Row normalisers of decomposed patterns: z[h, i] = logsumexp over j <= i of
  * alpha[h, j] + rho[h, i - j], for (H, S) fp32 alpha, rho and z with unit

@@ -32,6 +32,8 @@ Each function restates the reference's algorithm from its source
                           residual additions of Block.forward (:1214-1240)
   linear_gelu             nanogpt/model.py:1193-1207 (MLP: c_fc without bias,
                           then nn.GELU(), the exact erf form)
+  linear_rope             nanogpt/model.py:920-944 (the gathered QKV projection)
+                          followed by :57-99 (the rotation of the live q / k)
 
 How each is pinned (tests/test_oracle.py): torch SDPA as the library special
 case of the all-live case (torch.nn.functional.layer_norm likewise for
@@ -461,6 +463,21 @@ def linear_gelu(x, weight):
     from scipy.special import erf
     u = _f64(x) @ _f64(weight).T
     return u * 0.5 * (1.0 + erf(u / math.sqrt(2.0)))
+
+
+def linear_rope(x, weight, n_rope, head_dim, cos, sin, seq_len):
+    """The gathered QKV projection with its rotary embedding (nanogpt/model.py:
+    920-944, :57-99): u = x w^T for rows r = b T + t; the first n_rope columns
+    are heads of head_dim columns, each rotated at position t = r mod T by
+    apply_rope with the given (>= T, head_dim) cos / sin rows; the remaining
+    columns are u itself.  float64."""
+    u = _f64(x) @ _f64(weight).T
+    out = u.copy()
+    t = np.arange(u.shape[0]) % seq_len
+    c, s = _f64(cos)[t, :head_dim], _f64(sin)[t, :head_dim]
+    for h0 in range(0, n_rope, head_dim):
+        out[:, h0:h0 + head_dim] = apply_rope(u[:, h0:h0 + head_dim], c, s)
+    return out
 
 
 def add_layernorm(x, delta, weight, bias=None, eps=1e-5, round_fn=None):

@@ -15,7 +15,7 @@ CSRC = os.path.join(HERE, "csrc")
 BUILD = os.path.join(HERE, "_build")
 OUT = os.path.join(HERE, "kernel", "libsafattn.so")
 SOURCES = ("saf_capi.hip", "flash_fwd.hip", "frozen_pv.hip", "frozen_scan.hip", "rope.hip", "layernorm.hip",
-           "attn_bwd.hip", "decomp_logz.hip", "attn_f32.hip", "gemm_gelu.hip")
+           "attn_bwd.hip", "decomp_logz.hip", "attn_f32.hip", "proj_gemm.hip")
 ARCH = "gfx950"
 
 HIPCC_FLAGS = [

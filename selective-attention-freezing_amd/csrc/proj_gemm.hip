@@ -1,18 +1,27 @@
-// MLP up-projection with the exact GELU fused into the GEMM's epilogue, on
-// gfx950 (the caller side of the attention path: /root/reference/nanogpt/
-// model.py:1193-1207, c_fc followed by nn.GELU()):
+// Projection GEMMs with fused epilogues, on gfx950: C = epi(A W^T) for A
+// (M x K) activations, W (N x K) an nn.Linear weight without bias and C
+// (M x N), all bf16 / fp16 and row-major (N a multiple of 256, K of 128, any
+// M); fp32 accumulation, the epilogue in fp32 on the accumulator, one
+// rounding of C.  Two epilogues (the caller side of the attention path):
 //
-//   C[m][n] = gelu(sum_k A[m][k] W[n][k]),  gelu(u) = u Phi(u) = u (1 + erf(u / sqrt 2)) / 2
-//
-// A (M x K) the LayerNorm output, W (N x K) the nn.Linear weight, C (M x N),
-// all bf16 / fp16 and row-major (N a multiple of 256, K of 128, any M); fp32
-// accumulation, the GELU in fp32 on the accumulator, one rounding of C.
-// Fusing the activation removes the separate pass that reads and writes C
-// again.  Phi comes from an odd polynomial fitted to it on |u| <= 3.5 and,
-// beyond, from Abramowitz and Stegun's rational approximation of erfc
-// (7.1.26, Handbook of Mathematical Functions, 1964, absolute error at most
-// 1.5e-7); either way the GELU is within 5.3e-6 of the exact value, far below
-// the output's half-ulp for values of that size.
+// * the exact GELU of the MLP's up-projection (/root/reference/nanogpt/
+//   model.py:1193-1207, c_fc followed by nn.GELU()):
+//     C[m][n] = gelu(u) = u Phi(u) = u (1 + erf(u / sqrt 2)) / 2,  u = (A W^T)[m][n]
+//   Phi comes from an odd polynomial fitted to it on |u| <= 3.5 and, beyond,
+//   from Abramowitz and Stegun's rational approximation of erfc (7.1.26,
+//   Handbook of Mathematical Functions, 1964, absolute error at most 1.5e-7);
+//   either way the GELU is within 5.3e-6 of the exact value, far below the
+//   output's half-ulp for values of that size.  Fusing it removes the pass that
+//   reads and writes C again.
+// * the rotary embedding of the indexed QKV projection (the gathered
+//   [Wq[live]; Wk[live]; Wv] weight of nanogpt/model.py:920-944 and the Llama
+//   half rotation of :57-99 applied to the live q / k at :1003-1008): the
+//   first n_rope columns are heads of hd columns, each rotated at position
+//   t = m mod T,
+//     C[m][d] = u[d] cos[t][d] - u[d + hd/2] sin[t][d]            d <  hd/2
+//     C[m][d] = u[d] cos[t][d] + u[d - hd/2] sin[t][d]            d >= hd/2
+//   and the columns after them (V, zero padding) are stored as they are.
+//   Fusing it removes the pass over q and k.
 //
 // Tiling: 256 x 256 tiles of C, one persistent workgroup of 8 waves per CU
 // walking its tiles in turn; wave w computes the 64 (rows of A) x 128 (rows
@@ -20,13 +29,13 @@
 // (C^T = W A^T on v_mfma_f32_32x32x16): W rows are the MFMA's A operand, A
 // rows its B operand, both read with ds_read_b128 (8 consecutive k of a row)
 // from LDS tiles of 256 rows x 32 k, so each lane's accumulator holds 4 runs
-// of 4 consecutive columns of one row of C, paired across the wave's halves
-// into 16-byte pieces for the stores.  The k
-// tiles arrive by buffer_load ... lds DMA into four LDS stages, three k steps
-// ahead, as one stream over the workgroup's tiles: the last steps of a tile
-// load the first k tiles of the next, which land while the epilogue runs.
-// The 16-byte chunks of a tile row are XOR-swizzled by the row so that the
-// reads of a 16-lane group hit distinct banks.
+// of 4 consecutive columns of one row of C (a rotation pair d, d + hd/2 sits
+// in one lane), paired across the wave's halves into 16-byte pieces for the
+// stores.  The k tiles arrive by buffer_load ... lds DMA into four LDS stages,
+// three k steps ahead, as one stream over the workgroup's tiles: the last
+// steps of a tile load the first k tiles of the next, which land while the
+// epilogue runs.  The 16-byte chunks of a tile row are XOR-swizzled by the
+// row so that the reads of a 16-lane group hit distinct banks.
 #include "saf_kernels.h"
 
 namespace saf {
@@ -105,9 +114,12 @@ __device__ __forceinline__ void gelu_group(float (&x)[n]) {
   for (int i = 0; i < n; ++i) x[i] = v[i];
 }
 
-template <typename T>
+enum : int { kEpiGelu = 0, kEpiRope = 1 };
+
+// EPI: kEpiGelu, or kEpiRope with head dimension HD (64 or 128)
+template <typename T, int EPI, int HD>
 __global__ __launch_bounds__(64 * kGWaves) __attribute__((amdgpu_waves_per_eu(2, 2)))
-void gemm_gelu_kernel(const GemmGeluParams p) {
+void proj_gemm_kernel(const ProjGemmParams p) {
   // one array per operand and stage, so that the compiler's wait insertion
   // sees that a read of one stage does not depend on the DMAs into the others
   __shared__ __align__(16) char sw0[kGTileBytes], sw1[kGTileBytes], sw2[kGTileBytes], sw3[kGTileBytes];
@@ -279,6 +291,50 @@ void gemm_gelu_kernel(const GemmGeluParams p) {
 #pragma unroll
     for (int mt = 0; mt < 2; ++mt) {
       const int row = m0 + 64 * wm + 32 * mt + n32;
+      if constexpr (EPI == kEpiRope) {
+        // the wave's 128 columns are two heads (hd 64: pairs nt 0 / 1 and
+        // 2 / 3, the same d for both) or one (hd 128: pairs nt 0 / 2 and 1 / 3),
+        // all rotated or none (n_rope is a multiple of 128)
+        if (n0 + 128 * wn < p.n_rope) {
+          const int t = (row < p.M ? row : 0) % p.T;
+          const uint16_t* cs = reinterpret_cast<const uint16_t*>(p.cos) + (int64_t)t * p.cs_st + 4 * g;
+          const uint16_t* sn = reinterpret_cast<const uint16_t*>(p.sin) + (int64_t)t * p.sn_st + 4 * g;
+          constexpr int kHalf = HD / 2, kPairs = HD == 64 ? 1 : 2;
+#pragma unroll
+          for (int pi = 0; pi < kPairs; ++pi) {
+            // cos / sin at d1 = 32 pi + 8 q + 4 g + e and d1 + hd/2, in the
+            // activation dtype, four per 8-byte load
+            uint2 c1[4], s1[4], c2[4], s2[4];
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+              const int d1 = 32 * pi + 8 * q;
+              c1[q] = *reinterpret_cast<const uint2*>(cs + d1);
+              s1[q] = *reinterpret_cast<const uint2*>(sn + d1);
+              c2[q] = *reinterpret_cast<const uint2*>(cs + d1 + kHalf);
+              s2[q] = *reinterpret_cast<const uint2*>(sn + d1 + kHalf);
+            }
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+#pragma unroll
+              for (int e = 0; e < 4; ++e) {
+                const uint32_t wc1 = e < 2 ? c1[q].x : c1[q].y, ws1 = e < 2 ? s1[q].x : s1[q].y;
+                const uint32_t wc2 = e < 2 ? c2[q].x : c2[q].y, ws2 = e < 2 ? s2[q].x : s2[q].y;
+                const float fc1 = e % 2 ? Elem<T>::hi(wc1) : Elem<T>::lo(wc1);
+                const float fs1 = e % 2 ? Elem<T>::hi(ws1) : Elem<T>::lo(ws1);
+                const float fc2 = e % 2 ? Elem<T>::hi(wc2) : Elem<T>::lo(wc2);
+                const float fs2 = e % 2 ? Elem<T>::hi(ws2) : Elem<T>::lo(ws2);
+#pragma unroll
+                for (int hh = 0; hh < 2 / kPairs; ++hh) {
+                  const int lo = HD == 64 ? 2 * hh : pi, hi = HD == 64 ? 2 * hh + 1 : pi + 2;
+                  const float x1 = acc[lo][mt][4 * q + e], x2 = acc[hi][mt][4 * q + e];
+                  acc[lo][mt][4 * q + e] = x1 * fc1 - x2 * fs1;
+                  acc[hi][mt][4 * q + e] = x2 * fc2 + x1 * fs2;
+                }
+              }
+            __builtin_amdgcn_sched_barrier(0);  // one pair's cos / sin live at a time
+          }
+        }
+      }
       T* crow = reinterpret_cast<T*>(p.c) + (int64_t)row * p.c_rs + n0 + 128 * wn + 8 * g;
 #pragma unroll
       for (int nt = 0; nt < 4; ++nt)
@@ -288,7 +344,7 @@ void gemm_gelu_kernel(const GemmGeluParams p) {
           float y[8];
 #pragma unroll
           for (int i = 0; i < 8; ++i) y[i] = a[8 * r + i];
-          gelu_group(y);
+          if constexpr (EPI == kEpiGelu) gelu_group(y);
           uint32_t pc[2][2];
 #pragma unroll
           for (int h = 0; h < 2; ++h) {
@@ -314,23 +370,41 @@ void gemm_gelu_kernel(const GemmGeluParams p) {
 
 }  // namespace
 
-bool gemm_gelu_shape_ok(int64_t M, int64_t N, int64_t K) {
+bool proj_gemm_shape_ok(int64_t M, int64_t N, int64_t K) {
   return M > 0 && N > 0 && K > 0 && N % kGBN == 0 && K % (kGBK * kGStages) == 0;
 }
 
-hipError_t launch_gemm_gelu(const GemmGeluParams& p, int dtype, hipStream_t s) {
-  // one workgroup per CU (a multiple of the 8 XCDs), fewer for small problems
+namespace {
+
+// one workgroup per CU (a multiple of the 8 XCDs), fewer for small problems
+dim3 proj_grid(const ProjGemmParams& p) {
   const int tiles = ((p.M + kGBM - 1) / kGBM) * (p.N / kGBN);
   const int per_xcd = (tiles + 7) / 8;
   const int n_local = max(1, min(p.n_cu / 8, per_xcd));
-  const dim3 grid((unsigned)(8 * n_local));
+  return dim3((unsigned)(8 * n_local));
+}
+
+template <int EPI, int HD>
+hipError_t launch_proj(const ProjGemmParams& p, int dtype, hipStream_t s) {
   if (dtype == kBF16)
-    hipLaunchKernelGGL(gemm_gelu_kernel<__bf16>, grid, dim3(64 * kGWaves), 0, s, p);
+    hipLaunchKernelGGL((proj_gemm_kernel<__bf16, EPI, HD>), proj_grid(p), dim3(64 * kGWaves), 0, s, p);
   else if (dtype == kF16)
-    hipLaunchKernelGGL(gemm_gelu_kernel<_Float16>, grid, dim3(64 * kGWaves), 0, s, p);
+    hipLaunchKernelGGL((proj_gemm_kernel<_Float16, EPI, HD>), proj_grid(p), dim3(64 * kGWaves), 0, s, p);
   else
     return hipErrorInvalidValue;
   return hipGetLastError();
+}
+
+}  // namespace
+
+hipError_t launch_gemm_gelu(const ProjGemmParams& p, int dtype, hipStream_t s) {
+  return launch_proj<kEpiGelu, 0>(p, dtype, s);
+}
+
+hipError_t launch_gemm_rope(const ProjGemmParams& p, int dtype, hipStream_t s) {
+  if (p.hd == 64) return launch_proj<kEpiRope, 64>(p, dtype, s);
+  if (p.hd == 128) return launch_proj<kEpiRope, 128>(p, dtype, s);
+  return hipErrorInvalidValue;
 }
 
 }  // namespace saf

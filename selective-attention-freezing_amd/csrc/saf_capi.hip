@@ -775,6 +775,49 @@ int run(const saf_mixed_attn_args* a, unsigned which, void* stream, bool may_for
   return rc == SAF_OK ? jrc : rc;
 }
 
+// Shared checks of the projection GEMMs: x (M, K), weight (N, K) and out
+// (M, N) of one 16-bit dtype; fills the GEMM part of p.
+int proj_common(const char* what, const saf_tensor_t* x, const saf_tensor_t* weight, const saf_tensor_t* out,
+                ProjGemmParams& p) {
+  if (x == nullptr || weight == nullptr || out == nullptr || !present(*x) || !present(*weight) || !present(*out))
+    return fail(SAF_EINVAL, "x, weight and out are required");
+  if (x->ndim != 2 || weight->ndim != 2 || out->ndim != 2)
+    return fail(SAF_EINVAL, "x (M, K), weight (N, K) and out (M, N) must be 2-D");
+  if (x->dtype != SAF_BF16 && x->dtype != SAF_F16)
+    return fail(SAF_EUNSUPPORTED, "%s supports bf16 / fp16 (got %s)", what, dtype_name(x->dtype));
+  if (weight->dtype != x->dtype || out->dtype != x->dtype)
+    return fail(SAF_EINVAL, "x, weight and out must share one dtype");
+  const int64_t M = x->size[0], K = x->size[1], N = weight->size[0];
+  if (weight->size[1] != K || out->size[0] != M || out->size[1] != N)
+    return fail(SAF_EINVAL, "shapes do not chain: x (%lld, %lld), weight (%lld, %lld), out (%lld, %lld)",
+                (long long)M, (long long)K, (long long)weight->size[0], (long long)weight->size[1],
+                (long long)out->size[0], (long long)out->size[1]);
+  if (x->stride[1] != 1 || weight->stride[1] != 1 || out->stride[1] != 1)
+    return fail(SAF_EALIGN, "x, weight and out need a unit column stride");
+  if (M > 0 && (!proj_gemm_shape_ok(M, N, K) || M > 0x7fffffff))
+    return fail(SAF_EUNSUPPORTED, "%s: N = %lld must be a multiple of 256 and K = %lld of 128", what, (long long)N,
+                (long long)K);
+  // 16-byte pieces of x and weight rows, 16-byte pieces of out rows; the
+  // buffer descriptors span 256 rows of x and weight
+  auto rows_ok = [](const saf_tensor_t& t, int align) {
+    return reinterpret_cast<uintptr_t>(t.data) % align == 0 && (t.stride[0] * 2) % align == 0 &&
+           t.stride[0] >= t.size[1] && t.stride[0] < (1 << 22);
+  };
+  if (M > 0 && (!rows_ok(*x, 16) || !rows_ok(*weight, 16) || !rows_ok(*out, 16)))
+    return fail(SAF_EALIGN, "x, weight and out rows must be 16-byte aligned (row strides below 2^22 elements)");
+  p.a = x->data;
+  p.w = weight->data;
+  p.c = out->data;
+  p.M = (int)M;
+  p.N = (int)N;
+  p.K = (int)K;
+  p.a_rs = (int)x->stride[0];
+  p.w_rs = (int)weight->stride[0];
+  p.c_rs = (int)out->stride[0];
+  p.n_cu = cu_count();
+  return SAF_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -997,47 +1040,45 @@ int saf_add_layernorm(const saf_tensor_t* x, const saf_tensor_t* delta, const sa
 }
 
 int saf_linear_gelu(const saf_tensor_t* x, const saf_tensor_t* weight, const saf_tensor_t* out, void* stream) {
-  if (x == nullptr || weight == nullptr || out == nullptr || !present(*x) || !present(*weight) || !present(*out))
-    return fail(SAF_EINVAL, "x, weight and out are required");
-  if (x->ndim != 2 || weight->ndim != 2 || out->ndim != 2)
-    return fail(SAF_EINVAL, "x (M, K), weight (N, K) and out (M, N) must be 2-D");
-  if (x->dtype != SAF_BF16 && x->dtype != SAF_F16)
-    return fail(SAF_EUNSUPPORTED, "linear_gelu supports bf16 / fp16 (got %s)", dtype_name(x->dtype));
-  if (weight->dtype != x->dtype || out->dtype != x->dtype)
-    return fail(SAF_EINVAL, "x, weight and out must share one dtype");
-  const int64_t M = x->size[0], K = x->size[1], N = weight->size[0];
-  if (weight->size[1] != K || out->size[0] != M || out->size[1] != N)
-    return fail(SAF_EINVAL, "shapes do not chain: x (%lld, %lld), weight (%lld, %lld), out (%lld, %lld)",
-                (long long)M, (long long)K, (long long)weight->size[0], (long long)weight->size[1],
-                (long long)out->size[0], (long long)out->size[1]);
-  if (x->stride[1] != 1 || weight->stride[1] != 1 || out->stride[1] != 1)
-    return fail(SAF_EALIGN, "x, weight and out need a unit column stride");
-  if (M == 0) return SAF_OK;
-  if (!gemm_gelu_shape_ok(M, N, K) || M > 0x7fffffff)
-    return fail(SAF_EUNSUPPORTED, "linear_gelu: N = %lld must be a multiple of 256 and K = %lld of 128",
-                (long long)N, (long long)K);
-  // 16-byte pieces of x and weight rows, 8-byte pieces of out rows; the
-  // buffer descriptors span 256 rows of x and weight
-  auto rows_ok = [](const saf_tensor_t& t, int align) {
-    return reinterpret_cast<uintptr_t>(t.data) % align == 0 && (t.stride[0] * 2) % align == 0 &&
-           t.stride[0] >= t.size[1] && t.stride[0] < (1 << 22);
-  };
-  if (!rows_ok(*x, 16) || !rows_ok(*weight, 16) || !rows_ok(*out, 8))
-    return fail(SAF_EALIGN, "x and weight rows must be 16-byte aligned and out rows 8-byte aligned "
-                            "(row strides below 2^22 elements)");
-  GemmGeluParams p{};
-  p.a = x->data;
-  p.w = weight->data;
-  p.c = out->data;
-  p.M = (int)M;
-  p.N = (int)N;
-  p.K = (int)K;
-  p.a_rs = (int)x->stride[0];
-  p.w_rs = (int)weight->stride[0];
-  p.c_rs = (int)out->stride[0];
-  p.n_cu = cu_count();
+  ProjGemmParams p{};
+  if (int rc = proj_common("linear_gelu", x, weight, out, p)) return rc;
+  if (p.M == 0) return SAF_OK;
   const hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   return launched(timed([&] { return launch_gemm_gelu(p, x->dtype, s); }, s), "linear_gelu");
+}
+
+int saf_linear_rope(const saf_tensor_t* x, const saf_tensor_t* weight, const saf_tensor_t* out, int32_t n_rope,
+                    int32_t head_dim, int32_t seq_len, const saf_tensor_t* cos, const saf_tensor_t* sin,
+                    void* stream) {
+  ProjGemmParams p{};
+  if (int rc = proj_common("linear_rope", x, weight, out, p)) return rc;
+  if (head_dim != 64 && head_dim != 128)
+    return fail(SAF_EUNSUPPORTED, "linear_rope: head_dim %d is not supported (64 or 128)", (int)head_dim);
+  if (n_rope < 0 || n_rope > p.N || n_rope % 128 != 0)
+    return fail(SAF_EINVAL, "linear_rope: n_rope = %d must be a multiple of 128 in [0, N = %d]", (int)n_rope, p.N);
+  if (seq_len < 1 || p.M % seq_len != 0)
+    return fail(SAF_EINVAL, "linear_rope: the %d rows are not whole sequences of %d", p.M, (int)seq_len);
+  if (n_rope > 0) {
+    if (cos == nullptr || sin == nullptr || !present(*cos) || !present(*sin))
+      return fail(SAF_EINVAL, "linear_rope: cos and sin are required");
+    for (const saf_tensor_t* c : {cos, sin}) {
+      if (c->ndim != 2 || c->dtype != x->dtype || c->size[0] < seq_len || c->size[1] < head_dim || c->stride[1] != 1)
+        return fail(SAF_EINVAL, "linear_rope: cos / sin must be (>= %d, >= %d) in x's dtype with unit column stride",
+                    (int)seq_len, (int)head_dim);
+      if (reinterpret_cast<uintptr_t>(c->data) % 8 != 0 || (c->stride[0] * 2) % 8 != 0)
+        return fail(SAF_EALIGN, "linear_rope: cos / sin rows must be 8-byte aligned");
+    }
+    p.cos = cos->data;
+    p.sin = sin->data;
+    p.cs_st = cos->stride[0];
+    p.sn_st = sin->stride[0];
+  }
+  p.n_rope = n_rope;
+  p.hd = head_dim;
+  p.T = seq_len;
+  if (p.M == 0) return SAF_OK;
+  const hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  return launched(timed([&] { return launch_gemm_rope(p, x->dtype, s); }, s), "linear_rope");
 }
 
 int saf_decomposed_logz(const saf_tensor_t* alpha, const saf_tensor_t* rho, const saf_tensor_t* z, void* stream) {

@@ -180,16 +180,24 @@ struct AddLnParams {
   int vec16;
 };
 
-// MLP up-projection with its activation: c = gelu(a w^T) for (M, K)
+// Projection GEMMs with a fused epilogue: c = epi(a w^T) for (M, K)
 // activations a, (N, K) weight w and (M, N) output c, row-major with unit
-// column stride; N a multiple of 256, K of 128 (any M).
-struct GemmGeluParams {
+// column stride; N a multiple of 256, K of 128 (any M).  The epilogue is the
+// exact GELU (MLP up-projection) or the rotary embedding of the first n_rope
+// columns (the live heads' q and k of the QKV projection, head dim hd,
+// position t = row mod T, cos / sin caches (>= T, hd) in the activation
+// dtype with row strides cs_st / sn_st in elements).
+struct ProjGemmParams {
   const void* a;
   const void* w;
   void* c;
   int M, N, K;
   int a_rs, w_rs, c_rs;  // row strides in elements
   int n_cu;              // compute units of the device (persistent workgroups)
+  int n_rope, hd, T;
+  const void* cos;
+  const void* sin;
+  int64_t cs_st, sn_st;
 };
 
 // Rows of one scan chunk for a head dimension (must match ScanShape in the
@@ -207,8 +215,9 @@ hipError_t launch_scan(const ScanParams& p, int dtype, int hd, hipStream_t s);
 hipError_t launch_zero_u32(uint32_t* ptr, int64_t n, hipStream_t s);
 hipError_t launch_rope(const RopeParams& p, int dtype, hipStream_t s);
 hipError_t launch_add_layernorm(const AddLnParams& p, int dtype, hipStream_t s);
-bool gemm_gelu_shape_ok(int64_t M, int64_t N, int64_t K);
-hipError_t launch_gemm_gelu(const GemmGeluParams& p, int dtype, hipStream_t s);
+bool proj_gemm_shape_ok(int64_t M, int64_t N, int64_t K);
+hipError_t launch_gemm_gelu(const ProjGemmParams& p, int dtype, hipStream_t s);
+hipError_t launch_gemm_rope(const ProjGemmParams& p, int dtype, hipStream_t s);
 
 // Row normalisers of decomposed patterns, z[h, i] = logsumexp_{j<=i}(alpha[h, j]
 // + rho[h, i - j]) for i < S; (H, S) fp32 rows with unit column stride.

@@ -462,6 +462,14 @@ class CausalSelfAttention(nn.Module):
             return F.linear(y, wc, self.c_proj.bias)
         return self.c_proj(self.attend(x, rope))
 
+    # K (input features) up to which the QKV projection runs as the fused
+    # GEMM + RoPE kernel (measured against the library GEMM plus the RoPE pass)
+    FUSED_ROPE_MAX_K = 1024
+
+    def _fused_rope_ok(self, x, w, wb, nqk, rope):
+        return (wb is None and nqk > 0 and w.size(1) <= self.FUSED_ROPE_MAX_K
+                and _kernel_mod.linear_rope_usable(x, w, nqk, self.head_dim, rope[0]))
+
     def head_outputs(self, x, rope=None):
         """(y, W): head outputs before c_proj and the c_proj weight whose
         input columns match their order (inference)."""
@@ -492,17 +500,23 @@ class CausalSelfAttention(nn.Module):
                         raise ValueError("RoPE Q/K requested without a rotary cache")
                     qu, ku = apply_rotary_pos_emb(qu, ku, *rope)
         else:
-            # one GEMM for live Q/K and every V; RoPE rotates Q/K in place
+            # one GEMM for live Q/K and every V; RoPE rotates Q/K in place, or
+            # inside the GEMM's epilogue (linear_rope) where that kernel runs
             w, wb = self._infer_weight_cache()
-            qkv = F.linear(x, w, wb)
             nqk = 2 * nuf * hd
+            rotated = False
+            if self.position_encoding == "rope" and rope is not None and self._fused_rope_ok(x, w, wb, nqk, rope):
+                qkv = _kernel_mod.linear_rope(x, w, nqk, hd, *rope)
+                rotated = True
+            else:
+                qkv = F.linear(x, w, wb)
             v = qkv[..., nqk:nqk + nh * hd].view(B, T, nh, hd).transpose(1, 2)
             if nuf == 0:
                 qu = ku = v[:, :0]
             else:
                 qk = qkv[..., :nqk].view(B, T, 2, nuf, hd)
                 qu, ku = qk[:, :, 0].transpose(1, 2), qk[:, :, 1].transpose(1, 2)
-                if self.position_encoding == "rope":
+                if self.position_encoding == "rope" and not rotated:
                     if rope is None:
                         raise ValueError("RoPE Q/K requested without a rotary cache")
                     if qu.dtype in (torch.bfloat16, torch.float16):

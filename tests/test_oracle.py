@@ -248,6 +248,30 @@ def test_linear_gelu_matches_torch_and_the_normal_cdf():
     assert np.allclose(orc.linear_gelu(v, np.eye(97)) - orc.linear_gelu(-v, np.eye(97)), v, atol=1e-13)
 
 
+def test_linear_rope_special_cases_and_invariants():
+    rng = np.random.default_rng(31)
+    T, B, K, hd, nh = 10, 2, 16, 8, 5
+    x, w = rng.standard_normal((B * T, K)), rng.standard_normal((nh * hd, K))
+    cos, sin = orc.rope_cache(hd, T)
+    u = x @ w.T
+    y = orc.linear_rope(x, w, 3 * hd, hd, cos, sin, T)
+    # columns past n_rope are the plain product; position 0 of each sequence
+    # is not rotated (cos 1, sin 0)
+    np.testing.assert_allclose(y[:, 3 * hd:], u[:, 3 * hd:], atol=1e-13)
+    np.testing.assert_allclose(y[[0, T]], u[[0, T]], atol=1e-13)
+    np.testing.assert_allclose(orc.linear_rope(x, w, 0, hd, cos, sin, T), u, atol=1e-13)
+    # each (d, d + hd/2) pair turns by the angle t * inv_freq[d]: the complex
+    # product (u_d + i u_{d+hd/2}) e^{i t f_d}, which also keeps its modulus
+    half = hd // 2
+    inv = 1.0 / (10000.0 ** (np.arange(0, hd, 2) / hd))
+    for r in (3, 7, T + 5):
+        t = r % T
+        for h0 in (0, hd, 2 * hd):
+            z = (u[r, h0:h0 + half] + 1j * u[r, h0 + half:h0 + hd]) * np.exp(1j * t * inv)
+            np.testing.assert_allclose(y[r, h0:h0 + half], z.real, atol=1e-12)
+            np.testing.assert_allclose(y[r, h0 + half:h0 + hd], z.imag, atol=1e-12)
+
+
 def test_planted_oracle_mistake_is_caught():
     """A transposed pattern (a plausible slip) breaks the causal-mean check."""
     T = 12
