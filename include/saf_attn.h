@@ -251,6 +251,16 @@ int saf_add_layernorm(const saf_tensor_t* x, const saf_tensor_t* delta, const sa
  * gelu in MLP.forward (nanogpt/model.py:1202-1204) on the prefill path. */
 int saf_linear_gelu(const saf_tensor_t* x, const saf_tensor_t* weight, const saf_tensor_t* out, void* stream);
 
+/* SwiGLU half of a gated MLP in one kernel: out = silu(x Wg^T) * (x Wu^T),
+ * silu(u) = u / (1 + e^-u), for x (M, K) and weight (N, K) holding the gate
+ * and up rows interleaved in blocks of 64 (gate rows 64b..64b+63, then up
+ * rows 64b..64b+63, for b = 0, 1, ...), out (M, N / 2); fp32 accumulation and
+ * activation, one rounding of out.  Same dtype, N / K and alignment rules as
+ * saf_linear_gelu (so the MLP width N / 2 is a multiple of 128).  No
+ * workspace.  Replaces act_fn(gate_proj(x)) * up_proj(x) of transformers'
+ * Qwen3MLP (the C4 caller's MLP, SiLU activation) on the prefill path. */
+int saf_linear_swiglu(const saf_tensor_t* x, const saf_tensor_t* weight, const saf_tensor_t* out, void* stream);
+
 /* Indexed QKV projection with the rotary embedding in one kernel:
  * out = x weight^T for x (M, K) = (B T, K) and weight (N, K) the gathered
  * [Wq[live]; Wk[live]; Wv] rows (zero rows may pad N), with the first n_rope

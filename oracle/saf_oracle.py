@@ -32,13 +32,16 @@ Each function restates the reference's algorithm from its source
                           residual additions of Block.forward (:1214-1240)
   linear_gelu             nanogpt/model.py:1193-1207 (MLP: c_fc without bias,
                           then nn.GELU(), the exact erf form)
+  linear_swiglu           transformers' Qwen3MLP (the C4 caller's MLP, SiLU):
+                          act_fn(gate_proj(x)) * up_proj(x), before down_proj
   linear_rope             nanogpt/model.py:920-944 (the gathered QKV projection)
                           followed by :57-99 (the rotation of the live q / k)
 
 How each is pinned (tests/test_oracle.py): torch SDPA as the library special
 case of the all-live case (torch.nn.functional.layer_norm likewise for
 add_layernorm, torch.nn.functional.gelu and the normal CDF's closed values
-for linear_gelu); brute-force pure-Python loops on tiny inputs;
+for linear_gelu, torch.nn.functional.silu and the logistic's closed values for
+linear_swiglu); brute-force pure-Python loops on tiny inputs;
 closed forms (prefix sums, IIR recurrences, box filters) against the dense
 patterns; invariants (rows sum to 1, T = 1 gives y = v, frozen heads ignore
 Q/K, head-permutation equivariance); routing tables brute-forced over every
@@ -463,6 +466,15 @@ def linear_gelu(x, weight):
     from scipy.special import erf
     u = _f64(x) @ _f64(weight).T
     return u * 0.5 * (1.0 + erf(u / math.sqrt(2.0)))
+
+
+def linear_swiglu(x, w_gate, w_up):
+    """The gated MLP's front half of transformers' Qwen3MLP with SiLU (the
+    Qwen caller's MLP): silu(x Wg^T) * (x Wu^T), silu(u) = u sigma(u).
+    float64."""
+    from scipy.special import expit
+    g = _f64(x) @ _f64(w_gate).T
+    return g * expit(g) * (_f64(x) @ _f64(w_up).T)
 
 
 def linear_rope(x, weight, n_rope, head_dim, cos, sin, seq_len):

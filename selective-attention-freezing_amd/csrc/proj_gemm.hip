@@ -22,6 +22,11 @@
 //     C[m][d] = u[d] cos[t][d] + u[d - hd/2] sin[t][d]            d >= hd/2
 //   and the columns after them (V, zero padding) are stored as they are.
 //   Fusing it removes the pass over q and k.
+// * the SwiGLU of a Qwen3 MLP (transformers' Qwen3MLP, the C4 caller's
+//   down_proj(act_fn(gate_proj(x)) * up_proj(x)) with act_fn = SiLU): W holds
+//   the gate and up rows interleaved in blocks of 64 (gate rows 64 b.., then
+//   the up rows 64 b..), and C (M x N/2) = silu(x Wg^T) * (x Wu^T), silu(u) =
+//   u / (1 + e^-u); the two products never reach memory.
 //
 // Tiling: 256 x 256 tiles of C, one persistent workgroup of 8 waves per CU
 // walking its tiles in turn; wave w computes the 64 (rows of A) x 128 (rows
@@ -114,7 +119,7 @@ __device__ __forceinline__ void gelu_group(float (&x)[n]) {
   for (int i = 0; i < n; ++i) x[i] = v[i];
 }
 
-enum : int { kEpiGelu = 0, kEpiRope = 1 };
+enum : int { kEpiGelu = 0, kEpiRope = 1, kEpiSwiglu = 2 };
 
 // EPI: kEpiGelu, or kEpiRope with head dimension HD (64 or 128)
 template <typename T, int EPI, int HD>
@@ -335,9 +340,14 @@ void proj_gemm_kernel(const ProjGemmParams p) {
           }
         }
       }
-      T* crow = reinterpret_cast<T*>(p.c) + (int64_t)row * p.c_rs + n0 + 128 * wn + 8 * g;
+      // SwiGLU: the wave's 128 columns are 64 gate features (nt 0, 1) and the
+      // same 64 up features (nt 2, 3); it writes their 64 products at output
+      // column n0 / 2 + 64 wn + d, d = 32 nt + 8 q + 4 g + e
+      constexpr int kOutTiles = EPI == kEpiSwiglu ? 2 : 4;
+      T* crow = reinterpret_cast<T*>(p.c) + (int64_t)row * p.c_rs +
+                (EPI == kEpiSwiglu ? n0 / 2 + 64 * wn : n0 + 128 * wn) + 8 * g;
 #pragma unroll
-      for (int nt = 0; nt < 4; ++nt)
+      for (int nt = 0; nt < kOutTiles; ++nt)
 #pragma unroll
         for (int r = 0; r < 2; ++r) {
           const f32x16_t& a = acc[nt][mt];
@@ -345,6 +355,15 @@ void proj_gemm_kernel(const ProjGemmParams p) {
 #pragma unroll
           for (int i = 0; i < 8; ++i) y[i] = a[8 * r + i];
           if constexpr (EPI == kEpiGelu) gelu_group(y);
+          if constexpr (EPI == kEpiSwiglu) {
+            // silu(x) = x / (1 + e^-x), in fp32, times the up projection
+            const f32x16_t& up = acc[nt + 2][mt];
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+              const float x = y[i];
+              y[i] = x * __builtin_amdgcn_rcpf(1.f + __builtin_amdgcn_exp2f(x * -kLog2e)) * up[8 * r + i];
+            }
+          }
           uint32_t pc[2][2];
 #pragma unroll
           for (int h = 0; h < 2; ++h) {
@@ -399,6 +418,10 @@ hipError_t launch_proj(const ProjGemmParams& p, int dtype, hipStream_t s) {
 
 hipError_t launch_gemm_gelu(const ProjGemmParams& p, int dtype, hipStream_t s) {
   return launch_proj<kEpiGelu, 0>(p, dtype, s);
+}
+
+hipError_t launch_gemm_swiglu(const ProjGemmParams& p, int dtype, hipStream_t s) {
+  return launch_proj<kEpiSwiglu, 0>(p, dtype, s);
 }
 
 hipError_t launch_gemm_rope(const ProjGemmParams& p, int dtype, hipStream_t s) {

@@ -776,9 +776,9 @@ int run(const saf_mixed_attn_args* a, unsigned which, void* stream, bool may_for
 }
 
 // Shared checks of the projection GEMMs: x (M, K), weight (N, K) and out
-// (M, N) of one 16-bit dtype; fills the GEMM part of p.
+// (M, N / out_div) of one 16-bit dtype; fills the GEMM part of p.
 int proj_common(const char* what, const saf_tensor_t* x, const saf_tensor_t* weight, const saf_tensor_t* out,
-                ProjGemmParams& p) {
+                ProjGemmParams& p, int out_div = 1) {
   if (x == nullptr || weight == nullptr || out == nullptr || !present(*x) || !present(*weight) || !present(*out))
     return fail(SAF_EINVAL, "x, weight and out are required");
   if (x->ndim != 2 || weight->ndim != 2 || out->ndim != 2)
@@ -788,7 +788,7 @@ int proj_common(const char* what, const saf_tensor_t* x, const saf_tensor_t* wei
   if (weight->dtype != x->dtype || out->dtype != x->dtype)
     return fail(SAF_EINVAL, "x, weight and out must share one dtype");
   const int64_t M = x->size[0], K = x->size[1], N = weight->size[0];
-  if (weight->size[1] != K || out->size[0] != M || out->size[1] != N)
+  if (weight->size[1] != K || out->size[0] != M || out->size[1] * out_div != N)
     return fail(SAF_EINVAL, "shapes do not chain: x (%lld, %lld), weight (%lld, %lld), out (%lld, %lld)",
                 (long long)M, (long long)K, (long long)weight->size[0], (long long)weight->size[1],
                 (long long)out->size[0], (long long)out->size[1]);
@@ -1045,6 +1045,14 @@ int saf_linear_gelu(const saf_tensor_t* x, const saf_tensor_t* weight, const saf
   if (p.M == 0) return SAF_OK;
   const hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   return launched(timed([&] { return launch_gemm_gelu(p, x->dtype, s); }, s), "linear_gelu");
+}
+
+int saf_linear_swiglu(const saf_tensor_t* x, const saf_tensor_t* weight, const saf_tensor_t* out, void* stream) {
+  ProjGemmParams p{};
+  if (int rc = proj_common("linear_swiglu", x, weight, out, p, 2)) return rc;
+  if (p.M == 0) return SAF_OK;
+  const hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  return launched(timed([&] { return launch_gemm_swiglu(p, x->dtype, s); }, s), "linear_swiglu");
 }
 
 int saf_linear_rope(const saf_tensor_t* x, const saf_tensor_t* weight, const saf_tensor_t* out, int32_t n_rope,

@@ -218,6 +218,8 @@ hipError_t launch_add_layernorm(const AddLnParams& p, int dtype, hipStream_t s);
 bool proj_gemm_shape_ok(int64_t M, int64_t N, int64_t K);
 hipError_t launch_gemm_gelu(const ProjGemmParams& p, int dtype, hipStream_t s);
 hipError_t launch_gemm_rope(const ProjGemmParams& p, int dtype, hipStream_t s);
+// SwiGLU: w holds 64-row blocks of gate and up rows in turn; c is (M, N / 2)
+hipError_t launch_gemm_swiglu(const ProjGemmParams& p, int dtype, hipStream_t s);
 
 // Row normalisers of decomposed patterns, z[h, i] = logsumexp_{j<=i}(alpha[h, j]
 // + rho[h, i - j]) for i < S; (H, S) fp32 rows with unit column stride.

@@ -15,7 +15,8 @@ from .frozen_attn import frozen_pv, frozen_pv_usable, HAVE_TRITON
 from .indexed_linear import linear_rows, linear_rows2, linear_permuted_cols
 from .rope import rope_qk_, qk_rmsnorm_rope_
 from .layernorm import add_layernorm_
-from .projection import linear_gelu, linear_gelu_usable, linear_rope, linear_rope_usable
+from .projection import (linear_gelu, linear_gelu_usable, linear_rope, linear_rope_usable, linear_swiglu,
+                         linear_swiglu_usable, swiglu_weight)
 from .fused_attn import (fused_mixed_attn, fused_attn_usable, decomposed_logz,
                          decomp_log_normalizers, decomp_log_normalizers_fft,
                          decomp_logits, make_rho_band, BAND_ROWS,
@@ -30,4 +31,4 @@ __all__ = ["frozen_pv", "frozen_pv_usable", "HAVE_TRITON",
            "classify_closed_form", "CLOSED_NONE", "CLOSED_MEAN",
            "CLOSED_DECAY", "CLOSED_WINDOW", "KernelTimer", "set_kernel_timer",
            "rope_qk_", "qk_rmsnorm_rope_", "add_layernorm_", "linear_gelu", "linear_gelu_usable",
-           "linear_rope", "linear_rope_usable"]
+           "linear_rope", "linear_rope_usable", "linear_swiglu", "linear_swiglu_usable", "swiglu_weight"]

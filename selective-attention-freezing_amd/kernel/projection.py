@@ -6,6 +6,10 @@ into one HIP kernel each (libsafattn.so, forward only, no bias).
   erf-based GELU).  The reference's up-projection writes its (rows, 4 C)
   output and the activation reads and writes it again; here the GELU runs on
   the GEMM's fp32 accumulator and the activation is written once, rounded once.
+* ``linear_swiglu`` (``saf_linear_swiglu``): ``act_fn(gate_proj(x)) *
+  up_proj(x)`` of transformers' Qwen3MLP (SiLU), the MLP of the Qwen caller,
+  from one GEMM over the gate and up rows interleaved in blocks of 64
+  (``swiglu_weight``); the two (rows, I) products never reach memory.
 * ``linear_rope`` (``saf_linear_rope``): the indexed QKV projection of the
   gathered ``[Wq[live]; Wk[live]; Wv]`` weight (nanogpt/model.py:920-944) with
   the rotary embedding of the live q and k (:57-99, :1007-1008) applied to the
@@ -55,6 +59,40 @@ def linear_gelu(x, weight):
                            _ext.current_stream_ptr(x.device))
     _ext.check(rc)
     return out.view(*x.shape[:-1], w.size(0))
+
+
+SWIGLU_BLOCK = 64  # rows per gate / up block of the interleaved weight
+
+
+def swiglu_weight(w_gate, w_up):
+    """(2 I, K) weight of linear_swiglu from the gate and up projections'
+    (I, K) weights: 64-row blocks of gate rows and up rows in turn."""
+    I, K = w_gate.shape
+    if w_up.shape != (I, K) or I % SWIGLU_BLOCK:
+        raise ValueError("gate and up weights must share a shape (I, K) with I a multiple of 64")
+    nb = I // SWIGLU_BLOCK
+    return torch.stack([w_gate.reshape(nb, SWIGLU_BLOCK, K), w_up.reshape(nb, SWIGLU_BLOCK, K)], 1).reshape(2 * I, K)
+
+
+def linear_swiglu_usable(x, weight):
+    """True when linear_swiglu runs x (..., K) against the interleaved (2 I, K) weight."""
+    return _gemm_usable(x, weight)
+
+
+def linear_swiglu(x, weight):
+    """silu(x @ Wg.T) * (x @ Wu.T) for x (..., K) and the interleaved weight
+    of swiglu_weight(Wg, Wu); returns (..., I)."""
+    if not x.is_cuda:
+        raise RuntimeError("linear_swiglu runs on HIP devices only (got a CPU tensor)")
+    x2, w = _rows(x, weight)
+    out = torch.empty(x2.size(0), w.size(0) // 2, device=x.device, dtype=x.dtype)
+    if out.numel() == 0:
+        return out.view(*x.shape[:-1], w.size(0) // 2)
+    L = _ext.lib()
+    rc = L.saf_linear_swiglu(_ext.tensor_desc(x2), _ext.tensor_desc(w), _ext.tensor_desc(out),
+                             _ext.current_stream_ptr(x.device))
+    _ext.check(rc)
+    return out.view(*x.shape[:-1], w.size(0) // 2)
 
 
 def linear_rope_usable(x, weight, n_rope, head_dim, cos):

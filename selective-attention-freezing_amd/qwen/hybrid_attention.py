@@ -418,6 +418,61 @@ def discover_softmax_attention(model: nn.Module) -> List[SoftmaxAttentionTarget]
     return []
 
 
+# ---------------------------------------------------------------------------
+# gated MLP of the decoder blocks (transformers' Qwen3MLP:
+# down_proj(act_fn(gate_proj(x)) * up_proj(x)), SiLU)
+# ---------------------------------------------------------------------------
+
+# K (hidden size) up to which the gate / up half runs as one HIP kernel
+# (kernel.linear_swiglu), measured against two library GEMMs plus torch's SiLU
+# and product at the C4 shape
+FUSED_SWIGLU_MAX_K = 1024
+_PLAIN_FORWARD = object()  # restore marker: drop the instance's fused forward
+
+
+def _is_silu(fn):
+    return isinstance(fn, nn.SiLU) or type(fn).__name__ in ("SiLUActivation", "SiLU")
+
+
+def _gated_mlp_fusable(mlp):
+    return (all(isinstance(getattr(mlp, n, None), nn.Linear) for n in ("gate_proj", "up_proj", "down_proj"))
+            and mlp.gate_proj.bias is None and mlp.up_proj.bias is None and _is_silu(getattr(mlp, "act_fn", None))
+            and mlp.gate_proj.weight.shape == mlp.up_proj.weight.shape)
+
+
+def _swiglu_weight_cache(mlp):
+    """The interleaved [gate; up] weight of kernel.linear_swiglu, rebuilt when
+    either weight changes (version, storage, dtype or device)."""
+    wg, wu = mlp.gate_proj.weight, mlp.up_proj.weight
+    key = (wg._version, wu._version, wg.data_ptr(), wu.data_ptr(), wg.dtype, wg.device)
+    cache = mlp.__dict__.get("_swiglu_cache")
+    if cache is None or cache[0] != key:
+        with torch.no_grad():
+            cache = (key, _kernel_mod.swiglu_weight(wg.detach(), wu.detach()))
+        mlp.__dict__["_swiglu_cache"] = cache
+    return cache[1]
+
+
+def _fused_gated_mlp_forward(mlp, x):
+    """Qwen3MLP.forward with the gate / up half as one HIP kernel (the SiLU
+    and the product on the GEMM's fp32 accumulators) on the no-grad device
+    path; torch's modules otherwise."""
+    if (not torch.is_grad_enabled() and x.is_cuda and x.dtype in (torch.bfloat16, torch.float16)
+            and x.size(-1) <= FUSED_SWIGLU_MAX_K and mlp.gate_proj.weight.size(0) % 128 == 0):
+        w = _swiglu_weight_cache(mlp)
+        if _kernel_mod.linear_swiglu_usable(x, w):
+            return mlp.down_proj(_kernel_mod.linear_swiglu(x, w))
+    return mlp.down_proj(mlp.act_fn(mlp.gate_proj(x)) * mlp.up_proj(x))
+
+
+def _fuse_block_mlp(block, saved):
+    mlp = getattr(block, "mlp", None)
+    if mlp is None or "forward" in mlp.__dict__ or not _gated_mlp_fusable(mlp):
+        return
+    mlp.forward = lambda x, _m=mlp: _fused_gated_mlp_forward(_m, x)
+    saved.append((mlp, "forward", _PLAIN_FORWARD))
+
+
 def convert_targets_to_hybrid(model, targets, mean_attn, head_masks, device, dtype,
                               use_triton=True, assume_causal_prefill=False, decomp=None,
                               fuse_live_only=False):
@@ -442,6 +497,9 @@ def convert_targets_to_hybrid(model, targets, mean_attn, head_masks, device, dty
             blocks = blocks or iter_blocks(model)
             parent = blocks[t.layer_idx]
         original = getattr(parent, t.attr_name)
+        # the block's gated MLP (same function, one HIP kernel for its gate /
+        # up half on the prefill path) whatever its heads
+        _fuse_block_mlp(parent, saved)
         if not bool(torch.as_tensor(mask).any()) and not fuse_live_only:
             saved.append((parent, t.attr_name, None))
             continue
@@ -461,5 +519,8 @@ def convert_targets_to_hybrid(model, targets, mean_attn, head_masks, device, dty
 def restore_originals(saved):
     """Undo convert_targets_to_hybrid."""
     for parent, attr_name, original in saved:
-        if original is not None:
+        if original is _PLAIN_FORWARD:
+            parent.__dict__.pop(attr_name, None)
+            parent.__dict__.pop("_swiglu_cache", None)
+        elif original is not None:
             setattr(parent, attr_name, original)

@@ -248,6 +248,30 @@ def test_linear_gelu_matches_torch_and_the_normal_cdf():
     assert np.allclose(orc.linear_gelu(v, np.eye(97)) - orc.linear_gelu(-v, np.eye(97)), v, atol=1e-13)
 
 
+def test_linear_swiglu_matches_torch_and_closed_values():
+    g = torch.Generator().manual_seed(13)
+    x = torch.randn(6, 32, generator=g, dtype=torch.float64)
+    wg, wu = torch.randn(24, 32, generator=g, dtype=torch.float64), torch.randn(24, 32, generator=g, dtype=torch.float64)
+    y = orc.linear_swiglu(x.numpy(), wg.numpy(), wu.numpy())
+    ref = torch.nn.functional.silu(x @ wg.T) * (x @ wu.T)
+    assert np.allclose(y, ref.numpy(), atol=1e-12, rtol=1e-12)
+    # identity gate and up rows give silu(u) * u with silu(u) = u / (1 + e^-u):
+    # silu(0) = 0, silu(1) = 0.7310585786300049, silu(-1) = -0.2689414213699951
+    u = np.array([[0.0, 1.0, -1.0, 40.0, -40.0]])
+    want = np.array([0.0, 0.7310585786300049, -0.2689414213699951, 40.0, -40.0 * math.exp(-40.0)]) * u
+    assert np.allclose(orc.linear_swiglu(u, np.eye(5), np.eye(5)), want, rtol=1e-12, atol=1e-300)
+    # up rows reading a constant-1 column give silu itself, whose odd part is
+    # the identity: silu(v) - silu(-v) = v (a dropped sign in the logistic breaks it)
+    n = 33
+    v = np.linspace(-8, 8, n)
+    xv = np.concatenate([v, [1.0]])[None, :]
+    xm = np.concatenate([-v, [1.0]])[None, :]
+    gate = np.eye(n, n + 1)
+    up = np.zeros((n, n + 1))
+    up[:, n] = 1.0
+    assert np.allclose(orc.linear_swiglu(xv, gate, up) - orc.linear_swiglu(xm, gate, up), v[None, :], atol=1e-13)
+
+
 def test_linear_rope_special_cases_and_invariants():
     rng = np.random.default_rng(31)
     T, B, K, hd, nh = 10, 2, 16, 8, 5
