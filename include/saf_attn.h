@@ -241,6 +241,16 @@ int saf_qk_rmsnorm_rope_inplace(const saf_tensor_t* q, const saf_tensor_t* k, co
 int saf_add_layernorm(const saf_tensor_t* x, const saf_tensor_t* delta, const saf_tensor_t* weight,
                       const saf_tensor_t* bias, float eps, const saf_tensor_t* out, void* stream);
 
+/* Residual add + RMSNorm of a Qwen3 decoder block, with the operand rules of
+ * saf_add_layernorm (no bias): x += delta when delta is present, then
+ * out = weight * round(x * rsqrt(mean(x^2) + eps)) over C, the mean of
+ * squares in fp32 from the rounded x, the normalised x rounded to x's dtype
+ * before the weight multiplies it and the product rounded again.  Replaces
+ * transformers' Qwen3RMSNorm.forward on the decoder blocks of the Qwen caller
+ * (input_layernorm, post_attention_layernorm, the final norm). */
+int saf_add_rmsnorm(const saf_tensor_t* x, const saf_tensor_t* delta, const saf_tensor_t* weight, float eps,
+                    const saf_tensor_t* out, void* stream);
+
 /* MLP up-projection and activation of the GPT block in one kernel:
  * out = gelu(x weight^T) with gelu(u) = u / 2 (1 + erf(u / sqrt 2)) (the exact
  * GELU, nn.GELU's default), for x (M, K), weight (N, K) (an nn.Linear weight

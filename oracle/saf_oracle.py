@@ -30,6 +30,8 @@ Each function restates the reference's algorithm from its source
   rope                    nanogpt/model.py:57-99
   add_layernorm           nanogpt/model.py:45-54 (LayerNorm, eps 1e-5) with the
                           residual additions of Block.forward (:1214-1240)
+  add_rmsnorm             transformers' Qwen3RMSNorm (the Qwen caller's decoder
+                          norms) with the same optional residual update
   linear_gelu             nanogpt/model.py:1193-1207 (MLP: c_fc without bias,
                           then nn.GELU(), the exact erf form)
   linear_swiglu           transformers' Qwen3MLP (the C4 caller's MLP, SiLU):
@@ -39,7 +41,8 @@ Each function restates the reference's algorithm from its source
 
 How each is pinned (tests/test_oracle.py): torch SDPA as the library special
 case of the all-live case (torch.nn.functional.layer_norm likewise for
-add_layernorm, torch.nn.functional.gelu and the normal CDF's closed values
+add_layernorm, transformers' Qwen3RMSNorm in float64 for add_rmsnorm,
+torch.nn.functional.gelu and the normal CDF's closed values
 for linear_gelu, torch.nn.functional.silu and the logistic's closed values for
 linear_swiglu); brute-force pure-Python loops on tiny inputs;
 closed forms (prefix sums, IIR recurrences, box filters) against the dense
@@ -490,6 +493,21 @@ def linear_rope(x, weight, n_rope, head_dim, cos, sin, seq_len):
     for h0 in range(0, n_rope, head_dim):
         out[:, h0:h0 + head_dim] = apply_rope(u[:, h0:h0 + head_dim], c, s)
     return out
+
+
+def add_rmsnorm(x, delta, weight, eps=1e-6, round_fn=None):
+    """Residual update and Qwen3RMSNorm (transformers modeling_qwen3): x' = x
+    + delta rounded by round_fn (the activation dtype's add), then
+    y = w * round_fn(x' / sqrt(mean(x'^2) + eps)) over the last axis (the
+    normalised value is cast back to the activation dtype before the weight
+    multiplies it).  Returns (x', y) in float64, y before its own rounding."""
+    xn = _f64(x) if delta is None else _f64(x) + _f64(delta)
+    if round_fn is not None and delta is not None:
+        xn = round_fn(xn)
+    h = xn / np.sqrt((xn ** 2).mean(-1, keepdims=True) + eps)
+    if round_fn is not None:
+        h = round_fn(h)
+    return xn, h * _f64(weight)
 
 
 def add_layernorm(x, delta, weight, bias=None, eps=1e-5, round_fn=None):

@@ -6,7 +6,10 @@
 // One wave per row: x += delta (one rounding to the activation dtype, as
 // torch's bf16/fp16 add), then y = (x - mean) * rsqrt(var + eps) * w + b
 // from the rounded x in fp32 (two passes over registers: mean, then the
-// centred sum of squares), one rounding of y.  Each lane holds NCH chunks of
+// centred sum of squares), one rounding of y.  The same kernels run the
+// RMSNorm of the Qwen caller's decoder blocks (transformers' Qwen3RMSNorm:
+// fp32 mean of squares, x * rsqrt(. + eps) rounded to the activation dtype,
+// then times the weight and rounded again) when p.rms is set.  Each lane holds NCH chunks of
 // VEC consecutive channels, chunk k at channel VEC * (64 k + lane), so every
 // load and store of the wave is one coalesced run; chunks past C are idle.
 #include "saf_kernels.h"
@@ -31,6 +34,9 @@ template <typename T> struct Vec<T, 2> {
   __device__ static inline void unpack(raw r, float (&f)[2]) { f[0] = Elem<T>::lo(r); f[1] = Elem<T>::hi(r); }
   __device__ static inline raw pack(const float (&f)[2]) { return Elem<T>::pack2(f[0], f[1]); }
 };
+
+template <typename T>
+__device__ inline float round_to_elem(float x) { return (float)static_cast<T>(x); }
 
 __device__ inline float wave_sum(float v) {
 #pragma unroll
@@ -74,7 +80,7 @@ __global__ __launch_bounds__(256) void add_layernorm_kernel(const AddLnParams p)
 #pragma unroll
     for (int e = 0; e < VEC; ++e) s += v[k][e];
   const float inv_c = 1.f / (float)C;
-  const float mean = wave_sum(s) * inv_c;
+  const float mean = p.rms ? 0.f : wave_sum(s) * inv_c;
   float q = 0.f;
 #pragma unroll
   for (int k = 0; k < NCH; ++k)
@@ -94,7 +100,7 @@ __global__ __launch_bounds__(256) void add_layernorm_kernel(const AddLnParams p)
     for (int e = 0; e < VEC; ++e) {
       const float w = load_as_f32(p.w, c + e, p.wb_dtype);
       const float b = p.b ? load_as_f32(p.b, c + e, p.wb_dtype) : 0.f;
-      o[e] = fmaf((v[k][e] - mean) * rstd, w, b);
+      o[e] = p.rms ? round_to_elem<T>(v[k][e] * rstd) * w : fmaf((v[k][e] - mean) * rstd, w, b);
     }
     *reinterpret_cast<raw*>(yr + c) = V::pack(o);
   }
@@ -176,7 +182,7 @@ __global__ __launch_bounds__(256) void add_layernorm_hw_kernel(const AddLnParams
 #pragma unroll
     for (int e = 0; e < 8; ++e) s += v[k][e];
   const float inv_c = 1.f / (float)C;
-  const float mean = half_sum(s) * inv_c;
+  const float mean = p.rms ? 0.f : half_sum(s) * inv_c;
   float q = 0.f;
 #pragma unroll
   for (int k = 0; k < NCH; ++k)
@@ -199,7 +205,8 @@ __global__ __launch_bounds__(256) void add_layernorm_hw_kernel(const AddLnParams
     }
     float o[8];
 #pragma unroll
-    for (int e = 0; e < 8; ++e) o[e] = fmaf((v[k][e] - mean) * rstd, w[e], b[e]);
+    for (int e = 0; e < 8; ++e)
+      o[e] = p.rms ? round_to_elem<T>(v[k][e] * rstd) * w[e] : fmaf((v[k][e] - mean) * rstd, w[e], b[e]);
     const uint2 r0 = V::pack(*reinterpret_cast<float(*)[4]>(o));
     const uint2 r1 = V::pack(*reinterpret_cast<float(*)[4]>(o + 4));
     *reinterpret_cast<uint4*>(yr + c) = make_uint4(r0.x, r0.y, r1.x, r1.y);

@@ -818,6 +818,60 @@ int proj_common(const char* what, const saf_tensor_t* x, const saf_tensor_t* wei
   return SAF_OK;
 }
 
+int add_norm(const char* what, bool rms, const saf_tensor_t* x, const saf_tensor_t* delta, const saf_tensor_t* weight,
+             const saf_tensor_t* bias, float eps, const saf_tensor_t* out, void* stream) {
+  if (x == nullptr || weight == nullptr || out == nullptr || !present(*x) || !present(*weight) || !present(*out))
+    return fail(SAF_EINVAL, "x, weight and out are required");
+  const bool has_d = delta != nullptr && present(*delta);
+  const bool has_b = bias != nullptr && present(*bias);
+  if (x->ndim != 2 || out->ndim != 2 || (has_d && delta->ndim != 2))
+    return fail(SAF_EINVAL, "x, delta and out must be 2-D (rows, C)");
+  if (x->dtype != SAF_BF16 && x->dtype != SAF_F16)
+    return fail(SAF_EUNSUPPORTED, "%s supports bf16 / fp16 activations (got %s)", what, dtype_name(x->dtype));
+  const int64_t rows = x->size[0], C = x->size[1];
+  if (out->dtype != x->dtype || out->size[0] != rows || out->size[1] != C)
+    return fail(SAF_EINVAL, "out must match x in shape and dtype");
+  if (has_d && (delta->dtype != x->dtype || delta->size[0] != rows || delta->size[1] != C))
+    return fail(SAF_EINVAL, "delta must match x in shape and dtype");
+  if (x->stride[1] != 1 || out->stride[1] != 1 || (has_d && delta->stride[1] != 1))
+    return fail(SAF_EALIGN, "x, delta and out need a unit channel stride");
+  if (C < 2 || C > 2048 || C % 2 != 0)
+    return fail(SAF_EUNSUPPORTED, "%s: C = %lld is not supported (even, at most 2048)", what, (long long)C);
+  const int vec_bytes = (C % 256 == 0 ? 4 : 2) * 2;
+  auto aligned = [&](const saf_tensor_t& t) {
+    return reinterpret_cast<uintptr_t>(t.data) % vec_bytes == 0 && (t.size[0] <= 1 || (t.stride[0] * 2) % vec_bytes == 0);
+  };
+  if (!aligned(*x) || !aligned(*out) || (has_d && !aligned(*delta)))
+    return fail(SAF_EALIGN, "x, delta and out rows must be %d-byte aligned", vec_bytes);
+  if (weight->ndim != 1 || weight->size[0] != C || weight->stride[0] != 1 ||
+      (has_b && (bias->ndim != 1 || bias->size[0] != C || bias->stride[0] != 1 || bias->dtype != weight->dtype)))
+    return fail(SAF_EINVAL, "weight and bias must be contiguous (C,) of one dtype");
+  if (weight->dtype != SAF_F32 && weight->dtype != SAF_BF16 && weight->dtype != SAF_F16)
+    return fail(SAF_EUNSUPPORTED, "weight dtype %s is not supported", dtype_name(weight->dtype));
+  if (rows == 0) return SAF_OK;
+  AddLnParams p{};
+  p.x = x->data;
+  p.delta = has_d ? delta->data : nullptr;
+  p.y = out->data;
+  p.w = weight->data;
+  p.b = has_b ? bias->data : nullptr;
+  p.rows = rows;
+  p.C = C;
+  p.x_rs = x->stride[0];
+  p.d_rs = has_d ? delta->stride[0] : 0;
+  p.y_rs = out->stride[0];
+  p.eps = eps;
+  p.wb_dtype = weight->dtype;
+  auto al16 = [&](const saf_tensor_t& t) {
+    return reinterpret_cast<uintptr_t>(t.data) % 16 == 0 && (t.size[0] <= 1 || (t.stride[0] * 2) % 16 == 0);
+  };
+  p.vec16 = C % 256 == 0 && al16(*x) && al16(*out) && (!has_d || al16(*delta)) &&
+            reinterpret_cast<uintptr_t>(weight->data) % 16 == 0 &&
+            (!has_b || reinterpret_cast<uintptr_t>(bias->data) % 16 == 0);
+  p.rms = rms ? 1 : 0;
+  return launched(launch_add_layernorm(p, x->dtype, reinterpret_cast<hipStream_t>(stream)), what);
+}
+
 }  // namespace
 
 extern "C" {
@@ -988,55 +1042,12 @@ int saf_qk_rmsnorm_rope_inplace(const saf_tensor_t* q, const saf_tensor_t* k, co
 
 int saf_add_layernorm(const saf_tensor_t* x, const saf_tensor_t* delta, const saf_tensor_t* weight,
                       const saf_tensor_t* bias, float eps, const saf_tensor_t* out, void* stream) {
-  if (x == nullptr || weight == nullptr || out == nullptr || !present(*x) || !present(*weight) || !present(*out))
-    return fail(SAF_EINVAL, "x, weight and out are required");
-  const bool has_d = delta != nullptr && present(*delta);
-  const bool has_b = bias != nullptr && present(*bias);
-  if (x->ndim != 2 || out->ndim != 2 || (has_d && delta->ndim != 2))
-    return fail(SAF_EINVAL, "x, delta and out must be 2-D (rows, C)");
-  if (x->dtype != SAF_BF16 && x->dtype != SAF_F16)
-    return fail(SAF_EUNSUPPORTED, "add_layernorm supports bf16 / fp16 activations (got %s)", dtype_name(x->dtype));
-  const int64_t rows = x->size[0], C = x->size[1];
-  if (out->dtype != x->dtype || out->size[0] != rows || out->size[1] != C)
-    return fail(SAF_EINVAL, "out must match x in shape and dtype");
-  if (has_d && (delta->dtype != x->dtype || delta->size[0] != rows || delta->size[1] != C))
-    return fail(SAF_EINVAL, "delta must match x in shape and dtype");
-  if (x->stride[1] != 1 || out->stride[1] != 1 || (has_d && delta->stride[1] != 1))
-    return fail(SAF_EALIGN, "x, delta and out need a unit channel stride");
-  if (C < 2 || C > 2048 || C % 2 != 0)
-    return fail(SAF_EUNSUPPORTED, "add_layernorm: C = %lld is not supported (even, at most 2048)", (long long)C);
-  const int vec_bytes = (C % 256 == 0 ? 4 : 2) * 2;
-  auto aligned = [&](const saf_tensor_t& t) {
-    return reinterpret_cast<uintptr_t>(t.data) % vec_bytes == 0 && (t.size[0] <= 1 || (t.stride[0] * 2) % vec_bytes == 0);
-  };
-  if (!aligned(*x) || !aligned(*out) || (has_d && !aligned(*delta)))
-    return fail(SAF_EALIGN, "x, delta and out rows must be %d-byte aligned", vec_bytes);
-  if (weight->ndim != 1 || weight->size[0] != C || weight->stride[0] != 1 ||
-      (has_b && (bias->ndim != 1 || bias->size[0] != C || bias->stride[0] != 1 || bias->dtype != weight->dtype)))
-    return fail(SAF_EINVAL, "weight and bias must be contiguous (C,) of one dtype");
-  if (weight->dtype != SAF_F32 && weight->dtype != SAF_BF16 && weight->dtype != SAF_F16)
-    return fail(SAF_EUNSUPPORTED, "weight dtype %s is not supported", dtype_name(weight->dtype));
-  if (rows == 0) return SAF_OK;
-  AddLnParams p{};
-  p.x = x->data;
-  p.delta = has_d ? delta->data : nullptr;
-  p.y = out->data;
-  p.w = weight->data;
-  p.b = has_b ? bias->data : nullptr;
-  p.rows = rows;
-  p.C = C;
-  p.x_rs = x->stride[0];
-  p.d_rs = has_d ? delta->stride[0] : 0;
-  p.y_rs = out->stride[0];
-  p.eps = eps;
-  p.wb_dtype = weight->dtype;
-  auto al16 = [&](const saf_tensor_t& t) {
-    return reinterpret_cast<uintptr_t>(t.data) % 16 == 0 && (t.size[0] <= 1 || (t.stride[0] * 2) % 16 == 0);
-  };
-  p.vec16 = C % 256 == 0 && al16(*x) && al16(*out) && (!has_d || al16(*delta)) &&
-            reinterpret_cast<uintptr_t>(weight->data) % 16 == 0 &&
-            (!has_b || reinterpret_cast<uintptr_t>(bias->data) % 16 == 0);
-  return launched(launch_add_layernorm(p, x->dtype, reinterpret_cast<hipStream_t>(stream)), "add_layernorm");
+  return add_norm("add_layernorm", false, x, delta, weight, bias, eps, out, stream);
+}
+
+int saf_add_rmsnorm(const saf_tensor_t* x, const saf_tensor_t* delta, const saf_tensor_t* weight, float eps,
+                    const saf_tensor_t* out, void* stream) {
+  return add_norm("add_rmsnorm", true, x, delta, weight, nullptr, eps, out, stream);
 }
 
 int saf_linear_gelu(const saf_tensor_t* x, const saf_tensor_t* weight, const saf_tensor_t* out, void* stream) {

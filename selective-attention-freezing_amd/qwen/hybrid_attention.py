@@ -473,6 +473,37 @@ def _fuse_block_mlp(block, saved):
     saved.append((mlp, "forward", _PLAIN_FORWARD))
 
 
+# transformers' RMSNorm classes with Qwen3RMSNorm's function
+# (weight * round(x * rsqrt(mean(x^2) + eps))); Qwen3.5's (1 + w) norm is not one
+_RMSNORM_CLASSES = ("Qwen3RMSNorm", "Qwen2RMSNorm", "LlamaRMSNorm")
+
+
+def _rmsnorm_fusable(mod):
+    w = getattr(mod, "weight", None)
+    return (type(mod).__name__ in _RMSNORM_CLASSES and isinstance(w, torch.Tensor) and w.dim() == 1
+            and hasattr(mod, "variance_epsilon"))
+
+
+def _fused_rmsnorm_forward(mod, x):
+    """Qwen3RMSNorm.forward as one HIP kernel (fp32 statistics, the same two
+    roundings) on the no-grad device path; torch's ops otherwise."""
+    C = x.size(-1)
+    if (not torch.is_grad_enabled() and x.is_cuda and x.dtype in (torch.bfloat16, torch.float16)
+            and mod.weight.dtype == x.dtype and C % 2 == 0 and C <= 2048 and x.is_contiguous()):
+        return _kernel_mod.add_rmsnorm_(x, None, mod.weight, mod.variance_epsilon)
+    input_dtype = x.dtype
+    h = x.to(torch.float32)
+    h = h * torch.rsqrt(h.pow(2).mean(-1, keepdim=True) + mod.variance_epsilon)
+    return mod.weight * h.to(input_dtype)
+
+
+def _fuse_norm(mod, saved):
+    if mod is None or "forward" in mod.__dict__ or not _rmsnorm_fusable(mod):
+        return
+    mod.forward = lambda x, _m=mod: _fused_rmsnorm_forward(_m, x)
+    saved.append((mod, "forward", _PLAIN_FORWARD))
+
+
 def convert_targets_to_hybrid(model, targets, mean_attn, head_masks, device, dtype,
                               use_triton=True, assume_causal_prefill=False, decomp=None,
                               fuse_live_only=False):
@@ -497,9 +528,11 @@ def convert_targets_to_hybrid(model, targets, mean_attn, head_masks, device, dty
             blocks = blocks or iter_blocks(model)
             parent = blocks[t.layer_idx]
         original = getattr(parent, t.attr_name)
-        # the block's gated MLP (same function, one HIP kernel for its gate /
-        # up half on the prefill path) whatever its heads
+        # the block's gated MLP and RMSNorms (same functions, one HIP kernel
+        # each on the prefill path) whatever its heads
         _fuse_block_mlp(parent, saved)
+        _fuse_norm(getattr(parent, "input_layernorm", None), saved)
+        _fuse_norm(getattr(parent, "post_attention_layernorm", None), saved)
         if not bool(torch.as_tensor(mask).any()) and not fuse_live_only:
             saved.append((parent, t.attr_name, None))
             continue
@@ -513,6 +546,9 @@ def convert_targets_to_hybrid(model, targets, mean_attn, head_masks, device, dty
         hybrid.train(original.training)
         setattr(parent, t.attr_name, hybrid)
         saved.append((parent, t.attr_name, original))
+    # the backbone's final norm
+    backbone = getattr(model, "model", model)
+    _fuse_norm(getattr(backbone, "norm", None), saved)
     return saved
 
 

@@ -83,3 +83,43 @@ def test_add_layernorm_alignment_paths(C, rows, offset):
                               round_fn=_round(torch.bfloat16))
     err = np.abs(y.double().cpu().numpy() - yr).max()
     assert err <= 3e-2, f"C={C} rows={rows} offset={offset}: max-abs {err:.3e}"
+
+
+@pytest.mark.parametrize("C", [64, 130, 768, 896, 1024, 2048])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("with_delta", [True, False])
+def test_add_rmsnorm_matches_oracle(C, dtype, with_delta):
+    """saf_add_rmsnorm against the oracle's restatement of transformers'
+    Qwen3RMSNorm (with its intermediate rounding) and the residual update."""
+    import kernel
+    g = torch.Generator().manual_seed(C + (3 if with_delta else 0))
+    rows = 37 if C > 1000 else 1000
+    x = (torch.randn(rows, C, generator=g) * 2 + 0.5).to(dtype)
+    d = torch.randn(rows, C, generator=g).to(dtype) if with_delta else None
+    w = (1 + 0.1 * torch.randn(C, generator=g)).to(dtype)
+    xd = x.cuda()
+    y = kernel.add_rmsnorm_(xd, None if d is None else d.cuda(), w.cuda(), 1e-6)
+    torch.cuda.synchronize()
+    ref_x = (x.cuda() + d.cuda()).cpu() if with_delta else x
+    assert torch.equal(xd.cpu(), ref_x), "residual update must be bit-exact with torch's add"
+    _, yr = orc.add_rmsnorm(x.double().numpy(), None if d is None else d.double().numpy(), w.double().numpy(), 1e-6,
+                            round_fn=_round(dtype))
+    err = np.abs(y.double().cpu().numpy() - yr).max()
+    tol = 3e-2 if dtype == torch.bfloat16 else 4e-3   # the final rounding (and a flip of the intermediate one)
+    assert err <= tol, f"C={C} {dtype}: max-abs {err:.3e} > {tol}"
+
+
+def test_add_rmsnorm_is_transformers_qwen3_rmsnorm_on_device():
+    """Against transformers' Qwen3RMSNorm module run by torch on the GPU in
+    bf16 (the C4 model's norms: C = 896)."""
+    import kernel
+    from transformers.models.qwen3.modeling_qwen3 import Qwen3RMSNorm
+    norm = Qwen3RMSNorm(896, eps=1e-6).cuda().to(torch.bfloat16)
+    with torch.no_grad():
+        norm.weight.copy_(1 + 0.2 * torch.randn(896, device="cuda"))
+        x = torch.randn(4, 4096, 896, device="cuda").to(torch.bfloat16)
+        ref = norm(x)
+    y = kernel.add_rmsnorm_(x.clone(), None, norm.weight, 1e-6)
+    diff = (y.float() - ref.float()).abs()
+    assert diff.max().item() <= 2 * 2.0 ** -8 * ref.float().abs().max().item()
+    assert (diff == 0).float().mean().item() > 0.99, "nearly every output equals torch's to the bit"

@@ -231,6 +231,23 @@ def test_add_layernorm_matches_torch_layer_norm():
     assert np.allclose(y1.mean(-1), 0, atol=1e-12) and np.allclose(y1.var(-1), 1 / (1 + 1e-5 / (x + d).numpy().var(-1)))
 
 
+def test_add_rmsnorm_matches_transformers_qwen3_rmsnorm():
+    # the library special case: transformers' own Qwen3RMSNorm module in float64
+    from transformers.models.qwen3.modeling_qwen3 import Qwen3RMSNorm
+    g = torch.Generator().manual_seed(17)
+    x, d = torch.randn(5, 96, generator=g, dtype=torch.float64), torch.randn(5, 96, generator=g, dtype=torch.float64)
+    norm = Qwen3RMSNorm(96, eps=1e-6).double()
+    with torch.no_grad():
+        norm.weight.copy_(torch.randn(96, generator=g, dtype=torch.float64))
+        ref = norm(x + d)
+    xn, y = orc.add_rmsnorm(x.numpy(), d.numpy(), norm.weight.detach().numpy(), 1e-6)
+    assert np.allclose(xn, (x + d).numpy()) and np.allclose(y, ref.numpy(), atol=1e-12)
+    # scale invariance with eps = 0, unit mean square with unit weight
+    _, y1 = orc.add_rmsnorm(x.numpy(), None, np.ones(96), 0.0)
+    _, y2 = orc.add_rmsnorm(3.5 * x.numpy(), None, np.ones(96), 0.0)
+    assert np.allclose(y1, y2, atol=1e-12) and np.allclose((y1 ** 2).mean(-1), 1.0, atol=1e-12)
+
+
 def test_linear_gelu_matches_torch_and_the_normal_cdf():
     # the library special case: torch's exact GELU of the float64 product
     g = torch.Generator().manual_seed(11)
