@@ -29,6 +29,25 @@ template <typename T> struct Vec<T, 4> {
     return r;
   }
 };
+template <typename T> struct Vec<T, 8> {
+  using raw = uint4;
+  __device__ static inline void unpack(raw r, float (&f)[8]) {
+    const uint32_t w[4] = {r.x, r.y, r.z, r.w};
+#pragma unroll
+    for (int m = 0; m < 4; ++m) {
+      f[2 * m] = Elem<T>::lo(w[m]);
+      f[2 * m + 1] = Elem<T>::hi(w[m]);
+    }
+  }
+  __device__ static inline raw pack(const float (&f)[8]) {
+    raw r;
+    r.x = Elem<T>::pack2(f[0], f[1]);
+    r.y = Elem<T>::pack2(f[2], f[3]);
+    r.z = Elem<T>::pack2(f[4], f[5]);
+    r.w = Elem<T>::pack2(f[6], f[7]);
+    return r;
+  }
+};
 template <typename T> struct Vec<T, 2> {
   using raw = uint32_t;
   __device__ static inline void unpack(raw r, float (&f)[2]) { f[0] = Elem<T>::lo(r); f[1] = Elem<T>::hi(r); }
@@ -42,6 +61,28 @@ __device__ inline float wave_sum(float v) {
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
   return v;
+}
+
+// Eight channels of a weight / bias vector as fp32, from fp32, bf16 or fp16.
+__device__ inline void load8_f32(const void* p, int c, int dtype, float (&f)[8]) {
+  if (dtype == kF32) {
+    const float4 a = *reinterpret_cast<const float4*>(reinterpret_cast<const float*>(p) + c);
+    const float4 b = *reinterpret_cast<const float4*>(reinterpret_cast<const float*>(p) + c + 4);
+    f[0] = a.x; f[1] = a.y; f[2] = a.z; f[3] = a.w; f[4] = b.x; f[5] = b.y; f[6] = b.z; f[7] = b.w;
+    return;
+  }
+  const uint4 r = *reinterpret_cast<const uint4*>(reinterpret_cast<const uint16_t*>(p) + c);
+  const uint32_t w[4] = {r.x, r.y, r.z, r.w};
+#pragma unroll
+  for (int m = 0; m < 4; ++m) {
+    if (dtype == kBF16) {
+      f[2 * m] = Elem<__bf16>::lo(w[m]);
+      f[2 * m + 1] = Elem<__bf16>::hi(w[m]);
+    } else {
+      f[2 * m] = Elem<_Float16>::lo(w[m]);
+      f[2 * m + 1] = Elem<_Float16>::hi(w[m]);
+    }
+  }
 }
 
 template <typename T, int VEC, int NCH>
@@ -95,36 +136,23 @@ __global__ __launch_bounds__(256) void add_layernorm_kernel(const AddLnParams p)
   for (int k = 0; k < NCH; ++k) {
     const int c = VEC * (64 * k + lane);
     if (c >= C) continue;
-    float o[VEC];
+    float o[VEC], w[VEC], b[VEC];
+    if constexpr (VEC == 8) {  // 16-byte aligned weight / bias (the host checks)
+      load8_f32(p.w, c, p.wb_dtype, w);
+      if (p.b) load8_f32(p.b, c, p.wb_dtype, b);
+    } else {
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) {
+        w[e] = load_as_f32(p.w, c + e, p.wb_dtype);
+        if (p.b) b[e] = load_as_f32(p.b, c + e, p.wb_dtype);
+      }
+    }
 #pragma unroll
     for (int e = 0; e < VEC; ++e) {
-      const float w = load_as_f32(p.w, c + e, p.wb_dtype);
-      const float b = p.b ? load_as_f32(p.b, c + e, p.wb_dtype) : 0.f;
-      o[e] = p.rms ? round_to_elem<T>(v[k][e] * rstd) * w : fmaf((v[k][e] - mean) * rstd, w, b);
+      const float be = p.b ? b[e] : 0.f;
+      o[e] = p.rms ? round_to_elem<T>(v[k][e] * rstd) * w[e] : fmaf((v[k][e] - mean) * rstd, w[e], be);
     }
     *reinterpret_cast<raw*>(yr + c) = V::pack(o);
-  }
-}
-
-// Eight channels of a weight / bias vector as fp32, from fp32, bf16 or fp16.
-__device__ inline void load8_f32(const void* p, int c, int dtype, float (&f)[8]) {
-  if (dtype == kF32) {
-    const float4 a = *reinterpret_cast<const float4*>(reinterpret_cast<const float*>(p) + c);
-    const float4 b = *reinterpret_cast<const float4*>(reinterpret_cast<const float*>(p) + c + 4);
-    f[0] = a.x; f[1] = a.y; f[2] = a.z; f[3] = a.w; f[4] = b.x; f[5] = b.y; f[6] = b.z; f[7] = b.w;
-    return;
-  }
-  const uint4 r = *reinterpret_cast<const uint4*>(reinterpret_cast<const uint16_t*>(p) + c);
-  const uint32_t w[4] = {r.x, r.y, r.z, r.w};
-#pragma unroll
-  for (int m = 0; m < 4; ++m) {
-    if (dtype == kBF16) {
-      f[2 * m] = Elem<__bf16>::lo(w[m]);
-      f[2 * m + 1] = Elem<__bf16>::hi(w[m]);
-    } else {
-      f[2 * m] = Elem<_Float16>::lo(w[m]);
-      f[2 * m + 1] = Elem<_Float16>::hi(w[m]);
-    }
   }
 }
 
@@ -225,8 +253,10 @@ static hipError_t launch_ln_t(const AddLnParams& p, hipStream_t s) {
   return hipGetLastError();
 }
 
-// Channel layouts: multiples of 256 use 8-byte chunks (VEC 4), other even C
-// up to 2048 4-byte chunks (VEC 2) with the tail lanes idle.
+// Channel layouts: multiples of 256 use 8-byte chunks (VEC 4); other
+// multiples of 8 with 16-byte aligned rows 16-byte chunks (VEC 8: C = 896 of
+// the Qwen caller is 1.75 chunks per lane); other even C up to 2048 4-byte
+// chunks (VEC 2); the tail lanes idle.
 template <typename T>
 static hipError_t launch_ln_dt(const AddLnParams& p, hipStream_t s) {
   if (p.vec16) {
@@ -252,6 +282,15 @@ static hipError_t launch_ln_dt(const AddLnParams& p, hipStream_t s) {
       case 6: return launch_ln_t<T, 4, 6>(p, s);
       case 7: return launch_ln_t<T, 4, 7>(p, s);
       case 8: return launch_ln_t<T, 4, 8>(p, s);
+      default: return hipErrorInvalidValue;
+    }
+  }
+  if (p.vec16_rows && p.C % 8 == 0) {
+    switch ((p.C + 511) / 512) {
+      case 1: return launch_ln_t<T, 8, 1>(p, s);
+      case 2: return launch_ln_t<T, 8, 2>(p, s);
+      case 3: return launch_ln_t<T, 8, 3>(p, s);
+      case 4: return launch_ln_t<T, 8, 4>(p, s);
       default: return hipErrorInvalidValue;
     }
   }

@@ -865,9 +865,10 @@ int add_norm(const char* what, bool rms, const saf_tensor_t* x, const saf_tensor
   auto al16 = [&](const saf_tensor_t& t) {
     return reinterpret_cast<uintptr_t>(t.data) % 16 == 0 && (t.size[0] <= 1 || (t.stride[0] * 2) % 16 == 0);
   };
-  p.vec16 = C % 256 == 0 && al16(*x) && al16(*out) && (!has_d || al16(*delta)) &&
-            reinterpret_cast<uintptr_t>(weight->data) % 16 == 0 &&
-            (!has_b || reinterpret_cast<uintptr_t>(bias->data) % 16 == 0);
+  p.vec16_rows = al16(*x) && al16(*out) && (!has_d || al16(*delta)) &&
+                 reinterpret_cast<uintptr_t>(weight->data) % 16 == 0 &&
+                 (!has_b || reinterpret_cast<uintptr_t>(bias->data) % 16 == 0);
+  p.vec16 = C % 256 == 0 && p.vec16_rows;
   p.rms = rms ? 1 : 0;
   return launched(launch_add_layernorm(p, x->dtype, reinterpret_cast<hipStream_t>(stream)), what);
 }

@@ -178,6 +178,9 @@ struct AddLnParams {
   // C % 256 == 0, every row and the weight / bias 16-byte aligned: the
   // half-wave-per-row kernel with 16-byte pieces
   int vec16;
+  // every row and the weight / bias 16-byte aligned (any C): 16-byte chunks
+  // when C % 8 == 0
+  int vec16_rows;
   // RMSNorm instead (Qwen3RMSNorm): y = w * round(x * rsqrt(mean(x^2) + eps)),
   // no centring, no bias, the normalised x rounded to the activation dtype
   // before the weight multiplies it and the product rounded again
