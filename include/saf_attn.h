@@ -261,6 +261,14 @@ int saf_add_rmsnorm(const saf_tensor_t* x, const saf_tensor_t* delta, const saf_
  * gelu in MLP.forward (nanogpt/model.py:1202-1204) on the prefill path. */
 int saf_linear_gelu(const saf_tensor_t* x, const saf_tensor_t* weight, const saf_tensor_t* out, void* stream);
 
+/* Exact GELU (nn.GELU()) of a contiguous bf16 / fp16 tensor x in place:
+ * x <- x Phi(x), in fp32 (the polynomial / A&S evaluation of
+ * saf_linear_gelu, within 5.3e-6 of exact), one rounding; the element count a
+ * multiple of 8 and x 16-byte aligned.  For the MLP whose up-projection runs
+ * as a library GEMM (K above the fused kernel's range): replaces the GELU of
+ * MLP.forward (nanogpt/model.py:1204). */
+int saf_gelu_inplace(const saf_tensor_t* x, void* stream);
+
 /* SwiGLU half of a gated MLP in one kernel: out = silu(x Wg^T) * (x Wu^T),
  * silu(u) = u / (1 + e^-u), for x (M, K) and weight (N, K) holding the gate
  * and up rows interleaved in blocks of 64 (gate rows 64b..64b+63, then up

@@ -389,6 +389,46 @@ void proj_gemm_kernel(const ProjGemmParams p) {
 
 }  // namespace
 
+namespace {
+
+// In-place exact GELU over n elements (n % 8 == 0, 16-byte aligned), for a
+// GEMM output that the fused kernel does not produce (the 1B-class model's
+// MLP at K = 2048): eight elements per thread and grid-stride step, the
+// polynomial for every group of eight whose wave holds no value beyond its
+// range, else the tail formula, as the fused epilogue.
+template <typename T>
+__global__ __launch_bounds__(256) void gelu_inplace_kernel(T* x, int64_t n8) {
+  uint4* v = reinterpret_cast<uint4*>(x);
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n8; i += (int64_t)gridDim.x * 256) {
+    const uint4 r = v[i];
+    const uint32_t w[4] = {r.x, r.y, r.z, r.w};
+    float y[8];
+#pragma unroll
+    for (int m = 0; m < 4; ++m) {
+      y[2 * m] = Elem<T>::lo(w[m]);
+      y[2 * m + 1] = Elem<T>::hi(w[m]);
+    }
+    gelu_group(y);
+    v[i] = make_uint4(Elem<T>::pack2(y[0], y[1]), Elem<T>::pack2(y[2], y[3]), Elem<T>::pack2(y[4], y[5]),
+                      Elem<T>::pack2(y[6], y[7]));
+  }
+}
+
+}  // namespace
+
+hipError_t launch_gelu_inplace(void* x, int64_t n, int dtype, int n_cu, hipStream_t s) {
+  const int64_t n8 = n / 8;
+  const unsigned grid = (unsigned)std::min<int64_t>((n8 + 255) / 256, (int64_t)n_cu * 16);
+  if (n8 == 0) return hipSuccess;
+  if (dtype == kBF16)
+    hipLaunchKernelGGL(gelu_inplace_kernel<__bf16>, dim3(grid), dim3(256), 0, s, reinterpret_cast<__bf16*>(x), n8);
+  else if (dtype == kF16)
+    hipLaunchKernelGGL(gelu_inplace_kernel<_Float16>, dim3(grid), dim3(256), 0, s, reinterpret_cast<_Float16*>(x), n8);
+  else
+    return hipErrorInvalidValue;
+  return hipGetLastError();
+}
+
 bool proj_gemm_shape_ok(int64_t M, int64_t N, int64_t K) {
   return M > 0 && N > 0 && K > 0 && N % kGBN == 0 && K % (kGBK * kGStages) == 0;
 }

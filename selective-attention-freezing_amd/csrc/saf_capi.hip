@@ -1059,6 +1059,23 @@ int saf_linear_gelu(const saf_tensor_t* x, const saf_tensor_t* weight, const saf
   return launched(timed([&] { return launch_gemm_gelu(p, x->dtype, s); }, s), "linear_gelu");
 }
 
+int saf_gelu_inplace(const saf_tensor_t* x, void* stream) {
+  if (x == nullptr || !present(*x)) return fail(SAF_EINVAL, "x is required");
+  if (x->dtype != SAF_BF16 && x->dtype != SAF_F16)
+    return fail(SAF_EUNSUPPORTED, "gelu_inplace supports bf16 / fp16 (got %s)", dtype_name(x->dtype));
+  int64_t n = 1, expect = 1;
+  for (int d = x->ndim - 1; d >= 0; --d) {
+    if (x->size[d] != 1 && x->stride[d] != expect) return fail(SAF_EALIGN, "gelu_inplace needs a contiguous x");
+    expect *= x->size[d];
+    n *= x->size[d];
+  }
+  if (n == 0) return SAF_OK;
+  if (n % 8 != 0 || reinterpret_cast<uintptr_t>(x->data) % 16 != 0)
+    return fail(SAF_EALIGN, "gelu_inplace needs a 16-byte aligned x of a multiple of 8 elements");
+  return launched(launch_gelu_inplace(x->data, n, x->dtype, cu_count(), reinterpret_cast<hipStream_t>(stream)),
+                  "gelu_inplace");
+}
+
 int saf_linear_swiglu(const saf_tensor_t* x, const saf_tensor_t* weight, const saf_tensor_t* out, void* stream) {
   ProjGemmParams p{};
   if (int rc = proj_common("linear_swiglu", x, weight, out, p, 2)) return rc;

@@ -223,6 +223,8 @@ hipError_t launch_zero_u32(uint32_t* ptr, int64_t n, hipStream_t s);
 hipError_t launch_rope(const RopeParams& p, int dtype, hipStream_t s);
 hipError_t launch_add_layernorm(const AddLnParams& p, int dtype, hipStream_t s);
 bool proj_gemm_shape_ok(int64_t M, int64_t N, int64_t K);
+// exact GELU in place over n elements (n % 8 == 0, 16-byte aligned)
+hipError_t launch_gelu_inplace(void* x, int64_t n, int dtype, int n_cu, hipStream_t s);
 hipError_t launch_gemm_gelu(const ProjGemmParams& p, int dtype, hipStream_t s);
 hipError_t launch_gemm_rope(const ProjGemmParams& p, int dtype, hipStream_t s);
 // SwiGLU: w holds 64-row blocks of gate and up rows in turn; c is (M, N / 2)

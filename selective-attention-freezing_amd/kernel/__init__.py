@@ -15,7 +15,7 @@ from .frozen_attn import frozen_pv, frozen_pv_usable, HAVE_TRITON
 from .indexed_linear import linear_rows, linear_rows2, linear_permuted_cols
 from .rope import rope_qk_, qk_rmsnorm_rope_
 from .layernorm import add_layernorm_, add_rmsnorm_
-from .projection import (linear_gelu, linear_gelu_usable, linear_rope, linear_rope_usable, linear_swiglu,
+from .projection import (gelu_, gelu_usable, linear_gelu, linear_gelu_usable, linear_rope, linear_rope_usable, linear_swiglu,
                          linear_swiglu_usable, swiglu_weight)
 from .fused_attn import (fused_mixed_attn, fused_attn_usable, decomposed_logz,
                          decomp_log_normalizers, decomp_log_normalizers_fft,
@@ -30,5 +30,5 @@ __all__ = ["frozen_pv", "frozen_pv_usable", "HAVE_TRITON",
            "decomp_logits", "make_rho_band", "BAND_ROWS",
            "classify_closed_form", "CLOSED_NONE", "CLOSED_MEAN",
            "CLOSED_DECAY", "CLOSED_WINDOW", "KernelTimer", "set_kernel_timer",
-           "rope_qk_", "qk_rmsnorm_rope_", "add_layernorm_", "add_rmsnorm_", "linear_gelu", "linear_gelu_usable",
+           "rope_qk_", "qk_rmsnorm_rope_", "add_layernorm_", "add_rmsnorm_", "gelu_", "gelu_usable", "linear_gelu", "linear_gelu_usable",
            "linear_rope", "linear_rope_usable", "linear_swiglu", "linear_swiglu_usable", "swiglu_weight"]

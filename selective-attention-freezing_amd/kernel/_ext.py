@@ -25,7 +25,7 @@ EXPORTS = ("saf_mixed_attn_fwd", "saf_mixed_attn_fwd_noalloc", "saf_flash_fwd", 
            "saf_mixed_attn_bwd_workspace_bytes", "saf_decomp_param_bwd", "saf_decomp_param_bwd_workspace_bytes",
            "saf_frozen_pv_fwd", "saf_frozen_pv_bwd",
            "saf_rope_qk_inplace", "saf_qk_rmsnorm_rope_inplace", "saf_add_layernorm",
-           "saf_add_rmsnorm", "saf_linear_gelu", "saf_linear_swiglu", "saf_linear_rope", "saf_decomposed_logz",
+           "saf_add_rmsnorm", "saf_linear_gelu", "saf_gelu_inplace", "saf_linear_swiglu", "saf_linear_rope", "saf_decomposed_logz",
            "saf_decomposed_logz_bwd", "saf_workspace_bytes", "saf_mixed_attn_workspace_bytes", "saf_workspace_error",
            "saf_time_next_kernel", "saf_last_error", "saf_version")
 
@@ -104,6 +104,8 @@ def lib():
         L.saf_add_rmsnorm.restype = ctypes.c_int
         L.saf_linear_gelu.argtypes = [P(SafTensor)] * 3 + [ctypes.c_void_p]
         L.saf_linear_gelu.restype = ctypes.c_int
+        L.saf_gelu_inplace.argtypes = [P(SafTensor), ctypes.c_void_p]
+        L.saf_gelu_inplace.restype = ctypes.c_int
         L.saf_linear_swiglu.argtypes = [P(SafTensor)] * 3 + [ctypes.c_void_p]
         L.saf_linear_swiglu.restype = ctypes.c_int
         L.saf_linear_rope.argtypes = [P(SafTensor)] * 3 + [ctypes.c_int32] * 3 + [P(SafTensor)] * 2 + [ctypes.c_void_p]

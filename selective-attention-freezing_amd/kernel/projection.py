@@ -6,6 +6,8 @@ into one HIP kernel each (libsafattn.so, forward only, no bias).
   erf-based GELU).  The reference's up-projection writes its (rows, 4 C)
   output and the activation reads and writes it again; here the GELU runs on
   the GEMM's fp32 accumulator and the activation is written once, rounded once.
+* ``gelu_`` (``saf_gelu_inplace``): the same GELU evaluation in place on a
+  GEMM output, for MLPs whose up-projection stays a library GEMM.
 * ``linear_swiglu`` (``saf_linear_swiglu``): ``act_fn(gate_proj(x)) *
   up_proj(x)`` of transformers' Qwen3MLP (SiLU), the MLP of the Qwen caller,
   from one GEMM over the gate and up rows interleaved in blocks of 64
@@ -44,6 +46,24 @@ def _rows(x, weight):
 def linear_gelu_usable(x, weight):
     """True when linear_gelu runs x (..., K) against weight (N, K)."""
     return _gemm_usable(x, weight)
+
+
+def gelu_usable(x):
+    """True when gelu_ runs on x in place."""
+    return (x.is_cuda and x.dtype in (torch.bfloat16, torch.float16) and x.is_contiguous()
+            and x.numel() % 8 == 0 and x.data_ptr() % 16 == 0)
+
+
+def gelu_(x):
+    """Exact GELU of x in place (``saf_gelu_inplace``, the fused kernel's
+    evaluation); returns x."""
+    if not x.is_cuda:
+        raise RuntimeError("gelu_ runs on HIP devices only (got a CPU tensor)")
+    if x.numel() == 0:
+        return x
+    L = _ext.lib()
+    _ext.check(L.saf_gelu_inplace(_ext.tensor_desc(x.view(-1)), _ext.current_stream_ptr(x.device)))
+    return x
 
 
 def linear_gelu(x, weight):

@@ -558,12 +558,17 @@ class MLP(nn.Module):
 
     def fc_gelu(self, x):
         """gelu(c_fc(x)) for the prefill path: one HIP kernel (the GELU on
-        the GEMM's fp32 accumulator) when the shape allows, else torch."""
+        the GEMM's fp32 accumulator) when the shape allows; above that K the
+        library GEMM and the HIP GELU in place on its output; else torch."""
         w = self.c_fc.weight
-        if (self.c_fc.bias is None and self.gelu.approximate == "none" and w.size(1) <= self.FUSED_GELU_MAX_K
+        exact = self.gelu.approximate == "none"
+        if (self.c_fc.bias is None and exact and w.size(1) <= self.FUSED_GELU_MAX_K
                 and _kernel_mod.linear_gelu_usable(x, w)):
             return _kernel_mod.linear_gelu(x, w)
-        return self.gelu(self.c_fc(x))
+        u = self.c_fc(x)
+        if exact and _kernel_mod.gelu_usable(u):
+            return _kernel_mod.gelu_(u)
+        return self.gelu(u)
 
 
 class Block(nn.Module):

@@ -120,3 +120,24 @@ def test_linear_gelu_rejections():
     assert kernel.linear_gelu(torch.zeros(0, 128, **bf), torch.zeros(256, 128, **bf)).shape == (0, 256)
     assert not kernel.linear_gelu_usable(torch.zeros(4, 128, **bf), torch.zeros(200, 128, **bf))
     assert kernel.linear_gelu_usable(torch.zeros(4, 768, **bf), torch.zeros(3072, 768, **bf))
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_gelu_inplace_matches_oracle(dtype):
+    """saf_gelu_inplace against the oracle's exact GELU (the linear_gelu
+    restatement with an identity weight), over values that take both the
+    polynomial and the tail formula, and torch's own bf16 / fp16 GELU."""
+    import kernel
+    g = torch.Generator().manual_seed(21)
+    u = (torch.randn(3, 1000, 64, generator=g) * torch.logspace(-3, 1.5, 64)).to(dtype)
+    y = kernel.gelu_(u.cuda().clone())
+    ref = orc.linear_gelu(u.reshape(-1, 1).double().numpy(), np.eye(1)).reshape(u.shape)
+    _check(y.reshape(-1, 64), ref.reshape(-1, 64), dtype, f"gelu_ {dtype}")
+    # torch's own GELU rounds the same exact function once: the two agree to
+    # two roundings plus the evaluations' absolute errors (the kernel's 5.3e-6,
+    # fp32 erf's cancellation in the negative tail)
+    y2 = torch.nn.functional.gelu(u.cuda())
+    assert bool(((y.float() - y2.float()).abs() <= 2 * _RTOL[dtype] * y2.float().abs() + _ATOL).all())
+    assert kernel.gelu_(torch.zeros(0, device="cuda", dtype=dtype)).numel() == 0
+    with pytest.raises(ValueError, match="multiple of 8"):
+        kernel.gelu_(torch.zeros(12, device="cuda", dtype=dtype))
