@@ -504,6 +504,42 @@ def _fuse_norm(mod, saved):
     saved.append((mod, "forward", _PLAIN_FORWARD))
 
 
+def _fused_decoder_forward(layer, hidden_states, attention_mask=None, position_ids=None, past_key_values=None,
+                           use_cache=False, position_embeddings=None, **kwargs):
+    """Qwen3DecoderLayer.forward with the post-attention residual addition
+    inside the post-attention RMSNorm's kernel (saf_add_rmsnorm: the
+    attention output, a fresh tensor, becomes residual + attention in place,
+    one rounding as torch's add, and the norm reads it), on the no-grad device
+    path; the original forward otherwise.  The layer's input is not written."""
+    norm = layer.post_attention_layernorm
+    x = hidden_states
+    if not (not torch.is_grad_enabled() and x.is_cuda and x.dtype in (torch.bfloat16, torch.float16)
+            and x.is_contiguous() and norm.weight.dtype == x.dtype and x.size(-1) % 2 == 0 and x.size(-1) <= 2048):
+        return type(layer).forward(layer, hidden_states, attention_mask=attention_mask, position_ids=position_ids,
+                                   past_key_values=past_key_values, use_cache=use_cache,
+                                   position_embeddings=position_embeddings, **kwargs)
+    h = layer.input_layernorm(x)
+    h, _ = layer.self_attn(hidden_states=h, attention_mask=attention_mask, position_ids=position_ids,
+                           past_key_values=past_key_values, use_cache=use_cache,
+                           position_embeddings=position_embeddings, **kwargs)
+    if not h.is_contiguous() or h.shape != x.shape:
+        h = h + x
+        return h + layer.mlp(layer.post_attention_layernorm(h))
+    normed = _kernel_mod.add_rmsnorm_(h, x, norm.weight, norm.variance_epsilon)
+    out = layer.mlp(normed)
+    out += h
+    return out
+
+
+def _fuse_decoder_layer(block, saved):
+    if (type(block).__name__ != "Qwen3DecoderLayer" or "forward" in block.__dict__
+            or not _rmsnorm_fusable(getattr(block, "post_attention_layernorm", None))
+            or not hasattr(block, "input_layernorm") or not hasattr(block, "mlp")):
+        return
+    block.forward = lambda *a, _b=block, **k: _fused_decoder_forward(_b, *a, **k)
+    saved.append((block, "forward", _PLAIN_FORWARD))
+
+
 def convert_targets_to_hybrid(model, targets, mean_attn, head_masks, device, dtype,
                               use_triton=True, assume_causal_prefill=False, decomp=None,
                               fuse_live_only=False):
@@ -533,6 +569,7 @@ def convert_targets_to_hybrid(model, targets, mean_attn, head_masks, device, dty
         _fuse_block_mlp(parent, saved)
         _fuse_norm(getattr(parent, "input_layernorm", None), saved)
         _fuse_norm(getattr(parent, "post_attention_layernorm", None), saved)
+        _fuse_decoder_layer(parent, saved)
         if not bool(torch.as_tensor(mask).any()) and not fuse_live_only:
             saved.append((parent, t.attr_name, None))
             continue

@@ -127,10 +127,11 @@ def test_c4_heads_model_vs_oracle(rate, repr):
                 p.copy_(1 + 0.2 * torch.randn_like(p))
     sd = {k: v.detach().float().cpu() for k, v in m.state_dict().items()}
     saved, masks = qwen.convert_with_rate(m, rate, T, repr=repr, fuse_live_only=rate == 0.0)
-    # one attention entry per layer, plus each block's fused gated MLP and
-    # two RMSNorms, and the final norm
+    # one attention entry per layer, plus each block's fused gated MLP, two
+    # RMSNorms and its own forward (the post-attention residual add in the
+    # norm's kernel), and the final norm
     assert sum(1 for e in saved if e[1] != "forward") == cfg.num_hidden_layers
-    assert sum(1 for e in saved if e[1] == "forward") == 3 * cfg.num_hidden_layers + 1
+    assert sum(1 for e in saved if e[1] == "forward") == 4 * cfg.num_hidden_layers + 1
     g = torch.Generator().manual_seed(9)
     ids = torch.randint(0, 1024, (2, T), generator=g)
     n0 = qwen.fused_dispatch_count()
