@@ -453,16 +453,21 @@ def _swiglu_weight_cache(mlp):
     return cache[1]
 
 
-def _fused_gated_mlp_forward(mlp, x):
-    """Qwen3MLP.forward with the gate / up half as one HIP kernel (the SiLU
-    and the product on the GEMM's fp32 accumulators) on the no-grad device
-    path; torch's modules otherwise."""
+def _gated_mlp_act(mlp, x):
+    """act_fn(gate_proj(x)) * up_proj(x) of a Qwen3MLP: one HIP kernel (the
+    SiLU and the product on the GEMM's fp32 accumulators) on the no-grad
+    device path, torch's modules otherwise."""
     if (not torch.is_grad_enabled() and x.is_cuda and x.dtype in (torch.bfloat16, torch.float16)
             and x.size(-1) <= FUSED_SWIGLU_MAX_K and mlp.gate_proj.weight.size(0) % 128 == 0):
         w = _swiglu_weight_cache(mlp)
         if _kernel_mod.linear_swiglu_usable(x, w):
-            return mlp.down_proj(_kernel_mod.linear_swiglu(x, w))
-    return mlp.down_proj(mlp.act_fn(mlp.gate_proj(x)) * mlp.up_proj(x))
+            return _kernel_mod.linear_swiglu(x, w)
+    return mlp.act_fn(mlp.gate_proj(x)) * mlp.up_proj(x)
+
+
+def _fused_gated_mlp_forward(mlp, x):
+    """Qwen3MLP.forward with its gate / up half from _gated_mlp_act."""
+    return mlp.down_proj(_gated_mlp_act(mlp, x))
 
 
 def _fuse_block_mlp(block, saved):
@@ -506,11 +511,13 @@ def _fuse_norm(mod, saved):
 
 def _fused_decoder_forward(layer, hidden_states, attention_mask=None, position_ids=None, past_key_values=None,
                            use_cache=False, position_embeddings=None, **kwargs):
-    """Qwen3DecoderLayer.forward with the post-attention residual addition
-    inside the post-attention RMSNorm's kernel (saf_add_rmsnorm: the
+    """Qwen3DecoderLayer.forward with both residual additions fused, on the
+    no-grad device path (the original forward otherwise): the post-attention
+    one inside the post-attention RMSNorm's kernel (saf_add_rmsnorm: the
     attention output, a fresh tensor, becomes residual + attention in place,
-    one rounding as torch's add, and the norm reads it), on the no-grad device
-    path; the original forward otherwise.  The layer's input is not written."""
+    one rounding as torch's add, and the norm reads it), the last one inside
+    the down projection's GEMM (that sum += act W_down^T, beta = 1).  The
+    layer's input is not written."""
     norm = layer.post_attention_layernorm
     x = hidden_states
     if not (not torch.is_grad_enabled() and x.is_cuda and x.dtype in (torch.bfloat16, torch.float16)
@@ -526,7 +533,15 @@ def _fused_decoder_forward(layer, hidden_states, attention_mask=None, position_i
         h = h + x
         return h + layer.mlp(layer.post_attention_layernorm(h))
     normed = _kernel_mod.add_rmsnorm_(h, x, norm.weight, norm.variance_epsilon)
-    out = layer.mlp(normed)
+    mlp = layer.mlp
+    if _gated_mlp_fusable(mlp) and mlp.down_proj.bias is None and mlp.down_proj.weight.dtype == h.dtype:
+        # the block's last residual addition inside the down projection's GEMM
+        # (h += act W_down^T: beta = 1, one rounding), h being the fresh sum
+        act = _gated_mlp_act(mlp, normed)
+        C = h.size(-1)
+        h.view(-1, C).addmm_(act.reshape(-1, act.size(-1)), mlp.down_proj.weight.t())
+        return h
+    out = mlp(normed)
     out += h
     return out
 
